@@ -1,0 +1,103 @@
+// Shared definitions of libaffx.so (gfx950, wave64). Device layout, fp8 helpers, status plumbing.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "../../include/affx.h"
+
+namespace affx {
+
+// ---- format (AFF_Q2P875_Q4): block 16, 10-bit quad codes, 6-bit fields, bf16 row scale -------
+// src/quant/blockquant.cpp:22-30, src/format/aff_format.h:117-121
+constexpr int kBlock = 16;
+constexpr int kLut = 1024;
+constexpr int kVariants = 2;
+
+// ---- device layout ---------------------------------------------------------------------------
+// A "unit" is one row's 256-column segment: 80 bytes of codes (64 codes) + 12 bytes of fields
+// (16 fields), a contiguous byte run of each row-major stream. A wave tile is 16 rows x 1024
+// columns = 64 units, one per lane: lane = (row % 16) + 16 * (segment % 4). Tiles are stored
+// row-tile major, column-tile minor: tile (rt, st) at index rt * (cols / 1024) + st. Inside a
+// tile the code plane holds five 1 KiB chunks [chunk j][lane][16 B] (chunk j = unit bytes
+// 16j..16j+15) and the field plane one 768 B run [lane][12 B].
+constexpr int kTileRows = 16;
+constexpr int kTileCols = 1024;
+constexpr int kSegCols = 256;
+constexpr int kUnitCodeBytes = 80;
+constexpr int kUnitFieldBytes = 12;
+constexpr int kTileCodeBytes = 64 * kUnitCodeBytes;    // 5120
+constexpr int kTileFieldBytes = 64 * kUnitFieldBytes;  // 768
+
+inline uint64_t code_row_bytes(uint64_t cols) { return cols * 10 / 32; }
+inline uint64_t field_row_bytes(uint64_t cols) { return cols * 6 / 128; }
+
+// ---- activations as exact fp8 sums -------------------------------------------------------------
+// An activation v is fed to the fp8 MFMA as kTerms E4M3 values: v * 2^sigma ~= t0 + t1/16 +
+// t2/256, each term in its own B column. Residual after three terms <= 2^-12 relative.
+constexpr int kTerms = 3;
+constexpr int kMaxTok = AFFX_MAX_DECODE_TOKENS;
+constexpr int kMaxSlots = AFFX_MAX_DECODE_TOKENS * AFFX_MAX_TOPK;  // distinct experts of a batch
+
+// Plan the decode prep kernel writes: the distinct experts of the batch (ascending id), which
+// tokens each one serves and with what weight, and each token's activation exponent.
+struct DecodePlan {
+  uint32_t n_slots;
+  uint32_t m_tokens;
+  int32_t x_sigma[kMaxTok];
+  uint32_t expert[kMaxSlots];
+  uint32_t tok_mask[kMaxSlots];
+  float w[kMaxSlots][kMaxTok];
+};
+
+// ---- status ------------------------------------------------------------------------------------
+int set_error(int code, const char* fmt, ...);
+int check_hip(hipError_t e, const char* what);
+int check_launch(const char* what);
+
+// ---- device helpers ----------------------------------------------------------------------------
+
+// Exact E4M3 (OCP fn) -> f32 for a non-NaN byte.
+__device__ __forceinline__ float e4m3_to_f32(uint32_t b) {
+  const uint32_t e = (b >> 3) & 15u, m = b & 7u;
+  float v = e ? __uint_as_float(((e + 120u) << 23) | (m << 20)) : (float)m * 0.001953125f;
+  return __uint_as_float(__float_as_uint(v) | ((b & 0x80u) << 24));
+}
+
+// f32 -> E4M3 (OCP fn), round to nearest even, saturating at +-448 (never NaN).
+__device__ __forceinline__ uint32_t f32_to_e4m3(float v) {
+  const uint32_t s = (__float_as_uint(v) >> 24) & 0x80u;
+  const float a = fabsf(v);
+  if (!(a < 464.0f)) return s | 0x7Eu;
+  if (a < 0.015625f) return s | (uint32_t)rintf(a * 512.0f);  // 8 -> 0x08, the least normal
+  const uint32_t au = __float_as_uint(a);
+  int e = (int)(au >> 23) - 127;
+  uint32_t m3 = (au >> 20) & 7u;
+  const uint32_t rem = au & 0xFFFFFu;
+  if (rem > 0x80000u || (rem == 0x80000u && (m3 & 1u))) {
+    if (++m3 == 8u) { m3 = 0; ++e; }
+  }
+  return s | ((uint32_t)(e + 7) << 3) | m3;
+}
+
+// The packed-dword block transform of the reference decode (src/gpu/expert_kernel.hip:594-617):
+// sign = XOR 0x80 per byte, block scale 2^s = +s on every byte's exponent (stored exponent 1..7
+// plus s <= 7 stays <= 14: no carry, never NaN). Rotation is applied by table choice.
+__device__ __forceinline__ uint32_t block_xor(uint32_t f) { return (f & 8u) ? 0x80808080u : 0u; }
+__device__ __forceinline__ uint32_t block_add(uint32_t f) {
+  return __builtin_amdgcn_perm(0u, (f & 7u) << 3, 0u);  // (s<<3) replicated into all 4 bytes
+}
+
+// Bits [pos, pos+n) of a little-endian stream held in registers (pos, n compile-time after
+// unrolling).
+template <int N>
+__device__ __forceinline__ uint32_t stream_bits(const uint32_t* d, int pos, int n) {
+  const int i = pos >> 5, sh = pos & 31;
+  uint32_t v = d[i] >> sh;
+  if (sh + n > 32 && i + 1 < N) v = __builtin_amdgcn_alignbit(d[i + 1], d[i], sh);
+  return v & ((1u << n) - 1u);
+}
+
+}  // namespace affx

@@ -1,0 +1,579 @@
+// Decode path (M <= 8 tokens, top-k routing): fused unpack -> codebook dequant -> fp8 MFMA for
+// gate/up -> SwiGLU -> down -> weighted combine. Three kernels, stream-ordered:
+//
+//   decode_prep    plan (distinct experts ascending, token masks, summed weights) and every
+//                  token's activation split into three exact-ish E4M3 terms (xq)
+//   decode_gateup  grid (row tile of inter, expert slot); 4 waves = 4 column super-segments;
+//                  gate and up tiles decoded from the packed codes through an LDS codebook and
+//                  multiplied on the fp8 MFMA; fixed-order cross-wave sum, row scale, SwiGLU;
+//                  the activation is written back as E4M3 terms (aq)
+//   decode_down    grid (row tile of hidden); waves stride over (slot, super-segment) units,
+//                  combine terms * row scale * route weight per token, fixed-order cross-wave sum
+//
+// Why fp8 MFMA at batch 1: a decoded weight is a codebook E4M3 byte with +s added to its
+// exponent and the sign flipped, i.e. still an exact E4M3 value, so the weight side needs no
+// conversion at all. The activation side is carried as t0 + t1/16 + t2/256 in three B columns
+// (five tokens per 16-column MFMA), which keeps the product error near 2^-12 relative while the
+// VALU only does code extraction, one LDS lookup and one xor-add per four weights.
+//
+// Reference counterparts: expert_ffn_hip (src/gpu/expert_kernel.hip:2737-2808) with its
+// tr_mat_dot_rb GEMV (1084-1188), swiglu_all_kernel (114-129) and expert_gemv_kernel_tr
+// (1201-1258); the fixed-order reductions follow the reference's no-atomics rule (1219-1244).
+#include "affx_common.h"
+
+namespace affx {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+struct DecodeArgs {
+  const uint8_t* base;  // layer expert pool, device layout
+  uint64_t stride;
+  uint64_t off[9];      // plane offsets inside an expert
+  uint32_t hidden, inter, m_tokens;
+  const uint32_t* codebook;
+  const DecodePlan* plan;
+  const uint8_t* xq;    // [M][3][hidden]
+  uint8_t* aq;          // [slot][M][3][inter]
+  const uint8_t* zeros; // 256 zero bytes: the B source of unused columns
+  float limit;
+  int32_t sigma_a;      // exponent applied to the SwiGLU output before its E4M3 split
+  float* y;
+  uint64_t y_ts, y_ds;
+  int accumulate;
+};
+
+// ------------------------------------------------------------------------------------------------
+// prep
+// ------------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) decode_prep_kernel(const float* __restrict__ x, uint64_t xts,
+                                                          uint64_t xds, uint32_t M,
+                                                          const uint32_t* __restrict__ sel,
+                                                          const float* __restrict__ w, uint32_t K,
+                                                          uint32_t n_experts, uint32_t hidden,
+                                                          DecodePlan* __restrict__ plan,
+                                                          uint8_t* __restrict__ xq,
+                                                          uint8_t* __restrict__ zeros) {
+  const uint32_t t = blockIdx.x, tid = threadIdx.x;
+  __shared__ float red[4];
+  __shared__ uint32_t present[AFFX_MAX_EXPERTS / 32];
+  __shared__ uint32_t prefix[AFFX_MAX_EXPERTS / 32 + 1];
+  __shared__ uint32_t mask_s[kMaxSlots];
+  __shared__ float w_s[kMaxSlots][kMaxTok];
+
+  // ---- token t: exponent and three E4M3 terms --------------------------------------------------
+  float amax = 0.f;
+  for (uint32_t h = tid; h < hidden; h += 256) amax = fmaxf(amax, fabsf(x[t * xts + h * xds]));
+  for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+  if ((tid & 63) == 0) red[tid >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  // amax * 2^sigma in [128, 256): below E4M3's 448, one binade of headroom
+  const int sigma = amax > 0.f ? 7 - ilogbf(amax) : 0;
+  for (uint32_t h4 = tid * 4; h4 < hidden; h4 += 1024) {
+    uint32_t q0 = 0, q1 = 0, q2 = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float v = ldexpf(x[t * xts + (h4 + i) * xds], sigma);
+      const uint32_t b0 = f32_to_e4m3(v);
+      const float r1 = (v - e4m3_to_f32(b0)) * 16.0f;
+      const uint32_t b1 = f32_to_e4m3(r1);
+      const float r2 = (r1 - e4m3_to_f32(b1)) * 16.0f;
+      const uint32_t b2 = f32_to_e4m3(r2);
+      q0 |= b0 << (8 * i);
+      q1 |= b1 << (8 * i);
+      q2 |= b2 << (8 * i);
+    }
+    uint32_t* dst = reinterpret_cast<uint32_t*>(xq + (uint64_t)t * kTerms * hidden + h4);
+    dst[0] = q0;
+    dst[hidden / 4] = q1;
+    dst[2 * (hidden / 4)] = q2;
+  }
+  if (tid == 0) plan->x_sigma[t] = sigma;
+  if (t != 0) return;
+  if (tid < 64) reinterpret_cast<uint32_t*>(zeros)[tid] = 0u;
+
+  // ---- block 0: the plan -----------------------------------------------------------------------
+  for (uint32_t i = tid; i < AFFX_MAX_EXPERTS / 32; i += 256) present[i] = 0;
+  for (uint32_t i = tid; i < kMaxSlots; i += 256) {
+    mask_s[i] = 0;
+#pragma unroll
+    for (int j = 0; j < kMaxTok; ++j) w_s[i][j] = 0.f;
+  }
+  __syncthreads();
+  if (tid < M * K) {
+    const uint32_t e = sel[tid];
+    if (e < n_experts) atomicOr(&present[e >> 5], 1u << (e & 31));
+  }
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t s = 0;
+    for (int i = 0; i < AFFX_MAX_EXPERTS / 32; ++i) { prefix[i] = s; s += __popc(present[i]); }
+    prefix[AFFX_MAX_EXPERTS / 32] = s;
+    plan->n_slots = s;
+    plan->m_tokens = M;
+  }
+  __syncthreads();
+  for (uint32_t e = tid; e < n_experts; e += 256) {
+    const uint32_t word = present[e >> 5];
+    if ((word >> (e & 31)) & 1u) {
+      const uint32_t slot = prefix[e >> 5] + __popc(word & ((1u << (e & 31)) - 1u));
+      plan->expert[slot] = e;
+    }
+  }
+  // token tid sums its (possibly repeated) experts' weights in route order: deterministic
+  if (tid < M) {
+    for (uint32_t j = 0; j < K; ++j) {
+      const uint32_t e = sel[tid * K + j];
+      if (e >= n_experts) continue;
+      const uint32_t word = present[e >> 5];
+      const uint32_t slot = prefix[e >> 5] + __popc(word & ((1u << (e & 31)) - 1u));
+      atomicOr(&mask_s[slot], 1u << tid);
+      w_s[slot][tid] += w[tid * K + j];
+    }
+  }
+  __syncthreads();
+  const uint32_t ns = prefix[AFFX_MAX_EXPERTS / 32];
+  for (uint32_t i = tid; i < ns; i += 256) {
+    plan->tok_mask[i] = mask_s[i];
+#pragma unroll
+    for (int j = 0; j < kMaxTok; ++j) plan->w[i][j] = w_s[i][j];
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// shared pieces of the two GEMV kernels
+// ------------------------------------------------------------------------------------------------
+
+// A unit's packed data: 20 code dwords + 3 field dwords.
+struct Unit {
+  uint32_t c[20];
+  uint32_t f[3];
+};
+
+__device__ __forceinline__ void load_unit(Unit& u, const uint8_t* codes, const uint8_t* fields,
+                                          uint64_t tile, uint32_t lane) {
+  const uint8_t* cp = codes + tile * kTileCodeBytes + lane * 16;
+#pragma unroll
+  for (int j = 0; j < 5; ++j) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(cp + j * 1024));
+    u.c[4 * j] = v[0]; u.c[4 * j + 1] = v[1]; u.c[4 * j + 2] = v[2]; u.c[4 * j + 3] = v[3];
+  }
+  const uint32_t* fp = reinterpret_cast<const uint32_t*>(fields + tile * kTileFieldBytes + lane * 12);
+  u.f[0] = __builtin_nontemporal_load(fp);
+  u.f[1] = __builtin_nontemporal_load(fp + 1);
+  u.f[2] = __builtin_nontemporal_load(fp + 2);
+}
+
+// Makes the unit's registers opaque at this point of the program. Called at the top of every
+// MFMA step, it stops the compiler from hoisting all eight steps' code extraction and address
+// arithmetic (pure ALU, free to move) in front of the first step, which would keep ~100 extra
+// VGPRs live and halve occupancy. No instructions are emitted.
+__device__ __forceinline__ void pin(Unit& u) {
+#pragma unroll
+  for (int i = 0; i < 20; ++i) asm volatile("" : "+v"(u.c[i]));
+#pragma unroll
+  for (int i = 0; i < 3; ++i) asm volatile("" : "+v"(u.f[i]));
+}
+
+// The A fragment of MFMA step m: codes 8m..8m+7 of the unit (blocks 2m, 2m+1), each looked up
+// in the LDS table of its block's (variant, rotation) and xor/add-transformed.
+template <int MSTEP>
+__device__ __forceinline__ v8i decode_a(const Unit& u, const uint32_t* tbl) {
+  v8i a;
+#pragma unroll
+  for (int bb = 0; bb < 2; ++bb) {
+    const int b = 2 * MSTEP + bb;
+    const uint32_t fb = stream_bits<3>(u.f, 6 * b, 6);
+    const uint32_t base = (fb >> 4) << 10;
+    const uint32_t x = block_xor(fb), ad = block_add(fb);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t code = stream_bits<20>(u.c, 10 * (4 * b + i), 10);
+      a[bb * 4 + i] = (int)((tbl[base + code] ^ x) + ad);
+    }
+  }
+  return a;
+}
+
+// B operand of one unit: per lane, 256 consecutive activation bytes of one (token, term) column
+// (MFMA step m reads bytes 32m..32m+31). Lanes whose column is unused (column 15, tokens beyond
+// M or not routed to this expert) read nothing and feed zeros.
+template <int CG>
+struct BSrc {
+  const u32x4* p[CG];
+};
+
+template <int CG>
+__device__ __forceinline__ BSrc<CG> b_source(const uint8_t* src_base, uint64_t term_stride,
+                                             uint64_t col0, uint32_t lane, uint32_t M,
+                                             uint32_t mask, const uint8_t* zeros) {
+  BSrc<CG> s;
+  const uint32_t c = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int cg = 0; cg < CG; ++cg) {
+    const uint32_t t = cg * 5 + c / 3, tau = c % 3;
+    const bool valid = c < 15 && t < M && ((mask >> t) & 1u);
+    s.p[cg] = valid ? reinterpret_cast<const u32x4*>(src_base + (uint64_t)(t * kTerms + tau) * term_stride +
+                                                     col0 + g * kSegCols)
+                    : reinterpret_cast<const u32x4*>(zeros);
+  }
+  return s;
+}
+
+__device__ __forceinline__ v8i b_step(const u32x4* p, int m) {
+  const u32x4 lo = p[2 * m], hi = p[2 * m + 1];
+  v8i v;
+  v[0] = (int)lo[0]; v[1] = (int)lo[1]; v[2] = (int)lo[2]; v[3] = (int)lo[3];
+  v[4] = (int)hi[0]; v[5] = (int)hi[1]; v[6] = (int)hi[2]; v[7] = (int)hi[3];
+  return v;
+}
+
+__device__ __forceinline__ v4f mfma(v8i a, v8i b, v4f c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+}
+
+// LDS codebook: table t = rot + 2*variant (= field >> 4), entry c = codebook dword, rotated by
+// 16 bits for rot = 1 (quad (a,b,c,d) read as (c,d,a,b): src/quant/blockquant.cpp:826-828).
+__device__ __forceinline__ void build_table(uint32_t* tbl, const uint32_t* __restrict__ cb) {
+  for (uint32_t i = threadIdx.x; i < kVariants * kLut; i += blockDim.x) {
+    const uint32_t d = cb[i], v = i >> 10, c = i & 1023u;
+    tbl[(2 * v) * kLut + c] = d;
+    tbl[(2 * v + 1) * kLut + c] = __builtin_amdgcn_alignbit(d, d, 16);
+  }
+}
+
+// y = x - low terms: the value of three E4M3 terms t0 + t1/16 + t2/256 from a lane's column c
+// and its two right neighbours (same 16-lane row group).
+__device__ __forceinline__ float combine_terms(float d) {
+  const float d1 = __shfl_down(d, 1, 16), d2 = __shfl_down(d, 2, 16);
+  return d + d1 * 0.0625f + d2 * 0.00390625f;
+}
+
+// ------------------------------------------------------------------------------------------------
+// gate/up + SwiGLU
+// ------------------------------------------------------------------------------------------------
+template <int CG>
+__global__ void __launch_bounds__(256) decode_gateup_kernel(DecodeArgs A) {
+  const uint32_t slot = blockIdx.y;
+  if (slot >= A.plan->n_slots) return;
+  const uint32_t rt = blockIdx.x, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const uint32_t e = A.plan->expert[slot], mask = A.plan->tok_mask[slot], M = A.m_tokens;
+  const uint8_t* ex = A.base + (uint64_t)e * A.stride;
+  const uint32_t nst = A.hidden / kTileCols;
+
+  __shared__ uint32_t tbl[4 * kLut];
+  __shared__ float part[4][2][CG][16][16];
+
+  v4f acc[2][CG];
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int cg = 0; cg < CG; ++cg) acc[m][cg] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  // one column super-segment per wave (hidden <= 4096); its loads go out before the LDS table
+  // is built, so both overlap
+  const uint32_t S = wv;
+  Unit ug, uu;
+  if (S < nst) {
+    const uint64_t tile = (uint64_t)rt * nst + S;
+    load_unit(ug, ex + A.off[0], ex + A.off[3], tile, lane);
+    load_unit(uu, ex + A.off[1], ex + A.off[4], tile, lane);
+  }
+  build_table(tbl, A.codebook);
+  __syncthreads();
+  if (S < nst) {
+    const BSrc<CG> b = b_source<CG>(A.xq, A.hidden, (uint64_t)S * kTileCols, lane, M, mask, A.zeros);
+    v8i bc[CG];
+#pragma unroll
+    for (int cg = 0; cg < CG; ++cg) bc[cg] = b_step(b.p[cg], 0);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      // operands of step m+1 are requested before step m computes; the scheduling barrier keeps
+      // the compiler from hoisting all eight steps' loads and lookups (register blow-up)
+      v8i bn[CG];
+      if (m < 7) {
+#pragma unroll
+        for (int cg = 0; cg < CG; ++cg) bn[cg] = b_step(b.p[cg], m + 1);
+      }
+      pin(ug);
+      pin(uu);
+      v8i ag, au;
+      switch (m) {
+        case 0: ag = decode_a<0>(ug, tbl); au = decode_a<0>(uu, tbl); break;
+        case 1: ag = decode_a<1>(ug, tbl); au = decode_a<1>(uu, tbl); break;
+        case 2: ag = decode_a<2>(ug, tbl); au = decode_a<2>(uu, tbl); break;
+        case 3: ag = decode_a<3>(ug, tbl); au = decode_a<3>(uu, tbl); break;
+        case 4: ag = decode_a<4>(ug, tbl); au = decode_a<4>(uu, tbl); break;
+        case 5: ag = decode_a<5>(ug, tbl); au = decode_a<5>(uu, tbl); break;
+        case 6: ag = decode_a<6>(ug, tbl); au = decode_a<6>(uu, tbl); break;
+        default: ag = decode_a<7>(ug, tbl); au = decode_a<7>(uu, tbl); break;
+      }
+#pragma unroll
+      for (int cg = 0; cg < CG; ++cg) {
+        acc[0][cg] = mfma(ag, bc[cg], acc[0][cg]);
+        acc[1][cg] = mfma(au, bc[cg], acc[1][cg]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("" ::: "memory");
+      if (m < 7) {
+#pragma unroll
+        for (int cg = 0; cg < CG; ++cg) bc[cg] = bn[cg];
+      }
+    }
+  }
+
+  // accumulator lane l, element v = D[row 4*(l/16)+v][col l%16]
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int cg = 0; cg < CG; ++cg)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) part[wv][m][cg][4 * (lane >> 4) + v][lane & 15] = acc[m][cg][v];
+  __syncthreads();
+
+  const uint32_t tid = threadIdx.x;
+  if (tid < 16 * M) {
+    const uint32_t r = tid & 15, t = tid >> 4;
+    if ((mask >> t) & 1u) {
+      const uint32_t cg = t / 5, col = (t % 5) * 3;
+      const uint32_t nw = nst < 4 ? nst : 4;
+      float s[2];
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        float sum = 0.f;
+        for (uint32_t q = 0; q < nw; ++q)
+          sum += part[q][m][cg][r][col] + part[q][m][cg][r][col + 1] * 0.0625f +
+                 part[q][m][cg][r][col + 2] * 0.00390625f;
+        s[m] = sum;
+      }
+      const uint32_t row = rt * 16 + r;
+      const float rg = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(ex + A.off[2])[row] << 16);
+      const float ru = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(ex + A.off[5])[row] << 16);
+      const int sig = A.plan->x_sigma[t];
+      float g = ldexpf(s[0], -sig) * rg;
+      float u = ldexpf(s[1], -sig) * ru;
+      // SwiGLU with the asymmetric clamp: src/engine/ops.cpp:47-60
+      const float L = A.limit;
+      g = (L < g) ? L : g;
+      const float lo = (-L < u) ? u : -L;
+      u = (lo < L) ? lo : L;
+      const float a = (g / (1.0f + expf(-g))) * u;
+      const float v = ldexpf(a, A.sigma_a);
+      const uint32_t b0 = f32_to_e4m3(v);
+      const float r1 = (v - e4m3_to_f32(b0)) * 16.0f;
+      const uint32_t b1 = f32_to_e4m3(r1);
+      const float r2 = (r1 - e4m3_to_f32(b1)) * 16.0f;
+      const uint32_t b2 = f32_to_e4m3(r2);
+      uint8_t* dst = A.aq + ((uint64_t)(slot * M + t) * kTerms) * A.inter + row;
+      dst[0] = (uint8_t)b0;
+      dst[A.inter] = (uint8_t)b1;
+      dst[2 * (uint64_t)A.inter] = (uint8_t)b2;
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// down + weighted combine
+// ------------------------------------------------------------------------------------------------
+template <int CG>
+__global__ void __launch_bounds__(256) decode_down_kernel(DecodeArgs A) {
+  const uint32_t rt = blockIdx.x, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const uint32_t M = A.m_tokens, ns = A.plan->n_slots;
+  const uint32_t nst = A.inter / kTileCols, units = ns * nst;
+  const uint32_t c = lane & 15, rg = lane >> 4;
+
+  __shared__ uint32_t tbl[4 * kLut];
+  __shared__ float part[4][CG][16][16];
+
+  float yacc[CG][4];
+#pragma unroll
+  for (int cg = 0; cg < CG; ++cg)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) yacc[cg][v] = 0.f;
+
+  Unit cur;
+  if (wv < units) {
+    const uint32_t slot = wv / nst, S = wv % nst;
+    const uint8_t* ex = A.base + (uint64_t)A.plan->expert[slot] * A.stride;
+    load_unit(cur, ex + A.off[6], ex + A.off[7], (uint64_t)rt * nst + S, lane);
+  }
+  build_table(tbl, A.codebook);
+  __syncthreads();
+
+  for (uint32_t u = wv; u < units; u += 4) {
+    const uint32_t slot = u / nst, S = u % nst;
+    const uint32_t e = A.plan->expert[slot], mask = A.plan->tok_mask[slot];
+    const uint8_t* ex = A.base + (uint64_t)e * A.stride;
+    const BSrc<CG> b = b_source<CG>(A.aq + (uint64_t)slot * M * kTerms * A.inter, A.inter,
+                                    (uint64_t)S * kTileCols, lane, M, mask, A.zeros);
+    Unit nxt;
+    const uint32_t un = u + 4;
+    if (un < units) {
+      const uint32_t sn = un / nst, Sn = un % nst;
+      const uint8_t* exn = A.base + (uint64_t)A.plan->expert[sn] * A.stride;
+      load_unit(nxt, exn + A.off[6], exn + A.off[7], (uint64_t)rt * nst + Sn, lane);
+    }
+    const uint2 rsv = *reinterpret_cast<const uint2*>(ex + A.off[8] + (uint64_t)(rt * 16 + 4 * rg) * 2);
+    __builtin_amdgcn_sched_barrier(0);
+    v4f acc[CG];
+#pragma unroll
+    for (int cg = 0; cg < CG; ++cg) acc[cg] = v4f{0.f, 0.f, 0.f, 0.f};
+    v8i bc[CG];
+#pragma unroll
+    for (int cg = 0; cg < CG; ++cg) bc[cg] = b_step(b.p[cg], 0);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      v8i bn[CG];
+      if (m < 7) {
+#pragma unroll
+        for (int cg = 0; cg < CG; ++cg) bn[cg] = b_step(b.p[cg], m + 1);
+      }
+      pin(cur);
+      v8i a;
+      switch (m) {
+        case 0: a = decode_a<0>(cur, tbl); break;
+        case 1: a = decode_a<1>(cur, tbl); break;
+        case 2: a = decode_a<2>(cur, tbl); break;
+        case 3: a = decode_a<3>(cur, tbl); break;
+        case 4: a = decode_a<4>(cur, tbl); break;
+        case 5: a = decode_a<5>(cur, tbl); break;
+        case 6: a = decode_a<6>(cur, tbl); break;
+        default: a = decode_a<7>(cur, tbl); break;
+      }
+#pragma unroll
+      for (int cg = 0; cg < CG; ++cg) acc[cg] = mfma(a, bc[cg], acc[cg]);
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("" ::: "memory");
+      if (m < 7) {
+#pragma unroll
+        for (int cg = 0; cg < CG; ++cg) bc[cg] = bn[cg];
+      }
+    }
+    const float rs[4] = {__uint_as_float(rsv.x << 16), __uint_as_float(rsv.x & 0xFFFF0000u),
+                         __uint_as_float(rsv.y << 16), __uint_as_float(rsv.y & 0xFFFF0000u)};
+#pragma unroll
+    for (int cg = 0; cg < CG; ++cg) {
+      const uint32_t t = cg * 5 + c / 3;
+      const bool mine = c < 15 && (c % 3) == 0 && t < M && ((mask >> t) & 1u);
+      const float wt = mine ? ldexpf(A.plan->w[slot][t], -A.sigma_a) : 0.f;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float val = combine_terms(acc[cg][v]);
+        if (mine) yacc[cg][v] += val * rs[v] * wt;
+      }
+    }
+    if (un < units) cur = nxt;
+  }
+
+#pragma unroll
+  for (int cg = 0; cg < CG; ++cg)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) part[wv][cg][4 * rg + v][c] = yacc[cg][v];
+  __syncthreads();
+  const uint32_t tid = threadIdx.x;
+  if (tid < 16 * M) {
+    const uint32_t r = tid & 15, t = tid >> 4;
+    const uint32_t cg = t / 5, col = (t % 5) * 3;
+    float sum = 0.f;
+    for (int q = 0; q < 4; ++q) sum += part[q][cg][r][col];
+    float* dst = A.y + (uint64_t)t * A.y_ts + (uint64_t)(rt * 16 + r) * A.y_ds;
+    *dst = A.accumulate ? *dst + sum : sum;
+  }
+}
+
+}  // namespace affx
+
+using namespace affx;
+
+static uint64_t align256(uint64_t v) { return (v + 255) / 256 * 256; }
+
+struct DecodeWs {
+  uint64_t plan, zeros, xq, aq, total;
+};
+
+static DecodeWs decode_ws(uint32_t M, uint32_t K, uint32_t hidden, uint32_t inter) {
+  DecodeWs w;
+  const uint64_t slots = (uint64_t)M * K;
+  w.plan = 0;
+  w.zeros = align256(sizeof(DecodePlan));
+  w.xq = w.zeros + 256;
+  w.aq = w.xq + align256((uint64_t)M * kTerms * hidden);
+  w.total = w.aq + align256(slots * M * kTerms * inter);
+  return w;
+}
+
+extern "C" {
+
+size_t affx_decode_workspace_size(uint32_t m, uint32_t k, uint32_t hidden, uint32_t inter) {
+  return (size_t)decode_ws(m, k, hidden, inter).total;
+}
+
+int affx_expert_ffn_decode(const affx_layer* L, const float* x, uint64_t x_ts, uint64_t x_ds,
+                           uint32_t M, const uint32_t* sel, const float* w, uint32_t K, float* y,
+                           uint64_t y_ts, uint64_t y_ds, int accumulate, void* ws,
+                           size_t ws_bytes, void* stream) {
+  if (!L || !x || !sel || !w || !y || !ws || !L->base || !L->codebook)
+    return set_error(AFFX_ERR_ARG, "ffn_decode: null pointer");
+  if (M == 0 || M > kMaxTok || K == 0 || K > AFFX_MAX_TOPK)
+    return set_error(AFFX_DECLINED, "ffn_decode: m_tokens must be 1..%d and top_k 1..%d (got %u, %u)",
+                     kMaxTok, AFFX_MAX_TOPK, M, K);
+  if (L->n_experts == 0 || L->n_experts > AFFX_MAX_EXPERTS)
+    return set_error(AFFX_DECLINED, "ffn_decode: n_experts must be 1..%d", AFFX_MAX_EXPERTS);
+  if (L->hidden % kTileCols || L->inter % kTileCols || L->hidden == 0 || L->inter == 0 ||
+      L->hidden > 4 * kTileCols)
+    return set_error(AFFX_DECLINED, "ffn_decode: hidden must be 1024..4096 and inter a multiple of "
+                     "1024 (got %u, %u)", L->hidden, L->inter);
+  if (!(L->swiglu_limit > 0.f) || L->swiglu_limit > 1e6f)
+    return set_error(AFFX_DECLINED, "ffn_decode: needs a SwiGLU clamp limit in (0, 1e6]");
+  const DecodeWs lay = decode_ws(M, K, L->hidden, L->inter);
+  if (ws_bytes < lay.total)
+    return set_error(AFFX_ERR_ARG, "ffn_decode: workspace %zu < %llu bytes", ws_bytes,
+                     (unsigned long long)lay.total);
+  uint64_t off9[9];
+  const uint64_t stride = affx_expert_layout(L->hidden, L->inter, off9, nullptr);
+  if (L->stride < stride) return set_error(AFFX_ERR_ARG, "ffn_decode: layer stride below expert size");
+
+  uint8_t* base = (uint8_t*)ws;
+  DecodePlan* plan = (DecodePlan*)(base + lay.plan);
+  DecodeArgs A;
+  A.base = (const uint8_t*)L->base;
+  A.stride = L->stride;
+  for (int i = 0; i < 9; ++i) A.off[i] = off9[i];
+  A.hidden = L->hidden;
+  A.inter = L->inter;
+  A.m_tokens = M;
+  A.codebook = (const uint32_t*)L->codebook;
+  A.plan = plan;
+  A.xq = base + lay.xq;
+  A.aq = base + lay.aq;
+  A.zeros = base + lay.zeros;
+  A.limit = L->swiglu_limit;
+  // |SwiGLU| <= L * L under the clamp; scale so that it stays below 256 < 448
+  A.sigma_a = 7 - ilogbf(L->swiglu_limit * L->swiglu_limit);
+  A.y = y;
+  A.y_ts = y_ts;
+  A.y_ds = y_ds;
+  A.accumulate = accumulate;
+  hipStream_t s = (hipStream_t)stream;
+
+  hipLaunchKernelGGL(decode_prep_kernel, dim3(M), dim3(256), 0, s, x, x_ts, x_ds, M, sel, w, K,
+                     L->n_experts, L->hidden, plan, base + lay.xq, base + lay.zeros);
+  int rc = check_launch("decode_prep_kernel");
+  if (rc) return rc;
+  const uint32_t max_slots = M * K < L->n_experts ? M * K : L->n_experts;
+  const dim3 g1(L->inter / kTileRows, max_slots), g2(L->hidden / kTileRows);
+  if (M <= 5) {
+    hipLaunchKernelGGL(decode_gateup_kernel<1>, g1, dim3(256), 0, s, A);
+    if ((rc = check_launch("decode_gateup_kernel<1>"))) return rc;
+    hipLaunchKernelGGL(decode_down_kernel<1>, g2, dim3(256), 0, s, A);
+    return check_launch("decode_down_kernel<1>");
+  }
+  hipLaunchKernelGGL(decode_gateup_kernel<2>, g1, dim3(256), 0, s, A);
+  if ((rc = check_launch("decode_gateup_kernel<2>"))) return rc;
+  hipLaunchKernelGGL(decode_down_kernel<2>, g2, dim3(256), 0, s, A);
+  return check_launch("decode_down_kernel<2>");
+}
+
+}  // extern "C"

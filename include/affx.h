@@ -1,0 +1,193 @@
+/*
+ * affx.h -- C-ABI of the MI355X (gfx950) routed-expert library, libaffx.so.
+ *
+ * The library runs the hot path of affinity's routed experts on the 2.875-bpw quad-codebook
+ * format (AFF_Q2P875_Q4): fused unpack -> codebook dequantisation -> SwiGLU expert FFN, for
+ * batch-1/speculative decode (M <= 8 tokens) and for grouped prefill. Every entry point replaces
+ * one of the reference engine's C++ entry points; the comment on each names it (file:line in the
+ * reference tree). Plain pointers and sizes only: no C++ or torch types cross this boundary.
+ *
+ * Conventions
+ *  - Device pointers are `const void*` / `void*` and must be device memory of the current HIP
+ *    device; host pointers are marked `host`. Streams are `hipStream_t` passed as `void*`
+ *    (NULL = the default stream). Every call is stream-ordered and does not synchronise, except
+ *    where noted.
+ *  - Status: 0 = done, AFFX_DECLINED (>0) = preconditions not met and nothing was launched (the
+ *    caller falls back, the reference's `bool` false), negative = error. `affx_last_error()`
+ *    returns the message of the calling thread's last non-zero status. The reference aborts on
+ *    any HIP failure (AFF_HIP_CHECK, src/gpu/hip_common.h:38-46); the C++ shim in INTEGRATION.md
+ *    restores that by aborting on a negative status.
+ *  - Expert bytes. A *container expert* is the reference's on-disk expert: nine planes
+ *    (gate/up/down x codes/fields/rscales) at the offsets `affx_expert_layout` returns,
+ *    stride = 9,060,352 B at hidden 4096 / inter 2048 (src/format/aff_format.cpp:45-91). A
+ *    *device expert* has the same stride and the same plane offsets, but inside each code and
+ *    field plane the 80-byte code runs and 12-byte field runs of every 256-column row segment
+ *    are permuted into wave tiles (16 rows x 1024 columns, one run per lane) so that one
+ *    128-bit load per lane per run is coalesced. Row scales are unchanged. The permutation is a
+ *    bijection on bytes (`affx_expert_to_device_layout` / `..._from_device_layout`).
+ *  - The codebook is the container's `__codebook`: uint32[2 variants x 1024], dword v*1024+c,
+ *    byte p = E4M3 (OCP fn) encoding of quad element p, every stored exponent in 1..7.
+ *  - Shapes: hidden % 1024 == 0, inter % 1024 == 0 (the V4 shapes 4096 / 2048).
+ */
+#ifndef AFFX_H
+#define AFFX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AFFX_OK 0
+#define AFFX_DECLINED 1
+#define AFFX_ERR_ARG (-1)
+#define AFFX_ERR_HIP (-2)
+#define AFFX_ERR_DEVICE (-3)
+#define AFFX_ERR_CODEBOOK (-4)
+
+#define AFFX_MAX_DECODE_TOKENS 8 /* M of the multi-row decode path */
+#define AFFX_MAX_TOPK 16         /* the reference's plan limit (src/gpu/moe_plan.hip:407-420) */
+#define AFFX_MAX_EXPERTS 512
+
+/* One quantised matrix in device layout. Mirrors DeviceMatrix{data,scales,rscales,rows,cols}
+ * (src/gpu/expert_kernel_hip.h:133-138); codes/fields are the permuted planes. */
+typedef struct affx_matrix {
+  const void* codes;   /* device: rows*cols*10/32 bytes, wave-tile order */
+  const void* fields;  /* device: rows*cols*6/128 bytes, wave-tile order */
+  const void* rscales; /* device: bf16[rows] */
+  uint32_t rows, cols;
+} affx_matrix;
+
+/* Where a layer's experts live: expert e at base + e*stride (device layout), the O(1)
+ * addressing of AffReader::expert_ptr (src/format/aff_reader.h:45-48). */
+typedef struct affx_layer {
+  const void* base;
+  uint64_t stride;
+  uint32_t n_experts;
+  uint32_t hidden, inter;
+  const void* codebook; /* device: uint32[2048] */
+  float swiglu_limit;   /* src/engine/model.h:52 (10 for V4-Flash); <= 0 disables the clamp */
+} affx_layer;
+
+/* ---- library / device --------------------------------------------------------------------- */
+
+/* Checks that the current device is gfx950 and records its CU count. The reference's
+ * hip_available() (src/gpu/expert_kernel_hip.h:410). */
+int affx_init(void);
+const char* affx_last_error(void);
+const char* affx_version(void);
+
+/* ---- format ------------------------------------------------------------------------------- */
+
+/* Plane offsets/sizes of one expert (order gate/up/down x codes/fields/rscales) and the stride.
+ * compute_expert_layout (src/format/aff_format.cpp:45-91). Host-only, no device needed. */
+uint64_t affx_expert_layout(uint64_t hidden, uint64_t inter, uint64_t off9[9], uint64_t size9[9]);
+
+/* 1 when every byte of the packed codebook has stored exponent 1..7 (so a block scale is an
+ * exponent add that cannot reach NaN), else 0. The load-time check of StaticPlacement::init
+ * (src/gpu/static_placement.hip:938-951). host pointer. */
+int affx_codebook_valid(const uint32_t* codebook_host);
+
+/* Host byte permutation of one expert, container -> device layout and back.
+ * expert_transpose_planes_host (src/gpu/expert_kernel.hip:2889-2907, expert_kernel_hip.h:78-84).
+ * host pointers, `stride` bytes each, src != dst. */
+int affx_expert_to_device_layout(const void* src_host, void* dst_host, uint64_t hidden,
+                                 uint64_t inter);
+int affx_expert_from_device_layout(const void* src_host, void* dst_host, uint64_t hidden,
+                                   uint64_t inter);
+
+/* The same permutation on the GPU for n experts uploaded in container layout (src and dst are
+ * device buffers of n*stride bytes, not overlapping). The upload step of StaticPlacement::init
+ * (src/gpu/static_placement.hip:1094-1097), moved onto the device. */
+int affx_permute_experts(const void* src_container, void* dst_device, uint64_t n_experts,
+                         uint64_t hidden, uint64_t inter, void* stream);
+
+/* ---- dequantisation (validation path) ------------------------------------------------------ */
+
+/* out[r*cols + c] = the float the reference's dequantize_matrix produces (bit-exact):
+ * rscale * 2^s * (+-1) * e[v][code][(p+rh)%4]. src/quant/blockquant.cpp:793-833; on the GPU the
+ * reference checks the same identity through its decode (src/gpu/expert_kernel.hip:594-619). */
+int affx_dequant_matrix(const affx_matrix* m, const void* codebook, float* out, void* stream);
+
+/* ---- decode: M <= 8 tokens, fused gate/up -> SwiGLU -> down -> weighted combine ------------- */
+
+/* Workspace bytes affx_expert_ffn_decode needs for m tokens with top-k routing. */
+size_t affx_decode_workspace_size(uint32_t m_tokens, uint32_t top_k, uint32_t hidden,
+                                  uint32_t inter);
+
+/* y[t] (+)= sum_j w[t][j] * FFN_{sel[t][j]}(x[t]) for t < m_tokens (<= 8), j < top_k.
+ *  x: device f32, element (t, h) at x[t*x_tok_stride + h*x_dim_stride]; y likewise with
+ *  y_tok_stride/y_dim_stride. The engine's dim-major arenas d_x/d_block f32 [H][nb_stride]
+ *  are tok_stride 1, dim_stride nb_stride. `accumulate` = 1 adds into y (the engine's d_block),
+ *  0 overwrites.
+ *  sel: device uint32 [m_tokens][top_k]; ids >= n_experts are padding and are skipped (as the
+ *  reference's plan does, src/gpu/moe_plan.h:146). w: device f32 [m_tokens][top_k].
+ * Replaces the batch-1 GPU FFN expert_ffn_hip (src/gpu/expert_kernel.hip:2737-2808,
+ * expert_kernel_hip.h:273) and the narrow NT=1 arm of the W8A8 GEMM that the engine's decode uses
+ * (expert_kernel.hip:3049-3058). Three kernels, no host synchronisation. */
+int affx_expert_ffn_decode(const affx_layer* layer, const float* x, uint64_t x_tok_stride,
+                           uint64_t x_dim_stride, uint32_t m_tokens, const uint32_t* sel,
+                           const float* w, uint32_t top_k, float* y, uint64_t y_tok_stride,
+                           uint64_t y_dim_stride, int accumulate, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
+/* ---- prefill: grouped GEMM over an expert-sorted slot list ---------------------------------- */
+
+/* Workspace bytes of affx_moe_plan + affx_expert_ffn_grouped for n_tok tokens, top-k routing. */
+size_t affx_grouped_workspace_size(uint32_t n_tok, uint32_t top_k, uint32_t n_experts,
+                                   uint32_t hidden, uint32_t inter);
+
+/* y[t] (+)= sum_j w[t][j] * FFN_{sel[t][j]}(x[t]) for all n_tok tokens, grouped by expert:
+ * every expert's weights are decoded once per 128-row tile and reused for all of its tokens.
+ *  x: device bf16 [n_tok][hidden] (token-major); x_lo: optional second bf16 term (x = x + x_lo)
+ *  for f32 activations split hi/lo, or NULL.
+ *  sel/w: device [n_tok][top_k]; padding ids >= n_experts skipped.
+ *  y: device f32 [n_tok][hidden] (token-major).
+ * Replaces run_batch_device's prefill sequence (src/gpu/static_placement.hip:1348-1964):
+ * moe_plan_hip (src/gpu/moe_plan.hip:407-420) -> batch_quant_fp8_hip -> expert_gemm_wmma_hip
+ * gate/up (expert_kernel.hip:3018-3062) -> expert_swiglu_quant_hip -> expert_gemm_wmma_hip down
+ * -> expert_scatter_slots_hip (expert_kernel.hip:935-947). Deterministic: every output element
+ * is summed in a fixed order, no float atomics. */
+int affx_expert_ffn_grouped(const affx_layer* layer, const void* x, const void* x_lo,
+                            uint32_t n_tok, const uint32_t* sel, const float* w, uint32_t top_k,
+                            float* y, int accumulate, void* workspace, size_t workspace_bytes,
+                            void* stream);
+
+/* ---- engine hook ---------------------------------------------------------------------------- */
+
+/* State behind affx_expert_ffn_batch: the per-layer expert tables and the engine's device
+ * arenas, as the reference's lambda captures them (tools/affinity.cpp:1218-1235). */
+typedef struct affx_engine_ctx {
+  const affx_layer* layers; /* [n_layers] */
+  uint32_t n_layers;
+  const float* d_x;         /* f32 [hidden][nb_stride], dim-major (the engine's d_x) */
+  float* d_block;           /* f32 [hidden][nb_stride], accumulated into */
+  uint32_t nb_stride;
+  void* workspace;          /* device */
+  size_t workspace_bytes;
+  void* stream;
+} affx_engine_ctx;
+
+/* ExpertFfnBatch-shaped hook (src/engine/model.h:664-666): takes every (token, expert) pair of
+ * host arrays sel/w [nb_tok][k], runs them on the GPU into ctx->d_block, sets handled[b*k+j]=1
+ * for each pair taken, returns the count. Padding ids >= n_experts are neither taken nor marked.
+ * nb_tok <= 8 runs the decode path, larger batches the grouped path. Returns 0 (nothing taken)
+ * on any error; affx_last_error() says why. Synchronises the stream before returning (the
+ * routes arrive in host memory). */
+uint32_t affx_expert_ffn_batch(void* ctx, uint32_t layer, const uint32_t* sel, const float* w,
+                               uint32_t nb_tok, uint32_t k, uint8_t* handled);
+
+/* ---- diagnostics ---------------------------------------------------------------------------- */
+
+/* Runs one v_mfma_scale_f32_16x16x128_f8f6f4 (E4M3 x E4M3, unit scales) on a[64][32] and
+ * b[64][32] fp8 bytes (one row per lane) and writes the 64x4 f32 accumulator lanes to d.
+ * Device pointers. Lets a test pin the lane layout and the OCP E4M3 interpretation the decode
+ * kernels rely on. No reference counterpart (the reference's WMMA layout test, test_wmma, is
+ * absent from its tree: CMakeLists.txt:304). */
+int affx_selftest_mfma_fp8(const void* a, const void* b, float* d, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* AFFX_H */

@@ -1,0 +1,87 @@
+/*
+ * CPU oracle: a C restatement of the reference's CPU path for the 2.875-bpw quad-codebook
+ * routed experts (AFF_Q2P875_Q4). TEST INFRASTRUCTURE ONLY.
+ *
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load this library,
+ * and only as the checker. The product (affinity_amd/) never links, imports or calls it.
+ *
+ * Every function cites the reference file:line it restates (paths under the reference tree).
+ * How each one is pinned (golden vectors written by the compiled reference, closed forms,
+ * invariants, brute force) is listed in tests/test_oracle.py; none is "parity unpinned".
+ *
+ * Conventions:
+ *  - A matrix is row-major [rows x cols]; its planes are the container's: `codes` is an
+ *    LSB-first stream of 10-bit quad codes (rows*cols/4 of them), `fields` an LSB-first stream
+ *    of 6-bit block fields (rows*cols/16), `rscales` one bf16 per row.
+ *  - A float codebook is float[2 variants][1024 codes][4]; a packed codebook is uint32[2048]
+ *    (dword v*1024+c, byte p = E4M3 encoding of element p).
+ */
+#ifndef AFFX_ORACLE_H
+#define AFFX_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  ORC_BLOCK = 16, ORC_PAIR = 4, ORC_CODE_BITS = 10, ORC_FIELD_BITS = 6, ORC_SCALE_BITS = 3,
+  ORC_LUT = 1024, ORC_VARIANTS = 2, ORC_BIAS = 7
+};
+
+/* threads used by the parallel loops below (0 = OpenMP default) */
+void orc_set_threads(int n);
+int orc_get_threads(void);
+
+/* ---- element codecs ---- */
+float orc_e4m3_to_float(uint8_t b);
+uint16_t orc_f32_to_bf16(float f);
+float orc_bf16_to_f32(uint16_t h);
+
+/* ---- bit streams ---- */
+void orc_pack_bits(uint8_t* dst, uint64_t index, uint32_t bits, uint32_t value);
+uint32_t orc_unpack_bits(const uint8_t* src, uint64_t index, uint32_t bits);
+
+/* ---- synthetic inputs (BASELINE generator: splitmix64 + Box-Muller, bf16 RNE) ---- */
+uint64_t orc_splitmix_at(uint64_t seed, uint64_t k);
+void orc_gen_normal_bf16(uint64_t seed, uint64_t n, double scale, float* out);
+void orc_gen_normal_f64(uint64_t seed, uint64_t n, double* out);
+
+/* ---- container geometry ---- */
+uint64_t orc_expert_layout(uint64_t hidden, uint64_t inter, uint64_t* off9, uint64_t* size9);
+
+/* ---- codebook fitting ---- */
+uint64_t orc_collect_samples(const float* w, uint64_t rows, uint64_t cols, uint64_t budget,
+                             float* out, uint64_t cap);
+void orc_fit_codebook(const float* samples, uint64_t n_samples, uint32_t iters, uint64_t seed,
+                      float* cb);
+uint8_t orc_e4m3_nearest(float x);
+void orc_project_codebook(float* cb, uint64_t n);
+void orc_pack_codebook(const float* cb, uint32_t* packed);
+void orc_unpack_codebook(const uint32_t* packed, float* cb);
+int orc_codebook_exponents_ok(const uint32_t* packed);
+
+/* ---- quantise / dequantise one matrix ---- */
+int orc_quantize_matrix(const float* w, uint64_t rows, uint64_t cols, const float* cb,
+                        const float* col_importance, uint8_t* codes, uint8_t* fields,
+                        uint16_t* rscales);
+int orc_dequantize_matrix(const uint8_t* codes, const uint8_t* fields, const uint16_t* rscales,
+                          uint64_t rows, uint64_t cols, const float* cb, float* out);
+
+/* ---- CPU expert compute ---- */
+void orc_expert_gemv(const uint8_t* codes, const uint8_t* fields, const uint16_t* rscales,
+                     uint64_t rows, uint64_t cols, const float* cb, const float* x, float w,
+                     float* y);
+void orc_swiglu(const float* gate, const float* up, uint64_t n, float limit, float* out);
+void orc_expert_ffn(const uint8_t* expert, uint64_t hidden, uint64_t inter, const float* cb,
+                    const float* x, float w, float limit, float* y);
+
+/* ---- routing used by the synthetic configs ---- */
+void orc_route_softmax_topk(const float* logits, uint32_t n_expert, uint32_t k, uint32_t* sel,
+                            float* w);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

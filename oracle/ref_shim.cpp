@@ -1,0 +1,157 @@
+// C-ABI shim over the reference's own CPU path, compiled together with the reference sources
+// from /root/reference by oracle/Makefile into oracle/_ref/libaffref.so.
+//
+// This file is test infrastructure. It holds no algorithm: every function forwards to the
+// reference implementation it names so that tests/golden/make_golden.py (fixture generation),
+// the oracle cross-checks in tests/ and bench.py's cpu_baseline leg can call the reference
+// through ctypes. The planes use the reference's row-major container layout
+// (src/format/aff_format.cpp:45-91); the codebook is float[variant][code][4]
+// (src/quant/blockquant.h:87-97).
+#include "quant/blockquant.h"
+#include "quant/source_dtypes.h"
+#include "format/aff_format.h"
+#include "engine/expert_kernel.h"
+#include "engine/ops.h"
+
+#include <cstring>
+#include <vector>
+
+using namespace aff;
+
+namespace {
+
+QuantSpec q4_spec() { return expert_quant_spec((uint32_t)AFF_Q2P875_Q4); }
+
+Codebook codebook_from(const float* cb) {
+  const QuantSpec sp = q4_spec();
+  Codebook c;
+  c.pair = sp.pair;
+  c.variants = sp.variants();
+  c.k = sp.lut_size();
+  c.v.assign(cb, cb + (size_t)c.variants * c.k * c.pair);
+  return c;
+}
+
+ExpertMatrixView view(const uint8_t* codes, const uint8_t* fields, const uint8_t* rscales,
+                      uint64_t rows, uint64_t cols) {
+  ExpertMatrixView m;
+  m.data = codes;
+  m.scales = fields;
+  m.rscales = rscales;
+  m.rows = rows;
+  m.cols = cols;
+  m.spec = q4_spec();
+  return m;
+}
+
+}  // namespace
+
+extern "C" {
+
+// src/quant/blockquant.cpp:386-423
+uint64_t affref_collect_samples(const float* w, uint64_t rows, uint64_t cols, uint64_t budget,
+                                float* out, uint64_t cap) {
+  std::vector<float> s;
+  collect_normalized_samples(w, rows, cols, q4_spec(), &s, budget, nullptr, nullptr);
+  const uint64_t n = s.size() < cap ? s.size() : cap;
+  if (out && n) std::memcpy(out, s.data(), n * sizeof(float));
+  return s.size();
+}
+
+// src/quant/blockquant.cpp:252-384 (fit) then 463-466 (projection onto E4M3, pow2 constraint),
+// the order tools/aff_quantize.cpp:429-434 uses.
+void affref_fit_codebook(const float* samples, uint64_t n, uint32_t iters, uint64_t seed,
+                         int project, float* cb_out) {
+  Codebook cb = fit_codebook(samples, n, q4_spec(), nullptr, iters, seed);
+  if (project) project_codebook_e4m3(&cb, true);
+  std::memcpy(cb_out, cb.v.data(), cb.v.size() * sizeof(float));
+}
+
+// src/quant/blockquant.cpp:468-480
+void affref_pack_codebook(const float* cb, uint32_t* packed) {
+  const std::vector<uint32_t> p = pack_codebook_e4m3_quads(codebook_from(cb));
+  std::memcpy(packed, p.data(), p.size() * sizeof(uint32_t));
+}
+
+// src/quant/blockquant.cpp:482-492
+void affref_unpack_codebook(const uint32_t* packed, float* cb) {
+  const QuantSpec sp = q4_spec();
+  Codebook c;
+  unpack_codebook_e4m3_quads(packed, sp.variants(), sp.lut_size(), &c);
+  std::memcpy(cb, c.v.data(), c.v.size() * sizeof(float));
+}
+
+// src/quant/blockquant.cpp:498-556: the acceleration grid aff-quantize builds once per codebook.
+void* affref_search_new(const float* cb) {
+  CodebookSearch* s = new CodebookSearch;
+  build_codebook_search(codebook_from(cb), s);
+  return s;
+}
+void affref_search_free(void* s) { delete static_cast<CodebookSearch*>(s); }
+
+// src/quant/blockquant.cpp:586-791. `search` may be null (plain scan).
+int affref_quantize_matrix(const float* w, uint64_t rows, uint64_t cols, const float* cb,
+                           const float* col_importance, void* search, uint8_t* codes,
+                           uint8_t* fields, uint8_t* rscales) {
+  QuantizedMatrix q;
+  std::string err;
+  if (!quantize_matrix(w, rows, cols, q4_spec(), codebook_from(cb), &q, &err, col_importance,
+                       static_cast<CodebookSearch*>(search)))
+    return -1;
+  std::memcpy(codes, q.data.data(), q.data.size());
+  std::memcpy(fields, q.scales.data(), q.scales.size());
+  std::memcpy(rscales, q.rscales.data(), q.rscales.size());
+  return 0;
+}
+
+// src/quant/blockquant.cpp:793-833
+int affref_dequantize_matrix(const uint8_t* codes, const uint8_t* fields, const uint8_t* rscales,
+                             uint64_t rows, uint64_t cols, const float* cb, float* out) {
+  const QuantSpec sp = q4_spec();
+  QuantizedMatrix q;
+  q.rows = rows;
+  q.cols = cols;
+  q.spec = sp;
+  q.data.assign(codes, codes + rows * cols / sp.pair * sp.code_bits / 8);
+  q.scales.assign(fields, fields + rows * (cols / sp.block) * sp.block_field_bits() / 8);
+  q.rscales.assign(rscales, rscales + rows * 2);
+  std::string err;
+  return dequantize_matrix(q, codebook_from(cb), out, &err) ? 0 : -1;
+}
+
+// src/engine/expert_kernel.cpp:119-139: y[r] += w * (W x)[r]; mt selects expert_gemv_scaled_mt
+// (rows split over the reference's global pool, sized to hardware_concurrency).
+void affref_expert_gemv_scaled(const uint8_t* codes, const uint8_t* fields,
+                               const uint8_t* rscales, uint64_t rows, uint64_t cols,
+                               const float* cb, const float* x, float w, float* y, int mt) {
+  const Codebook c = codebook_from(cb);
+  const ExpertMatrixView m = view(codes, fields, rscales, rows, cols);
+  if (mt) expert_gemv_scaled_mt(m, c, x, w, y);
+  else expert_gemv_scaled(m, c, x, w, y);
+}
+
+// src/engine/ops.cpp:47-60
+void affref_swiglu(const float* gate, const float* up, uint64_t n, float limit, float* out) {
+  swiglu(gate, up, n, limit, out);
+}
+
+// src/quant/source_dtypes.cpp:91-112, 133 and source_dtypes.h:33-46
+float affref_e4m3_to_float(uint8_t b) { return fp8_e4m3_to_float(b); }
+uint16_t affref_float_to_bf16(float f) { return float_to_bf16(f); }
+float affref_bf16_to_float(uint16_t h) { return bf16_to_float(h); }
+
+// src/format/aff_format.cpp:45-91: offsets and sizes of the nine planes of one expert, in the
+// order gate/up/down x data/scale/rscale; returns the stride.
+uint64_t affref_expert_layout(uint64_t hidden, uint64_t inter, uint64_t* off9, uint64_t* size9) {
+  ExpertGeometry g{hidden, inter, AFF_Q2P875_Q4, AFF_Q2P875_Q4, AFF_Q2P875_Q4};
+  AffMatrixDesc d[3];
+  const uint64_t stride = compute_expert_layout(g, d[0], d[1], d[2]);
+  for (int m = 0; m < 3; ++m) {
+    off9[3 * m + 0] = d[m].data_off;   size9[3 * m + 0] = d[m].data_size;
+    off9[3 * m + 1] = d[m].scale_off;  size9[3 * m + 1] = d[m].scale_size;
+    off9[3 * m + 2] = d[m].rscale_off; size9[3 * m + 2] = d[m].rscale_size;
+  }
+  return stride;
+}
+
+}  // extern "C"

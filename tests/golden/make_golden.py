@@ -1,0 +1,180 @@
+"""Writes the golden fixtures under tests/golden/ from the reference's own CPU path.
+
+Run in the build container (the only place the reference tree exists):
+
+    make -C oracle && python tests/golden/make_golden.py
+
+The reference functions run from oracle/_ref/libaffref.so, which oracle/Makefile compiles from
+the reference sources where they lie (blockquant.cpp, aff_format.cpp, source_dtypes.cpp,
+expert_kernel.cpp, threadpool.cpp, ops.cpp, log.cpp) plus a C-ABI forwarder. Inputs come from
+the synthetic generator (splitmix64 + Box-Muller, bf16 RNE; seeds fixed by the benchmark
+configs); the generator itself is pinned separately by tests/test_oracle.py.
+
+Fixtures (data only: inputs and the reference's outputs):
+  c1_codebook.bin   uint32[2048]  packed E4M3 quad codebook fitted on the config-1 expert
+                                  (samples 2^19 per matrix, fit_codebook(50, seed 1), projection)
+  c1_manifest.json  SHA-256 of the config-1 inputs, of the nine quantised planes, of the
+                    dequantised matrices and of the FFN intermediates; sampled plane rows
+  c1_ffn_y.bin      float32[4096] FFN output y = W_d . swiglu(W_g x, W_u x) (weight 1)
+  small.npz         small matrices (edge rows, importance, odd shapes) with the reference's
+                    planes, dequantised values and GEMV outputs
+  scalars.npz       E4M3 table, bf16 rounding cases, swiglu cases
+"""
+from __future__ import annotations
+
+import hashlib
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+sys.path.insert(0, ROOT)
+
+from oracle import load_oracle, load_ref  # noqa: E402
+from oracle.binding import H, I  # noqa: E402
+
+OUT = os.path.dirname(os.path.abspath(__file__))
+S_W, S_X = 1000, 7
+
+
+def sha(a: np.ndarray) -> str:
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+def c1_inputs(O):
+    wg = O.normal_bf16(S_W + 0, I * H, 0.02).reshape(I, H)
+    wu = O.normal_bf16(S_W + 1, I * H, 0.02).reshape(I, H)
+    wd = O.normal_bf16(S_W + 2, H * I, 0.02).reshape(H, I)
+    x = O.normal_bf16(S_X, H, 1.0)
+    return wg, wu, wd, x
+
+
+def row_slices(planes, rows, cols, pick):
+    """hex of selected rows of each plane (codes, fields, rscales)."""
+    codes, fields, rs = planes
+    cb_row, f_row = cols * 10 // 32, cols * 6 // 128
+    out = {}
+    for r in pick:
+        out[str(r)] = {
+            "codes": codes[r * cb_row:(r + 1) * cb_row].tobytes().hex(),
+            "fields": fields[r * f_row:(r + 1) * f_row].tobytes().hex(),
+            "rscale": int(rs[r]),
+        }
+    return out
+
+
+def make_c1(O, R):
+    t0 = time.time()
+    wg, wu, wd, x = c1_inputs(O)
+    samples = np.concatenate([R.collect_samples(w, 1 << 19) for w in (wg, wu, wd)])
+    print(f"samples: {samples.size} floats", flush=True)
+    cb = R.fit_codebook(samples, 50, 1, project=True)
+    packed = R.pack_codebook(cb)
+    assert np.array_equal(R.unpack_codebook(packed).view(np.uint32), cb.view(np.uint32))
+    packed.astype("<u4").tofile(os.path.join(OUT, "c1_codebook.bin"))
+    print(f"codebook fitted in {time.time() - t0:.0f} s", flush=True)
+
+    man = {"seeds": {"S_W": S_W, "S_X": S_X, "fit_seed": 1, "fit_iters": 50, "budget": 1 << 19},
+           "inputs": {"gate": sha(wg), "up": sha(wu), "down": sha(wd), "x": sha(x)},
+           "codebook_f32": sha(cb), "planes": {}, "dequant": {}, "rows": {}}
+    mats = {"gate": (wg, I, H), "up": (wu, I, H), "down": (wd, H, I)}
+    deq = {}
+    qs = {}
+    for name, (w, rows, cols) in mats.items():
+        t = time.time()
+        q = R.quantize(w, cb, None, search=True)
+        qs[name] = q
+        man["planes"][name] = {"codes": sha(q[0]), "fields": sha(q[1]), "rscales": sha(q[2])}
+        man["rows"][name] = row_slices(q, rows, cols, [0, 1, rows // 2 + 3, rows - 1])
+        d = R.dequantize(*q, rows, cols, cb)
+        deq[name] = d
+        man["dequant"][name] = sha(d)
+        print(f"{name}: quantised in {time.time() - t:.0f} s", flush=True)
+    # importance = all ones gives the same bytes as none (the config-1 "uniform importance")
+    ones = np.ones(H, np.float32)
+    qi = R.quantize(wg[:64].copy(), cb, ones, search=True)
+    man["gate64_ones_importance_equals_none"] = bool(
+        sha(qi[0]) == sha(qs["gate"][0][: 64 * H * 10 // 32]) and sha(qi[1]) == sha(qs["gate"][1][: 64 * H * 6 // 128]))
+
+    g = R.gemv(*qs["gate"], I, H, cb, x)
+    u = R.gemv(*qs["up"], I, H, cb, x)
+    a = R.swiglu(g, u, 10.0)
+    y = R.gemv(*qs["down"], H, I, cb, a, 1.0)
+    man["ffn"] = {"g": sha(g), "u": sha(u), "a": sha(a), "y": sha(y)}
+    y.astype("<f4").tofile(os.path.join(OUT, "c1_ffn_y.bin"))
+    with open(os.path.join(OUT, "c1_manifest.json"), "w") as f:
+        json.dump(man, f, indent=1, sort_keys=True)
+    print(f"config 1 done in {time.time() - t0:.0f} s", flush=True)
+    return cb
+
+
+def make_small(O, R, cb):
+    rng = np.random.default_rng(20261201)
+    cases = {}
+    # shapes: the smallest legal row (64 cols keeps rows byte-aligned), ragged row counts
+    for name, rows, cols in (("a", 5, 64), ("b", 16, 256), ("c", 33, 512), ("d", 8, 4096)):
+        w = O.normal_bf16(5000 + rows * 7 + cols, rows * cols, 0.02).reshape(rows, cols).copy()
+        if rows >= 5:
+            w[1] = 0.0                                    # an all-zero row
+            w[2, 16:32] = 0.0                             # an all-zero block
+            w[3, 5] = 3.0                                 # one outlier dominates the row scale
+            w[4] *= -1.0
+        imp = rng.uniform(0.1, 4.0, cols).astype(np.float32)
+        q = R.quantize(w, cb, None, search=True)
+        qn = R.quantize(w, cb, None, search=False)
+        qi = R.quantize(w, cb, imp, search=True)
+        x = O.normal_bf16(6000 + cols, cols, 1.0)
+        d = R.dequantize(*q, rows, cols, cb)
+        y = R.gemv(*q, rows, cols, cb, x, 0.75)
+        cases.update({f"{name}_w": w, f"{name}_imp": imp, f"{name}_x": x,
+                      f"{name}_codes": q[0], f"{name}_fields": q[1], f"{name}_rs": q[2],
+                      f"{name}_codes_nosearch": qn[0], f"{name}_fields_nosearch": qn[1],
+                      f"{name}_codes_imp": qi[0], f"{name}_fields_imp": qi[1],
+                      f"{name}_deq": d, f"{name}_gemv": y})
+    # arbitrary planes (every field value, random codes) dequantised by the reference
+    rows, cols = 16, 256
+    codes = rng.integers(0, 256, rows * cols * 10 // 32, dtype=np.uint8)
+    fields = rng.integers(0, 256, rows * cols * 6 // 128, dtype=np.uint8)
+    rs = np.array([R.float_to_bf16(v) for v in rng.uniform(1e-4, 1e-1, rows).astype(np.float32)], np.uint16)
+    cases["rand_codes"], cases["rand_fields"], cases["rand_rs"] = codes, fields, rs
+    cases["rand_deq"] = R.dequantize(codes, fields, rs, rows, cols, cb)
+    xr = O.normal_bf16(6100, cols, 1.0)
+    cases["rand_x"] = xr
+    cases["rand_gemv"] = R.gemv(codes, fields, rs, rows, cols, cb, xr, 1.0)
+    # a small codebook fit (trajectory check at a size the CPU suite can rerun)
+    w = O.normal_bf16(7000, 256 * 1024, 0.02).reshape(256, 1024)
+    s = R.collect_samples(w, 1 << 16)
+    cases["fit_samples"] = s
+    cases["fit_cb_raw"] = R.fit_codebook(s, 50, 1, project=False)
+    cases["fit_cb_proj"] = R.fit_codebook(s, 50, 1, project=True)
+    np.savez_compressed(os.path.join(OUT, "small.npz"), **cases)
+
+
+def make_scalars(O, R):
+    e4 = np.array([R.e4m3_to_float(b) for b in range(256)], np.float32)
+    rng = np.random.default_rng(7)
+    f = np.concatenate([rng.standard_normal(4000).astype(np.float32) * 10.0 ** rng.integers(-30, 30, 4000),
+                        np.array([0.0, -0.0, 1.0, 1.00390625, 1.0078125, 1.01171875, 3.3895314e38,
+                                  1e-40, -1e-40, 65504.0], np.float32)]).astype(np.float32)
+    bf = np.array([R.float_to_bf16(v) for v in f], np.uint16)
+    g = np.concatenate([np.linspace(-30, 30, 601, dtype=np.float32), rng.standard_normal(500).astype(np.float32) * 5])
+    u = np.concatenate([np.linspace(30, -30, 601, dtype=np.float32), rng.standard_normal(500).astype(np.float32) * 5])
+    sw = R.swiglu(g, u, 10.0)
+    sw0 = R.swiglu(g, u, 0.0)
+    np.savez_compressed(os.path.join(OUT, "scalars.npz"), e4m3=e4, bf_in=f, bf_out=bf, sw_g=g, sw_u=u,
+                        sw_out=sw, sw_out_nolimit=sw0)
+
+
+def main():
+    O, R = load_oracle(), load_ref()
+    make_scalars(O, R)
+    cb = make_c1(O, R)
+    make_small(O, R, cb)
+    print("fixtures written to", OUT)
+
+
+if __name__ == "__main__":
+    main()
