@@ -1,0 +1,98 @@
+"""ctypes binding of libaffx.so (include/affx.h). Fails loudly when the library is missing."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libaffx.so")
+
+AFFX_OK = 0
+AFFX_DECLINED = 1
+
+_vp = C.c_void_p
+_u32 = C.c_uint32
+_u64 = C.c_uint64
+_u64p = C.POINTER(C.c_uint64)
+
+
+class AffxMatrix(C.Structure):
+    _fields_ = [("codes", _vp), ("fields", _vp), ("rscales", _vp), ("rows", _u32), ("cols", _u32)]
+
+
+class AffxLayer(C.Structure):
+    _fields_ = [("base", _vp), ("stride", _u64), ("n_experts", _u32), ("hidden", _u32),
+                ("inter", _u32), ("codebook", _vp), ("swiglu_limit", C.c_float)]
+
+
+class AffxEngineCtx(C.Structure):
+    _fields_ = [("layers", C.POINTER(AffxLayer)), ("n_layers", _u32), ("d_x", _vp),
+                ("d_block", _vp), ("nb_stride", _u32), ("workspace", _vp),
+                ("workspace_bytes", C.c_size_t), ("stream", _vp)]
+
+
+class AffxError(RuntimeError):
+    pass
+
+
+class AffxDeclined(AffxError):
+    """Preconditions not met, nothing launched (the reference's `false` return)."""
+
+
+_SIGS = {
+    "affx_init": ([], C.c_int),
+    "affx_last_error": ([], C.c_char_p),
+    "affx_version": ([], C.c_char_p),
+    "affx_expert_layout": ([_u64, _u64, _u64p, _u64p], _u64),
+    "affx_codebook_valid": ([_vp], C.c_int),
+    "affx_expert_to_device_layout": ([_vp, _vp, _u64, _u64], C.c_int),
+    "affx_expert_from_device_layout": ([_vp, _vp, _u64, _u64], C.c_int),
+    "affx_permute_experts": ([_vp, _vp, _u64, _u64, _u64, _vp], C.c_int),
+    "affx_dequant_matrix": ([C.POINTER(AffxMatrix), _vp, _vp, _vp], C.c_int),
+    "affx_decode_workspace_size": ([_u32, _u32, _u32, _u32], C.c_size_t),
+    "affx_expert_ffn_decode": ([C.POINTER(AffxLayer), _vp, _u64, _u64, _u32, _vp, _vp, _u32, _vp,
+                                _u64, _u64, C.c_int, _vp, C.c_size_t, _vp], C.c_int),
+    "affx_grouped_workspace_size": ([_u32, _u32, _u32, _u32, _u32], C.c_size_t),
+    "affx_expert_ffn_grouped": ([C.POINTER(AffxLayer), _vp, _vp, _u32, _vp, _vp, _u32, _vp, C.c_int,
+                                 _vp, C.c_size_t, _vp], C.c_int),
+    "affx_expert_ffn_batch": ([_vp, _u32, _vp, _vp, _u32, _u32, _vp], _u32),
+    "affx_batch_workspace_size": ([_u32, _u32, _u32, _u32, _u32], C.c_size_t),
+    "affx_selftest_mfma_fp8": ([_vp, _vp, _vp, _vp], C.c_int),
+    "affx_gen_normal": ([_u64, _u64, C.c_double, _vp, C.c_int, _vp], C.c_int),
+    "affx_quantize_matrix": ([_vp, _u32, _u32, _vp, _vp, _vp, _vp, _vp, _vp], C.c_int),
+    "affx_fill_expert": ([_vp, _u64, _u64, _vp, _u32, _vp, _vp], C.c_int),
+}
+
+# every symbol include/affx.h declares (tests check the library exports them all)
+HEADER_SYMBOLS = tuple(_SIGS)
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise AffxError(f"{LIB_PATH} is missing: build it with `python -m affinity_amd.build` "
+                            "(there is no CPU fallback)")
+        L = C.CDLL(LIB_PATH)
+        for name, (args, res) in _SIGS.items():
+            f = getattr(L, name, None)
+            if f is None:
+                continue
+            f.argtypes = args
+            f.restype = res
+        _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    return lib().affx_last_error().decode(errors="replace")
+
+
+def check(rc: int, what: str) -> int:
+    if rc == AFFX_OK:
+        return rc
+    if rc == AFFX_DECLINED:
+        raise AffxDeclined(f"{what}: {last_error()}")
+    raise AffxError(f"{what} failed ({rc}): {last_error()}")

@@ -31,6 +31,14 @@ constexpr int kUnitFieldBytes = 12;
 constexpr int kTileCodeBytes = 64 * kUnitCodeBytes;    // 5120
 constexpr int kTileFieldBytes = 64 * kUnitFieldBytes;  // 768
 
+// Index of each plane in the off9/size9 arrays of affx_expert_layout: matrix-major
+// (gate, up, down), plane-minor (codes, fields, row scales).
+enum Plane : int {
+  kGateCodes = 0, kGateFields = 1, kGateRs = 2,
+  kUpCodes = 3, kUpFields = 4, kUpRs = 5,
+  kDownCodes = 6, kDownFields = 7, kDownRs = 8
+};
+
 inline uint64_t code_row_bytes(uint64_t cols) { return cols * 10 / 32; }
 inline uint64_t field_row_bytes(uint64_t cols) { return cols * 6 / 128; }
 

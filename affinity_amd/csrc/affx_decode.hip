@@ -19,13 +19,9 @@
 // Reference counterparts: expert_ffn_hip (src/gpu/expert_kernel.hip:2737-2808) with its
 // tr_mat_dot_rb GEMV (1084-1188), swiglu_all_kernel (114-129) and expert_gemv_kernel_tr
 // (1201-1258); the fixed-order reductions follow the reference's no-atomics rule (1219-1244).
-#include "affx_common.h"
+#include "affx_tile.h"
 
 namespace affx {
-
-typedef int v8i __attribute__((ext_vector_type(8)));
-typedef float v4f __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 struct DecodeArgs {
   const uint8_t* base;  // layer expert pool, device layout
@@ -142,108 +138,6 @@ __global__ void __launch_bounds__(256) decode_prep_kernel(const float* __restric
   }
 }
 
-// ------------------------------------------------------------------------------------------------
-// shared pieces of the two GEMV kernels
-// ------------------------------------------------------------------------------------------------
-
-// A unit's packed data: 20 code dwords + 3 field dwords.
-struct Unit {
-  uint32_t c[20];
-  uint32_t f[3];
-};
-
-__device__ __forceinline__ void load_unit(Unit& u, const uint8_t* codes, const uint8_t* fields,
-                                          uint64_t tile, uint32_t lane) {
-  const uint8_t* cp = codes + tile * kTileCodeBytes + lane * 16;
-#pragma unroll
-  for (int j = 0; j < 5; ++j) {
-    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(cp + j * 1024));
-    u.c[4 * j] = v[0]; u.c[4 * j + 1] = v[1]; u.c[4 * j + 2] = v[2]; u.c[4 * j + 3] = v[3];
-  }
-  const uint32_t* fp = reinterpret_cast<const uint32_t*>(fields + tile * kTileFieldBytes + lane * 12);
-  u.f[0] = __builtin_nontemporal_load(fp);
-  u.f[1] = __builtin_nontemporal_load(fp + 1);
-  u.f[2] = __builtin_nontemporal_load(fp + 2);
-}
-
-// Makes the unit's registers opaque at this point of the program. Called at the top of every
-// MFMA step, it stops the compiler from hoisting all eight steps' code extraction and address
-// arithmetic (pure ALU, free to move) in front of the first step, which would keep ~100 extra
-// VGPRs live and halve occupancy. No instructions are emitted.
-__device__ __forceinline__ void pin(Unit& u) {
-#pragma unroll
-  for (int i = 0; i < 20; ++i) asm volatile("" : "+v"(u.c[i]));
-#pragma unroll
-  for (int i = 0; i < 3; ++i) asm volatile("" : "+v"(u.f[i]));
-}
-
-// The A fragment of MFMA step m: codes 8m..8m+7 of the unit (blocks 2m, 2m+1), each looked up
-// in the LDS table of its block's (variant, rotation) and xor/add-transformed.
-template <int MSTEP>
-__device__ __forceinline__ v8i decode_a(const Unit& u, const uint32_t* tbl) {
-  v8i a;
-#pragma unroll
-  for (int bb = 0; bb < 2; ++bb) {
-    const int b = 2 * MSTEP + bb;
-    const uint32_t fb = stream_bits<3>(u.f, 6 * b, 6);
-    const uint32_t base = (fb >> 4) << 10;
-    const uint32_t x = block_xor(fb), ad = block_add(fb);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t code = stream_bits<20>(u.c, 10 * (4 * b + i), 10);
-      a[bb * 4 + i] = (int)((tbl[base + code] ^ x) + ad);
-    }
-  }
-  return a;
-}
-
-// B operand of one unit: per lane, 256 consecutive activation bytes of one (token, term) column
-// (MFMA step m reads bytes 32m..32m+31). Lanes whose column is unused (column 15, tokens beyond
-// M or not routed to this expert) read nothing and feed zeros.
-template <int CG>
-struct BSrc {
-  const u32x4* p[CG];
-};
-
-template <int CG>
-__device__ __forceinline__ BSrc<CG> b_source(const uint8_t* src_base, uint64_t term_stride,
-                                             uint64_t col0, uint32_t lane, uint32_t M,
-                                             uint32_t mask, const uint8_t* zeros) {
-  BSrc<CG> s;
-  const uint32_t c = lane & 15, g = lane >> 4;
-#pragma unroll
-  for (int cg = 0; cg < CG; ++cg) {
-    const uint32_t t = cg * 5 + c / 3, tau = c % 3;
-    const bool valid = c < 15 && t < M && ((mask >> t) & 1u);
-    s.p[cg] = valid ? reinterpret_cast<const u32x4*>(src_base + (uint64_t)(t * kTerms + tau) * term_stride +
-                                                     col0 + g * kSegCols)
-                    : reinterpret_cast<const u32x4*>(zeros);
-  }
-  return s;
-}
-
-__device__ __forceinline__ v8i b_step(const u32x4* p, int m) {
-  const u32x4 lo = p[2 * m], hi = p[2 * m + 1];
-  v8i v;
-  v[0] = (int)lo[0]; v[1] = (int)lo[1]; v[2] = (int)lo[2]; v[3] = (int)lo[3];
-  v[4] = (int)hi[0]; v[5] = (int)hi[1]; v[6] = (int)hi[2]; v[7] = (int)hi[3];
-  return v;
-}
-
-__device__ __forceinline__ v4f mfma(v8i a, v8i b, v4f c) {
-  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
-}
-
-// LDS codebook: table t = rot + 2*variant (= field >> 4), entry c = codebook dword, rotated by
-// 16 bits for rot = 1 (quad (a,b,c,d) read as (c,d,a,b): src/quant/blockquant.cpp:826-828).
-__device__ __forceinline__ void build_table(uint32_t* tbl, const uint32_t* __restrict__ cb) {
-  for (uint32_t i = threadIdx.x; i < kVariants * kLut; i += blockDim.x) {
-    const uint32_t d = cb[i], v = i >> 10, c = i & 1023u;
-    tbl[(2 * v) * kLut + c] = d;
-    tbl[(2 * v + 1) * kLut + c] = __builtin_amdgcn_alignbit(d, d, 16);
-  }
-}
-
 // y = x - low terms: the value of three E4M3 terms t0 + t1/16 + t2/256 from a lane's column c
 // and its two right neighbours (same 16-lane row group).
 __device__ __forceinline__ float combine_terms(float d) {
@@ -278,8 +172,8 @@ __global__ void __launch_bounds__(256) decode_gateup_kernel(DecodeArgs A) {
   Unit ug, uu;
   if (S < nst) {
     const uint64_t tile = (uint64_t)rt * nst + S;
-    load_unit(ug, ex + A.off[0], ex + A.off[3], tile, lane);
-    load_unit(uu, ex + A.off[1], ex + A.off[4], tile, lane);
+    load_unit(ug, ex + A.off[kGateCodes], ex + A.off[kGateFields], tile, lane);
+    load_unit(uu, ex + A.off[kUpCodes], ex + A.off[kUpFields], tile, lane);
   }
   build_table(tbl, A.codebook);
   __syncthreads();
@@ -349,8 +243,8 @@ __global__ void __launch_bounds__(256) decode_gateup_kernel(DecodeArgs A) {
         s[m] = sum;
       }
       const uint32_t row = rt * 16 + r;
-      const float rg = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(ex + A.off[2])[row] << 16);
-      const float ru = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(ex + A.off[5])[row] << 16);
+      const float rg = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(ex + A.off[kGateRs])[row] << 16);
+      const float ru = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(ex + A.off[kUpRs])[row] << 16);
       const int sig = A.plan->x_sigma[t];
       float g = ldexpf(s[0], -sig) * rg;
       float u = ldexpf(s[1], -sig) * ru;
@@ -397,7 +291,7 @@ __global__ void __launch_bounds__(256) decode_down_kernel(DecodeArgs A) {
   if (wv < units) {
     const uint32_t slot = wv / nst, S = wv % nst;
     const uint8_t* ex = A.base + (uint64_t)A.plan->expert[slot] * A.stride;
-    load_unit(cur, ex + A.off[6], ex + A.off[7], (uint64_t)rt * nst + S, lane);
+    load_unit(cur, ex + A.off[kDownCodes], ex + A.off[kDownFields], (uint64_t)rt * nst + S, lane);
   }
   build_table(tbl, A.codebook);
   __syncthreads();
@@ -413,9 +307,9 @@ __global__ void __launch_bounds__(256) decode_down_kernel(DecodeArgs A) {
     if (un < units) {
       const uint32_t sn = un / nst, Sn = un % nst;
       const uint8_t* exn = A.base + (uint64_t)A.plan->expert[sn] * A.stride;
-      load_unit(nxt, exn + A.off[6], exn + A.off[7], (uint64_t)rt * nst + Sn, lane);
+      load_unit(nxt, exn + A.off[kDownCodes], exn + A.off[kDownFields], (uint64_t)rt * nst + Sn, lane);
     }
-    const uint2 rsv = *reinterpret_cast<const uint2*>(ex + A.off[8] + (uint64_t)(rt * 16 + 4 * rg) * 2);
+    const uint2 rsv = *reinterpret_cast<const uint2*>(ex + A.off[kDownRs] + (uint64_t)(rt * 16 + 4 * rg) * 2);
     __builtin_amdgcn_sched_barrier(0);
     v4f acc[CG];
 #pragma unroll

@@ -1,0 +1,276 @@
+// Producer side on the GPU: the synthetic-weight generator and the codebook quantiser.
+//
+// affx_quantize_matrix is the reference's quantize_matrix for the quad format
+// (src/quant/blockquant.cpp:586-791) run per row on the GPU, bit-exact: every float operation
+// is the reference's, in its order, with explicit round-to-nearest intrinsics so that nothing is
+// contracted into an FMA. The nearest-quad search is exhaustive (each lane scores 16 of the 1024
+// entries, then a wave reduction keeps the minimum, or the lowest index among equal minima),
+// which returns exactly what the reference's scan and its acceleration grid return
+// (src/quant/blockquant.cpp:162-174, 558-578).
+//
+// affx_gen_normal is the benchmark's synthetic generator: splitmix64 in counter form plus
+// Box-Muller in double (the generator of src/quant/blockquant.cpp:37-42, 862-869), rounded to
+// f32 and then to bf16.
+#include "affx_common.h"
+
+namespace affx {
+
+// ---- generator ---------------------------------------------------------------------------------
+
+__device__ __forceinline__ uint64_t splitmix_at(uint64_t seed, uint64_t k) {
+  uint64_t x = seed + (k + 1) * 0x9E3779B97F4A7C15ull;
+  x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+  x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+  return x ^ (x >> 31);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+__global__ void gen_normal_kernel(uint64_t seed, uint64_t n, double scale, float* __restrict__ out,
+                                  int bf16_round) {
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const double u1 = (double)((splitmix_at(seed, 2 * i) >> 11) + 1) * (1.0 / 9007199254740992.0);
+  const double u2 = (double)((splitmix_at(seed, 2 * i + 1) >> 11) + 1) * (1.0 / 9007199254740992.0);
+  const double z = sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
+  float f = (float)(scale * z);
+  if (bf16_round) f = __uint_as_float((uint32_t)f32_to_bf16_rne(f) << 16);
+  out[i] = f;
+}
+
+// ---- quantiser ---------------------------------------------------------------------------------
+
+__device__ __forceinline__ float wave_min(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fminf(v, __shfl_xor(v, o));
+  return v;
+}
+
+// (value, index) minimum; equal values keep the lower index.
+__device__ __forceinline__ void wave_argmin(float& v, uint32_t& i) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(v, o);
+    const uint32_t oi = __shfl_xor(i, o);
+    if (ov < v || (ov == v && oi < i)) { v = ov; i = oi; }
+  }
+}
+
+// Squared distance of target t to entry e, dimensions summed in order, no contraction.
+__device__ __forceinline__ float qdist(const float4 e, const float t0, const float t1,
+                                       const float t2, const float t3) {
+  const float a = __fsub_rn(e.x, t0), b = __fsub_rn(e.y, t1), c = __fsub_rn(e.z, t2),
+              d = __fsub_rn(e.w, t3);
+  float s = __fmul_rn(a, a);
+  s = __fadd_rn(s, __fmul_rn(b, b));
+  s = __fadd_rn(s, __fmul_rn(c, c));
+  s = __fadd_rn(s, __fmul_rn(d, d));
+  return s;
+}
+
+// Minimum distance of one quad target to the entries of one variant (wave-uniform result).
+// The reference's scan starts from FLT_MAX and keeps strict improvements, so a minimum of
+// FLT_MAX or more (or NaN) reads as FLT_MAX.
+__device__ __forceinline__ float quad_min(const float4* __restrict__ ent, uint32_t lane, float t0,
+                                          float t1, float t2, float t3) {
+  float m = 3.402823466e38f;
+#pragma unroll 4
+  for (int j = 0; j < 16; ++j) {
+    const float s = qdist(ent[lane + 64 * j], t0, t1, t2, t3);
+    m = s < m ? s : m;
+  }
+  return wave_min(m);
+}
+
+__device__ __forceinline__ uint32_t quad_argmin(const float4* __restrict__ ent, uint32_t lane,
+                                                float t0, float t1, float t2, float t3) {
+  float m = 3.402823466e38f;
+  uint32_t bi = 0xFFFFFFFFu;
+  for (int j = 0; j < 16; ++j) {
+    const uint32_t c = lane + 64 * j;
+    const float s = qdist(ent[c], t0, t1, t2, t3);
+    if (s < m) { m = s; bi = c; }
+  }
+  wave_argmin(m, bi);
+  return bi == 0xFFFFFFFFu ? 0u : bi;  // nothing below FLT_MAX: the scan's default, code 0
+}
+
+// One workgroup per row: 4 waves split the row's 16-blocks; the row's bit streams are built in
+// LDS with atomicOr (disjoint bits) and written out as whole bytes.
+constexpr int kQuantMaxCols = 8192;
+
+__global__ void __launch_bounds__(256) quantize_rows_kernel(
+    const float* __restrict__ w, uint32_t rows, uint32_t cols, const float4* __restrict__ cb,
+    const float* __restrict__ imp, uint8_t* __restrict__ codes, uint8_t* __restrict__ fields,
+    uint16_t* __restrict__ rscales) {
+  const uint32_t r = blockIdx.x;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  __shared__ float4 ent[kVariants * kLut];                      // 32 KiB
+  __shared__ uint32_t cbits[kQuantMaxCols * 10 / 128];          // row code stream
+  __shared__ uint32_t fbits[kQuantMaxCols * 6 / 512 + 1];       // row field stream
+  __shared__ float red[4];
+  for (uint32_t i = tid; i < kVariants * kLut; i += 256) ent[i] = cb[i];
+  const uint32_t ncw = cols * 10 / 128, nfw = (cols * 6 / 16 + 31) / 32;
+  for (uint32_t i = tid; i < ncw; i += 256) cbits[i] = 0;
+  for (uint32_t i = tid; i < nfw; i += 256) fbits[i] = 0;
+
+  const float* row = w + (uint64_t)r * cols;
+  float rmax = 0.f;
+  for (uint32_t c = tid; c < cols; c += 256) {
+    const float a = fabsf(row[c]);
+    rmax = rmax < a ? a : rmax;
+  }
+  rmax = -wave_min(-rmax);
+  if (lane == 0) red[wv] = rmax;
+  __syncthreads();
+  rmax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float rscale = rmax > 0.f ? ldexpf(rmax, -7) : 0.f;
+  const uint16_t h = f32_to_bf16_rne(rscale);
+  rscale = __uint_as_float((uint32_t)h << 16);
+  if (tid == 0) rscales[r] = h;
+
+  const uint32_t nblk = cols / kBlock;
+  for (uint32_t b = wv; b < nblk; b += 4) {
+    float blk[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) blk[i] = row[b * 16 + i];
+    float bmax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) { const float a = fabsf(blk[i]); bmax = bmax < a ? a : bmax; }
+    float wt[4] = {1.f, 1.f, 1.f, 1.f};
+    if (imp) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float s = 0.f;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) s = __fadd_rn(s, imp[b * 16 + 4 * i + p]);
+        wt[i] = __fdiv_rn(s, 4.0f);
+      }
+    }
+    uint32_t best_s = 0, best_v = 0, best_g = 0;
+    double best_err = 1.7976931348623157e308;
+    if (bmax > 0.f && rscale > 0.f) {
+      const double ideal = __ddiv_rn((double)bmax, (double)rscale);
+      uint32_t mid = 0;
+      double bd = 1.7976931348623157e308;
+      for (uint32_t s = 0; s <= 7; ++s) {
+        const double d = fabs((double)(float)(1u << s) - ideal);
+        if (d < bd) { bd = d; mid = s; }
+      }
+      const int lo = (int)mid - 1 > 0 ? (int)mid - 1 : 0;
+      const int hi = (int)mid + 1 < 7 ? (int)mid + 1 : 7;
+      for (uint32_t v = 0; v < 2; ++v) {
+        const float4* ev = ent + v * kLut;
+        for (int s = lo; s <= hi; ++s) {
+          const float bs = __fmul_rn(rscale, (float)(1u << s));
+          if (bs <= 0.f) continue;
+          const float inv = __fdiv_rn(1.0f, bs);
+          for (uint32_t g = 0; g < 4; ++g) {
+            const float sg = (g & 1u) ? -inv : inv;
+            const uint32_t rh = (g & 2u) ? 2u : 0u;
+            float acc = 0.f;
+            for (int i = 0; i < 4; ++i) {
+              const float t0 = __fmul_rn(blk[4 * i + (0 + rh) % 4], sg);
+              const float t1 = __fmul_rn(blk[4 * i + (1 + rh) % 4], sg);
+              const float t2 = __fmul_rn(blk[4 * i + (2 + rh) % 4], sg);
+              const float t3 = __fmul_rn(blk[4 * i + (3 + rh) % 4], sg);
+              const float d = quad_min(ev, lane, t0, t1, t2, t3);
+              acc = __fadd_rn(acc, __fmul_rn(d, wt[i]));
+            }
+            const double e = __dmul_rn(__dmul_rn((double)acc, (double)bs), (double)bs);
+            if (e < best_err) { best_err = e; best_s = (uint32_t)s; best_v = v; best_g = g; }
+          }
+        }
+      }
+    }
+    const uint32_t field = (best_v << 5) | (best_g << 3) | best_s;
+    const float mag = __fmul_rn(rscale, (float)(1u << best_s));
+    const float bs = (best_g & 1u) ? -mag : mag;
+    const uint32_t rh = (best_g & 2u) ? 2u : 0u;
+    uint32_t code[4] = {0, 0, 0, 0};
+    if (mag > 0.f) {
+      for (int i = 0; i < 4; ++i) {
+        const float t0 = __fdiv_rn(blk[4 * i + (0 + rh) % 4], bs);
+        const float t1 = __fdiv_rn(blk[4 * i + (1 + rh) % 4], bs);
+        const float t2 = __fdiv_rn(blk[4 * i + (2 + rh) % 4], bs);
+        const float t3 = __fdiv_rn(blk[4 * i + (3 + rh) % 4], bs);
+        code[i] = quad_argmin(ent + best_v * kLut, lane, t0, t1, t2, t3);
+      }
+    }
+    if (lane == 0) {
+      const uint32_t fpos = b * 6;
+      atomicOr(&fbits[fpos >> 5], field << (fpos & 31));
+      if ((fpos & 31) > 26) atomicOr(&fbits[(fpos >> 5) + 1], field >> (32 - (fpos & 31)));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t cpos = (b * 4 + i) * 10;
+        atomicOr(&cbits[cpos >> 5], code[i] << (cpos & 31));
+        if ((cpos & 31) > 22) atomicOr(&cbits[(cpos >> 5) + 1], code[i] >> (32 - (cpos & 31)));
+      }
+    }
+  }
+  __syncthreads();
+  // a row's streams are whole bytes (cols % 64 == 0): 5*cols/16 code bytes, 3*cols/64 field bytes
+  const uint32_t ncb = cols * 10 / 32, nfb = cols * 6 / 128;
+  const uint8_t* cs = reinterpret_cast<const uint8_t*>(cbits);
+  const uint8_t* fs = reinterpret_cast<const uint8_t*>(fbits);
+  for (uint32_t i = tid; i < ncb; i += 256) codes[(uint64_t)r * ncb + i] = cs[i];
+  for (uint32_t i = tid; i < nfb; i += 256) fields[(uint64_t)r * nfb + i] = fs[i];
+}
+
+}  // namespace affx
+
+using namespace affx;
+
+extern "C" {
+
+int affx_gen_normal(uint64_t seed, uint64_t n, double scale, void* out, int bf16_round,
+                    void* stream) {
+  if (!out) return set_error(AFFX_ERR_ARG, "gen_normal: null output");
+  if (n == 0) return AFFX_OK;
+  const uint64_t blocks = (n + 255) / 256;
+  if (blocks > 0x7FFFFFFFull) return set_error(AFFX_ERR_ARG, "gen_normal: n too large");
+  hipLaunchKernelGGL(gen_normal_kernel, dim3((uint32_t)blocks), dim3(256), 0, (hipStream_t)stream,
+                     seed, n, scale, (float*)out, bf16_round);
+  return check_launch("gen_normal_kernel");
+}
+
+int affx_quantize_matrix(const void* w, uint32_t rows, uint32_t cols, const void* codebook_f32,
+                         const void* importance, void* codes, void* fields, void* rscales,
+                         void* stream) {
+  if (!w || !codebook_f32 || !codes || !fields || !rscales)
+    return set_error(AFFX_ERR_ARG, "quantize_matrix: null pointer");
+  if (rows == 0 || cols == 0 || cols % 64 || cols > kQuantMaxCols)
+    return set_error(AFFX_ERR_ARG, "quantize_matrix: cols must be a multiple of 64 and <= %d",
+                     kQuantMaxCols);
+  hipLaunchKernelGGL(quantize_rows_kernel, dim3(rows), dim3(256), 0, (hipStream_t)stream,
+                     (const float*)w, rows, cols, (const float4*)codebook_f32,
+                     (const float*)importance, (uint8_t*)codes, (uint8_t*)fields,
+                     (uint16_t*)rscales);
+  return check_launch("quantize_rows_kernel");
+}
+
+// One synthetic expert in container layout: gate/up/down = bf16(0.02 * N(0,1)) with seeds
+// seed + 0/1/2, quantised against `codebook_f32`. `scratch` holds rows*cols floats of the largest
+// matrix (inter*hidden).
+int affx_fill_expert(void* expert, uint64_t hidden, uint64_t inter, const void* codebook_f32,
+                     uint32_t seed, void* scratch, void* stream) {
+  if (!expert || !codebook_f32 || !scratch) return set_error(AFFX_ERR_ARG, "fill_expert: null pointer");
+  uint64_t off[9];
+  affx_expert_layout(hidden, inter, off, nullptr);
+  const uint64_t rows[3] = {inter, inter, hidden}, cols[3] = {hidden, hidden, inter};
+  uint8_t* e = (uint8_t*)expert;
+  for (int m = 0; m < 3; ++m) {
+    int rc = affx_gen_normal((uint64_t)seed + m, rows[m] * cols[m], 0.02, scratch, 1, stream);
+    if (rc) return rc;
+    rc = affx_quantize_matrix(scratch, (uint32_t)rows[m], (uint32_t)cols[m], codebook_f32, nullptr,
+                              e + off[3 * m], e + off[3 * m + 1], e + off[3 * m + 2], stream);
+    if (rc) return rc;
+  }
+  return AFFX_OK;
+}
+
+}  // extern "C"

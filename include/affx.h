@@ -178,6 +178,34 @@ typedef struct affx_engine_ctx {
 uint32_t affx_expert_ffn_batch(void* ctx, uint32_t layer, const uint32_t* sel, const float* w,
                                uint32_t nb_tok, uint32_t k, uint8_t* handled);
 
+/* Workspace bytes affx_expert_ffn_batch needs for a batch of nb_tok tokens (the reference sizes
+ * its per-rank arenas the same way, growing them on demand: grow_w8a8,
+ * src/gpu/static_placement.hip:1254-1346). */
+size_t affx_batch_workspace_size(uint32_t nb_tok, uint32_t top_k, uint32_t n_experts,
+                                 uint32_t hidden, uint32_t inter);
+
+/* ---- producer: synthetic weights and the codebook quantiser on the GPU ---------------------- */
+
+/* out[i] = bf16_RNE((float)(scale * N_i)) (or the plain float when bf16_round == 0), with N_i
+ * the i-th Box-Muller normal of a splitmix64 stream seeded `seed`, two draws per normal: the
+ * generator of src/quant/blockquant.cpp:37-42, 862-869 in counter form. out: device f32[n]. */
+int affx_gen_normal(uint64_t seed, uint64_t n, double scale, void* out, int bf16_round,
+                    void* stream);
+
+/* quantize_matrix (src/quant/blockquant.cpp:586-791) for the quad format on the GPU, bit-exact:
+ * w f32 [rows][cols] (cols % 64 == 0, <= 8192) -> codes/fields/rscales in the container's
+ * row-major streams. codebook_f32: float[2][1024][4] (the projected E4M3 values). importance:
+ * optional f32[cols] column importance, or NULL. All device pointers. */
+int affx_quantize_matrix(const void* w, uint32_t rows, uint32_t cols, const void* codebook_f32,
+                         const void* importance, void* codes, void* fields, void* rscales,
+                         void* stream);
+
+/* One synthetic expert in container layout: gate/up/down = bf16(0.02 N(0,1)) from seeds
+ * seed+0/1/2, quantised against codebook_f32. scratch: device f32[inter*hidden]. The quantiser
+ * loop of tools/aff_quantize.cpp:589-616 for one expert, with synthetic weights. */
+int affx_fill_expert(void* expert, uint64_t hidden, uint64_t inter, const void* codebook_f32,
+                     uint32_t seed, void* scratch, void* stream);
+
 /* ---- diagnostics ---------------------------------------------------------------------------- */
 
 /* Runs one v_mfma_scale_f32_16x16x128_f8f6f4 (E4M3 x E4M3, unit scales) on a[64][32] and

@@ -1,0 +1,216 @@
+// Runs libaffx's kernels on the CPU (see hip/hip_runtime.h) against the C oracle.
+// Test infrastructure: built with AddressSanitizer by tests/test_cpu_emulation.py.
+//
+//   emu_main decode  hidden inter n_experts M K seed      -> rel_l2 of the decode FFN
+//   emu_main grouped hidden inter n_experts T K seed lo   -> rel_l2 of the grouped FFN
+//   emu_main quant   rows cols seed                       -> planes bit-exact vs the oracle
+//   emu_main dequant hidden inter seed                    -> dequant bit-exact vs the oracle
+//
+// Exit status 0 when the check passes.
+#include <hip/hip_runtime.h>
+
+thread_local emu_dim3 threadIdx, blockIdx;
+emu_dim3 blockDim, gridDim;
+thread_local EmuBlock* emu_blk;
+
+#define AFFX_PIN(x) ((void)0)
+#include "../../affinity_amd/csrc/affx_layout.hip"
+#include "../../affinity_amd/csrc/affx_decode.hip"
+#include "../../affinity_amd/csrc/affx_quant.hip"
+#include "../../affinity_amd/csrc/affx_grouped.hip"
+
+extern "C" {
+#include "../../oracle/oracle.h"
+}
+
+#include <random>
+#include <string>
+
+namespace {
+
+uint16_t bf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return (uint16_t)((u + 0x7FFF + ((u >> 16) & 1)) >> 16);
+}
+
+std::vector<uint32_t> load_codebook() {
+  std::vector<uint32_t> cb(2048);
+  FILE* f = fopen("tests/golden/c1_codebook.bin", "rb");
+  if (!f || fread(cb.data(), 4, 2048, f) != 2048) { fprintf(stderr, "codebook fixture missing\n"); exit(2); }
+  fclose(f);
+  return cb;
+}
+
+// Random planes (every field value) with bf16 row scales in [4e-4, 2e-3).
+void random_expert(std::mt19937_64& rng, uint8_t* ex, const uint64_t* off, const uint64_t* size) {
+  for (int p = 0; p < 9; ++p) {
+    if (p % 3 == 2) {
+      for (uint64_t r = 0; r < size[p] / 2; ++r) {
+        const uint16_t h = bf16(4e-4f + 1.6e-3f * (float)(rng() % 1000) / 1000.f);
+        memcpy(ex + off[p] + 2 * r, &h, 2);
+      }
+    } else {
+      for (uint64_t i = 0; i < size[p]; ++i) ex[off[p] + i] = rng() & 0xff;
+    }
+  }
+}
+
+double rel_l2(const std::vector<float>& a, const std::vector<float>& b) {
+  double num = 0, den = 0;
+  for (size_t i = 0; i < a.size(); ++i) {
+    num += ((double)a[i] - b[i]) * ((double)a[i] - b[i]);
+    den += (double)b[i] * b[i];
+  }
+  return den > 0 ? sqrt(num / den) : sqrt(num);
+}
+
+struct Layer {
+  uint32_t hidden, inter, n;
+  uint64_t stride, off[9], size[9];
+  std::vector<uint8_t> cont, dev;
+  std::vector<uint32_t> cb;
+  std::vector<float> cbf;
+  Layer(uint32_t h, uint32_t i, uint32_t n_, std::mt19937_64& rng) : hidden(h), inter(i), n(n_) {
+    stride = affx_expert_layout(h, i, off, size);
+    cont.assign(n * stride, 0);
+    dev.assign(n * stride, 0);
+    for (uint32_t e = 0; e < n; ++e) {
+      random_expert(rng, cont.data() + e * stride, off, size);
+      if (affx_expert_to_device_layout(cont.data() + e * stride, dev.data() + e * stride, h, i)) exit(3);
+    }
+    cb = load_codebook();
+    cbf.assign(8192, 0.f);
+    orc_unpack_codebook(cb.data(), cbf.data());
+  }
+  affx_layer abi() { return affx_layer{dev.data(), stride, n, hidden, inter, cb.data(), 10.0f}; }
+  void oracle(const float* x, const uint32_t* sel, const float* w, uint32_t T, uint32_t K, float* y) {
+    for (uint32_t t = 0; t < T; ++t)
+      for (uint32_t j = 0; j < K; ++j) {
+        const uint32_t e = sel[t * K + j];
+        if (e >= n) continue;
+        orc_expert_ffn(cont.data() + (uint64_t)e * stride, hidden, inter, cbf.data(), x + (uint64_t)t * hidden,
+                       w[t * K + j], 10.0f, y + (uint64_t)t * hidden);
+      }
+  }
+};
+
+void routes(std::mt19937_64& rng, uint32_t T, uint32_t K, uint32_t n, std::vector<uint32_t>& sel,
+            std::vector<float>& w) {
+  sel.resize(T * K);
+  w.resize(T * K);
+  std::vector<uint32_t> ids(n);
+  for (uint32_t t = 0; t < T; ++t) {
+    for (uint32_t i = 0; i < n; ++i) ids[i] = i;
+    std::shuffle(ids.begin(), ids.end(), rng);
+    for (uint32_t j = 0; j < K; ++j) {
+      sel[t * K + j] = ids[j % n];
+      w[t * K + j] = 0.05f + (float)(rng() % 1000) / 1000.f;
+    }
+  }
+}
+
+int run_decode(int argc, char** argv) {
+  const uint32_t hidden = atoi(argv[2]), inter = atoi(argv[3]), n = atoi(argv[4]), M = atoi(argv[5]),
+                 K = atoi(argv[6]);
+  std::mt19937_64 rng(atoi(argv[7]));
+  Layer L(hidden, inter, n, rng);
+  std::vector<float> x(M * hidden), y(M * hidden, 0.f), yref(M * hidden, 0.f), w;
+  std::vector<uint32_t> sel;
+  std::normal_distribution<float> nd;
+  for (auto& v : x) v = 0.5f * nd(rng);
+  routes(rng, M, K, n, sel, w);
+  if (M > 1) sel[K - 1] = n + 7;  // a padding id
+  affx_layer abi = L.abi();
+  const size_t wsb = affx_decode_workspace_size(M, K, hidden, inter);
+  std::vector<uint8_t> ws(wsb);
+  const int rc = affx_expert_ffn_decode(&abi, x.data(), hidden, 1, M, sel.data(), w.data(), K, y.data(),
+                                        hidden, 1, 0, ws.data(), wsb, nullptr);
+  L.oracle(x.data(), sel.data(), w.data(), M, K, yref.data());
+  const double e = rel_l2(y, yref);
+  printf("decode rc=%d rel_l2=%.3e\n", rc, e);
+  return rc == 0 && e <= 1e-3 ? 0 : 1;
+}
+
+int run_grouped(int argc, char** argv) {
+  const uint32_t hidden = atoi(argv[2]), inter = atoi(argv[3]), n = atoi(argv[4]), T = atoi(argv[5]),
+                 K = atoi(argv[6]);
+  std::mt19937_64 rng(atoi(argv[7]));
+  const bool lo = argc > 8 && atoi(argv[8]);
+  Layer L(hidden, inter, n, rng);
+  std::vector<uint16_t> xb(T * hidden), xl(T * hidden);
+  std::vector<float> x(T * hidden), y(T * hidden, 0.f), yref(T * hidden, 0.f), w;
+  std::vector<uint32_t> sel;
+  std::normal_distribution<float> nd;
+  for (size_t i = 0; i < x.size(); ++i) {
+    const float v = nd(rng);
+    xb[i] = bf16(v);
+    const float hi = __uint_as_float((uint32_t)xb[i] << 16);
+    xl[i] = bf16(v - hi);
+    x[i] = lo ? hi + __uint_as_float((uint32_t)xl[i] << 16) : hi;
+  }
+  routes(rng, T, K, n, sel, w);
+  sel[K] = n + 1;  // a padding id
+  affx_layer abi = L.abi();
+  const size_t wsb = affx_grouped_workspace_size(T, K, n, hidden, inter);
+  std::vector<uint8_t> ws(wsb);
+  const int rc = affx_expert_ffn_grouped(&abi, xb.data(), lo ? xl.data() : nullptr, T, sel.data(), w.data(),
+                                         K, y.data(), 0, ws.data(), wsb, nullptr);
+  L.oracle(x.data(), sel.data(), w.data(), T, K, yref.data());
+  const double e = rel_l2(y, yref);
+  printf("grouped rc=%d rel_l2=%.3e %s\n", rc, e, affx_last_error());
+  return rc == 0 && e <= 1e-3 ? 0 : 1;
+}
+
+int run_quant(int argc, char** argv) {
+  const uint32_t rows = atoi(argv[2]), cols = atoi(argv[3]);
+  std::mt19937_64 rng(atoi(argv[4]));
+  std::vector<float> w(rows * cols);
+  std::normal_distribution<float> nd;
+  for (auto& v : w) v = 0.02f * nd(rng);
+  for (uint32_t c = 0; c < 16 && c < cols; ++c) w[c] = 0.f;  // an all-zero block
+  const auto cb = load_codebook();
+  std::vector<float> cbf(8192);
+  orc_unpack_codebook(cb.data(), cbf.data());
+  const uint64_t nc = rows * cols * 10 / 32, nf = rows * cols * 6 / 128;
+  std::vector<uint8_t> c1(nc), f1(nf), c2(nc), f2(nf);
+  std::vector<uint16_t> r1(rows), r2(rows);
+  int rc = affx_quantize_matrix(w.data(), rows, cols, cbf.data(), nullptr, c1.data(), f1.data(), r1.data(), nullptr);
+  orc_quantize_matrix(w.data(), rows, cols, cbf.data(), nullptr, c2.data(), f2.data(), r2.data());
+  const bool ok = c1 == c2 && f1 == f2 && r1 == r2;
+  printf("quant rc=%d exact=%d\n", rc, (int)ok);
+  return rc == 0 && ok ? 0 : 1;
+}
+
+int run_dequant(int argc, char** argv) {
+  const uint32_t hidden = atoi(argv[2]), inter = atoi(argv[3]);
+  std::mt19937_64 rng(atoi(argv[4]));
+  Layer L(hidden, inter, 1, rng);
+  bool ok = true;
+  for (int m = 0; m < 3; ++m) {
+    const uint32_t rows = m < 2 ? inter : hidden, cols = m < 2 ? hidden : inter;
+    affx_matrix mat{L.dev.data() + L.off[3 * m], L.dev.data() + L.off[3 * m + 1], L.dev.data() + L.off[3 * m + 2],
+                    rows, cols};
+    std::vector<float> got(rows * cols), ref(rows * cols);
+    if (affx_dequant_matrix(&mat, L.cb.data(), got.data(), nullptr)) return 1;
+    orc_dequantize_matrix(L.cont.data() + L.off[3 * m], L.cont.data() + L.off[3 * m + 1],
+                          (const uint16_t*)(L.cont.data() + L.off[3 * m + 2]), rows, cols, L.cbf.data(), ref.data());
+    ok = ok && memcmp(got.data(), ref.data(), got.size() * 4) == 0;
+  }
+  printf("dequant exact=%d\n", (int)ok);
+  return ok ? 0 : 1;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  if (argc < 2) return 2;
+  orc_set_threads(4);
+  const std::string cmd = argv[1];
+  if (cmd == "decode" && argc >= 8) return run_decode(argc, argv);
+  if (cmd == "grouped" && argc >= 8) return run_grouped(argc, argv);
+  if (cmd == "quant" && argc >= 5) return run_quant(argc, argv);
+  if (cmd == "dequant" && argc >= 5) return run_dequant(argc, argv);
+  fprintf(stderr, "usage: see header\n");
+  return 2;
+}

@@ -1,0 +1,170 @@
+// CPU emulation of the HIP surface libaffx's kernels use (test infrastructure, never shipped).
+//
+// A kernel launch runs one workgroup at a time with one std::thread per work-item; __syncthreads
+// is a real block barrier and every cross-lane operation (shuffles, ballot, the MFMA) exchanges
+// values through per-wave slots between two wave barriers. Device memory is ordinary host memory,
+// so building with -fsanitize=address turns any out-of-bounds access of a kernel into an ASan
+// report on the CPU. The fp8 MFMA is computed exactly (double accumulation) with the gfx950 lane
+// layout the kernels assume (A/B lane l = row/column l%16 and k-group l/16, D lane l element v =
+// D[4*(l/16)+v][l%16]); tests/test_gpu_decode.py pins that layout on the hardware.
+#pragma once
+#include <barrier>
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <functional>
+#include <thread>
+#include <vector>
+#include <algorithm>
+
+#define __global__
+#define __device__
+#define __host__
+#define __forceinline__ inline
+#define __launch_bounds__(...)
+#define __restrict__
+#define __shared__ static
+
+struct emu_dim3 { uint32_t x = 1, y = 1, z = 1; };
+struct dim3 { uint32_t x, y, z; dim3(uint32_t a = 1, uint32_t b = 1, uint32_t c = 1) : x(a), y(b), z(c) {} };
+extern thread_local emu_dim3 threadIdx, blockIdx;
+extern emu_dim3 blockDim, gridDim;
+
+typedef int hipError_t;
+typedef void* hipStream_t;
+#define hipSuccess 0
+inline const char* hipGetErrorString(int) { return "emu"; }
+inline int hipGetLastError() { return 0; }
+inline int hipGetDevice(int* d) { *d = 0; return 0; }
+struct hipDeviceProp_t { char gcnArchName[64]; int multiProcessorCount; };
+inline int hipGetDeviceProperties(hipDeviceProp_t* p, int) { strcpy(p->gcnArchName, "gfx950"); p->multiProcessorCount = 256; return 0; }
+inline int hipMemsetAsync(void* p, int v, size_t n, hipStream_t) { memset(p, v, n); return 0; }
+
+struct uint2 { uint32_t x, y; };
+struct uint4 { uint32_t x, y, z, w; };
+struct float4 { float x, y, z, w; };
+inline uint4 make_uint4(uint32_t a, uint32_t b, uint32_t c, uint32_t d) { return {a, b, c, d}; }
+inline float4 make_float4(float a, float b, float c, float d) { return {a, b, c, d}; }
+
+inline float __uint_as_float(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+inline uint32_t __float_as_uint(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+inline int __popc(uint32_t v) { return __builtin_popcount(v); }
+inline int __popcll(uint64_t v) { return __builtin_popcountll(v); }
+inline float __fsub_rn(float a, float b) { volatile float r = a - b; return r; }
+inline float __fadd_rn(float a, float b) { volatile float r = a + b; return r; }
+inline float __fmul_rn(float a, float b) { volatile float r = a * b; return r; }
+inline float __fdiv_rn(float a, float b) { volatile float r = a / b; return r; }
+inline double __dmul_rn(double a, double b) { volatile double r = a * b; return r; }
+inline double __ddiv_rn(double a, double b) { volatile double r = a / b; return r; }
+
+inline uint32_t __builtin_amdgcn_alignbit(uint32_t hi, uint32_t lo, uint32_t s) {
+  return (uint32_t)((((uint64_t)hi << 32) | lo) >> (s & 31));
+}
+inline uint32_t __builtin_amdgcn_perm(uint32_t s0, uint32_t s1, uint32_t sel) {
+  uint8_t bytes[8];
+  for (int i = 0; i < 4; ++i) { bytes[i] = (s1 >> (8 * i)) & 0xff; bytes[4 + i] = (s0 >> (8 * i)) & 0xff; }
+  uint32_t out = 0;
+  for (int i = 0; i < 4; ++i) {
+    uint32_t sb = (sel >> (8 * i)) & 0xff, v;
+    if (sb < 8) v = bytes[sb]; else if (sb == 12) v = 0; else if (sb >= 13) v = 0xff; else { fprintf(stderr, "perm sel\n"); abort(); }
+    out |= v << (8 * i);
+  }
+  return out;
+}
+#define __builtin_amdgcn_sched_barrier(x) ((void)0)
+#define __builtin_nontemporal_load(p) (*(p))
+
+// ---- wave / block synchronisation ----
+struct EmuBlock {
+  std::barrier<>* block_bar;
+  std::barrier<>* wave_bar[16];
+  uint64_t xfer[16][64][16];   // per-wave lane exchange (up to 16 x 32-bit words... in 64-bit slots)
+};
+extern thread_local EmuBlock* emu_blk;
+inline void __syncthreads() { emu_blk->block_bar->arrive_and_wait(); }
+inline uint32_t emu_lane() { return threadIdx.x & 63; }
+inline uint32_t emu_wave() { return threadIdx.x >> 6; }
+inline void emu_wave_sync() { emu_blk->wave_bar[emu_wave()]->arrive_and_wait(); }
+
+template <typename T>
+inline T emu_exchange(T v, uint32_t src) {
+  static_assert(sizeof(T) <= 8, "");
+  uint64_t bits = 0; memcpy(&bits, &v, sizeof(T));
+  emu_blk->xfer[emu_wave()][emu_lane()][0] = bits;
+  emu_wave_sync();
+  uint64_t got = emu_blk->xfer[emu_wave()][src & 63][0];
+  emu_wave_sync();
+  T r; memcpy(&r, &got, sizeof(T)); return r;
+}
+template <typename T> inline T __shfl_xor(T v, int o, int width = 64) { return emu_exchange(v, emu_lane() ^ o); }
+template <typename T> inline T __shfl_down(T v, int d, int width = 64) {
+  uint32_t l = emu_lane(); uint32_t src = ((l % width) + d < (uint32_t)width) ? l + d : l;
+  return emu_exchange(v, src);
+}
+inline uint64_t __ballot(int pred) {
+  emu_blk->xfer[emu_wave()][emu_lane()][0] = pred ? 1 : 0;
+  emu_wave_sync();
+  uint64_t m = 0;
+  for (int i = 0; i < 64; ++i) if (emu_blk->xfer[emu_wave()][i][0]) m |= 1ull << i;
+  emu_wave_sync();
+  return m;
+}
+inline uint32_t atomicOr(uint32_t* p, uint32_t v) { return __atomic_fetch_or(p, v, __ATOMIC_SEQ_CST); }
+inline uint32_t atomicAdd(uint32_t* p, uint32_t v) { return __atomic_fetch_add(p, v, __ATOMIC_SEQ_CST); }
+inline uint32_t min(uint32_t a, uint32_t b) { return a < b ? a : b; }
+
+// ---- MFMA 16x16x128 fp8 x fp8 -> f32, lane layout as on gfx950 ----
+typedef int emu_v8i __attribute__((ext_vector_type(8)));
+typedef float emu_v4f __attribute__((ext_vector_type(4)));
+inline float emu_e4m3(uint32_t b) {
+  const int s = (b >> 7) & 1, e = (b >> 3) & 15, m = b & 7;
+  float f = e == 0 ? ldexpf(m / 8.0f, -6) : (e == 15 && m == 7 ? NAN : ldexpf(1.0f + m / 8.0f, e - 7));
+  return s ? -f : f;
+}
+inline emu_v4f __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(emu_v8i a, emu_v8i b, emu_v4f c, int, int, int, int, int, int) {
+  uint32_t w = emu_wave(), l = emu_lane();
+  for (int i = 0; i < 8; ++i) emu_blk->xfer[w][l][i] = (uint32_t)a[i] | ((uint64_t)(uint32_t)b[i] << 32);
+  emu_wave_sync();
+  emu_v4f d = c;
+  for (int v = 0; v < 4; ++v) {
+    const uint32_t row = 4 * (l / 16) + v, col = l % 16;
+    double acc = 0;
+    for (int g = 0; g < 4; ++g)
+      for (int i = 0; i < 8; ++i) {
+        uint32_t A = (uint32_t)emu_blk->xfer[w][row + 16 * g][i], B = (uint32_t)(emu_blk->xfer[w][col + 16 * g][i] >> 32);
+        for (int p = 0; p < 4; ++p) acc += (double)emu_e4m3((A >> (8 * p)) & 0xff) * emu_e4m3((B >> (8 * p)) & 0xff);
+      }
+    d[v] = c[v] + (float)acc;
+  }
+  emu_wave_sync();
+  return d;
+}
+
+// ---- launch: one block at a time, blockDim.x threads ----
+template <typename F, typename... Args>
+void emu_launch(F kernel, dim3 grid, dim3 block, Args... args) {
+  gridDim = {grid.x, grid.y, grid.z};
+  blockDim = {block.x, block.y, block.z};
+  const uint32_t nt = block.x;
+  for (uint32_t bz = 0; bz < grid.z; ++bz)
+    for (uint32_t by = 0; by < grid.y; ++by)
+      for (uint32_t bx = 0; bx < grid.x; ++bx) {
+        std::barrier<> bb(nt);
+        EmuBlock blk;
+        blk.block_bar = &bb;
+        std::vector<std::barrier<>*> wbs;
+        for (uint32_t w = 0; w < (nt + 63) / 64; ++w) { wbs.push_back(new std::barrier<>(std::min<uint32_t>(64, nt - 64 * w))); blk.wave_bar[w] = wbs.back(); }
+        std::vector<std::thread> ts;
+        for (uint32_t t = 0; t < nt; ++t)
+          ts.emplace_back([&, t]() {
+            threadIdx = {t, 0, 0}; blockIdx = {bx, by, bz}; emu_blk = &blk;
+            kernel(args...);
+            // a returning work-item keeps the barriers balanced for the others
+          });
+        for (auto& th : ts) th.join();
+        for (auto* b : wbs) delete b;
+      }
+}
+#define hipLaunchKernelGGL(k, g, b, shm, s, ...) emu_launch(k, dim3(g), dim3(b), __VA_ARGS__)

@@ -1,0 +1,195 @@
+"""GPU parity of the decode path: layout, dequant (bit-exact), fp8-MFMA decode FFN (rel-L2).
+
+Every compute call goes through libaffx.so's C-ABI; the CPU oracle (oracle/liboracle.so) is the
+checker. Arbitrary planes (random code and field bytes) exercise every field value; the
+quantised synthetic experts of the benchmark configs come from the GPU quantiser, whose bytes
+test_gpu_quant.py pins to the reference's golden hashes.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+import pytest
+
+from gpu_util import planes, random_expert_container, rel_l2
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3  # expert outputs: relative L2 vs the CPU path (fp32 accumulate)
+
+
+@pytest.fixture(scope="module")
+def ax():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import affinity_amd.experts as ax
+    ax.init()
+    return ax
+
+
+def _pool_from_numpy(ax, experts: np.ndarray, cb_packed, hidden, inter):
+    t = torch.from_numpy(experts.reshape(-1)).cuda()
+    pool = ax.ExpertPool.from_container(t, cb_packed, hidden, inter)
+    torch.cuda.synchronize()
+    return pool
+
+
+def _mfma(lib, a, b):
+    ga, gb = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
+    d = torch.zeros(64 * 4, dtype=torch.float32, device="cuda")
+    assert lib().affx_selftest_mfma_fp8(ga.data_ptr(), gb.data_ptr(), d.data_ptr(), 0) == 0
+    torch.cuda.synchronize()
+    d = d.cpu().numpy().reshape(64, 4)
+    got = np.zeros((16, 16))
+    for l in range(64):
+        for v in range(4):
+            got[4 * (l // 16) + v, l % 16] = d[l, v]
+    return got
+
+
+def _lane_product(tbl, a, b):
+    av, bv = tbl[a].astype(np.float64), tbl[b].astype(np.float64)
+    ref = np.zeros((16, 16))
+    for i in range(16):
+        for j in range(16):
+            ref[i, j] = sum(np.dot(av[i + 16 * g], bv[j + 16 * g]) for g in range(4))
+    return ref
+
+
+def test_mfma_fp8_lane_layout(ax):
+    """A/B lane l = (row/col l%16, k-group l/16) with the same k order; D lane l elem v =
+    D[4*(l/16)+v][l%16]; bytes read as OCP E4M3 (bias 7)."""
+    from affinity_amd._lib import lib
+    rng = np.random.default_rng(1)
+    tbl = ax.e4m3_table()
+    # exact case: entries +-{0.5, 1, 2, 4} (E4M3 0x30/0x38/0x40/0x48 and negatives) give integer
+    # multiples of 1/4 whose sums are exact in any accumulator
+    pick = np.array([0x30, 0x38, 0x40, 0x48, 0xB0, 0xB8, 0xC0, 0xC8], np.uint8)
+    a = pick[rng.integers(0, 8, (64, 32))]
+    b = pick[rng.integers(0, 8, (64, 32))]
+    np.testing.assert_array_equal(_mfma(lib, a, b), _lane_product(tbl, a, b))
+    # whole range (no NaN encodings): the accumulation is not IEEE-exact over 2^-9..448 products,
+    # so check the layout to a loose relative tolerance
+    def rand_bytes():
+        x = rng.integers(0, 256, (64, 32), dtype=np.uint8)
+        x[(x & 0x7F) == 0x7F] ^= 1
+        return x
+    a, b = rand_bytes(), rand_bytes()
+    ref = _lane_product(tbl, a, b)
+    got = _mfma(lib, a, b)
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 1e-3
+
+
+@pytest.mark.parametrize("hidden,inter", [(1024, 1024), (4096, 2048)])
+def test_device_permutation_matches_host(ax, hidden, inter):
+    from affinity_amd._lib import lib
+    rng = np.random.default_rng(hidden + inter)
+    lay = ax.expert_layout(hidden, inter)
+    src = np.stack([random_expert_container(rng, hidden, inter, lay) for _ in range(2)])
+    host = np.zeros_like(src)
+    for e in range(2):
+        assert lib().affx_expert_to_device_layout(src[e].ctypes.data, host[e].ctypes.data, hidden, inter) == 0
+    pool = _pool_from_numpy(ax, src, np.full(2048, 0x38383838, np.uint32), hidden, inter)
+    dev = pool.data.cpu().numpy().reshape(2, -1)
+    _, off, size = lay
+    for p in range(9):  # compare planes (padding between planes is not copied)
+        np.testing.assert_array_equal(dev[:, off[p]:off[p] + size[p]], host[:, off[p]:off[p] + size[p]])
+
+
+@pytest.mark.parametrize("hidden,inter", [(1024, 1024), (4096, 2048)])
+def test_dequant_bit_exact_random_planes(ax, orc, c1_codebook, hidden, inter):
+    rng = np.random.default_rng(7 + hidden)
+    lay = ax.expert_layout(hidden, inter)
+    ex = random_expert_container(rng, hidden, inter, lay)
+    pool = _pool_from_numpy(ax, ex[None], c1_codebook, hidden, inter)
+    cbf = orc.unpack_codebook(c1_codebook)
+    for which in range(3):
+        rows, cols = ((inter, hidden), (inter, hidden), (hidden, inter))[which]
+        got = ax.dequant_matrix(pool, 0, which).cpu().numpy()
+        ref = orc.dequantize(*planes(ex, lay, which), rows, cols, cbf)
+        np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def _oracle_ffn(orc, experts, cbf, x, sel, w, hidden, inter, limit=10.0):
+    M = x.shape[0]
+    y = np.zeros((M, hidden), np.float32)
+    for t in range(M):
+        for j in range(sel.shape[1]):
+            e = int(sel[t, j])
+            if e >= experts.shape[0]:
+                continue
+            orc.expert_ffn(np.ascontiguousarray(experts[e]), cbf, x[t], float(w[t, j]), limit, y[t],
+                           hidden, inter)
+    return y
+
+
+def _run_decode(ax, pool, x, sel, w, **kw):
+    gx = torch.from_numpy(x).cuda()
+    gs = torch.from_numpy(sel.astype(np.int32)).cuda()
+    gw = torch.from_numpy(w.astype(np.float32)).cuda()
+    y = ax.expert_ffn_decode(pool, gx, gs, gw, **kw)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+@pytest.fixture(scope="module")
+def random_layer(ax, c1_codebook):
+    hidden, inter, n = 2048, 1024, 12
+    rng = np.random.default_rng(99)
+    lay = ax.expert_layout(hidden, inter)
+    ex = np.stack([random_expert_container(rng, hidden, inter, lay) for _ in range(n)])
+    return ex, _pool_from_numpy(ax, ex, c1_codebook, hidden, inter), hidden, inter
+
+
+@pytest.mark.parametrize("M,k", [(1, 6), (3, 4), (5, 6), (6, 6), (8, 6), (2, 1)])
+def test_decode_random_planes(ax, orc, c1_codebook, random_layer, M, k):
+    ex, pool, hidden, inter = random_layer
+    rng = np.random.default_rng(M * 10 + k)
+    x = (rng.standard_normal((M, hidden)) * 0.5).astype(np.float32)
+    sel = np.stack([rng.choice(ex.shape[0], k, replace=False) for _ in range(M)]).astype(np.uint32)
+    w = rng.uniform(0.05, 1.0, (M, k)).astype(np.float32)
+    got = _run_decode(ax, pool, x, sel, w)
+    ref = _oracle_ffn(orc, ex, orc.unpack_codebook(c1_codebook), x, sel, w, hidden, inter)
+    err = rel_l2(got, ref)
+    print(f"M={M} k={k} rel_l2={err:.3e}")
+    assert err <= TOL
+
+
+def test_decode_padding_duplicates_accumulate_dim_major(ax, orc, c1_codebook, random_layer):
+    """Padding ids (>= n_experts) are skipped, a repeated expert counts twice, accumulate adds
+    into y, and the dim-major [hidden][nb] arenas of the engine are addressed correctly."""
+    ex, pool, hidden, inter = random_layer
+    rng = np.random.default_rng(5)
+    M, k, n = 4, 6, ex.shape[0]
+    x = rng.standard_normal((M, hidden)).astype(np.float32)
+    sel = np.stack([rng.choice(n, k, replace=False) for _ in range(M)]).astype(np.uint32)
+    sel[0, 5] = n + 3          # padding
+    sel[1, 4] = sel[1, 0]      # duplicate
+    sel[2, :] = 1000           # a token with nothing routed
+    w = rng.uniform(0.1, 1.0, (M, k)).astype(np.float32)
+    y0 = rng.standard_normal((M, hidden)).astype(np.float32)
+    nb = 8                     # arena stride (nb_stride) larger than M
+    xd = np.zeros((hidden, nb), np.float32)
+    xd[:, :M] = x.T
+    yd = np.zeros((hidden, nb), np.float32)
+    yd[:, :M] = y0.T
+    gx, gy = torch.from_numpy(xd).cuda(), torch.from_numpy(yd).cuda()
+    ax.expert_ffn_decode(pool, gx[:, :M], torch.from_numpy(sel.astype(np.int32)).cuda(),
+                         torch.from_numpy(w).cuda(), y=gy[:, :M], accumulate=True, dim_major=True)
+    torch.cuda.synchronize()
+    got = gy.cpu().numpy()
+    ref = y0 + _oracle_ffn(orc, ex, orc.unpack_codebook(c1_codebook), x, sel, w, hidden, inter)
+    assert rel_l2(got[:, :M].T, ref) <= TOL
+    np.testing.assert_array_equal(got[:, M:], 0.0)      # columns beyond M untouched
+    np.testing.assert_array_equal(got[:, 2], y0[2])     # nothing routed: y unchanged
+
+
+def test_decode_declines(ax, random_layer):
+    from affinity_amd._lib import AffxDeclined
+    ex, pool, hidden, inter = random_layer
+    x = torch.zeros((9, hidden), device="cuda")
+    sel = torch.zeros((9, 6), dtype=torch.int32, device="cuda")
+    w = torch.zeros((9, 6), device="cuda")
+    with pytest.raises(AffxDeclined):
+        ax.expert_ffn_decode(pool, x, sel, w)

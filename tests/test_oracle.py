@@ -1,0 +1,363 @@
+"""Pins the CPU oracle (oracle/oracle.c) before anything is checked against it.
+
+Each oracle function is checked against at least one of:
+  * golden vectors the compiled reference wrote (tests/golden/*, make_golden.py);
+  * the reference library itself (oracle/_ref/libaffref.so) on fresh inputs, where it was built;
+  * closed forms and invariants fixed by the mathematics or the format.
+"""
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+H, I = 4096, 2048
+
+
+def sha(a) -> str:
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+@pytest.fixture(scope="module")
+def ref():
+    from oracle import load_ref, ref_available
+    if not ref_available():
+        pytest.skip("reference library not built here (needs the reference tree)")
+    return load_ref()
+
+
+@pytest.fixture(scope="module")
+def manifest():
+    return json.load(open(os.path.join(GOLDEN, "c1_manifest.json")))
+
+
+# ---------------------------------------------------------------------------------------------
+# element codecs
+# ---------------------------------------------------------------------------------------------
+
+def test_e4m3_closed_form_and_reference(orc, scalars):
+    got = np.array([orc.e4m3_to_float(b) for b in range(256)], np.float32)
+    b = np.arange(256)
+    e, m, s = (b >> 3) & 15, b & 7, np.where(b & 0x80, -1.0, 1.0)
+    closed = s * np.where(e == 0, m * 2.0 ** -9, (8 + m) * 2.0 ** (e - 10.0))
+    nan = (b & 0x7F) == 0x7F
+    np.testing.assert_array_equal(got[~nan], closed[~nan].astype(np.float32))
+    assert np.isnan(got[nan]).all() and nan.sum() == 2
+    np.testing.assert_array_equal(got.view(np.uint32)[~nan], scalars["e4m3"].view(np.uint32)[~nan])
+    assert got[0x7E] == 448.0 and got[0x08] == 2.0 ** -6 and got[0x01] == 2.0 ** -9
+
+
+def test_bf16_rne_reference_and_nearest_even(orc, scalars):
+    f = scalars["bf_in"]
+    got = np.array([orc.f32_to_bf16(float(v)) for v in f], np.uint16)
+    np.testing.assert_array_equal(got, scalars["bf_out"])
+    # nearest with ties to even, for finite values whose result stays finite
+    for v, h in zip(f[:2000], got[:2000]):
+        u = np.float32(v).view(np.uint32)
+        lo = np.uint32(u & 0xFFFF0000)
+        hi = np.uint32(lo + 0x10000)
+        dlo = abs(float(np.float32(v)) - float(lo.view(np.float32)))
+        dhi = abs(float(hi.view(np.float32)) - float(np.float32(v)))
+        r = int(h) << 16
+        if not np.isfinite(hi.view(np.float32)):
+            continue
+        if dlo < dhi:
+            assert r == lo
+        elif dhi < dlo:
+            assert r == hi
+        else:
+            assert (r >> 16) % 2 == 0
+
+
+def test_bit_streams_lsb_first(orc):
+    buf = np.zeros(8, np.uint8)
+    orc.lib.orc_pack_bits(buf.ctypes.data_as(__import__("ctypes").POINTER(__import__("ctypes").c_uint8)), 0, 10, 0x3A5)
+    assert buf[0] == 0xA5 and buf[1] == 0x03
+    rng = np.random.default_rng(0)
+    vals = rng.integers(0, 1 << 10, 200)
+    s = np.zeros(250, np.uint8)
+    import ctypes as C
+    p = s.ctypes.data_as(C.POINTER(C.c_uint8))
+    for i, v in enumerate(vals):
+        orc.lib.orc_pack_bits(p, i, 10, int(v))
+    # closed form: value i occupies stream bits 10i..10i+9, LSB first
+    bits = np.unpackbits(s, bitorder="little")
+    for i, v in enumerate(vals):
+        assert int(sum(int(bits[10 * i + j]) << j for j in range(10))) == v
+        assert orc.lib.orc_unpack_bits(p, i, 10) == v
+
+
+# ---------------------------------------------------------------------------------------------
+# synthetic generator
+# ---------------------------------------------------------------------------------------------
+
+def _splitmix_np(seed: int, n: int) -> np.ndarray:
+    with np.errstate(over="ignore"):
+        k = np.arange(1, n + 1, dtype=np.uint64)
+        x = np.uint64(seed) + k * np.uint64(0x9E3779B97F4A7C15)
+        x = (x ^ (x >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        x = (x ^ (x >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        return x ^ (x >> np.uint64(31))
+
+
+def test_splitmix64_known_answers(orc):
+    # published first outputs of splitmix64 from seed 0 (Vigna's reference implementation)
+    assert [orc.splitmix_at(0, k) for k in range(3)] == [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4,
+                                                        0x06C45D188009454F]
+    np.testing.assert_array_equal(_splitmix_np(12345, 1000),
+                                  np.array([orc.splitmix_at(12345, k) for k in range(1000)], np.uint64))
+
+
+def test_generator_is_box_muller_bf16(orc, manifest):
+    n = 200_000
+    d = _splitmix_np(1000, 2 * n)
+    u1 = ((d[0::2] >> np.uint64(11)) + np.uint64(1)).astype(np.float64) * 2.0 ** -53
+    u2 = ((d[1::2] >> np.uint64(11)) + np.uint64(1)).astype(np.float64) * 2.0 ** -53
+    z = np.sqrt(-2.0 * np.log(u1)) * np.cos(6.283185307179586 * u2)
+    np.testing.assert_allclose(orc.normal_f64(1000, n), z, rtol=1e-14, atol=1e-14)
+    f = (0.02 * z).astype(np.float32).view(np.uint32).astype(np.uint64)
+    bf = (((f + 0x7FFF + ((f >> 16) & 1)) >> 16) << 16).astype(np.uint32).view(np.float32)
+    np.testing.assert_array_equal(orc.normal_bf16(1000, n, 0.02), bf)
+    # and the config-1 inputs the reference was run on
+    assert sha(orc.normal_bf16(7, H, 1.0)) == manifest["inputs"]["x"]
+
+
+# ---------------------------------------------------------------------------------------------
+# geometry
+# ---------------------------------------------------------------------------------------------
+
+def test_expert_layout_closed_form(orc):
+    stride, off, size = orc.expert_layout(H, I)
+    assert stride == 9_060_352
+    assert list(off) == [0, 7_864_320, 9_043_968, 2_621_440, 8_257_536, 9_048_064, 5_242_880,
+                         8_650_752, 9_052_160]
+    assert list(size[:3]) == [I * H * 10 // 32, I * H * 6 // 128, I * 2]
+
+
+def test_expert_layout_matches_reference(orc, ref):
+    for h, i in ((4096, 2048), (1024, 1024), (7168, 2048), (4096, 1536)):
+        s, o, z = orc.expert_layout(h, i)
+        rs, ro, rz = ref.expert_layout(h, i)
+        assert s == rs and list(o) == list(ro) and list(z) == list(rz)
+
+
+# ---------------------------------------------------------------------------------------------
+# codebook fit
+# ---------------------------------------------------------------------------------------------
+
+def test_collect_samples_closed_form(orc):
+    rng = np.random.default_rng(1)
+    w = rng.standard_normal((64, 128)).astype(np.float32)
+    w[16] = 0.0
+    w[32, :16] = 0.0
+    s = orc.collect_samples(w, 64 * 128 // 16)   # stride 16: rows 0, 16, 32, 48
+    exp = []
+    for r in (0, 32, 48):                        # row 16 is all zero
+        for b in range(8):
+            blk = w[r, 16 * b:16 * b + 16]
+            m = np.abs(blk).max()
+            if m > 0:
+                exp.append(blk / m)
+    np.testing.assert_array_equal(s, np.concatenate(exp).astype(np.float32))
+
+
+def test_collect_samples_matches_reference(orc, ref):
+    rng = np.random.default_rng(2)
+    for rows, cols, budget in ((100, 64, 1000), (256, 512, 1 << 12), (33, 4096, 1 << 20)):
+        w = rng.standard_normal((rows, cols)).astype(np.float32)
+        np.testing.assert_array_equal(orc.collect_samples(w, budget), ref.collect_samples(w, budget))
+
+
+def test_fit_small_matches_reference_fixture(orc, small):
+    s = small["fit_samples"]
+    raw = orc.fit_codebook(s, 50, 1)
+    np.testing.assert_array_equal(raw.view(np.uint32), small["fit_cb_raw"].view(np.uint32))
+    np.testing.assert_array_equal(orc.project_codebook(raw).view(np.uint32),
+                                  small["fit_cb_proj"].view(np.uint32))
+
+
+def test_fit_matches_reference_other_seeds(orc, ref):
+    rng = np.random.default_rng(3)
+    s = (rng.standard_normal(4 * 4 * 3000) * 0.3).astype(np.float32)
+    for seed, iters in ((1, 50), (9, 7)):
+        a = orc.fit_codebook(s, iters, seed)
+        b = ref.fit_codebook(s, iters, seed, project=False)
+        np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_projection_is_nearest_restricted_e4m3(orc):
+    tbl = np.array([orc.e4m3_to_float(b) for b in range(256)], np.float32)
+    allowed = np.array([((b >> 3) & 15) in range(1, 8) and (b & 0x7F) != 0x7F for b in range(256)])
+    rng = np.random.default_rng(4)
+    xs = np.concatenate([rng.uniform(-2.5, 2.5, 3000), [0.0, -0.0, 1e-9, 2.0, -1.875, 1.9375]]).astype(np.float32)
+    for x in xs:
+        b = orc.e4m3_nearest(float(x))
+        assert allowed[b]
+        d = np.abs(tbl[allowed] - x)
+        assert abs(tbl[b] - x) == d.min()
+        # ties resolve to the lowest byte
+        assert b == np.flatnonzero(allowed)[np.argmin(d)]
+
+
+def test_config1_codebook_matches_reference(orc):
+    """The full config-1 recipe (3 x 2^19 samples, fit_codebook(50, seed 1), projection, pack)
+    reproduces the reference's packed codebook bit for bit."""
+    wg = orc.normal_bf16(1000, I * H, 0.02).reshape(I, H)
+    wu = orc.normal_bf16(1001, I * H, 0.02).reshape(I, H)
+    wd = orc.normal_bf16(1002, H * I, 0.02).reshape(H, I)
+    s = np.concatenate([orc.collect_samples(w, 1 << 19) for w in (wg, wu, wd)])
+    assert s.size == 3 * (1 << 19)
+    cb = orc.project_codebook(orc.fit_codebook(s, 50, 1))
+    packed = np.fromfile(os.path.join(GOLDEN, "c1_codebook.bin"), dtype="<u4")
+    np.testing.assert_array_equal(orc.pack_codebook(cb), packed)
+    assert orc.codebook_exponents_ok(packed)
+    np.testing.assert_array_equal(orc.unpack_codebook(packed).view(np.uint32), cb.view(np.uint32))
+
+
+# ---------------------------------------------------------------------------------------------
+# quantise / dequantise
+# ---------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("case", ["a", "b", "c", "d"])
+def test_quantize_matches_reference_fixture(orc, small, c1_codebook, case):
+    cb = orc.unpack_codebook(c1_codebook)
+    w = small[f"{case}_w"]
+    c, f, r = orc.quantize(w, cb)
+    np.testing.assert_array_equal(c, small[f"{case}_codes"])
+    np.testing.assert_array_equal(f, small[f"{case}_fields"])
+    np.testing.assert_array_equal(r, small[f"{case}_rs"])
+    # the reference's acceleration grid is exact: same bytes as its plain scan
+    np.testing.assert_array_equal(small[f"{case}_codes"], small[f"{case}_codes_nosearch"])
+    np.testing.assert_array_equal(small[f"{case}_fields"], small[f"{case}_fields_nosearch"])
+    ci, fi, _ = orc.quantize(w, cb, small[f"{case}_imp"])
+    np.testing.assert_array_equal(ci, small[f"{case}_codes_imp"])
+    np.testing.assert_array_equal(fi, small[f"{case}_fields_imp"])
+    # uniform importance gives the bytes of no importance
+    c1, f1, _ = orc.quantize(w, cb, np.ones(w.shape[1], np.float32))
+    np.testing.assert_array_equal(c1, c)
+    np.testing.assert_array_equal(f1, f)
+
+
+def test_quantize_matches_reference_random(orc, ref, c1_codebook):
+    cb = orc.unpack_codebook(c1_codebook)
+    rng = np.random.default_rng(5)
+    for rows, cols in ((7, 128), (16, 1024)):
+        w = (rng.standard_normal((rows, cols)) * rng.uniform(0.001, 0.1, (rows, 1))).astype(np.float32)
+        w[0, :16] = 0
+        a = orc.quantize(w, cb)
+        b = ref.quantize(w, cb, None, search=True)
+        for x, y in zip(a, b):
+            np.testing.assert_array_equal(x, y)
+
+
+@pytest.fixture(scope="module")
+def c1_planes(orc, c1_codebook):
+    cb = orc.unpack_codebook(c1_codebook)
+    mats = {"gate": orc.normal_bf16(1000, I * H, 0.02).reshape(I, H),
+            "up": orc.normal_bf16(1001, I * H, 0.02).reshape(I, H),
+            "down": orc.normal_bf16(1002, H * I, 0.02).reshape(H, I)}
+    return cb, {k: orc.quantize(w, cb) for k, w in mats.items()}
+
+
+def test_config1_planes_match_reference(c1_planes, manifest):
+    _, q = c1_planes
+    for name in ("gate", "up", "down"):
+        for i, k in enumerate(("codes", "fields", "rscales")):
+            assert sha(q[name][i]) == manifest["planes"][name][k], (name, k)
+        rows = manifest["rows"][name]
+        for r, want in rows.items():
+            r = int(r)
+            cols = H if name != "down" else I
+            cb_row, f_row = cols * 10 // 32, cols * 6 // 128
+            assert q[name][0][r * cb_row:(r + 1) * cb_row].tobytes().hex() == want["codes"]
+            assert q[name][1][r * f_row:(r + 1) * f_row].tobytes().hex() == want["fields"]
+            assert int(q[name][2][r]) == want["rscale"]
+
+
+def test_config1_dequant_and_ffn_match_reference(orc, c1_planes, manifest):
+    cb, q = c1_planes
+    dims = {"gate": (I, H), "up": (I, H), "down": (H, I)}
+    for name in ("gate", "up", "down"):
+        assert sha(orc.dequantize(*q[name], *dims[name], cb)) == manifest["dequant"][name]
+    x = orc.normal_bf16(7, H, 1.0)
+    g = orc.gemv(*q["gate"], I, H, cb, x)
+    u = orc.gemv(*q["up"], I, H, cb, x)
+    a = orc.swiglu(g, u, 10.0)
+    y = orc.gemv(*q["down"], H, I, cb, a, 1.0)
+    assert sha(g) == manifest["ffn"]["g"] and sha(u) == manifest["ffn"]["u"]
+    assert sha(a) == manifest["ffn"]["a"] and sha(y) == manifest["ffn"]["y"]
+    np.testing.assert_array_equal(y, np.fromfile(os.path.join(GOLDEN, "c1_ffn_y.bin"), dtype="<f4"))
+
+
+def _numpy_dequant(codes, fields, rs, rows, cols, cb):
+    """Independent statement of the format: 10-bit codes and 6-bit fields LSB-first; field bits
+    [0..2] s, [3] sign, [4] rotate, [5] variant; w = rs * 2^s * (+-1) * e[v][code][(p+rh)%4]."""
+    cbits = np.unpackbits(codes, bitorder="little").reshape(-1, 10)
+    fbits = np.unpackbits(fields, bitorder="little").reshape(-1, 6)
+    code = (cbits * (1 << np.arange(10))).sum(1).reshape(rows, cols // 16, 4)
+    f = (fbits * (1 << np.arange(6))).sum(1).reshape(rows, cols // 16)
+    s, sign, rot, var = f & 7, (f >> 3) & 1, (f >> 4) & 1, f >> 5
+    e = cb.reshape(2, 1024, 4)[var[:, :, None], code]                     # rows, blk, quad, 4
+    e = np.where(rot[:, :, None, None] == 1, np.roll(e, -2, axis=3), e)    # position p <- (p+2)%4
+    scale = (rs.astype(np.uint32) << 16).view(np.float32)
+    bs = scale[:, None] * (2.0 ** s).astype(np.float32) * np.where(sign == 1, -1.0, 1.0).astype(np.float32)
+    return (bs[:, :, None, None].astype(np.float32) * e).reshape(rows, cols).astype(np.float32)
+
+
+def test_dequant_matches_reference_and_closed_form(orc, small, c1_codebook):
+    cb = orc.unpack_codebook(c1_codebook)
+    for case, (rows, cols) in (("a", (5, 64)), ("b", (16, 256)), ("c", (33, 512)), ("d", (8, 4096))):
+        got = orc.dequantize(small[f"{case}_codes"], small[f"{case}_fields"], small[f"{case}_rs"],
+                             rows, cols, cb)
+        np.testing.assert_array_equal(got.view(np.uint32), small[f"{case}_deq"].view(np.uint32))
+    got = orc.dequantize(small["rand_codes"], small["rand_fields"], small["rand_rs"], 16, 256, cb)
+    np.testing.assert_array_equal(got.view(np.uint32), small["rand_deq"].view(np.uint32))
+    closed = _numpy_dequant(small["rand_codes"], small["rand_fields"], small["rand_rs"], 16, 256, cb)
+    np.testing.assert_array_equal(got.view(np.uint32), closed.view(np.uint32))
+
+
+def test_gemv_matches_reference_and_dequant_dot(orc, small, c1_codebook):
+    """expert_gemv_reference = (float) of the double dot of the dequantised row, bit for bit."""
+    cb = orc.unpack_codebook(c1_codebook)
+    for case, (rows, cols) in (("b", (16, 256)), ("d", (8, 4096))):
+        x = small[f"{case}_x"]
+        y = orc.gemv(small[f"{case}_codes"], small[f"{case}_fields"], small[f"{case}_rs"], rows, cols,
+                     cb, x, 0.75)
+        np.testing.assert_array_equal(y.view(np.uint32), small[f"{case}_gemv"].view(np.uint32))
+        d = small[f"{case}_deq"].astype(np.float64)
+        acc = np.zeros(rows)
+        for r in range(rows):       # sequential double sum in column order
+            s = 0.0
+            for c in range(cols):
+                s += float(d[r, c]) * float(x[c])
+            acc[r] = s
+        tmp = acc.astype(np.float32)
+        np.testing.assert_array_equal(y, (np.float32(0.75) * tmp).astype(np.float32))
+    x = small["rand_x"]
+    y = orc.gemv(small["rand_codes"], small["rand_fields"], small["rand_rs"], 16, 256, cb, x, 1.0)
+    np.testing.assert_array_equal(y.view(np.uint32), small["rand_gemv"].view(np.uint32))
+
+
+def test_swiglu_matches_reference(orc, scalars):
+    g, u = scalars["sw_g"], scalars["sw_u"]
+    np.testing.assert_array_equal(orc.swiglu(g, u, 10.0).view(np.uint32), scalars["sw_out"].view(np.uint32))
+    np.testing.assert_array_equal(orc.swiglu(g, u, 0.0).view(np.uint32),
+                                  scalars["sw_out_nolimit"].view(np.uint32))
+    # closed form: silu(min(g, 10)) * clamp(u, -10, 10)
+    gg = np.minimum(g.astype(np.float64), 10.0)
+    uu = np.clip(u.astype(np.float64), -10.0, 10.0)
+    np.testing.assert_allclose(orc.swiglu(g, u, 10.0), gg / (1 + np.exp(-gg)) * uu, rtol=1e-5, atol=1e-6)
+
+
+def test_route_softmax_topk(orc):
+    rng = np.random.default_rng(6)
+    lg = rng.standard_normal(256).astype(np.float32)
+    lg[10] = lg[20] = 5.0                          # a tie: lower id first
+    sel, w = orc.route(lg, 6)
+    order = sorted(range(256), key=lambda e: (-lg[e], e))[:6]
+    assert list(sel) == order and sel[0] == 10 and sel[1] == 20
+    p = np.exp(lg[order].astype(np.float64) - lg.max())
+    np.testing.assert_allclose(w, p / p.sum(), rtol=1e-6)
+    assert abs(w.sum() - 1) < 1e-6
