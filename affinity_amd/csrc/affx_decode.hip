@@ -404,12 +404,14 @@ size_t affx_decode_workspace_size(uint32_t m, uint32_t k, uint32_t hidden, uint3
   return (size_t)decode_ws(m, k, hidden, inter).total;
 }
 
-int affx_expert_ffn_decode(const affx_layer* L, const float* x, uint64_t x_ts, uint64_t x_ds,
-                           uint32_t M, const uint32_t* sel, const float* w, uint32_t K, float* y,
-                           uint64_t y_ts, uint64_t y_ds, int accumulate, void* ws,
-                           size_t ws_bytes, void* stream) {
-  if (!L || !x || !sel || !w || !y || !ws || !L->base || !L->codebook)
-    return set_error(AFFX_ERR_ARG, "ffn_decode: null pointer");
+}  // extern "C"
+
+namespace {
+
+// Checks shared by the three stages; fills the kernel arguments.
+int decode_setup(const affx_layer* L, uint32_t M, uint32_t K, void* ws, size_t ws_bytes,
+                 DecodeArgs* A, DecodeWs* lay) {
+  if (!L || !ws || !L->base || !L->codebook) return set_error(AFFX_ERR_ARG, "ffn_decode: null pointer");
   if (M == 0 || M > kMaxTok || K == 0 || K > AFFX_MAX_TOPK)
     return set_error(AFFX_DECLINED, "ffn_decode: m_tokens must be 1..%d and top_k 1..%d (got %u, %u)",
                      kMaxTok, AFFX_MAX_TOPK, M, K);
@@ -421,53 +423,93 @@ int affx_expert_ffn_decode(const affx_layer* L, const float* x, uint64_t x_ts, u
                      "1024 (got %u, %u)", L->hidden, L->inter);
   if (!(L->swiglu_limit > 0.f) || L->swiglu_limit > 1e6f)
     return set_error(AFFX_DECLINED, "ffn_decode: needs a SwiGLU clamp limit in (0, 1e6]");
-  const DecodeWs lay = decode_ws(M, K, L->hidden, L->inter);
-  if (ws_bytes < lay.total)
+  *lay = decode_ws(M, K, L->hidden, L->inter);
+  if (ws_bytes < lay->total)
     return set_error(AFFX_ERR_ARG, "ffn_decode: workspace %zu < %llu bytes", ws_bytes,
-                     (unsigned long long)lay.total);
+                     (unsigned long long)lay->total);
   uint64_t off9[9];
   const uint64_t stride = affx_expert_layout(L->hidden, L->inter, off9, nullptr);
   if (L->stride < stride) return set_error(AFFX_ERR_ARG, "ffn_decode: layer stride below expert size");
-
   uint8_t* base = (uint8_t*)ws;
-  DecodePlan* plan = (DecodePlan*)(base + lay.plan);
-  DecodeArgs A;
-  A.base = (const uint8_t*)L->base;
-  A.stride = L->stride;
-  for (int i = 0; i < 9; ++i) A.off[i] = off9[i];
-  A.hidden = L->hidden;
-  A.inter = L->inter;
-  A.m_tokens = M;
-  A.codebook = (const uint32_t*)L->codebook;
-  A.plan = plan;
-  A.xq = base + lay.xq;
-  A.aq = base + lay.aq;
-  A.zeros = base + lay.zeros;
-  A.limit = L->swiglu_limit;
+  A->base = (const uint8_t*)L->base;
+  A->stride = L->stride;
+  for (int i = 0; i < 9; ++i) A->off[i] = off9[i];
+  A->hidden = L->hidden;
+  A->inter = L->inter;
+  A->m_tokens = M;
+  A->codebook = (const uint32_t*)L->codebook;
+  A->plan = (DecodePlan*)(base + lay->plan);
+  A->xq = base + lay->xq;
+  A->aq = base + lay->aq;
+  A->zeros = base + lay->zeros;
+  A->limit = L->swiglu_limit;
   // |SwiGLU| <= L * L under the clamp; scale so that it stays below 256 < 448
-  A.sigma_a = 7 - ilogbf(L->swiglu_limit * L->swiglu_limit);
+  A->sigma_a = 7 - ilogbf(L->swiglu_limit * L->swiglu_limit);
+  A->y = nullptr;
+  A->y_ts = A->y_ds = 0;
+  A->accumulate = 0;
+  return AFFX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int affx_decode_prepare(const affx_layer* L, const float* x, uint64_t x_ts, uint64_t x_ds,
+                        uint32_t M, const uint32_t* sel, const float* w, uint32_t K, void* ws,
+                        size_t ws_bytes, void* stream) {
+  DecodeArgs A;
+  DecodeWs lay;
+  if (!x || !sel || !w) return set_error(AFFX_ERR_ARG, "ffn_decode: null pointer");
+  int rc = decode_setup(L, M, K, ws, ws_bytes, &A, &lay);
+  if (rc) return rc;
+  uint8_t* base = (uint8_t*)ws;
+  hipLaunchKernelGGL(decode_prep_kernel, dim3(M), dim3(256), 0, (hipStream_t)stream, x, x_ts, x_ds,
+                     M, sel, w, K, L->n_experts, L->hidden, (DecodePlan*)(base + lay.plan),
+                     base + lay.xq, base + lay.zeros);
+  return check_launch("decode_prep_kernel");
+}
+
+int affx_decode_gateup(const affx_layer* L, uint32_t M, uint32_t K, void* ws, size_t ws_bytes,
+                       void* stream) {
+  DecodeArgs A;
+  DecodeWs lay;
+  int rc = decode_setup(L, M, K, ws, ws_bytes, &A, &lay);
+  if (rc) return rc;
+  const uint32_t max_slots = M * K < L->n_experts ? M * K : L->n_experts;
+  const dim3 g(L->inter / kTileRows, max_slots);
+  if (M <= 5) hipLaunchKernelGGL(decode_gateup_kernel<1>, g, dim3(256), 0, (hipStream_t)stream, A);
+  else hipLaunchKernelGGL(decode_gateup_kernel<2>, g, dim3(256), 0, (hipStream_t)stream, A);
+  return check_launch("decode_gateup_kernel");
+}
+
+int affx_decode_down(const affx_layer* L, uint32_t M, uint32_t K, float* y, uint64_t y_ts,
+                     uint64_t y_ds, int accumulate, void* ws, size_t ws_bytes, void* stream) {
+  DecodeArgs A;
+  DecodeWs lay;
+  if (!y) return set_error(AFFX_ERR_ARG, "ffn_decode: null pointer");
+  int rc = decode_setup(L, M, K, ws, ws_bytes, &A, &lay);
+  if (rc) return rc;
   A.y = y;
   A.y_ts = y_ts;
   A.y_ds = y_ds;
   A.accumulate = accumulate;
-  hipStream_t s = (hipStream_t)stream;
+  const dim3 g(L->hidden / kTileRows);
+  if (M <= 5) hipLaunchKernelGGL(decode_down_kernel<1>, g, dim3(256), 0, (hipStream_t)stream, A);
+  else hipLaunchKernelGGL(decode_down_kernel<2>, g, dim3(256), 0, (hipStream_t)stream, A);
+  return check_launch("decode_down_kernel");
+}
 
-  hipLaunchKernelGGL(decode_prep_kernel, dim3(M), dim3(256), 0, s, x, x_ts, x_ds, M, sel, w, K,
-                     L->n_experts, L->hidden, plan, base + lay.xq, base + lay.zeros);
-  int rc = check_launch("decode_prep_kernel");
+int affx_expert_ffn_decode(const affx_layer* L, const float* x, uint64_t x_ts, uint64_t x_ds,
+                           uint32_t M, const uint32_t* sel, const float* w, uint32_t K, float* y,
+                           uint64_t y_ts, uint64_t y_ds, int accumulate, void* ws,
+                           size_t ws_bytes, void* stream) {
+  if (!y) return set_error(AFFX_ERR_ARG, "ffn_decode: null pointer");
+  int rc = affx_decode_prepare(L, x, x_ts, x_ds, M, sel, w, K, ws, ws_bytes, stream);
   if (rc) return rc;
-  const uint32_t max_slots = M * K < L->n_experts ? M * K : L->n_experts;
-  const dim3 g1(L->inter / kTileRows, max_slots), g2(L->hidden / kTileRows);
-  if (M <= 5) {
-    hipLaunchKernelGGL(decode_gateup_kernel<1>, g1, dim3(256), 0, s, A);
-    if ((rc = check_launch("decode_gateup_kernel<1>"))) return rc;
-    hipLaunchKernelGGL(decode_down_kernel<1>, g2, dim3(256), 0, s, A);
-    return check_launch("decode_down_kernel<1>");
-  }
-  hipLaunchKernelGGL(decode_gateup_kernel<2>, g1, dim3(256), 0, s, A);
-  if ((rc = check_launch("decode_gateup_kernel<2>"))) return rc;
-  hipLaunchKernelGGL(decode_down_kernel<2>, g2, dim3(256), 0, s, A);
-  return check_launch("decode_down_kernel<2>");
+  rc = affx_decode_gateup(L, M, K, ws, ws_bytes, stream);
+  if (rc) return rc;
+  return affx_decode_down(L, M, K, y, y_ts, y_ds, accumulate, ws, ws_bytes, stream);
 }
 
 }  // extern "C"

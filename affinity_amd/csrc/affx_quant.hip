@@ -2,8 +2,7 @@
 //
 // affx_quantize_matrix is the reference's quantize_matrix for the quad format
 // (src/quant/blockquant.cpp:586-791) run per row on the GPU, bit-exact: every float operation
-// is the reference's, in its order, with explicit round-to-nearest intrinsics so that nothing is
-// contracted into an FMA. The nearest-quad search is exhaustive (each lane scores 16 of the 1024
+// is the reference's, in its order, with no contraction into FMAs. The nearest-quad search is exhaustive (each lane scores 16 of the 1024
 // entries, then a wave reduction keeps the minimum, or the lowest index among equal minima),
 // which returns exactly what the reference's scan and its acceleration grid return
 // (src/quant/blockquant.cpp:162-174, 558-578).
@@ -12,6 +11,12 @@
 // Box-Muller in double (the generator of src/quant/blockquant.cpp:37-42, 862-869), rounded to
 // f32 and then to bf16.
 #include "affx_common.h"
+
+// Every float operation below is the reference's, one rounding each. HIP contracts a*b+c into an
+// FMA by default, which moves distances by an ulp and flips near-tied nearest-code choices; the
+// pragma turns that off for the code written in this file (the HIP headers' __fadd_rn family are
+// plain operators compiled under the default, so they are not used here).
+#pragma clang fp contract(off)
 
 namespace affx {
 
@@ -62,12 +67,11 @@ __device__ __forceinline__ void wave_argmin(float& v, uint32_t& i) {
 // Squared distance of target t to entry e, dimensions summed in order, no contraction.
 __device__ __forceinline__ float qdist(const float4 e, const float t0, const float t1,
                                        const float t2, const float t3) {
-  const float a = __fsub_rn(e.x, t0), b = __fsub_rn(e.y, t1), c = __fsub_rn(e.z, t2),
-              d = __fsub_rn(e.w, t3);
-  float s = __fmul_rn(a, a);
-  s = __fadd_rn(s, __fmul_rn(b, b));
-  s = __fadd_rn(s, __fmul_rn(c, c));
-  s = __fadd_rn(s, __fmul_rn(d, d));
+  const float a = e.x - t0, b = e.y - t1, c = e.z - t2, d = e.w - t3;
+  float s = a * a;
+  s = s + b * b;
+  s = s + c * c;
+  s = s + d * d;
   return s;
 }
 
@@ -146,14 +150,14 @@ __global__ void __launch_bounds__(256) quantize_rows_kernel(
       for (int i = 0; i < 4; ++i) {
         float s = 0.f;
 #pragma unroll
-        for (int p = 0; p < 4; ++p) s = __fadd_rn(s, imp[b * 16 + 4 * i + p]);
-        wt[i] = __fdiv_rn(s, 4.0f);
+        for (int p = 0; p < 4; ++p) s = s + imp[b * 16 + 4 * i + p];
+        wt[i] = s / 4.0f;
       }
     }
     uint32_t best_s = 0, best_v = 0, best_g = 0;
     double best_err = 1.7976931348623157e308;
     if (bmax > 0.f && rscale > 0.f) {
-      const double ideal = __ddiv_rn((double)bmax, (double)rscale);
+      const double ideal = (double)bmax / (double)rscale;
       uint32_t mid = 0;
       double bd = 1.7976931348623157e308;
       for (uint32_t s = 0; s <= 7; ++s) {
@@ -165,38 +169,38 @@ __global__ void __launch_bounds__(256) quantize_rows_kernel(
       for (uint32_t v = 0; v < 2; ++v) {
         const float4* ev = ent + v * kLut;
         for (int s = lo; s <= hi; ++s) {
-          const float bs = __fmul_rn(rscale, (float)(1u << s));
+          const float bs = rscale * (float)(1u << s);
           if (bs <= 0.f) continue;
-          const float inv = __fdiv_rn(1.0f, bs);
+          const float inv = 1.0f / bs;
           for (uint32_t g = 0; g < 4; ++g) {
             const float sg = (g & 1u) ? -inv : inv;
             const uint32_t rh = (g & 2u) ? 2u : 0u;
             float acc = 0.f;
             for (int i = 0; i < 4; ++i) {
-              const float t0 = __fmul_rn(blk[4 * i + (0 + rh) % 4], sg);
-              const float t1 = __fmul_rn(blk[4 * i + (1 + rh) % 4], sg);
-              const float t2 = __fmul_rn(blk[4 * i + (2 + rh) % 4], sg);
-              const float t3 = __fmul_rn(blk[4 * i + (3 + rh) % 4], sg);
+              const float t0 = blk[4 * i + (0 + rh) % 4] * sg;
+              const float t1 = blk[4 * i + (1 + rh) % 4] * sg;
+              const float t2 = blk[4 * i + (2 + rh) % 4] * sg;
+              const float t3 = blk[4 * i + (3 + rh) % 4] * sg;
               const float d = quad_min(ev, lane, t0, t1, t2, t3);
-              acc = __fadd_rn(acc, __fmul_rn(d, wt[i]));
+              acc = acc + d * wt[i];
             }
-            const double e = __dmul_rn(__dmul_rn((double)acc, (double)bs), (double)bs);
+            const double e = (double)acc * (double)bs * (double)bs;
             if (e < best_err) { best_err = e; best_s = (uint32_t)s; best_v = v; best_g = g; }
           }
         }
       }
     }
     const uint32_t field = (best_v << 5) | (best_g << 3) | best_s;
-    const float mag = __fmul_rn(rscale, (float)(1u << best_s));
+    const float mag = rscale * (float)(1u << best_s);
     const float bs = (best_g & 1u) ? -mag : mag;
     const uint32_t rh = (best_g & 2u) ? 2u : 0u;
     uint32_t code[4] = {0, 0, 0, 0};
     if (mag > 0.f) {
       for (int i = 0; i < 4; ++i) {
-        const float t0 = __fdiv_rn(blk[4 * i + (0 + rh) % 4], bs);
-        const float t1 = __fdiv_rn(blk[4 * i + (1 + rh) % 4], bs);
-        const float t2 = __fdiv_rn(blk[4 * i + (2 + rh) % 4], bs);
-        const float t3 = __fdiv_rn(blk[4 * i + (3 + rh) % 4], bs);
+        const float t0 = blk[4 * i + (0 + rh) % 4] / bs;
+        const float t1 = blk[4 * i + (1 + rh) % 4] / bs;
+        const float t2 = blk[4 * i + (2 + rh) % 4] / bs;
+        const float t3 = blk[4 * i + (3 + rh) % 4] / bs;
         code[i] = quad_argmin(ent + best_v * kLut, lane, t0, t1, t2, t3);
       }
     }

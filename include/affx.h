@@ -132,6 +132,22 @@ int affx_expert_ffn_decode(const affx_layer* layer, const float* x, uint64_t x_t
                            uint64_t y_dim_stride, int accumulate, void* workspace,
                            size_t workspace_bytes, void* stream);
 
+/* The same three steps as separate stream-ordered calls (same workspace, same arguments), for
+ * callers that interleave other work or time the stages, as the reference's GPU FFN is three
+ * launches: activation prep + routing plan (batch_quant_fp8_hip, src/gpu/batch_kernels.h:124;
+ * moe_plan_hip, src/gpu/moe_plan.hip:407-420), gate/up + SwiGLU (expert_gemv_split_hip +
+ * swiglu_all_kernel, src/gpu/expert_kernel.hip:2616-2662, 114-129) and down + combine
+ * (expert_gemv_multix_hip, src/gpu/expert_kernel.hip:2573-2609). */
+int affx_decode_prepare(const affx_layer* layer, const float* x, uint64_t x_tok_stride,
+                        uint64_t x_dim_stride, uint32_t m_tokens, const uint32_t* sel,
+                        const float* w, uint32_t top_k, void* workspace, size_t workspace_bytes,
+                        void* stream);
+int affx_decode_gateup(const affx_layer* layer, uint32_t m_tokens, uint32_t top_k,
+                       void* workspace, size_t workspace_bytes, void* stream);
+int affx_decode_down(const affx_layer* layer, uint32_t m_tokens, uint32_t top_k, float* y,
+                     uint64_t y_tok_stride, uint64_t y_dim_stride, int accumulate,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- prefill: grouped GEMM over an expert-sorted slot list ---------------------------------- */
 
 /* Workspace bytes of affx_moe_plan + affx_expert_ffn_grouped for n_tok tokens, top-k routing. */

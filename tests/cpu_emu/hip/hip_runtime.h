@@ -142,29 +142,38 @@ inline emu_v4f __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(emu_v8i a, emu_v
   return d;
 }
 
-// ---- launch: one block at a time, blockDim.x threads ----
+// ---- launch: one block at a time, blockDim.x threads created once per launch ----
 template <typename F, typename... Args>
 void emu_launch(F kernel, dim3 grid, dim3 block, Args... args) {
   gridDim = {grid.x, grid.y, grid.z};
   blockDim = {block.x, block.y, block.z};
   const uint32_t nt = block.x;
-  for (uint32_t bz = 0; bz < grid.z; ++bz)
-    for (uint32_t by = 0; by < grid.y; ++by)
-      for (uint32_t bx = 0; bx < grid.x; ++bx) {
-        std::barrier<> bb(nt);
-        EmuBlock blk;
-        blk.block_bar = &bb;
-        std::vector<std::barrier<>*> wbs;
-        for (uint32_t w = 0; w < (nt + 63) / 64; ++w) { wbs.push_back(new std::barrier<>(std::min<uint32_t>(64, nt - 64 * w))); blk.wave_bar[w] = wbs.back(); }
-        std::vector<std::thread> ts;
-        for (uint32_t t = 0; t < nt; ++t)
-          ts.emplace_back([&, t]() {
-            threadIdx = {t, 0, 0}; blockIdx = {bx, by, bz}; emu_blk = &blk;
-            kernel(args...);
-            // a returning work-item keeps the barriers balanced for the others
-          });
-        for (auto& th : ts) th.join();
-        for (auto* b : wbs) delete b;
+  const uint64_t nblocks = (uint64_t)grid.x * grid.y * grid.z;
+  std::barrier<> start(nt + 1), done(nt + 1), bb(nt);
+  EmuBlock blk;
+  blk.block_bar = &bb;
+  std::vector<std::barrier<>*> wbs;
+  for (uint32_t w = 0; w < (nt + 63) / 64; ++w) {
+    wbs.push_back(new std::barrier<>(std::min<uint32_t>(64, nt - 64 * w)));
+    blk.wave_bar[w] = wbs.back();
+  }
+  std::vector<std::thread> ts;
+  for (uint32_t t = 0; t < nt; ++t)
+    ts.emplace_back([&, t]() {
+      emu_blk = &blk;
+      for (uint64_t b = 0; b < nblocks; ++b) {
+        start.arrive_and_wait();
+        threadIdx = {t, 0, 0};
+        blockIdx = {(uint32_t)(b % grid.x), (uint32_t)((b / grid.x) % grid.y), (uint32_t)(b / ((uint64_t)grid.x * grid.y))};
+        kernel(args...);
+        done.arrive_and_wait();
       }
+    });
+  for (uint64_t b = 0; b < nblocks; ++b) {
+    start.arrive_and_wait();
+    done.arrive_and_wait();
+  }
+  for (auto& th : ts) th.join();
+  for (auto* w : wbs) delete w;
 }
 #define hipLaunchKernelGGL(k, g, b, shm, s, ...) emu_launch(k, dim3(g), dim3(b), __VA_ARGS__)

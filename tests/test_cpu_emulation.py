@@ -1,0 +1,60 @@
+"""libaffx's kernels run on the CPU (tests/cpu_emu): every launch emulated with one thread per
+work-item, real barriers, exact MFMA, under AddressSanitizer. Checks bounds of every device
+access and the numerics against the oracle, without a GPU. Sizes are kept small: the emulation
+runs each work-item as an OS thread."""
+import os
+import shutil
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CLANG = "/opt/rocm/llvm/bin/clang"
+CLANGXX = "/opt/rocm/llvm/bin/clang++"
+
+
+@pytest.fixture(scope="module")
+def emu(tmp_path_factory):
+    if not (os.path.exists(CLANGXX) and os.path.exists(CLANG)):
+        pytest.skip("clang++ not available")
+    d = tmp_path_factory.mktemp("emu")
+    san = ["-fsanitize=address", "-fno-omit-frame-pointer", "-g", "-O1"]
+    subprocess.run([CLANG, *san, "-ffp-contract=off", "-fopenmp=libgomp", "-c",
+                    os.path.join(ROOT, "oracle", "oracle.c"), "-o", str(d / "oracle.o")], check=True)
+    # -ffp-contract=fast with FMA available mirrors the device compiler's default, so a kernel
+    # that needs exact float order has to say so itself
+    subprocess.run([CLANGXX, "-std=c++20", *san, "-march=x86-64-v3", "-ffp-contract=fast", "-w",
+                    "-I", os.path.join(ROOT, "tests", "cpu_emu"), "-I", os.path.join(ROOT, "affinity_amd", "csrc"),
+                    os.path.join(ROOT, "tests", "cpu_emu", "emu_main.cpp"), str(d / "oracle.o"),
+                    "-o", str(d / "emu_main"), "-lpthread", "-fopenmp=libgomp"], check=True)
+    return str(d / "emu_main")
+
+
+def run(emu, *args, timeout=600):
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=0")
+    r = subprocess.run([emu, *map(str, args)], cwd=ROOT, capture_output=True, text=True,
+                       timeout=timeout, env=env)
+    out = r.stdout + r.stderr
+    assert "AddressSanitizer" not in out, out[-4000:]
+    assert r.returncode == 0, out[-4000:]
+    return out
+
+
+def test_dequant_emulated(emu):
+    assert "exact=1" in run(emu, "dequant", 1024, 1024, 1)
+
+
+def test_decode_emulated_m1(emu):
+    assert "rel_l2" in run(emu, "decode", 1024, 1024, 7, 1, 6, 1)
+
+
+def test_decode_emulated_m6_two_column_groups(emu):
+    assert "rel_l2" in run(emu, "decode", 2048, 1024, 5, 6, 2, 2)
+
+
+def test_quantizer_emulated(emu):
+    assert "exact=1" in run(emu, "quant", 4, 256, 3)
+
+
+def test_grouped_emulated(emu):
+    assert "rel_l2" in run(emu, "grouped", 1024, 1024, 5, 12, 3, 4, 1, timeout=900)
