@@ -50,11 +50,13 @@ constexpr int kMaxTok = AFFX_MAX_DECODE_TOKENS;
 constexpr int kMaxSlots = AFFX_MAX_DECODE_TOKENS * AFFX_MAX_TOPK;  // distinct experts of a batch
 
 // Plan the decode prep kernel writes: the distinct experts of the batch (ascending id), which
-// tokens each one serves and with what weight, and each token's activation exponent.
+// tokens each one serves and with what weight, and the exponent of every activation segment.
+constexpr int kMaxSeg = 4;  // 1024-column super-segments of the decode input (hidden <= 4096)
+
 struct DecodePlan {
   uint32_t n_slots;
   uint32_t m_tokens;
-  int32_t x_sigma[kMaxTok];
+  int32_t x_sigma[kMaxTok][kMaxSeg];  // exponent of each (token, super-segment) activation split
   uint32_t expert[kMaxSlots];
   uint32_t tok_mask[kMaxSlots];
   float w[kMaxSlots][kMaxTok];

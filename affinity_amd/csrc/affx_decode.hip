@@ -41,7 +41,8 @@ struct DecodeArgs {
 };
 
 // ------------------------------------------------------------------------------------------------
-// prep
+// prep: blocks 0 .. M*nst-1 split one (token, 1024-column super-segment) of the activation into
+// three E4M3 terms with their own exponent; the last block builds the plan.
 // ------------------------------------------------------------------------------------------------
 __global__ void __launch_bounds__(256) decode_prep_kernel(const float* __restrict__ x, uint64_t xts,
                                                           uint64_t xds, uint32_t M,
@@ -51,52 +52,47 @@ __global__ void __launch_bounds__(256) decode_prep_kernel(const float* __restric
                                                           DecodePlan* __restrict__ plan,
                                                           uint8_t* __restrict__ xq,
                                                           uint8_t* __restrict__ zeros) {
-  const uint32_t t = blockIdx.x, tid = threadIdx.x;
-  __shared__ float red[4];
-  __shared__ uint32_t present[AFFX_MAX_EXPERTS / 32];
-  __shared__ uint32_t prefix[AFFX_MAX_EXPERTS / 32 + 1];
-  __shared__ uint32_t mask_s[kMaxSlots];
-  __shared__ float w_s[kMaxSlots][kMaxTok];
-
-  // ---- token t: exponent and three E4M3 terms --------------------------------------------------
-  float amax = 0.f;
-  for (uint32_t h = tid; h < hidden; h += 256) amax = fmaxf(amax, fabsf(x[t * xts + h * xds]));
-  for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
-  if ((tid & 63) == 0) red[tid >> 6] = amax;
-  __syncthreads();
-  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  // amax * 2^sigma in [128, 256): below E4M3's 448, one binade of headroom
-  const int sigma = amax > 0.f ? 7 - ilogbf(amax) : 0;
-  for (uint32_t h4 = tid * 4; h4 < hidden; h4 += 1024) {
+  const uint32_t nst = hidden / kTileCols, tid = threadIdx.x;
+  if (blockIdx.x < M * nst) {
+    const uint32_t t = blockIdx.x / nst, S = blockIdx.x % nst;
+    __shared__ float red[4];
+    const uint32_t h0 = S * kTileCols + 4 * tid;
+    float v[4];
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[i] = x[t * xts + (h0 + i) * xds];
+      amax = fmaxf(amax, fabsf(v[i]));
+    }
+    for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    if ((tid & 63) == 0) red[tid >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    // amax * 2^sigma in [128, 256): below E4M3's 448, one binade of headroom
+    const int sigma = amax > 0.f ? 7 - ilogbf(amax) : 0;
     uint32_t q0 = 0, q1 = 0, q2 = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float v = ldexpf(x[t * xts + (h4 + i) * xds], sigma);
-      const uint32_t b0 = f32_to_e4m3(v);
-      const float r1 = (v - e4m3_to_f32(b0)) * 16.0f;
-      const uint32_t b1 = f32_to_e4m3(r1);
-      const float r2 = (r1 - e4m3_to_f32(b1)) * 16.0f;
-      const uint32_t b2 = f32_to_e4m3(r2);
+      uint32_t b0, b1, b2;
+      split3(ldexpf(v[i], sigma), b0, b1, b2);
       q0 |= b0 << (8 * i);
       q1 |= b1 << (8 * i);
       q2 |= b2 << (8 * i);
     }
-    uint32_t* dst = reinterpret_cast<uint32_t*>(xq + (uint64_t)t * kTerms * hidden + h4);
+    uint32_t* dst = reinterpret_cast<uint32_t*>(xq + (uint64_t)t * kTerms * hidden + h0);
     dst[0] = q0;
     dst[hidden / 4] = q1;
     dst[2 * (hidden / 4)] = q2;
+    if (tid == 0) plan->x_sigma[t][S] = sigma;
+    return;
   }
-  if (tid == 0) plan->x_sigma[t] = sigma;
-  if (t != 0) return;
-  if (tid < 64) reinterpret_cast<uint32_t*>(zeros)[tid] = 0u;
 
-  // ---- block 0: the plan -----------------------------------------------------------------------
-  for (uint32_t i = tid; i < AFFX_MAX_EXPERTS / 32; i += 256) present[i] = 0;
-  for (uint32_t i = tid; i < kMaxSlots; i += 256) {
-    mask_s[i] = 0;
-#pragma unroll
-    for (int j = 0; j < kMaxTok; ++j) w_s[i][j] = 0.f;
-  }
+  // ---- the plan -------------------------------------------------------------------------------
+  __shared__ uint32_t present[AFFX_MAX_EXPERTS / 32];
+  __shared__ uint32_t prefix[AFFX_MAX_EXPERTS / 32 + 1];
+  __shared__ uint32_t slot_expert[kMaxSlots];
+  if (tid < 64) reinterpret_cast<uint32_t*>(zeros)[tid] = 0u;  // the B source of unused columns
+  if (tid < AFFX_MAX_EXPERTS / 32) present[tid] = 0;
   __syncthreads();
   if (tid < M * K) {
     const uint32_t e = sel[tid];
@@ -115,28 +111,31 @@ __global__ void __launch_bounds__(256) decode_prep_kernel(const float* __restric
     const uint32_t word = present[e >> 5];
     if ((word >> (e & 31)) & 1u) {
       const uint32_t slot = prefix[e >> 5] + __popc(word & ((1u << (e & 31)) - 1u));
+      slot_expert[slot] = e;
       plan->expert[slot] = e;
     }
   }
-  // token tid sums its (possibly repeated) experts' weights in route order: deterministic
-  if (tid < M) {
-    for (uint32_t j = 0; j < K; ++j) {
-      const uint32_t e = sel[tid * K + j];
-      if (e >= n_experts) continue;
-      const uint32_t word = present[e >> 5];
-      const uint32_t slot = prefix[e >> 5] + __popc(word & ((1u << (e & 31)) - 1u));
-      atomicOr(&mask_s[slot], 1u << tid);
-      w_s[slot][tid] += w[tid * K + j];
-    }
-  }
   __syncthreads();
+  // one thread per slot: which tokens it serves, with the summed weight of every route to it
+  // (a repeated expert counts once per route, summed in route order)
   const uint32_t ns = prefix[AFFX_MAX_EXPERTS / 32];
-  for (uint32_t i = tid; i < ns; i += 256) {
-    plan->tok_mask[i] = mask_s[i];
-#pragma unroll
-    for (int j = 0; j < kMaxTok; ++j) plan->w[i][j] = w_s[i][j];
+  if (tid < ns) {
+    const uint32_t e = slot_expert[tid];
+    uint32_t mask = 0;
+    for (uint32_t t = 0; t < kMaxTok; ++t) {
+      float ws = 0.f;
+      if (t < M)
+        for (uint32_t j = 0; j < K; ++j)
+          if (sel[t * K + j] == e) { ws += w[t * K + j]; mask |= 1u << t; }
+      plan->w[tid][t] = ws;
+    }
+    plan->tok_mask[tid] = mask;
   }
 }
+
+// ------------------------------------------------------------------------------------------------
+// shared pieces of the two GEMV kernels are in affx_tile.h
+// ------------------------------------------------------------------------------------------------
 
 // y = x - low terms: the value of three E4M3 terms t0 + t1/16 + t2/256 from a lane's column c
 // and its two right neighbours (same 16-lane row group).
@@ -179,39 +178,39 @@ __global__ void __launch_bounds__(256) decode_gateup_kernel(DecodeArgs A) {
   __syncthreads();
   if (S < nst) {
     const BSrc<CG> b = b_source<CG>(A.xq, A.hidden, (uint64_t)S * kTileCols, lane, M, mask, A.zeros);
+    // software pipeline: the table reads and B loads of step m+1 are issued before step m is
+    // finished and multiplied; the scheduling barrier keeps the compiler from hoisting all
+    // eight steps (register blow-up)
+    uint32_t rg[8], ru[8];
+    pin(ug);
+    pin(uu);
+    lookup_step(ug, tbl, 0, rg);
+    lookup_step(uu, tbl, 0, ru);
     v8i bc[CG];
 #pragma unroll
     for (int cg = 0; cg < CG; ++cg) bc[cg] = b_step(b.p[cg], 0);
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
-      // operands of step m+1 are requested before step m computes; the scheduling barrier keeps
-      // the compiler from hoisting all eight steps' loads and lookups (register blow-up)
+      uint32_t ng[8], nu[8];
       v8i bn[CG];
       if (m < 7) {
+        pin(ug);
+        pin(uu);
+        lookup_step(ug, tbl, m + 1, ng);
+        lookup_step(uu, tbl, m + 1, nu);
 #pragma unroll
         for (int cg = 0; cg < CG; ++cg) bn[cg] = b_step(b.p[cg], m + 1);
       }
-      pin(ug);
-      pin(uu);
-      v8i ag, au;
-      switch (m) {
-        case 0: ag = decode_a<0>(ug, tbl); au = decode_a<0>(uu, tbl); break;
-        case 1: ag = decode_a<1>(ug, tbl); au = decode_a<1>(uu, tbl); break;
-        case 2: ag = decode_a<2>(ug, tbl); au = decode_a<2>(uu, tbl); break;
-        case 3: ag = decode_a<3>(ug, tbl); au = decode_a<3>(uu, tbl); break;
-        case 4: ag = decode_a<4>(ug, tbl); au = decode_a<4>(uu, tbl); break;
-        case 5: ag = decode_a<5>(ug, tbl); au = decode_a<5>(uu, tbl); break;
-        case 6: ag = decode_a<6>(ug, tbl); au = decode_a<6>(uu, tbl); break;
-        default: ag = decode_a<7>(ug, tbl); au = decode_a<7>(uu, tbl); break;
-      }
+      const v8i ag = finish_step(ug, m, rg), au = finish_step(uu, m, ru);
 #pragma unroll
       for (int cg = 0; cg < CG; ++cg) {
         acc[0][cg] = mfma(ag, bc[cg], acc[0][cg]);
         acc[1][cg] = mfma(au, bc[cg], acc[1][cg]);
       }
       __builtin_amdgcn_sched_barrier(0);
-      asm volatile("" ::: "memory");
       if (m < 7) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) { rg[i] = ng[i]; ru[i] = nu[i]; }
 #pragma unroll
         for (int cg = 0; cg < CG; ++cg) bc[cg] = bn[cg];
       }
@@ -237,29 +236,25 @@ __global__ void __launch_bounds__(256) decode_gateup_kernel(DecodeArgs A) {
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
         float sum = 0.f;
-        for (uint32_t q = 0; q < nw; ++q)
-          sum += part[q][m][cg][r][col] + part[q][m][cg][r][col + 1] * 0.0625f +
-                 part[q][m][cg][r][col + 2] * 0.00390625f;
+        for (uint32_t q = 0; q < nw; ++q)  // super-segments in order, each at its own exponent
+          sum += ldexpf(part[q][m][cg][r][col] + part[q][m][cg][r][col + 1] * 0.0625f +
+                            part[q][m][cg][r][col + 2] * 0.00390625f,
+                        -A.plan->x_sigma[t][q]);
         s[m] = sum;
       }
       const uint32_t row = rt * 16 + r;
       const float rg = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(ex + A.off[kGateRs])[row] << 16);
       const float ru = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(ex + A.off[kUpRs])[row] << 16);
-      const int sig = A.plan->x_sigma[t];
-      float g = ldexpf(s[0], -sig) * rg;
-      float u = ldexpf(s[1], -sig) * ru;
+      float g = s[0] * rg;
+      float u = s[1] * ru;
       // SwiGLU with the asymmetric clamp: src/engine/ops.cpp:47-60
       const float L = A.limit;
       g = (L < g) ? L : g;
       const float lo = (-L < u) ? u : -L;
       u = (lo < L) ? lo : L;
       const float a = (g / (1.0f + expf(-g))) * u;
-      const float v = ldexpf(a, A.sigma_a);
-      const uint32_t b0 = f32_to_e4m3(v);
-      const float r1 = (v - e4m3_to_f32(b0)) * 16.0f;
-      const uint32_t b1 = f32_to_e4m3(r1);
-      const float r2 = (r1 - e4m3_to_f32(b1)) * 16.0f;
-      const uint32_t b2 = f32_to_e4m3(r2);
+      uint32_t b0, b1, b2;
+      split3(ldexpf(a, A.sigma_a), b0, b1, b2);
       uint8_t* dst = A.aq + ((uint64_t)(slot * M + t) * kTerms) * A.inter + row;
       dst[0] = (uint8_t)b0;
       dst[A.inter] = (uint8_t)b1;
@@ -269,17 +264,23 @@ __global__ void __launch_bounds__(256) decode_gateup_kernel(DecodeArgs A) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// down + weighted combine
+// down + weighted combine: one workgroup of 12 waves per 16-row tile of the output; the waves
+// take the (slot, super-segment) units in turn (all of a batch-1 layer's twelve at once) and
+// their per-token partials are summed in wave order.
 // ------------------------------------------------------------------------------------------------
-template <int CG>
-__global__ void __launch_bounds__(256) decode_down_kernel(DecodeArgs A) {
+constexpr int kDownWaves = 12;
+
+// SINGLE: every wave has at most one unit (units <= kDownWaves, e.g. batch 1: 6 experts x 2
+// super-segments), which lets the compiler keep the loop-free body in registers.
+template <int CG, bool SINGLE>
+__global__ void __launch_bounds__(kDownWaves * 64) decode_down_kernel(DecodeArgs A) {
   const uint32_t rt = blockIdx.x, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const uint32_t M = A.m_tokens, ns = A.plan->n_slots;
   const uint32_t nst = A.inter / kTileCols, units = ns * nst;
   const uint32_t c = lane & 15, rg = lane >> 4;
 
   __shared__ uint32_t tbl[4 * kLut];
-  __shared__ float part[4][CG][16][16];
+  __shared__ float part[kDownWaves][CG][16][16];
 
   float yacc[CG][4];
 #pragma unroll
@@ -287,6 +288,9 @@ __global__ void __launch_bounds__(256) decode_down_kernel(DecodeArgs A) {
 #pragma unroll
     for (int v = 0; v < 4; ++v) yacc[cg][v] = 0.f;
 
+  // the first unit's loads go out before the table is built; later units (batches with more
+  // units than waves) are loaded at the top of their iteration, the other waves of the CU
+  // covering the latency
   Unit cur;
   if (wv < units) {
     const uint32_t slot = wv / nst, S = wv % nst;
@@ -296,51 +300,42 @@ __global__ void __launch_bounds__(256) decode_down_kernel(DecodeArgs A) {
   build_table(tbl, A.codebook);
   __syncthreads();
 
-  for (uint32_t u = wv; u < units; u += 4) {
+#pragma unroll 1
+  for (uint32_t u = wv; u < (SINGLE ? (wv < units ? wv + 1 : 0) : units); u += kDownWaves) {
     const uint32_t slot = u / nst, S = u % nst;
     const uint32_t e = A.plan->expert[slot], mask = A.plan->tok_mask[slot];
     const uint8_t* ex = A.base + (uint64_t)e * A.stride;
+    if (!SINGLE && u != wv) load_unit(cur, ex + A.off[kDownCodes], ex + A.off[kDownFields], (uint64_t)rt * nst + S, lane);
     const BSrc<CG> b = b_source<CG>(A.aq + (uint64_t)slot * M * kTerms * A.inter, A.inter,
                                     (uint64_t)S * kTileCols, lane, M, mask, A.zeros);
-    Unit nxt;
-    const uint32_t un = u + 4;
-    if (un < units) {
-      const uint32_t sn = un / nst, Sn = un % nst;
-      const uint8_t* exn = A.base + (uint64_t)A.plan->expert[sn] * A.stride;
-      load_unit(nxt, exn + A.off[kDownCodes], exn + A.off[kDownFields], (uint64_t)rt * nst + Sn, lane);
-    }
     const uint2 rsv = *reinterpret_cast<const uint2*>(ex + A.off[kDownRs] + (uint64_t)(rt * 16 + 4 * rg) * 2);
     __builtin_amdgcn_sched_barrier(0);
     v4f acc[CG];
 #pragma unroll
     for (int cg = 0; cg < CG; ++cg) acc[cg] = v4f{0.f, 0.f, 0.f, 0.f};
+    uint32_t raw[8];
+    pin(cur);
+    lookup_step(cur, tbl, 0, raw);
     v8i bc[CG];
 #pragma unroll
     for (int cg = 0; cg < CG; ++cg) bc[cg] = b_step(b.p[cg], 0);
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
+      uint32_t nraw[8];
       v8i bn[CG];
       if (m < 7) {
+        pin(cur);
+        lookup_step(cur, tbl, m + 1, nraw);
 #pragma unroll
         for (int cg = 0; cg < CG; ++cg) bn[cg] = b_step(b.p[cg], m + 1);
       }
-      pin(cur);
-      v8i a;
-      switch (m) {
-        case 0: a = decode_a<0>(cur, tbl); break;
-        case 1: a = decode_a<1>(cur, tbl); break;
-        case 2: a = decode_a<2>(cur, tbl); break;
-        case 3: a = decode_a<3>(cur, tbl); break;
-        case 4: a = decode_a<4>(cur, tbl); break;
-        case 5: a = decode_a<5>(cur, tbl); break;
-        case 6: a = decode_a<6>(cur, tbl); break;
-        default: a = decode_a<7>(cur, tbl); break;
-      }
+      const v8i a = finish_step(cur, m, raw);
 #pragma unroll
       for (int cg = 0; cg < CG; ++cg) acc[cg] = mfma(a, bc[cg], acc[cg]);
       __builtin_amdgcn_sched_barrier(0);
-      asm volatile("" ::: "memory");
       if (m < 7) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) raw[i] = nraw[i];
 #pragma unroll
         for (int cg = 0; cg < CG; ++cg) bc[cg] = bn[cg];
       }
@@ -358,7 +353,6 @@ __global__ void __launch_bounds__(256) decode_down_kernel(DecodeArgs A) {
         if (mine) yacc[cg][v] += val * rs[v] * wt;
       }
     }
-    if (un < units) cur = nxt;
   }
 
 #pragma unroll
@@ -371,7 +365,7 @@ __global__ void __launch_bounds__(256) decode_down_kernel(DecodeArgs A) {
     const uint32_t r = tid & 15, t = tid >> 4;
     const uint32_t cg = t / 5, col = (t % 5) * 3;
     float sum = 0.f;
-    for (int q = 0; q < 4; ++q) sum += part[q][cg][r][col];
+    for (int q = 0; q < kDownWaves; ++q) sum += part[q][cg][r][col];
     float* dst = A.y + (uint64_t)t * A.y_ts + (uint64_t)(rt * 16 + r) * A.y_ds;
     *dst = A.accumulate ? *dst + sum : sum;
   }
@@ -464,7 +458,8 @@ int affx_decode_prepare(const affx_layer* L, const float* x, uint64_t x_ts, uint
   int rc = decode_setup(L, M, K, ws, ws_bytes, &A, &lay);
   if (rc) return rc;
   uint8_t* base = (uint8_t*)ws;
-  hipLaunchKernelGGL(decode_prep_kernel, dim3(M), dim3(256), 0, (hipStream_t)stream, x, x_ts, x_ds,
+  hipLaunchKernelGGL(decode_prep_kernel, dim3(M * (L->hidden / kTileCols) + 1), dim3(256), 0,
+                     (hipStream_t)stream, x, x_ts, x_ds,
                      M, sel, w, K, L->n_experts, L->hidden, (DecodePlan*)(base + lay.plan),
                      base + lay.xq, base + lay.zeros);
   return check_launch("decode_prep_kernel");
@@ -494,9 +489,16 @@ int affx_decode_down(const affx_layer* L, uint32_t M, uint32_t K, float* y, uint
   A.y_ts = y_ts;
   A.y_ds = y_ds;
   A.accumulate = accumulate;
-  const dim3 g(L->hidden / kTileRows);
-  if (M <= 5) hipLaunchKernelGGL(decode_down_kernel<1>, g, dim3(256), 0, (hipStream_t)stream, A);
-  else hipLaunchKernelGGL(decode_down_kernel<2>, g, dim3(256), 0, (hipStream_t)stream, A);
+  const dim3 g(L->hidden / kTileRows), blk(kDownWaves * 64);
+  // the number of units is known on the device only; M*K distinct experts bound it
+  const uint32_t max_units = (M * K < L->n_experts ? M * K : L->n_experts) * (L->inter / kTileCols);
+  hipStream_t st = (hipStream_t)stream;
+  if (M <= 5) {
+    if (max_units <= (uint32_t)kDownWaves) hipLaunchKernelGGL((decode_down_kernel<1, true>), g, blk, 0, st, A);
+    else hipLaunchKernelGGL((decode_down_kernel<1, false>), g, blk, 0, st, A);
+  } else {
+    hipLaunchKernelGGL((decode_down_kernel<2, false>), g, blk, 0, st, A);
+  }
   return check_launch("decode_down_kernel");
 }
 

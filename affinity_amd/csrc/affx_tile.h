@@ -68,6 +68,59 @@ __device__ __forceinline__ v8i decode_a(const Unit& u, const uint32_t* tbl) {
   return a;
 }
 
+// decode_a in two halves, so that the LDS lookups of step m+1 can be in flight while step m is
+// finished and multiplied: lookup_a issues the eight table reads, finish_a applies each block's
+// sign and exponent add.
+template <int MSTEP>
+__device__ __forceinline__ void lookup_a(const Unit& u, const uint32_t* tbl, uint32_t (&raw)[8]) {
+#pragma unroll
+  for (int bb = 0; bb < 2; ++bb) {
+    const int b = 2 * MSTEP + bb;
+    const uint32_t base = (stream_bits<3>(u.f, 6 * b, 6) >> 4) << 10;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) raw[bb * 4 + i] = tbl[base + stream_bits<20>(u.c, 10 * (4 * b + i), 10)];
+  }
+}
+
+template <int MSTEP>
+__device__ __forceinline__ v8i finish_a(const Unit& u, const uint32_t (&raw)[8]) {
+  v8i a;
+#pragma unroll
+  for (int bb = 0; bb < 2; ++bb) {
+    const uint32_t fb = stream_bits<3>(u.f, 6 * (2 * MSTEP + bb), 6);
+    const uint32_t x = block_xor(fb), ad = block_add(fb);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a[bb * 4 + i] = (int)((raw[bb * 4 + i] ^ x) + ad);
+  }
+  return a;
+}
+
+__device__ __forceinline__ void lookup_step(const Unit& u, const uint32_t* tbl, int m, uint32_t (&raw)[8]) {
+  switch (m) {
+    case 0: lookup_a<0>(u, tbl, raw); break;
+    case 1: lookup_a<1>(u, tbl, raw); break;
+    case 2: lookup_a<2>(u, tbl, raw); break;
+    case 3: lookup_a<3>(u, tbl, raw); break;
+    case 4: lookup_a<4>(u, tbl, raw); break;
+    case 5: lookup_a<5>(u, tbl, raw); break;
+    case 6: lookup_a<6>(u, tbl, raw); break;
+    default: lookup_a<7>(u, tbl, raw); break;
+  }
+}
+
+__device__ __forceinline__ v8i finish_step(const Unit& u, int m, const uint32_t (&raw)[8]) {
+  switch (m) {
+    case 0: return finish_a<0>(u, raw);
+    case 1: return finish_a<1>(u, raw);
+    case 2: return finish_a<2>(u, raw);
+    case 3: return finish_a<3>(u, raw);
+    case 4: return finish_a<4>(u, raw);
+    case 5: return finish_a<5>(u, raw);
+    case 6: return finish_a<6>(u, raw);
+    default: return finish_a<7>(u, raw);
+  }
+}
+
 // decode_a with a step index that is a compile-time constant after unrolling.
 __device__ __forceinline__ v8i decode_step(const Unit& u, const uint32_t* tbl, int m) {
   switch (m) {
