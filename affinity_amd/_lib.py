@@ -57,6 +57,8 @@ _SIGS = {
     "affx_decode_gateup": ([C.POINTER(AffxLayer), _u32, _u32, _vp, C.c_size_t, _vp], C.c_int),
     "affx_decode_down": ([C.POINTER(AffxLayer), _u32, _u32, _vp, _u64, _u64, C.c_int, _vp, C.c_size_t, _vp],
                          C.c_int),
+    "affx_decode_staged": ([C.POINTER(AffxLayer), _vp, _u64, _u64, _u32, _vp, _vp, _u32, _vp,
+                            _u64, _u64, C.c_int, _vp, C.c_size_t, _vp], C.c_int),
     "affx_grouped_workspace_size": ([_u32, _u32, _u32, _u32, _u32], C.c_size_t),
     "affx_expert_ffn_grouped": ([C.POINTER(AffxLayer), _vp, _vp, _u32, _vp, _vp, _u32, _vp, C.c_int,
                                  _vp, C.c_size_t, _vp], C.c_int),

@@ -62,6 +62,26 @@ struct DecodePlan {
   float w[kMaxSlots][kMaxTok];
 };
 
+// Phase markers of the persistent decode kernel: expand to nothing (a profiling build can define
+// them to record timestamps).
+#ifndef AFFX_TRACE
+#define AFFX_TRACE(k) ((void)0)
+#endif
+
+// Dynamic LDS of a kernel (one byte array; the kernel carves it up).
+#ifndef AFFX_DYN_LDS
+#define AFFX_DYN_LDS(name) extern __shared__ __align__(16) uint8_t name[]
+#endif
+
+// Decode workspace: [sync 256 B][plan][zeros][xq][aq] (affx_decode.hip). The first 256 bytes hold
+// the fused decode's cross-workgroup counters: zero before first use, left zero by every launch.
+struct DecodeWs {
+  uint64_t sync, plan, zeros, xq, aq, total;
+};
+DecodeWs decode_ws(uint32_t M, uint32_t K, uint32_t hidden, uint32_t inter);
+int decode_check(const affx_layer* L, uint32_t M, uint32_t K, const void* ws, size_t ws_bytes,
+                 DecodeWs* lay);
+
 // ---- status ------------------------------------------------------------------------------------
 int set_error(int code, const char* fmt, ...);
 int check_hip(hipError_t e, const char* what);

@@ -371,26 +371,24 @@ __global__ void __launch_bounds__(kDownWaves * 64) decode_down_kernel(DecodeArgs
   }
 }
 
-}  // namespace affx
-
-using namespace affx;
-
 static uint64_t align256(uint64_t v) { return (v + 255) / 256 * 256; }
 
-struct DecodeWs {
-  uint64_t plan, zeros, xq, aq, total;
-};
-
-static DecodeWs decode_ws(uint32_t M, uint32_t K, uint32_t hidden, uint32_t inter) {
+// Workspace: [sync 256 B: fused-decode counters, zero on first use][plan][zeros][xq][aq]
+DecodeWs decode_ws(uint32_t M, uint32_t K, uint32_t hidden, uint32_t inter) {
   DecodeWs w;
   const uint64_t slots = (uint64_t)M * K;
-  w.plan = 0;
-  w.zeros = align256(sizeof(DecodePlan));
+  w.sync = 0;
+  w.plan = 256;
+  w.zeros = w.plan + align256(sizeof(DecodePlan));
   w.xq = w.zeros + 256;
   w.aq = w.xq + align256((uint64_t)M * kTerms * hidden);
   w.total = w.aq + align256(slots * M * kTerms * inter);
   return w;
 }
+
+}  // namespace affx
+
+using namespace affx;
 
 extern "C" {
 
@@ -400,11 +398,11 @@ size_t affx_decode_workspace_size(uint32_t m, uint32_t k, uint32_t hidden, uint3
 
 }  // extern "C"
 
-namespace {
+namespace affx {
 
-// Checks shared by the three stages; fills the kernel arguments.
-int decode_setup(const affx_layer* L, uint32_t M, uint32_t K, void* ws, size_t ws_bytes,
-                 DecodeArgs* A, DecodeWs* lay) {
+// Checks shared by the staged and fused paths; the workspace layout.
+int decode_check(const affx_layer* L, uint32_t M, uint32_t K, const void* ws, size_t ws_bytes,
+                 DecodeWs* lay) {
   if (!L || !ws || !L->base || !L->codebook) return set_error(AFFX_ERR_ARG, "ffn_decode: null pointer");
   if (M == 0 || M > kMaxTok || K == 0 || K > AFFX_MAX_TOPK)
     return set_error(AFFX_DECLINED, "ffn_decode: m_tokens must be 1..%d and top_k 1..%d (got %u, %u)",
@@ -424,6 +422,16 @@ int decode_setup(const affx_layer* L, uint32_t M, uint32_t K, void* ws, size_t w
   uint64_t off9[9];
   const uint64_t stride = affx_expert_layout(L->hidden, L->inter, off9, nullptr);
   if (L->stride < stride) return set_error(AFFX_ERR_ARG, "ffn_decode: layer stride below expert size");
+  return AFFX_OK;
+}
+
+// decode_check, then the staged kernels' arguments.
+int decode_setup(const affx_layer* L, uint32_t M, uint32_t K, void* ws, size_t ws_bytes,
+                 DecodeArgs* A, DecodeWs* lay) {
+  const int rc = decode_check(L, M, K, ws, ws_bytes, lay);
+  if (rc) return rc;
+  uint64_t off9[9];
+  affx_expert_layout(L->hidden, L->inter, off9, nullptr);
   uint8_t* base = (uint8_t*)ws;
   A->base = (const uint8_t*)L->base;
   A->stride = L->stride;
@@ -445,7 +453,7 @@ int decode_setup(const affx_layer* L, uint32_t M, uint32_t K, void* ws, size_t w
   return AFFX_OK;
 }
 
-}  // namespace
+}  // namespace affx
 
 extern "C" {
 
@@ -502,7 +510,7 @@ int affx_decode_down(const affx_layer* L, uint32_t M, uint32_t K, float* y, uint
   return check_launch("decode_down_kernel");
 }
 
-int affx_expert_ffn_decode(const affx_layer* L, const float* x, uint64_t x_ts, uint64_t x_ds,
+int affx_decode_staged(const affx_layer* L, const float* x, uint64_t x_ts, uint64_t x_ds,
                            uint32_t M, const uint32_t* sel, const float* w, uint32_t K, float* y,
                            uint64_t y_ts, uint64_t y_ds, int accumulate, void* ws,
                            size_t ws_bytes, void* stream) {

@@ -1,0 +1,899 @@
+// Fused decode of one MoE layer (M <= 8 tokens): one launch runs routing plan, activation split,
+// gate/up + SwiGLU and down + weighted combine.
+//
+// One workgroup of 12 waves per CU, all resident at once (the grid never exceeds what the device
+// holds concurrently). Every workgroup
+//   1. builds the routing plan itself (distinct experts ascending, token masks, summed weights),
+//   2. issues the HBM loads of its gate/up tiles AND of its first down tile right away, so the
+//      down weights stream in while gate/up is computed,
+//   3. splits the activation into three E4M3 terms in LDS (hardware fp8 conversion) and stages
+//      the codebook in LDS as KC interleaved copies (lane-fixed copy: gathers from 64 lanes spread
+//      over the 64 banks instead of colliding at random),
+//   4. computes its gate/up items (16 rows x all columns of one expert; wave = 1024-column
+//      segment), sums the segments in fixed order, applies SwiGLU and writes the result as E4M3
+//      terms (aq) to global memory, then publishes its item count with an agent-scope release,
+//   5. waits (bounded spin) until every workgroup's items are published, then computes one
+//      16-row tile of the output from its (expert, segment) down units and writes y.
+// The last workgroup to finish resets the counters, so the workspace is reusable by the next
+// launch on the stream without a memset (graph-capture safe).
+//
+// Reference counterparts: the decode branch of ExpertFfnBatch (src/engine/model.cpp:6045-6121)
+// over expert_ffn_hip (src/gpu/expert_kernel.hip:2737-2808) and moe_plan (src/gpu/moe_plan.hip).
+#include <mutex>
+
+#include "affx_tile.h"
+
+namespace affx {
+
+constexpr int kFW = 12;                      // waves per workgroup
+constexpr int kFT = kFW * 64;                // threads per workgroup
+constexpr int kXqChunk = 272;                // LDS bytes of one 256-column chunk of an xq row
+constexpr int kXqRow = 16 * kXqChunk + 64;   // LDS bytes of one (token, term) row, hidden <= 4096
+constexpr uint32_t kSpinLimit = 1u << 22;    // polls (~2^22 x 128 cycles ~ 0.2 s) before giving up
+constexpr int kPlanRoutes = AFFX_MAX_DECODE_TOKENS * AFFX_MAX_TOPK;  // 128
+
+struct FusedArgs {
+  const uint8_t* base;
+  uint64_t stride;
+  uint64_t off[9];
+  uint32_t hidden, inter, M, K, n_experts, n_wg;
+  const uint32_t* codebook;
+  const float* x;
+  uint64_t xts, xds;
+  const uint32_t* sel;
+  const float* w;
+  uint8_t* aq;          // [slot][M][3][inter]
+  const uint8_t* zeros; // 256 zero bytes (B source of unused down columns)
+  uint32_t* sync;       // [0] gate/up items published, [1] workgroups finished, [2] error bits
+  float* y;
+  uint64_t yts, yds;
+  int accumulate;
+  float limit;
+  int32_t sigma_a;
+};
+
+// LDS layout in bytes (host and device agree): codebook copies, activation terms, zero run,
+// partial sums, plan.
+struct FusedLds {
+  uint32_t tbl, xq, zero, part, plan, total;
+};
+
+__host__ __device__ inline FusedLds fused_lds(uint32_t kc, uint32_t M) {
+  FusedLds L;
+  L.tbl = 0;
+  L.xq = kc * 2048u * 4u;
+  L.zero = L.xq + 3u * M * kXqRow;
+  L.part = L.zero + 256u;
+  const uint32_t part_bytes = (uint32_t)kFW * 2u * 16u * M * 4u;  // gate/up [wave][mat][row][tok]
+  L.plan = L.part + part_bytes;
+  // rank[128] w[128] slot_expert[128] slot_mask[128] rs[12][32] sigma[32] present[16] prefix[16]
+  // misc[4] slot_w[128][M]
+  L.total = L.plan + (4u * kPlanRoutes + kFW * 32u + 32u + 16u + 16u + 4u) * 4u + kPlanRoutes * M * 4u;
+  return L;
+}
+
+// ---- replicated codebook -------------------------------------------------------------------------
+// KC interleaved copies of the 2 x 1024 codebook dwords: entry (variant v, code c) of copy j at
+// dword ((v << 10 | c) * KC + j). A lane reads copy (lane >> 1) % KC, so the 64 gathers of one
+// instruction spread over the banks by lane instead of colliding at random.
+template <int KC>
+struct Lut {
+  static constexpr int kLog = KC == 16 ? 4 : KC == 8 ? 3 : 2;
+  static constexpr int kCodeSh = kLog + 2;       // byte-address bit of code bit 0
+  static constexpr int kVarSh = kCodeSh + 10;    // byte-address bit of the variant
+};
+
+template <int KC>
+__device__ __forceinline__ void build_lut(uint32_t* tbl, const uint32_t (&cbv)[3], uint32_t tid) {
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const uint32_t e = tid + (uint32_t)i * kFT;
+    if (e >= 2048u) break;
+    const uint32_t d = cbv[i];
+    const u32x4 v = {d, d, d, d};
+    u32x4* dst = reinterpret_cast<u32x4*>(tbl + e * KC);
+#pragma unroll
+    for (int q = 0; q < KC / 4; ++q) dst[q] = v;
+  }
+}
+
+// LDS byte address of code I (0..63) of the unit: the code's ten bits are brought to bit kCodeSh
+// of an alignbit window and inserted into vb (the block's variant and the lane's copy; bits
+// outside the code field come from vb).
+template <int KC, int I>
+__device__ __forceinline__ uint32_t code_addr(const uint32_t (&c)[20], uint32_t vb) {
+  constexpr int S = Lut<KC>::kCodeSh;
+  constexpr int q = 10 * I - S;
+  uint32_t x;
+  if constexpr (q < 0) {
+    x = __builtin_amdgcn_alignbit(c[0], c[0], q + 32);
+  } else {
+    constexpr int lo = q >> 5, sh = q & 31;
+    constexpr int hi = (sh + S + 10 > 32 && lo + 1 < 20) ? lo + 1 : lo;
+    x = sh == 0 ? c[lo] : __builtin_amdgcn_alignbit(c[hi], c[lo], sh);
+  }
+  return (x & (0x3FFu << S)) | vb;
+}
+
+// The eight table reads of MFMA step MSTEP (blocks 2m, 2m+1) and the two blocks' 6-bit fields
+// (bits 0-2 exponent add s, 3 sign, 4 rotation, 5 variant).
+template <int KC, int MSTEP>
+__device__ __forceinline__ void lut_lookup(const Unit& u, const uint8_t* lds, uint32_t copy4,
+                                           uint32_t (&raw)[8], uint32_t (&fb)[2]) {
+  fb[0] = stream_bits<3>(u.f, 12 * MSTEP, 6);
+  fb[1] = stream_bits<3>(u.f, 12 * MSTEP + 6, 6);
+  const uint32_t vb0 = ((fb[0] >> 5) << Lut<KC>::kVarSh) | copy4;
+  const uint32_t vb1 = ((fb[1] >> 5) << Lut<KC>::kVarSh) | copy4;
+  constexpr int I = 8 * MSTEP;
+  raw[0] = *reinterpret_cast<const uint32_t*>(lds + code_addr<KC, I + 0>(u.c, vb0));
+  raw[1] = *reinterpret_cast<const uint32_t*>(lds + code_addr<KC, I + 1>(u.c, vb0));
+  raw[2] = *reinterpret_cast<const uint32_t*>(lds + code_addr<KC, I + 2>(u.c, vb0));
+  raw[3] = *reinterpret_cast<const uint32_t*>(lds + code_addr<KC, I + 3>(u.c, vb0));
+  raw[4] = *reinterpret_cast<const uint32_t*>(lds + code_addr<KC, I + 4>(u.c, vb1));
+  raw[5] = *reinterpret_cast<const uint32_t*>(lds + code_addr<KC, I + 5>(u.c, vb1));
+  raw[6] = *reinterpret_cast<const uint32_t*>(lds + code_addr<KC, I + 6>(u.c, vb1));
+  raw[7] = *reinterpret_cast<const uint32_t*>(lds + code_addr<KC, I + 7>(u.c, vb1));
+}
+
+// A fragment from the table reads: rotation by table-entry halves, sign flip, exponent add
+// (src/gpu/expert_kernel.hip:594-617; rotation src/quant/blockquant.cpp:826-828).
+__device__ __forceinline__ v8i lut_finish(const uint32_t (&raw)[8], const uint32_t (&fb)[2]) {
+  v8i a;
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const uint32_t rsh = fb[b] & 16u, xm = block_xor(fb[b]), ad = (fb[b] & 7u) * 0x08080808u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t r = __builtin_amdgcn_alignbit(raw[4 * b + i], raw[4 * b + i], rsh);
+      a[4 * b + i] = (int)((r ^ xm) + ad);
+    }
+  }
+  return a;
+}
+
+template <int KC>
+__device__ __forceinline__ void lut_lookup_step(const Unit& u, const uint8_t* lds, uint32_t copy4,
+                                                int m, uint32_t (&raw)[8], uint32_t (&fb)[2]) {
+  switch (m) {
+    case 0: lut_lookup<KC, 0>(u, lds, copy4, raw, fb); break;
+    case 1: lut_lookup<KC, 1>(u, lds, copy4, raw, fb); break;
+    case 2: lut_lookup<KC, 2>(u, lds, copy4, raw, fb); break;
+    case 3: lut_lookup<KC, 3>(u, lds, copy4, raw, fb); break;
+    case 4: lut_lookup<KC, 4>(u, lds, copy4, raw, fb); break;
+    case 5: lut_lookup<KC, 5>(u, lds, copy4, raw, fb); break;
+    case 6: lut_lookup<KC, 6>(u, lds, copy4, raw, fb); break;
+    default: lut_lookup<KC, 7>(u, lds, copy4, raw, fb); break;
+  }
+}
+
+// Makes opaque, at the top of MFMA step MSTEP, only the registers that step reads (the code
+// dwords of codes 8m..8m+7 with their alignbit neighbours, the field dwords of blocks 2m, 2m+1):
+// the step's extraction cannot be hoisted above it, and the step waits only for the load chunks
+// it needs (chunk j = code dwords 4j..4j+3; loads complete in issue order).
+template <int MSTEP>
+__device__ __forceinline__ void pin_step(Unit& u) {
+  constexpr int k0 = (80 * MSTEP - 6) < 0 ? 0 : (80 * MSTEP - 6) >> 5;
+  constexpr int k1 = (80 * MSTEP + 79) >> 5 > 19 ? 19 : (80 * MSTEP + 79) >> 5;
+#pragma unroll
+  for (int k = k0; k <= k1; ++k) AFFX_PIN(u.c[k]);
+  AFFX_PIN(u.f[(12 * MSTEP) >> 5]);
+  if constexpr (((12 * MSTEP + 11) >> 5) != ((12 * MSTEP) >> 5)) AFFX_PIN(u.f[(12 * MSTEP + 11) >> 5]);
+}
+
+__device__ __forceinline__ void pin_step(Unit& u, int m) {
+  switch (m) {
+    case 0: pin_step<0>(u); break;
+    case 1: pin_step<1>(u); break;
+    case 2: pin_step<2>(u); break;
+    case 3: pin_step<3>(u); break;
+    case 4: pin_step<4>(u); break;
+    case 5: pin_step<5>(u); break;
+    case 6: pin_step<6>(u); break;
+    default: pin_step<7>(u); break;
+  }
+}
+
+// B operand of one MFMA step from the LDS activation rows: two 16-byte reads.
+__device__ __forceinline__ v8i b_step_lds(const uint8_t* p, int m) {
+  const u32x4 lo = *reinterpret_cast<const u32x4*>(p + 32 * m);
+  const u32x4 hi = *reinterpret_cast<const u32x4*>(p + 32 * m + 16);
+  v8i v;
+  v[0] = (int)lo[0]; v[1] = (int)lo[1]; v[2] = (int)lo[2]; v[3] = (int)lo[3];
+  v[4] = (int)hi[0]; v[5] = (int)hi[1]; v[6] = (int)hi[2]; v[7] = (int)hi[3];
+  return v;
+}
+
+// The gate and up units of one wave tile, loaded in the order the MFMA steps need them (both
+// field runs, then code chunk j of gate and of up for j = 0..4): loads complete in issue order, so
+// step m only waits for the chunks it reads. The scheduling barriers keep that order.
+__device__ __forceinline__ void load_pair(Unit& g, Unit& u, const uint8_t* gc, const uint8_t* gf,
+                                          const uint8_t* uc, const uint8_t* uf, uint64_t tile, uint32_t lane) {
+  const uint32_t* gfp = reinterpret_cast<const uint32_t*>(gf + tile * kTileFieldBytes + lane * 12);
+  const uint32_t* ufp = reinterpret_cast<const uint32_t*>(uf + tile * kTileFieldBytes + lane * 12);
+  g.f[0] = __builtin_nontemporal_load(gfp);
+  g.f[1] = __builtin_nontemporal_load(gfp + 1);
+  g.f[2] = __builtin_nontemporal_load(gfp + 2);
+  u.f[0] = __builtin_nontemporal_load(ufp);
+  u.f[1] = __builtin_nontemporal_load(ufp + 1);
+  u.f[2] = __builtin_nontemporal_load(ufp + 2);
+  __builtin_amdgcn_sched_barrier(0);
+  const uint8_t* gcp = gc + tile * kTileCodeBytes + lane * 16;
+  const uint8_t* ucp = uc + tile * kTileCodeBytes + lane * 16;
+#pragma unroll
+  for (int j = 0; j < 5; ++j) {
+    const u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(gcp + j * 1024));
+    const u32x4 b = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ucp + j * 1024));
+    g.c[4 * j] = a[0]; g.c[4 * j + 1] = a[1]; g.c[4 * j + 2] = a[2]; g.c[4 * j + 3] = a[3];
+    u.c[4 * j] = b[0]; u.c[4 * j + 1] = b[1]; u.c[4 * j + 2] = b[2]; u.c[4 * j + 3] = b[3];
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// One unit, fields first, then the code chunks in order.
+__device__ __forceinline__ void load_unit_ordered(Unit& u, const uint8_t* codes, const uint8_t* fields,
+                                                  uint64_t tile, uint32_t lane) {
+  const uint32_t* fp = reinterpret_cast<const uint32_t*>(fields + tile * kTileFieldBytes + lane * 12);
+  u.f[0] = __builtin_nontemporal_load(fp);
+  u.f[1] = __builtin_nontemporal_load(fp + 1);
+  u.f[2] = __builtin_nontemporal_load(fp + 2);
+  __builtin_amdgcn_sched_barrier(0);
+  const uint8_t* cp = codes + tile * kTileCodeBytes + lane * 16;
+#pragma unroll
+  for (int j = 0; j < 5; ++j) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(cp + j * 1024));
+    u.c[4 * j] = v[0]; u.c[4 * j + 1] = v[1]; u.c[4 * j + 2] = v[2]; u.c[4 * j + 3] = v[3];
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// value of the three E4M3 term columns c, c+1, c+2 (valid in lanes whose column is a multiple of 3)
+__device__ __forceinline__ float fused_terms(float d) {
+  const float d1 = __shfl_down(d, 1, 16), d2 = __shfl_down(d, 2, 16);
+  return d + d1 * 0.0625f + d2 * 0.00390625f;
+}
+
+// Three E4M3 terms of four values (|v| < 256) with the hardware conversion (round to nearest
+// even, identical to f32_to_e4m3 in this range): returns the packed bytes of each term.
+__device__ __forceinline__ void split3x4(float v0, float v1, float v2, float v3, uint32_t& q0,
+                                         uint32_t& q1, uint32_t& q2) {
+  typedef float v2f __attribute__((ext_vector_type(2)));
+  uint32_t t = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v0, v1, 0, false);
+  t = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v2, v3, (int)t, true);
+  q0 = t;
+  v2f a = __builtin_amdgcn_cvt_pk_f32_fp8((int)t, false), b = __builtin_amdgcn_cvt_pk_f32_fp8((int)t, true);
+  v0 = (v0 - a.x) * 16.0f; v1 = (v1 - a.y) * 16.0f; v2 = (v2 - b.x) * 16.0f; v3 = (v3 - b.y) * 16.0f;
+  t = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v0, v1, 0, false);
+  t = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v2, v3, (int)t, true);
+  q1 = t;
+  a = __builtin_amdgcn_cvt_pk_f32_fp8((int)t, false);
+  b = __builtin_amdgcn_cvt_pk_f32_fp8((int)t, true);
+  v0 = (v0 - a.x) * 16.0f; v1 = (v1 - a.y) * 16.0f; v2 = (v2 - b.x) * 16.0f; v3 = (v3 - b.y) * 16.0f;
+  t = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v0, v1, 0, false);
+  t = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v2, v3, (int)t, true);
+  q2 = t;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+// ------------------------------------------------------------------------------------------------
+// The kernel. CG: 16-column groups of the MFMA B operand (5 tokens each). KC: codebook copies.
+// MAXM: largest M this instantiation serves (sizes the per-thread activation registers).
+// The down weights of the first unit are prefetched during gate/up when CG = 1. SINGLE: at most
+// one gate/up item and one down unit (per output tile) per wave, which keeps those two phases
+// loop-free (batch 1).
+// ------------------------------------------------------------------------------------------------
+template <int CG, int KC, int MAXM, bool SINGLE>
+__global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
+  AFFX_DYN_LDS(lds);
+  // the first down unit is loaded while gate/up runs (one column group leaves the registers)
+  constexpr bool PREF = CG == 1;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, g = blockIdx.x;
+  const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar registers
+  const uint32_t M = A.M, K = A.K, R = M * K;
+  const uint32_t nst = A.hidden / kTileCols, nsi = A.inter / kTileCols;
+  const FusedLds L = fused_lds(KC, M);
+  uint32_t* tbl = reinterpret_cast<uint32_t*>(lds + L.tbl);
+  uint8_t* xq = lds + L.xq;
+  uint8_t* zero_l = lds + L.zero;
+  float* part = reinterpret_cast<float*>(lds + L.part);
+  uint32_t* rank_l = reinterpret_cast<uint32_t*>(lds + L.plan);
+  float* w_l = reinterpret_cast<float*>(rank_l + kPlanRoutes);
+  uint32_t* slot_expert = reinterpret_cast<uint32_t*>(w_l + kPlanRoutes);
+  uint32_t* slot_mask = slot_expert + kPlanRoutes;
+  float* rs_l = reinterpret_cast<float*>(slot_mask + kPlanRoutes);  // [group][gate 16 | up 16]
+  int32_t* sigma_l = reinterpret_cast<int32_t*>(rs_l + kFW * 32);
+  uint32_t* present = reinterpret_cast<uint32_t*>(sigma_l + 32);
+  uint32_t* prefix_l = present + 16;
+  uint32_t* misc = prefix_l + 16;
+  float* slot_w = reinterpret_cast<float*>(misc + 4);
+
+  AFFX_TRACE(0);
+  // ---- 1. small loads first (codebook, activation, routes: their waits never queue behind the
+  // weight stream, loads complete in issue order); per-quarter activation maxima; plan by wave 0
+  uint32_t cbv[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const uint32_t e = tid + (uint32_t)i * kFT;
+    cbv[i] = e < 2048u ? A.codebook[e] : 0u;
+  }
+  // activation: pair p = wv + 12 j is (token p / nst, 1024-column segment p % nst); its 1024
+  // values are loaded now (an absent pair loads pair 0 again, unused), split after the weight
+  // loads are issued
+  constexpr int NP = (MAXM * 4 + kFW - 1) / kFW;
+  float4 xr[NP][4];
+  {
+    const bool xvec = A.xds == 1 && (A.xts & 3u) == 0 && (reinterpret_cast<uintptr_t>(A.x) & 15u) == 0;
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+      const uint32_t p0 = wv + (uint32_t)j * kFW, p = p0 < M * nst ? p0 : 0u;
+      const uint32_t t = p / nst, Sx = p % nst;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t h = Sx * kTileCols + 4 * (lane + 64 * i);
+        if (xvec) {
+          xr[j][i] = *reinterpret_cast<const float4*>(A.x + t * A.xts + h);
+        } else {
+          const float* px = A.x + t * A.xts + h * A.xds;
+          xr[j][i] = make_float4(px[0], px[A.xds], px[2 * A.xds], px[3 * A.xds]);
+        }
+      }
+    }
+  }
+  // routes of the batch, loaded by every wave (no loads inside the plan's branch: the wait
+  // tracking then stays exact for the weight loads that follow)
+  uint32_t e[2];
+  float wr[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t r = lane + 64u * h, rr = r < R ? r : 0u;
+    e[h] = A.sel[rr];
+    wr[h] = A.w[rr];
+  }
+  if (wv == 0) {
+    // ids outside the layer are ignored, as in the staged path
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t r = lane + 64u * h;
+      if (r < R) {
+        e[h] = e[h] < A.n_experts ? e[h] : ~0u;
+        w_l[r] = wr[h];
+      } else {
+        e[h] = ~0u;
+      }
+    }
+    AFFX_TRACE(8);
+    if (lane < 16) present[lane] = 0;
+    slot_mask[lane] = 0;
+    slot_mask[lane + 64] = 0;
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      if (e[h] != ~0u) atomicOr(&present[e[h] >> 5], 1u << (e[h] & 31));
+    __builtin_amdgcn_wave_barrier();
+    // experts present in the words below each word (sixteen independent reads per lane)
+    if (lane < 16) {
+      uint32_t pre = 0;
+#pragma unroll
+      for (uint32_t j = 0; j < 16; ++j) {
+        const uint32_t c = __popc(present[j]);
+        pre += j < lane ? c : 0u;
+      }
+      prefix_l[lane] = pre;
+      if (lane == 15) misc[0] = pre + __popc(present[15]);
+    }
+    __builtin_amdgcn_wave_barrier();
+    // slot of a route: experts present below it, ascending ids
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t r = lane + 64u * h;
+      if (r < R) {
+        uint32_t s = ~0u;
+        if (e[h] != ~0u) {
+          s = prefix_l[e[h] >> 5] + __popc(present[e[h] >> 5] & ((1u << (e[h] & 31)) - 1u));
+          slot_expert[s] = e[h];
+        }
+        rank_l[r] = s;
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    // per (slot, token): summed weight of its routes in route order, and the token masks
+    const uint32_t ns0 = misc[0];
+    for (uint32_t p = lane; p < ns0 * M; p += 64) {
+      const uint32_t s = p / M, t = p % M;
+      float ws = 0.f;
+      bool hit = false;
+#pragma unroll
+      for (uint32_t j = 0; j < (uint32_t)AFFX_MAX_TOPK; ++j) {
+        const uint32_t jj = j < K ? j : K - 1;  // in bounds; j >= K contributes nothing
+        const bool m = j < K && rank_l[t * K + jj] == s;
+        const float wj = w_l[t * K + jj];
+        ws += m ? wj : 0.f;
+        hit = hit || m;
+      }
+      slot_w[p] = ws;
+      if (hit) atomicOr(&slot_mask[s], 1u << t);
+    }
+    AFFX_TRACE(9);
+  }
+  __syncthreads();  // the plan is visible
+  AFFX_TRACE(1);
+
+  const uint32_t ns = __builtin_amdgcn_readfirstlane(misc[0]);
+  const uint32_t rt_per = A.inter / kTileRows;          // gate/up row tiles per expert
+  const uint32_t NI = ns * rt_per;                      // gate/up items of the layer
+  const uint32_t groups = kFW / nst;                    // items in flight per workgroup
+  const uint32_t q = wv / nst, S = wv % nst;            // this wave: group, column segment
+  const uint32_t my_items = g < NI ? (NI - g + A.n_wg - 1) / A.n_wg : 0;
+  const uint32_t rounds = (my_items + groups - 1) / groups;
+  const uint32_t dtiles = A.hidden / kTileRows;
+  const uint32_t NU = ns * nsi;                         // down units per output tile
+  const uint32_t copy4 = ((lane >> 1) & (KC - 1)) * 4u;
+
+  // ---- 2. loads: gate/up pair of round 0 (+ its row scales), and the first down unit (+ row
+  // scales) when round 0 is the last; the compute below waits for them
+  Unit ug, uu, ud;
+  uint32_t rs_gu = 0;  // bf16 row scale: lanes 0-15 gate rows, 16-31 up rows (segment-0 waves)
+  uint2 rs_d = {0u, 0u};
+  auto gu_item = [&](uint32_t rho) -> uint32_t {
+    const uint32_t k = rho * groups + q;
+    return (q < groups && k < my_items) ? g + A.n_wg * k : ~0u;
+  };
+  // unconditional loads (an absent item or unit reads expert 0's first tile, never used): the
+  // wait-count tracking then sees straight-line code and waits for exactly what each step needs
+  auto load_gu = [&](uint32_t item) {
+    const bool ok = item != ~0u;
+    const uint32_t slot = ok ? item / rt_per : 0u, rt = ok ? item % rt_per : 0u;
+    const uint32_t e = ok ? __builtin_amdgcn_readfirstlane(slot_expert[slot]) : 0u;
+    const uint8_t* ex = A.base + (uint64_t)e * A.stride;
+    const uint64_t tile = ok ? (uint64_t)rt * nst + S : 0u;
+    load_pair(ug, uu, ex + A.off[kGateCodes], ex + A.off[kGateFields], ex + A.off[kUpCodes],
+              ex + A.off[kUpFields], tile, lane);
+    rs_gu = reinterpret_cast<const uint16_t*>(ex + A.off[lane < 16 ? kGateRs : kUpRs])[rt * 16 + (lane & 15)];
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto load_down = [&](bool ok, uint32_t td, uint32_t u) {
+    const uint32_t slot = ok ? u / nsi : 0u, S2 = ok ? u % nsi : 0u;
+    const uint32_t e = ok ? __builtin_amdgcn_readfirstlane(slot_expert[slot]) : 0u;
+    const uint8_t* ex = A.base + (uint64_t)e * A.stride;
+    const uint32_t tdd = ok ? td : 0u;
+    load_unit_ordered(ud, ex + A.off[kDownCodes], ex + A.off[kDownFields], (uint64_t)tdd * nsi + S2, lane);
+    rs_d = *reinterpret_cast<const uint2*>(ex + A.off[kDownRs] + (uint64_t)(tdd * 16 + 4 * (lane >> 4)) * 2);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  const bool has_down = g < dtiles && wv < NU;
+  // the waves that write the SwiGLU output drain their memory counter before the release
+  const uint32_t epi_waves = (groups * 16 * M + 63) / 64;
+  load_gu(rounds > 0 ? gu_item(0) : ~0u);
+  // (SINGLE: rounds <= 1 always, so no branch around the load for the wait tracking to merge)
+  if (PREF && (SINGLE || rounds <= 1)) load_down(has_down, g, wv);
+  AFFX_TRACE(2);
+
+  // ---- 3. activation terms and codebook copies into LDS, from the registers loaded up front
+#pragma unroll
+  for (int j = 0; j < NP; ++j) {
+    const uint32_t p = wv + (uint32_t)j * kFW;
+    if (p < M * nst) {
+      const uint32_t t = p / nst, Sx = p % nst;
+      float mx = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(xr[j][i].x), fabsf(xr[j][i].y)), fmaxf(fabsf(xr[j][i].z), fabsf(xr[j][i].w))));
+      mx = wave_max(mx);
+      // amax * 2^sigma in [128, 256): below E4M3's 448
+      const int sigma = mx > 0.f ? 7 - ilogbf(mx) : 0;
+      if (lane == 0) sigma_l[t * 4 + Sx] = sigma;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t q0, q1, q2;
+        split3x4(ldexpf(xr[j][i].x, sigma), ldexpf(xr[j][i].y, sigma), ldexpf(xr[j][i].z, sigma),
+                 ldexpf(xr[j][i].w, sigma), q0, q1, q2);
+        const uint32_t col = (Sx * 4 + i) * kXqChunk + 4 * lane;
+        *reinterpret_cast<uint32_t*>(xq + (t * 3 + 0) * kXqRow + col) = q0;
+        *reinterpret_cast<uint32_t*>(xq + (t * 3 + 1) * kXqRow + col) = q1;
+        *reinterpret_cast<uint32_t*>(xq + (t * 3 + 2) * kXqRow + col) = q2;
+      }
+    }
+  }
+  if (tid < 64) reinterpret_cast<uint32_t*>(zero_l)[tid] = 0u;
+  build_lut<KC>(tbl, cbv, tid);
+  __syncthreads();  // activation terms and codebook copies visible
+
+  // B source of this lane for gate/up: its (token, term) row at this wave's segment
+  const uint32_t c = lane & 15, kg = lane >> 4;
+  const uint8_t* bsrc[CG];
+
+  // ---- 4. gate/up rounds -----------------------------------------------------------------------
+  const uint32_t n_rounds = SINGLE ? (rounds > 0 ? 1u : 0u) : rounds;
+  for (uint32_t rho = 0; rho < n_rounds; ++rho) {
+    const uint32_t item = gu_item(rho);
+    if (rho > 0) {
+      load_gu(item);
+      if (PREF && rho == rounds - 1) load_down(has_down, g, wv);
+    }
+    v4f acc[2][CG];
+#pragma unroll
+    for (int mm = 0; mm < 2; ++mm)
+#pragma unroll
+      for (int cg = 0; cg < CG; ++cg) acc[mm][cg] = v4f{0.f, 0.f, 0.f, 0.f};
+    uint32_t mask = 0;
+    if (item != ~0u) {
+      const uint32_t slot = item / rt_per;
+      mask = __builtin_amdgcn_readfirstlane(slot_mask[slot]);
+#pragma unroll
+      for (int cg = 0; cg < CG; ++cg) {
+        const uint32_t t = cg * 5 + c / 3, tau = c % 3;
+        const bool valid = c < 15 && t < M && ((mask >> t) & 1u);
+        bsrc[cg] = valid ? xq + (t * 3 + tau) * kXqRow + (S * 4 + kg) * kXqChunk : zero_l;
+      }
+      uint32_t rg[8], ru[8];
+      uint32_t bg[2], bu[2];
+      pin_step(ug, 0);
+      pin_step(uu, 0);
+      lut_lookup_step<KC>(ug, lds, copy4, 0, rg, bg);
+      lut_lookup_step<KC>(uu, lds, copy4, 0, ru, bu);
+      v8i bc[CG];
+#pragma unroll
+      for (int cg = 0; cg < CG; ++cg) bc[cg] = b_step_lds(bsrc[cg], 0);
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        uint32_t ng[8], nu[8];
+        uint32_t nbg[2], nbu[2];
+        v8i bn[CG];
+        if (m < 7) {
+#pragma unroll
+          for (int cg = 0; cg < CG; ++cg) { AFFX_PIN(acc[0][cg]); AFFX_PIN(acc[1][cg]); }
+          pin_step(ug, m + 1);
+          pin_step(uu, m + 1);
+          lut_lookup_step<KC>(ug, lds, copy4, m + 1, ng, nbg);
+          lut_lookup_step<KC>(uu, lds, copy4, m + 1, nu, nbu);
+#pragma unroll
+          for (int cg = 0; cg < CG; ++cg) bn[cg] = b_step_lds(bsrc[cg], m + 1);
+        }
+        const v8i ag = lut_finish(rg, bg), au = lut_finish(ru, bu);
+#pragma unroll
+        for (int cg = 0; cg < CG; ++cg) {
+          acc[0][cg] = mfma(ag, bc[cg], acc[0][cg]);
+          acc[1][cg] = mfma(au, bc[cg], acc[1][cg]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (m < 7) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) { rg[i] = ng[i]; ru[i] = nu[i]; }
+          bg[0] = nbg[0]; bg[1] = nbg[1]; bu[0] = nbu[0]; bu[1] = nbu[1];
+#pragma unroll
+          for (int cg = 0; cg < CG; ++cg) bc[cg] = bn[cg];
+        }
+      }
+    }
+    AFFX_TRACE(3);
+    if (item != ~0u && S == 0 && lane < 32) {
+      // opaque at the use: no conversion is hoisted next to the load (its wait would then cover
+      // every weight load issued before it)
+      uint32_t rv = rs_gu;
+      AFFX_PIN(rv);
+      rs_l[q * 32 + lane] = __uint_as_float(rv << 16);
+    }
+    // partial sums of this wave's segment, term-combined, at the segment's exponent:
+    // part[wave][mat][row][token]. Accumulator lane l, element v = D[4(l/16)+v][l%16].
+#pragma unroll
+    for (int mm = 0; mm < 2; ++mm)
+#pragma unroll
+      for (int cg = 0; cg < CG; ++cg)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float val = fused_terms(acc[mm][cg][v]);
+          const uint32_t t = cg * 5 + c / 3;
+          if (item != ~0u && c < 15 && c % 3 == 0 && t < M)
+            part[((wv * 2 + mm) * 16 + 4 * kg + v) * M + t] = ldexpf(val, -sigma_l[t * 4 + S]);
+        }
+    __syncthreads();
+
+    // epilogue: thread (group, row, token) sums the group's segments in order, SwiGLU, E4M3 terms
+    // (up to 12 groups x 16 rows x 8 tokens: two passes of the workgroup)
+    uint32_t et0 = tid;
+    AFFX_PIN(et0);  // epilogue index math stays after the compute (no live range across it)
+    // (a loop header here would make every wave with loads in flight wait for all of them, the
+    // down prefetch included: SINGLE, with at most 12 x 16 threads busy, takes one pass)
+    auto epilogue = [&](uint32_t et) {
+      const uint32_t qq = et / (16 * M), r = (et / M) % 16, t = et % M;
+      const uint32_t k = rho * groups + qq;
+      if (k < my_items) {
+        const uint32_t it = g + A.n_wg * k, slot = it / rt_per, rt = it % rt_per;
+        if ((slot_mask[slot] >> t) & 1u) {
+          float s2[2];
+#pragma unroll
+          for (int mm = 0; mm < 2; ++mm) {
+            float sum = 0.f;
+            for (uint32_t sg = 0; sg < nst; ++sg) sum += part[(((qq * nst + sg) * 2 + mm) * 16 + r) * M + t];
+            s2[mm] = sum;
+          }
+          const uint32_t row = rt * 16 + r;
+          float gg = s2[0] * rs_l[qq * 32 + r], uu2 = s2[1] * rs_l[qq * 32 + 16 + r];
+          // SwiGLU with the asymmetric clamp: src/engine/ops.cpp:47-60
+          const float Lm = A.limit;
+          gg = (Lm < gg) ? Lm : gg;
+          const float lo = (-Lm < uu2) ? uu2 : -Lm;
+          uu2 = (lo < Lm) ? lo : Lm;
+          const float a = (gg / (1.0f + expf(-gg))) * uu2;
+          uint32_t b0, b1, b2;
+          split3(ldexpf(a, A.sigma_a), b0, b1, b2);
+          // device-coherent stores (written through to the memory side before they complete)
+          uint8_t* dst = A.aq + ((uint64_t)(slot * M + t) * kTerms) * A.inter + row;
+          __hip_atomic_store(dst, (uint8_t)b0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(dst + A.inter, (uint8_t)b1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(dst + 2 * (uint64_t)A.inter, (uint8_t)b2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    };
+    if constexpr (SINGLE) {
+      if (et0 < groups * 16 * M) epilogue(et0);
+    } else {
+      for (uint32_t et = et0; et < groups * 16 * M; et += kFT) epilogue(et);
+    }
+    // publish: every wave that stored drains its memory counter (its device-coherent stores have
+    // completed), the barrier orders that before thread 0's counter update. No release fence: its
+    // L2 write-back, once per workgroup and serialised per L2, costs microseconds, and nothing
+    // else written here is read by other workgroups.
+    if (wv < epi_waves) __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+      const uint32_t done = my_items - rho * groups < groups ? my_items - rho * groups : groups;
+      __hip_atomic_fetch_add(&A.sync[0], done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+
+  AFFX_TRACE(4);
+  // ---- 5. wait for every gate/up item, then the down tiles ----------------------------------------
+  if (g < dtiles) {
+    if (tid == 0) {
+      uint32_t n = 0;
+      while (__hip_atomic_load(&A.sync[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < NI) {
+        if (++n > kSpinLimit) {
+          __hip_atomic_fetch_or(&A.sync[2], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
+    __syncthreads();
+    AFFX_TRACE(5);
+
+    const uint32_t rg4 = lane >> 4;
+    for (uint32_t td = g; td < dtiles; td += A.n_wg) {
+      float yacc[CG][4];
+#pragma unroll
+      for (int cg = 0; cg < CG; ++cg)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) yacc[cg][v] = 0.f;
+#pragma unroll 1
+      for (uint32_t u = wv; u < (SINGLE ? (wv < NU ? wv + 1 : 0u) : NU); u += kFW) {
+        if (!(PREF && td == g && u == wv)) load_down(true, td, u);  // else loaded during gate/up
+        const uint32_t slot = u / nsi, S2 = u % nsi;
+        const uint32_t e = __builtin_amdgcn_readfirstlane(slot_expert[slot]);
+        const uint32_t mask = __builtin_amdgcn_readfirstlane(slot_mask[slot]);
+        const uint8_t* ex = A.base + (uint64_t)e * A.stride;
+        const BSrc<CG> b = b_source<CG>(A.aq + (uint64_t)slot * M * kTerms * A.inter, A.inter,
+                                        (uint64_t)S2 * kTileCols, lane, M, mask, A.zeros);
+        uint2 rsv = rs_d;
+        AFFX_PIN(rsv.x);  // opaque at the use (see the gate/up row scales)
+        AFFX_PIN(rsv.y);
+        __builtin_amdgcn_sched_barrier(0);
+        v4f acc[CG];
+#pragma unroll
+        for (int cg = 0; cg < CG; ++cg) acc[cg] = v4f{0.f, 0.f, 0.f, 0.f};
+        uint32_t raw[8];
+        uint32_t bv[2];
+        pin_step(ud, 0);
+        lut_lookup_step<KC>(ud, lds, copy4, 0, raw, bv);
+        v8i bc[CG];
+#pragma unroll
+        for (int cg = 0; cg < CG; ++cg) bc[cg] = b_step(b.p[cg], 0);
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+          uint32_t nraw[8];
+          uint32_t nbv[2];
+          v8i bn[CG];
+          if (m < 7) {
+            // the previous step's MFMA stays ahead of these reads (else the compiler sinks every
+            // MFMA below all eight steps' table reads and holds them all in registers)
+#pragma unroll
+            for (int cg = 0; cg < CG; ++cg) AFFX_PIN(acc[cg]);
+            pin_step(ud, m + 1);
+            lut_lookup_step<KC>(ud, lds, copy4, m + 1, nraw, nbv);
+#pragma unroll
+            for (int cg = 0; cg < CG; ++cg) bn[cg] = b_step(b.p[cg], m + 1);
+          }
+          const v8i a = lut_finish(raw, bv);
+#pragma unroll
+          for (int cg = 0; cg < CG; ++cg) acc[cg] = mfma(a, bc[cg], acc[cg]);
+          __builtin_amdgcn_sched_barrier(0);
+          if (m < 7) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) raw[i] = nraw[i];
+            bv[0] = nbv[0]; bv[1] = nbv[1];
+#pragma unroll
+            for (int cg = 0; cg < CG; ++cg) bc[cg] = bn[cg];
+          }
+        }
+        const float rs[4] = {__uint_as_float(rsv.x << 16), __uint_as_float(rsv.x & 0xFFFF0000u),
+                             __uint_as_float(rsv.y << 16), __uint_as_float(rsv.y & 0xFFFF0000u)};
+#pragma unroll
+        for (int cg = 0; cg < CG; ++cg) {
+          const uint32_t t = cg * 5 + c / 3;
+          const bool mine = c < 15 && (c % 3) == 0 && t < M && ((mask >> t) & 1u);
+          const float wt = mine ? ldexpf(slot_w[slot * M + t], -A.sigma_a) : 0.f;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const float val = fused_terms(acc[cg][v]);
+            if (mine) yacc[cg][v] += val * rs[v] * wt;
+          }
+        }
+      }
+      AFFX_TRACE(6);
+      // per-wave partials [wave][row][token], summed over the waves in order
+#pragma unroll
+      for (int cg = 0; cg < CG; ++cg) {
+        const uint32_t t = cg * 5 + c / 3;
+        if (c < 15 && c % 3 == 0 && t < M)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) part[(wv * 16 + 4 * rg4 + v) * M + t] = yacc[cg][v];
+      }
+      __syncthreads();
+      uint32_t et = tid;
+      AFFX_PIN(et);
+      if (et < 16 * M) {
+        const uint32_t r = et / M, t = et % M;
+        float sum = 0.f;
+        for (int qw = 0; qw < kFW; ++qw) sum += part[(qw * 16 + r) * M + t];
+        float* dst = A.y + (uint64_t)t * A.yts + (uint64_t)(td * 16 + r) * A.yds;
+        *dst = A.accumulate ? *dst + sum : sum;
+      }
+      __syncthreads();
+    }
+  }
+
+  AFFX_TRACE(7);
+  // ---- 6. the last workgroup out resets the counters for the next launch ---------------------------
+  if (tid == 0) {
+    // (every workgroup got here after its own wait on sync[0]: the last one may clear it)
+    const uint32_t old = __hip_atomic_fetch_add(&A.sync[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (old == A.n_wg - 1) {
+      __hip_atomic_store(&A.sync[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&A.sync[1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+}  // namespace affx
+
+// ------------------------------------------------------------------------------------------------
+// host side
+// ------------------------------------------------------------------------------------------------
+using namespace affx;
+
+namespace {
+
+struct FusedVariant {
+  const void* fn;
+  uint32_t kc, maxm;
+  int max_wg;  // workgroups the device holds at once (0: cannot run)
+  bool ready;
+};
+
+constexpr int kMaxDev = 64;
+std::mutex g_fused_mu;
+FusedVariant g_fused[kMaxDev][4];
+
+// variants: 0 M = 1 in one pass (16 codebook copies), 1 M = 1 in rounds, 2 M <= 5 (8 copies),
+// 3 M <= 8 (4 copies, 2 column groups)
+int fused_variant(uint32_t M, bool single) { return M == 1 ? (single ? 0 : 1) : M <= 5 ? 2 : 3; }
+
+int fused_prepare(int dev, int v, FusedVariant* out) {
+  std::lock_guard<std::mutex> lk(g_fused_mu);
+  FusedVariant& f = g_fused[dev][v];
+  if (!f.ready) {
+    static const void* fns[4] = {(const void*)decode_fused_kernel<1, 16, 1, true>,
+                                 (const void*)decode_fused_kernel<1, 16, 1, false>,
+                                 (const void*)decode_fused_kernel<1, 8, 5, false>,
+                                 (const void*)decode_fused_kernel<2, 4, 8, false>};
+    static const uint32_t kcs[4] = {16, 16, 8, 4}, maxms[4] = {1, 1, 5, 8};
+    f.fn = fns[v];
+    f.kc = kcs[v];
+    f.maxm = maxms[v];
+    const uint32_t lds = fused_lds(f.kc, f.maxm).total;
+    int rc = check_hip(hipFuncSetAttribute(f.fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+                       "hipFuncSetAttribute(fused decode)");
+    if (rc) return rc;
+    int per_cu = 0, cus = 0;
+    rc = check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f.fn, kFT, lds),
+                   "hipOccupancyMaxActiveBlocksPerMultiprocessor");
+    if (rc) return rc;
+    rc = check_hip(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev),
+                   "hipDeviceGetAttribute");
+    if (rc) return rc;
+    f.max_wg = per_cu * cus;
+    f.ready = true;
+  }
+  *out = f;
+  return AFFX_OK;
+}
+
+}  // namespace
+
+extern "C" int affx_expert_ffn_decode(const affx_layer* L, const float* x, uint64_t x_ts,
+                                      uint64_t x_ds, uint32_t M, const uint32_t* sel, const float* w,
+                                      uint32_t K, float* y, uint64_t y_ts, uint64_t y_ds,
+                                      int accumulate, void* ws, size_t ws_bytes, void* stream) {
+  if (!x || !sel || !w || !y) return set_error(AFFX_ERR_ARG, "ffn_decode: null pointer");
+  DecodeWs lay;
+  int rc = decode_check(L, M, K, ws, ws_bytes, &lay);
+  if (rc) return rc;
+  if ((uint64_t)M * K > (uint64_t)kPlanRoutes)
+    return set_error(AFFX_DECLINED, "ffn_decode: m_tokens * top_k must be <= %d", kPlanRoutes);
+  int dev = 0;
+  rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
+  if (rc) return rc;
+  if (dev < 0 || dev >= kMaxDev) return set_error(AFFX_ERR_ARG, "ffn_decode: device id %d", dev);
+  const uint32_t nst = L->hidden / kTileCols, groups = kFW / nst;
+  const uint32_t slots_max = M * K < L->n_experts ? M * K : L->n_experts;
+  const uint32_t items_max = slots_max * (L->inter / kTileRows);
+  const uint32_t dtiles = L->hidden / kTileRows;
+  const uint32_t units_max = slots_max * (L->inter / kTileCols);
+  uint32_t want = (items_max + groups - 1) / groups;
+  if (want < dtiles) want = dtiles;
+  FusedVariant f;
+  rc = fused_prepare(dev, fused_variant(M, false), &f);  // any variant: the grid capacity
+  if (rc) return rc;
+  if (f.max_wg <= 0)
+    return affx_decode_staged(L, x, x_ts, x_ds, M, sel, w, K, y, y_ts, y_ds, accumulate, ws, ws_bytes, stream);
+  const uint32_t n_wg = want < (uint32_t)f.max_wg ? want : (uint32_t)f.max_wg;
+  // one pass: every gate/up item has its own wave group, every down unit of a tile its own wave
+  const bool single = items_max <= groups * n_wg && units_max <= (uint32_t)kFW;
+  const int v = fused_variant(M, single);
+  rc = fused_prepare(dev, v, &f);
+  if (rc) return rc;
+
+  FusedArgs A;
+  uint64_t off9[9];
+  affx_expert_layout(L->hidden, L->inter, off9, nullptr);
+  uint8_t* base = (uint8_t*)ws;
+  A.base = (const uint8_t*)L->base;
+  A.stride = L->stride;
+  for (int i = 0; i < 9; ++i) A.off[i] = off9[i];
+  A.hidden = L->hidden;
+  A.inter = L->inter;
+  A.M = M;
+  A.K = K;
+  A.n_experts = L->n_experts;
+  A.n_wg = n_wg;
+  A.codebook = (const uint32_t*)L->codebook;
+  A.x = x;
+  A.xts = x_ts;
+  A.xds = x_ds;
+  A.sel = sel;
+  A.w = w;
+  A.aq = base + lay.aq;
+  A.zeros = base + lay.zeros;
+  A.sync = (uint32_t*)(base + lay.sync);
+  A.y = y;
+  A.yts = y_ts;
+  A.yds = y_ds;
+  A.accumulate = accumulate;
+  A.limit = L->swiglu_limit;
+  A.sigma_a = 7 - ilogbf(L->swiglu_limit * L->swiglu_limit);
+  const uint32_t lds = fused_lds(f.kc, M).total;
+  hipStream_t st = (hipStream_t)stream;
+  // the down B operand's unused columns read the workspace's zero run: zero in a zero-filled
+  // workspace and only ever rewritten with zeros (by the staged prep kernel)
+  switch (v) {
+    case 0: hipLaunchKernelGGL((decode_fused_kernel<1, 16, 1, true>), dim3(n_wg), dim3(kFT), lds, st, A); break;
+    case 1: hipLaunchKernelGGL((decode_fused_kernel<1, 16, 1, false>), dim3(n_wg), dim3(kFT), lds, st, A); break;
+    case 2: hipLaunchKernelGGL((decode_fused_kernel<1, 8, 5, false>), dim3(n_wg), dim3(kFT), lds, st, A); break;
+    default: hipLaunchKernelGGL((decode_fused_kernel<2, 4, 8, false>), dim3(n_wg), dim3(kFT), lds, st, A); break;
+  }
+  return check_launch("decode_fused_kernel");
+}

@@ -128,17 +128,24 @@ class DecodeWorkspace:
     def __init__(self, m_tokens: int, top_k: int, hidden: int = HIDDEN, inter: int = INTER,
                  device="cuda"):
         self.bytes = int(lib().affx_decode_workspace_size(m_tokens, top_k, hidden, inter))
-        self.buf = torch.empty(self.bytes, dtype=torch.uint8, device=device)
+        # zero-filled: the fused decode keeps its cross-workgroup counters in the first 256 bytes
+        # and expects them zero on first use (each launch leaves them zero again)
+        self.buf = torch.zeros(self.bytes, dtype=torch.uint8, device=device)
+
+    def error_flags(self) -> int:
+        """Nonzero if a fused decode launch on this workspace gave up waiting (bounded spin)."""
+        return int(self.buf[8:12].view(torch.int32).item())
 
 
 def expert_ffn_decode(pool: ExpertPool, x: torch.Tensor, sel: torch.Tensor, w: torch.Tensor,
                       y: torch.Tensor | None = None, accumulate: bool = False,
                       workspace: DecodeWorkspace | None = None, stream=None,
-                      dim_major: bool = False) -> torch.Tensor:
+                      dim_major: bool = False, staged: bool = False) -> torch.Tensor:
     """y[t] (+)= sum_j w[t,j] * FFN_{sel[t,j]}(x[t]) for M <= 8 tokens.
 
     x: f32 [M, hidden] (token-major) or, with dim_major, [hidden, M] (the engine's d_x arena).
     sel: int32/uint32 [M, k] device; w: f32 [M, k] device.
+    staged: the three-launch form (affx_decode_staged) instead of the one persistent launch.
     """
     if dim_major:
         hidden, M = x.shape
@@ -154,10 +161,10 @@ def expert_ffn_decode(pool: ExpertPool, x: torch.Tensor, sel: torch.Tensor, w: t
     L = pool.layer()
     sel = sel.contiguous()
     w = w.contiguous()
-    check(lib().affx_expert_ffn_decode(C.byref(L), x.data_ptr(), xts, xds, M, sel.data_ptr(),
-                                       w.data_ptr(), k, y.data_ptr(), yts, yds, int(accumulate),
-                                       ws.buf.data_ptr(), ws.bytes, _stream(stream)),
-          "affx_expert_ffn_decode")
+    fn = lib().affx_decode_staged if staged else lib().affx_expert_ffn_decode
+    check(fn(C.byref(L), x.data_ptr(), xts, xds, M, sel.data_ptr(), w.data_ptr(), k, y.data_ptr(), yts,
+             yds, int(accumulate), ws.buf.data_ptr(), ws.bytes, _stream(stream)),
+          "affx_decode_staged" if staged else "affx_expert_ffn_decode")
     return y
 
 

@@ -12,8 +12,10 @@ library's own quantiser against the config-1 codebook the reference fitted):
   c3         M = 8 speculative-decode tokens per layer, same stack; bytes = distinct experts x stride.
   prefill    C4: 4096 tokens x hidden 4096 (bf16), Zipf(1.1) routes, one layer; TFLOP/s counts
              2*(2*I*H + H*I) per (token, expert) slot = 1.2370e12 FLOP per layer.
-  roofline   the dominant decode kernel (gate/up): its algorithmic bytes per launch over its
-             average duration, timed with HIP events on the launch stream.
+  roofline   the dominant decode kernel (the persistent per-layer launch): its algorithmic bytes
+             per launch (6 x 9,060,352 B) over its average duration, timed with HIP events on the
+             launch stream (the C5 graph holds only these launches); traffic = HBM bytes per
+             launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary.
   cpu_baseline  the reference's own CPU path (oracle/_ref/libaffref.so, else the oracle) on a
              bounded sample: one token through the 6 routed experts of layer 0.
 
@@ -113,6 +115,8 @@ def main() -> int:
     ap.add_argument("--prefill-steps", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["decode", "all"], default="all")
+    ap.add_argument("--staged", action="store_true",
+                    help="also time the three-launch (staged) decode for comparison")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run a plain 1 GiB device copy (the reference point for HBM counters)")
     args = ap.parse_args()
@@ -181,34 +185,32 @@ def main() -> int:
     log(f"C5 decode: {ms1 * 1e3:.1f} us/token over {L} layers -> {gbs:.0f} GB/s "
         f"({100 * gbs * 1e9 / HBM_PEAK:.1f}% of HBM peak)")
 
-    # ---- the dominant kernel: gate/up, timed with events on its stream ---------------------------
-    # each layer gets its own workspace so that all preps can run first; then the gate/up kernels
-    # of all layers go back to back between two events (the average includes the dispatch gap
-    # between consecutive launches, as a kernel trace's per-dispatch durations do not)
-    s = torch.cuda.current_stream()
-    wsl = [ax.DecodeWorkspace(1, K) for _ in range(L)]
-    for l in range(L):
-        sel, w = routes1[l]
-        check(lib().affx_decode_prepare(C.byref(layers[l]), x1.data_ptr(), H, 1, 1, sel.data_ptr(),
-                                        w.data_ptr(), K, wsl[l].buf.data_ptr(), wsl[l].bytes, s.cuda_stream),
-              "prep")
-    durs = []
-    for rep in range(6):
-        st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        st.record(s)
-        for l in range(L):
-            check(lib().affx_decode_gateup(C.byref(layers[l]), 1, K, wsl[l].buf.data_ptr(), wsl[l].bytes,
-                                           s.cuda_stream), "gateup")
-        en.record(s)
-        torch.cuda.synchronize()
-        if rep:
-            durs.append(st.elapsed_time(en) / L)
-    del wsl
-    gu_us = float(np.median(durs)) * 1e3
-    _, off, size = ax.expert_layout()
-    gu_bytes = K * sum(size[p] for p in (0, 1, 2, 3, 4, 5))
-    gu_achieved = gu_bytes / (gu_us * 1e-6) / 1e9
-    log(f"gate/up kernel: {gu_us:.2f} us/launch avg, {gu_bytes} B -> {gu_achieved:.0f} GB/s")
+    # ---- the dominant kernel: the persistent decode launch, one per layer ------------------------
+    # the C5 graph holds nothing but the L launches of decode_fused_kernel on the stream that the
+    # events above were recorded on, so its per-launch duration is the graph time over L
+    fu_us = ms1 * 1e3 / L
+    fu_bytes = K * STRIDE
+    fu_achieved = fu_bytes / (fu_us * 1e-6) / 1e9
+    log(f"decode_fused_kernel: {fu_us:.2f} us/launch avg, {fu_bytes} B -> {fu_achieved:.0f} GB/s")
+    traffic = None
+    tpath = os.path.join(HERE, "profiles", "decode_fused_c5_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    if args.staged:
+        def staged_step():
+            st = torch.cuda.current_stream().cuda_stream
+            for l in range(L):
+                sel, w = routes1[l]
+                check(lib().affx_decode_staged(C.byref(layers[l]), x1.data_ptr(), H, 1, 1, sel.data_ptr(),
+                                               w.data_ptr(), K, y1.data_ptr() + 4 * H * l, H, 1, 0,
+                                               ws1.buf.data_ptr(), ws1.bytes, st), "staged")
+            return y1
+        mss, _, _ = time_graph(torch, staged_step, args.steps, args.warmup)
+        assert torch.equal(y1, eager1), "staged decode differs from the fused decode"
+        log(f"C5 staged (3 launches per layer): {mss * 1e3:.1f} us/token -> "
+            f"{bytes_tok / (mss * 1e-3) / 1e9:.0f} GB/s")
 
     # ---- C3: M = 8 tokens ------------------------------------------------------------------------
     ms8, _, _ = time_graph(torch, lambda: decode_step(x8, routes8, ws8, y8, 8), args.steps, args.warmup)
@@ -234,10 +236,10 @@ def main() -> int:
                    "hbm_fraction": round(gbs * 1e9 / HBM_PEAK, 4),
                    "tokens_per_s_expert_only": round(1e3 / ms1, 1),
                    "bytes_per_token": bytes_tok},
-        "roofline": {"bound": "hbm", "achieved": round(gu_achieved, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                     "frac": round(gu_achieved * 1e9 / HBM_PEAK, 4), "traffic": None,
-                     "kernel": "decode_gateup_kernel<1>", "bytes_per_launch": gu_bytes,
-                     "us_per_launch": round(gu_us, 3)},
+        "roofline": {"bound": "hbm", "achieved": round(fu_achieved, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                     "frac": round(fu_achieved * 1e9 / HBM_PEAK, 4), "traffic": traffic,
+                     "kernel": "decode_fused_kernel<1,16,1,true>", "bytes_per_launch": fu_bytes,
+                     "us_per_launch": round(fu_us, 3)},
         "c3": {"gb_per_s": round(gbs8, 1), "us_per_step": round(ms8 * 1e3, 2),
                "distinct_experts_per_layer": round(distinct / L, 2)},
     }

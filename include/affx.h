@@ -112,7 +112,11 @@ int affx_dequant_matrix(const affx_matrix* m, const void* codebook, float* out, 
 
 /* ---- decode: M <= 8 tokens, fused gate/up -> SwiGLU -> down -> weighted combine ------------- */
 
-/* Workspace bytes affx_expert_ffn_decode needs for m tokens with top-k routing. */
+/* Workspace bytes affx_expert_ffn_decode needs for m tokens with top-k routing. The workspace
+ * must be zero-filled before its first use: its first 256 bytes hold the fused decode's
+ * cross-workgroup counters, which every launch leaves zero again (no memset per call, safe under
+ * graph capture). Word 2 (bytes 8..11) becomes nonzero if a launch ever gave up waiting for the
+ * other workgroups (its output is then invalid); it is sticky until the caller clears it. */
 size_t affx_decode_workspace_size(uint32_t m_tokens, uint32_t top_k, uint32_t hidden,
                                   uint32_t inter);
 
@@ -125,7 +129,10 @@ size_t affx_decode_workspace_size(uint32_t m_tokens, uint32_t top_k, uint32_t hi
  *  reference's plan does, src/gpu/moe_plan.h:146). w: device f32 [m_tokens][top_k].
  * Replaces the batch-1 GPU FFN expert_ffn_hip (src/gpu/expert_kernel.hip:2737-2808,
  * expert_kernel_hip.h:273) and the narrow NT=1 arm of the W8A8 GEMM that the engine's decode uses
- * (expert_kernel.hip:3049-3058). Three kernels, no host synchronisation. */
+ * (expert_kernel.hip:3049-3058). One persistent launch (routing plan, activation split, gate/up +
+ * SwiGLU, down + combine, with one agent-scope counter between gate/up and down); it needs every
+ * workgroup of its grid resident at once, so the grid is sized to the device, and it falls back to
+ * the staged launches below when the device cannot hold it. No host synchronisation. */
 int affx_expert_ffn_decode(const affx_layer* layer, const float* x, uint64_t x_tok_stride,
                            uint64_t x_dim_stride, uint32_t m_tokens, const uint32_t* sel,
                            const float* w, uint32_t top_k, float* y, uint64_t y_tok_stride,
@@ -147,6 +154,15 @@ int affx_decode_gateup(const affx_layer* layer, uint32_t m_tokens, uint32_t top_
 int affx_decode_down(const affx_layer* layer, uint32_t m_tokens, uint32_t top_k, float* y,
                      uint64_t y_tok_stride, uint64_t y_dim_stride, int accumulate,
                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* affx_expert_ffn_decode as the three staged launches above, in one call (same arguments; no
+ * counterpart of its own in the reference: it is the staged form of the same decode, for
+ * comparison and for devices that cannot hold the persistent grid). */
+int affx_decode_staged(const affx_layer* layer, const float* x, uint64_t x_tok_stride,
+                       uint64_t x_dim_stride, uint32_t m_tokens, const uint32_t* sel,
+                       const float* w, uint32_t top_k, float* y, uint64_t y_tok_stride,
+                       uint64_t y_dim_stride, int accumulate, void* workspace,
+                       size_t workspace_bytes, void* stream);
 
 /* ---- prefill: grouped GEMM over an expert-sorted slot list ---------------------------------- */
 

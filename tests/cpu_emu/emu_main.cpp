@@ -1,7 +1,8 @@
 // Runs libaffx's kernels on the CPU (see hip/hip_runtime.h) against the C oracle.
 // Test infrastructure: built with AddressSanitizer by tests/test_cpu_emulation.py.
 //
-//   emu_main decode  hidden inter n_experts M K seed      -> rel_l2 of the decode FFN
+//   emu_main decode  hidden inter n_experts M K seed [staged] -> rel_l2 of the decode FFN (the
+//                    fused launch, also checked equal to the staged launches; `staged` alone)
 //   emu_main grouped hidden inter n_experts T K seed lo   -> rel_l2 of the grouped FFN
 //   emu_main quant   rows cols seed                       -> planes bit-exact vs the oracle
 //   emu_main dequant hidden inter seed                    -> dequant bit-exact vs the oracle
@@ -16,6 +17,7 @@ thread_local EmuBlock* emu_blk;
 #define AFFX_PIN(x) ((void)0)
 #include "../../affinity_amd/csrc/affx_layout.hip"
 #include "../../affinity_amd/csrc/affx_decode.hip"
+#include "../../affinity_amd/csrc/affx_fused.hip"
 #include "../../affinity_amd/csrc/affx_quant.hip"
 #include "../../affinity_amd/csrc/affx_grouped.hip"
 
@@ -122,14 +124,29 @@ int run_decode(int argc, char** argv) {
   routes(rng, M, K, n, sel, w);
   if (M > 1) sel[K - 1] = n + 7;  // a padding id
   affx_layer abi = L.abi();
+  const bool staged_only = argc > 8 && std::string(argv[8]) == "staged";
   const size_t wsb = affx_decode_workspace_size(M, K, hidden, inter);
-  std::vector<uint8_t> ws(wsb);
-  const int rc = affx_expert_ffn_decode(&abi, x.data(), hidden, 1, M, sel.data(), w.data(), K, y.data(),
-                                        hidden, 1, 0, ws.data(), wsb, nullptr);
+  std::vector<uint8_t> ws(wsb, 0), ws2(wsb, 0);
+  std::vector<float> y2(M * hidden, 0.f);
+  int rc = affx_decode_staged(&abi, x.data(), hidden, 1, M, sel.data(), w.data(), K, y2.data(), hidden, 1, 0,
+                              ws2.data(), wsb, nullptr);
+  bool same = true;
+  if (!staged_only && rc == 0) {
+    // twice on one workspace: the second launch relies on the first leaving its counters zero
+    for (int rep = 0; rep < 2 && rc == 0; ++rep)
+      rc = affx_expert_ffn_decode(&abi, x.data(), hidden, 1, M, sel.data(), w.data(), K, y.data(), hidden, 1, 0,
+                                  ws.data(), wsb, nullptr);
+    uint32_t sync[3];
+    memcpy(sync, ws.data(), sizeof(sync));
+    same = memcmp(y.data(), y2.data(), y.size() * 4) == 0 && sync[0] == 0 && sync[1] == 0 && sync[2] == 0;
+    printf("fused: identical to staged=%d counters=%u,%u,%u\n", (int)same, sync[0], sync[1], sync[2]);
+  } else {
+    y = y2;
+  }
   L.oracle(x.data(), sel.data(), w.data(), M, K, yref.data());
   const double e = rel_l2(y, yref);
-  printf("decode rc=%d rel_l2=%.3e\n", rc, e);
-  return rc == 0 && e <= 1e-3 ? 0 : 1;
+  printf("decode rc=%d rel_l2=%.3e %s\n", rc, e, rc ? affx_last_error() : "");
+  return rc == 0 && same && e <= 1e-3 ? 0 : 1;
 }
 
 int run_grouped(int argc, char** argv) {

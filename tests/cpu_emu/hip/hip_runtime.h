@@ -1,6 +1,8 @@
 // CPU emulation of the HIP surface libaffx's kernels use (test infrastructure, never shipped).
 //
-// A kernel launch runs one workgroup at a time with one std::thread per work-item; __syncthreads
+// A kernel launch runs one workgroup at a time with one std::thread per work-item (launches with
+// dynamic LDS run all their workgroups at once instead, each with its own LDS block, as a kernel
+// that synchronises across workgroups needs them co-resident); __syncthreads
 // is a real block barrier and every cross-lane operation (shuffles, ballot, the MFMA) exchanges
 // values through per-wave slots between two wave barriers. Device memory is ordinary host memory,
 // so building with -fsanitize=address turns any out-of-bounds access of a kernel into an ASan
@@ -18,6 +20,8 @@
 #include <thread>
 #include <vector>
 #include <algorithm>
+#include <atomic>
+#include <mutex>
 
 #define __global__
 #define __device__
@@ -41,6 +45,12 @@ inline int hipGetDevice(int* d) { *d = 0; return 0; }
 struct hipDeviceProp_t { char gcnArchName[64]; int multiProcessorCount; };
 inline int hipGetDeviceProperties(hipDeviceProp_t* p, int) { strcpy(p->gcnArchName, "gfx950"); p->multiProcessorCount = 256; return 0; }
 inline int hipMemsetAsync(void* p, int v, size_t n, hipStream_t) { memset(p, v, n); return 0; }
+// device shape of the emulation: AFFX_EMU_CUS compute units (default 4), one resident workgroup each
+inline int emu_cus() { const char* e = getenv("AFFX_EMU_CUS"); return e ? atoi(e) : 4; }
+enum { hipDeviceAttributeMultiprocessorCount = 1, hipFuncAttributeMaxDynamicSharedMemorySize = 2 };
+inline int hipDeviceGetAttribute(int* v, int attr, int) { *v = attr == hipDeviceAttributeMultiprocessorCount ? emu_cus() : 0; return 0; }
+inline int hipFuncSetAttribute(const void*, int, int) { return 0; }
+inline int hipOccupancyMaxActiveBlocksPerMultiprocessor(int* n, const void*, int, size_t) { *n = 1; return 0; }
 
 struct uint2 { uint32_t x, y; };
 struct uint4 { uint32_t x, y, z, w; };
@@ -74,12 +84,21 @@ inline uint32_t __builtin_amdgcn_perm(uint32_t s0, uint32_t s1, uint32_t sel) {
   return out;
 }
 #define __builtin_amdgcn_sched_barrier(x) ((void)0)
+#define __builtin_amdgcn_s_sleep(x) std::this_thread::yield()
+#define __builtin_amdgcn_s_waitcnt(x) std::atomic_thread_fence(std::memory_order_seq_cst)
+// __hip_atomic_* are clang builtins on the host too; their scope constants are clang's
+#ifndef __HIP_MEMORY_SCOPE_AGENT
+#define __HIP_MEMORY_SCOPE_AGENT 4
+#endif
+#define __builtin_amdgcn_fence(order, scope) std::atomic_thread_fence(std::memory_order_seq_cst)
+template <typename T> inline T __builtin_amdgcn_readfirstlane(T v) { return v; }  // callers pass uniform values
 #define __builtin_nontemporal_load(p) (*(p))
 
 // ---- wave / block synchronisation ----
 struct EmuBlock {
   std::barrier<>* block_bar;
   std::barrier<>* wave_bar[16];
+  uint8_t* lds;                // dynamic LDS of the block (concurrent launches)
   uint64_t xfer[16][64][16];   // per-wave lane exchange (up to 16 x 32-bit words... in 64-bit slots)
 };
 extern thread_local EmuBlock* emu_blk;
@@ -87,6 +106,8 @@ inline void __syncthreads() { emu_blk->block_bar->arrive_and_wait(); }
 inline uint32_t emu_lane() { return threadIdx.x & 63; }
 inline uint32_t emu_wave() { return threadIdx.x >> 6; }
 inline void emu_wave_sync() { emu_blk->wave_bar[emu_wave()]->arrive_and_wait(); }
+#define __builtin_amdgcn_wave_barrier() emu_wave_sync()
+#define AFFX_DYN_LDS(name) uint8_t* name = emu_blk->lds
 
 template <typename T>
 inline T emu_exchange(T v, uint32_t src) {
@@ -123,6 +144,33 @@ inline float emu_e4m3(uint32_t b) {
   float f = e == 0 ? ldexpf(m / 8.0f, -6) : (e == 15 && m == 7 ? NAN : ldexpf(1.0f + m / 8.0f, e - 7));
   return s ? -f : f;
 }
+// hardware f32 -> E4M3 (OCP) conversion, round to nearest even, for the in-range values kernels
+// pass (|v| < 448)
+inline uint32_t emu_to_e4m3(float v) {
+  const uint32_t s = (__float_as_uint(v) >> 24) & 0x80u;
+  const float a = fabsf(v);
+  if (!(a < 448.f)) { fprintf(stderr, "cvt_pk_fp8_f32: out of range %g\n", v); abort(); }
+  if (a < 0.015625f) return s | (uint32_t)rintf(a * 512.0f);
+  const uint32_t au = __float_as_uint(a);
+  int e = (int)(au >> 23) - 127;
+  uint32_t m3 = (au >> 20) & 7u;
+  const uint32_t rem = au & 0xFFFFFu;
+  if (rem > 0x80000u || (rem == 0x80000u && (m3 & 1u))) { if (++m3 == 8u) { m3 = 0; ++e; } }
+  return s | ((uint32_t)(e + 7) << 3) | m3;
+}
+inline int __builtin_amdgcn_cvt_pk_fp8_f32(float a, float b, int old, bool hi) {
+  const uint32_t pair = emu_to_e4m3(a) | (emu_to_e4m3(b) << 8);
+  return (int)(hi ? (((uint32_t)old & 0xFFFFu) | (pair << 16)) : (((uint32_t)old & 0xFFFF0000u) | pair));
+}
+typedef float emu_v2f __attribute__((ext_vector_type(2)));
+inline emu_v2f __builtin_amdgcn_cvt_pk_f32_fp8(int w, bool hi) {
+  const uint32_t u = (uint32_t)w >> (hi ? 16 : 0);
+  emu_v2f r;
+  r.x = emu_e4m3(u & 0xFF);
+  r.y = emu_e4m3((u >> 8) & 0xFF);
+  return r;
+}
+
 inline emu_v4f __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(emu_v8i a, emu_v8i b, emu_v4f c, int, int, int, int, int, int) {
   uint32_t w = emu_wave(), l = emu_lane();
   for (int i = 0; i < 8; ++i) emu_blk->xfer[w][l][i] = (uint32_t)a[i] | ((uint64_t)(uint32_t)b[i] << 32);
@@ -142,9 +190,10 @@ inline emu_v4f __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(emu_v8i a, emu_v
   return d;
 }
 
-// ---- launch: one block at a time, blockDim.x threads created once per launch ----
+// ---- launch ----
+// Sequential: one block at a time, blockDim.x threads created once per launch.
 template <typename F, typename... Args>
-void emu_launch(F kernel, dim3 grid, dim3 block, Args... args) {
+void emu_launch_seq(F kernel, dim3 grid, dim3 block, Args... args) {
   gridDim = {grid.x, grid.y, grid.z};
   blockDim = {block.x, block.y, block.z};
   const uint32_t nt = block.x;
@@ -152,6 +201,7 @@ void emu_launch(F kernel, dim3 grid, dim3 block, Args... args) {
   std::barrier<> start(nt + 1), done(nt + 1), bb(nt);
   EmuBlock blk;
   blk.block_bar = &bb;
+  blk.lds = nullptr;
   std::vector<std::barrier<>*> wbs;
   for (uint32_t w = 0; w < (nt + 63) / 64; ++w) {
     wbs.push_back(new std::barrier<>(std::min<uint32_t>(64, nt - 64 * w)));
@@ -176,4 +226,44 @@ void emu_launch(F kernel, dim3 grid, dim3 block, Args... args) {
   for (auto& th : ts) th.join();
   for (auto* w : wbs) delete w;
 }
-#define hipLaunchKernelGGL(k, g, b, shm, s, ...) emu_launch(k, dim3(g), dim3(b), __VA_ARGS__)
+
+// Concurrent: every block at once (1-D grids), each with its own barriers and `shm` bytes of
+// dynamic LDS allocated as a separate heap block (ASan sees any access past it).
+template <typename F, typename... Args>
+void emu_launch_all(F kernel, dim3 grid, size_t shm, dim3 block, Args... args) {
+  gridDim = {grid.x, grid.y, grid.z};
+  blockDim = {block.x, block.y, block.z};
+  const uint32_t nt = block.x, nb = grid.x;
+  if (grid.y != 1 || grid.z != 1) { fprintf(stderr, "concurrent launch needs a 1-D grid\n"); abort(); }
+  std::vector<EmuBlock> blks(nb);
+  std::vector<std::barrier<>*> owned;
+  for (uint32_t b = 0; b < nb; ++b) {
+    owned.push_back(new std::barrier<>(nt));
+    blks[b].block_bar = owned.back();
+    for (uint32_t w = 0; w < (nt + 63) / 64; ++w) {
+      owned.push_back(new std::barrier<>(std::min<uint32_t>(64, nt - 64 * w)));
+      blks[b].wave_bar[w] = owned.back();
+    }
+    blks[b].lds = new uint8_t[shm];
+    memset(blks[b].lds, 0xA5, shm);  // LDS starts undefined on the device
+  }
+  std::vector<std::thread> ts;
+  for (uint32_t b = 0; b < nb; ++b)
+    for (uint32_t t = 0; t < nt; ++t)
+      ts.emplace_back([&, b, t]() {
+        emu_blk = &blks[b];
+        threadIdx = {t, 0, 0};
+        blockIdx = {b, 0, 0};
+        kernel(args...);
+      });
+  for (auto& th : ts) th.join();
+  for (auto& bl : blks) delete[] bl.lds;
+  for (auto* p : owned) delete p;
+}
+
+template <typename F, typename... Args>
+void emu_launch(F kernel, dim3 grid, dim3 block, size_t shm, Args... args) {
+  if (shm) emu_launch_all(kernel, grid, shm, block, args...);
+  else emu_launch_seq(kernel, grid, block, args...);
+}
+#define hipLaunchKernelGGL(k, g, b, shm, s, ...) emu_launch(k, dim3(g), dim3(b), (size_t)(shm), __VA_ARGS__)

@@ -30,8 +30,10 @@ def emu(tmp_path_factory):
     return str(d / "emu_main")
 
 
-def run(emu, *args, timeout=600):
-    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=0")
+def run(emu, *args, timeout=600, cus=4):
+    # cus: compute units of the emulated device; the fused decode sizes its grid (all workgroups
+    # resident, run concurrently here) to it
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=0", AFFX_EMU_CUS=str(cus))
     r = subprocess.run([emu, *map(str, args)], cwd=ROOT, capture_output=True, text=True,
                        timeout=timeout, env=env)
     out = r.stdout + r.stderr
@@ -44,12 +46,27 @@ def test_dequant_emulated(emu):
     assert "exact=1" in run(emu, "dequant", 1024, 1024, 1)
 
 
+# decode: the fused launch is checked bit-identical to the staged launches, its counters zero
+# after two launches on one workspace, and both against the oracle at 1e-3 relative L2
+
+
 def test_decode_emulated_m1(emu):
-    assert "rel_l2" in run(emu, "decode", 1024, 1024, 7, 1, 6, 1)
+    # 4 workgroups: gate/up in rounds, several output tiles per workgroup
+    assert "identical to staged=1" in run(emu, "decode", 1024, 1024, 7, 1, 6, 1)
+
+
+def test_decode_emulated_m1_single_pass(emu):
+    # 6 workgroups hold all 64 gate/up items: the straight-line batch-1 variant
+    assert "identical to staged=1" in run(emu, "decode", 1024, 1024, 5, 1, 1, 9, cus=6)
 
 
 def test_decode_emulated_m6_two_column_groups(emu):
-    assert "rel_l2" in run(emu, "decode", 2048, 1024, 5, 6, 2, 2)
+    assert "identical to staged=1" in run(emu, "decode", 2048, 1024, 5, 6, 2, 2)
+
+
+def test_decode_emulated_m8_wide_epilogue(emu):
+    # 12 gate/up groups x 16 rows x 8 tokens: the epilogue takes two passes of the workgroup
+    assert "identical to staged=1" in run(emu, "decode", 1024, 2048, 7, 8, 3, 6, cus=3)
 
 
 def test_quantizer_emulated(emu):

@@ -193,3 +193,87 @@ def test_decode_declines(ax, random_layer):
     w = torch.zeros((9, 6), device="cuda")
     with pytest.raises(AffxDeclined):
         ax.expert_ffn_decode(pool, x, sel, w)
+
+
+# ---- the persistent (fused) launch against the staged launches -----------------------------------
+
+def _random_device_pool(ax, c1_codebook, n, hidden, inter, seed):
+    """A pool filled on the device with arbitrary planes: random code/field bytes (any byte
+    permutation of random bytes is random, so they are written in device layout directly) and
+    bf16 row scales in [4e-4, 2e-3)."""
+    pool = ax.ExpertPool.empty(n, c1_codebook, hidden, inter)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    stride, off, size = ax.expert_layout(hidden, inter)
+    raw = pool.data.view(n, stride)
+    raw.copy_(torch.randint(0, 256, raw.shape, dtype=torch.uint8, device="cuda", generator=g))
+    for m in range(3):
+        o, sz = off[3 * m + 2], size[3 * m + 2]
+        rs = 4e-4 + 1.6e-3 * torch.rand((n, sz // 2), device="cuda", generator=g)
+        raw[:, o:o + sz] = rs.to(torch.bfloat16).view(torch.uint8)
+    torch.cuda.synchronize()
+    return pool
+
+
+@pytest.mark.parametrize("M,k", [(1, 6), (2, 6), (5, 6), (8, 6)])
+def test_fused_decode_identical_to_staged_full_layer(ax, orc, c1_codebook, M, k):
+    """The benchmark layer shape (256 experts, hidden 4096, inter 2048): the one-launch decode
+    equals the three staged launches bit for bit (same MFMA operands, same summation order),
+    leaves its counters zero, and (M = 1) matches the oracle."""
+    hidden, inter, n = 4096, 2048, 256
+    pool = _random_device_pool(ax, c1_codebook, n, hidden, inter, seed=17 + M)
+    rng = np.random.default_rng(100 + M)
+    x = torch.from_numpy((rng.standard_normal((M, hidden)) * 0.7).astype(np.float32)).cuda()
+    sel_np = np.stack([rng.choice(n, k, replace=False) for _ in range(M)]).astype(np.int32)
+    sel = torch.from_numpy(sel_np).cuda()
+    w = torch.from_numpy(rng.uniform(0.05, 1.0, (M, k)).astype(np.float32)).cuda()
+    ws = ax.DecodeWorkspace(M, k, hidden, inter)
+    ys = ax.expert_ffn_decode(pool, x, sel, w, staged=True, workspace=ax.DecodeWorkspace(M, k, hidden, inter))
+    y1 = ax.expert_ffn_decode(pool, x, sel, w, workspace=ws)
+    y2 = ax.expert_ffn_decode(pool, x, sel, w, workspace=ws)   # reuses the counters
+    torch.cuda.synchronize()
+    assert torch.equal(y1, ys) and torch.equal(y2, ys)
+    assert ws.error_flags() == 0
+    assert int(ws.buf[:8].view(torch.int32).abs().sum().item()) == 0, "counters not reset"
+    if M == 1:
+        # oracle on the six routed experts, brought back to container layout
+        stride, _, _ = ax.expert_layout(hidden, inter)
+        dev = pool.data.view(n, stride)[torch.from_numpy(sel_np[0].astype(np.int64)).cuda()].cpu().numpy()
+        from affinity_amd._lib import lib
+        cont = np.zeros_like(dev)
+        for j in range(k):
+            assert lib().affx_expert_from_device_layout(dev[j].ctypes.data, cont[j].ctypes.data, hidden, inter) == 0
+        ref = _oracle_ffn(orc, cont, orc.unpack_codebook(c1_codebook), x.cpu().numpy(),
+                          np.arange(k, dtype=np.uint32)[None, :], w.cpu().numpy(), hidden, inter)
+        err = rel_l2(y1.cpu().numpy(), ref)
+        print(f"fused M=1 full layer rel_l2={err:.3e}")
+        assert err <= TOL
+
+
+def test_fused_decode_graph_replays(ax, c1_codebook):
+    """Captured in a HIP graph, the persistent decode replays to the eager result every time
+    (its counters are reset by the kernel itself, nothing is memset)."""
+    hidden, inter, n, k = 4096, 2048, 64, 6
+    pool = _random_device_pool(ax, c1_codebook, n, hidden, inter, seed=5)
+    rng = np.random.default_rng(6)
+    x = torch.from_numpy(rng.standard_normal((1, hidden)).astype(np.float32)).cuda()
+    sel = torch.from_numpy(rng.choice(n, k, replace=False).astype(np.int32)[None, :]).cuda()
+    w = torch.from_numpy(rng.uniform(0.1, 1.0, (1, k)).astype(np.float32)).cuda()
+    ws = ax.DecodeWorkspace(1, k, hidden, inter)
+    y = torch.zeros((1, hidden), device="cuda")
+    ax.expert_ffn_decode(pool, x, sel, w, y=y, workspace=ws)
+    torch.cuda.synchronize()
+    eager = y.clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            ax.expert_ffn_decode(pool, x, sel, w, y=y, workspace=ws, stream=s)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        y.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager)
+    assert ws.error_flags() == 0
