@@ -67,14 +67,24 @@ struct DecodePlan {
 #ifndef AFFX_TRACE
 #define AFFX_TRACE(k) ((void)0)
 #endif
+#ifndef AFFX_TRACE_INIT
+#define AFFX_TRACE_INIT ((void)0)
+#endif
 
 // Dynamic LDS of a kernel (one byte array; the kernel carves it up).
 #ifndef AFFX_DYN_LDS
 #define AFFX_DYN_LDS(name) extern __shared__ __align__(16) uint8_t name[]
 #endif
 
-// Decode workspace: [sync 256 B][plan][zeros][xq][aq] (affx_decode.hip). The first 256 bytes hold
-// the fused decode's cross-workgroup counters: zero before first use, left zero by every launch.
+// Decode workspace: [sync][plan][zeros][xq][aq] (affx_decode.hip). The sync run holds the fused
+// decode's cross-workgroup state: a 256-byte header (dword 0: gate/up items published, dword 2:
+// error bits, dwords 8-9 reserved) and one release flag per waiting workgroup, 128 bytes apart so
+// that no two workgroups poll the same line. Zero before first use, left zero by every launch
+// (the error bits excepted).
+constexpr uint32_t kSyncHeader = 256;
+constexpr uint32_t kSyncFlagStride = 128;
+constexpr uint32_t kSyncFlags = 256;  // down-phase workgroups: output row tiles, hidden / 16 <= 256
+constexpr uint32_t kSyncBytes = kSyncHeader + kSyncFlags * kSyncFlagStride;
 struct DecodeWs {
   uint64_t sync, plan, zeros, xq, aq, total;
 };

@@ -1,7 +1,7 @@
 // Decode path (M <= 8 tokens, top-k routing): fused unpack -> codebook dequant -> fp8 MFMA for
 // gate/up -> SwiGLU -> down -> weighted combine. Three kernels, stream-ordered:
 //
-//   decode_prep    plan (distinct experts ascending, token masks, summed weights) and every
+//   decode_prep    plan (distinct experts by first occurrence, token masks, summed weights) and every
 //                  token's activation split into three exact-ish E4M3 terms (xq)
 //   decode_gateup  grid (row tile of inter, expert slot); 4 waves = 4 column super-segments;
 //                  gate and up tiles decoded from the packed codes through an LDS codebook and
@@ -87,46 +87,57 @@ __global__ void __launch_bounds__(256) decode_prep_kernel(const float* __restric
     return;
   }
 
-  // ---- the plan -------------------------------------------------------------------------------
-  __shared__ uint32_t present[AFFX_MAX_EXPERTS / 32];
-  __shared__ uint32_t prefix[AFFX_MAX_EXPERTS / 32 + 1];
+  // ---- the plan: the distinct experts of the batch in order of first occurrence in the route
+  // list (the persistent decode kernel uses the same order, so both give identical sums) ---------
+  __shared__ uint32_t sel_l[kMaxSlots];
+  __shared__ uint32_t first_l[kMaxSlots];
+  __shared__ uint32_t first_slot[kMaxSlots];  // slot of a first-occurrence route
+  __shared__ uint32_t rank_l[kMaxSlots];      // slot of every route
   __shared__ uint32_t slot_expert[kMaxSlots];
+  __shared__ uint32_t ns_l;
   if (tid < 64) reinterpret_cast<uint32_t*>(zeros)[tid] = 0u;  // the B source of unused columns
-  if (tid < AFFX_MAX_EXPERTS / 32) present[tid] = 0;
-  __syncthreads();
-  if (tid < M * K) {
+  const uint32_t R = M * K;
+  if (tid < R) {
     const uint32_t e = sel[tid];
-    if (e < n_experts) atomicOr(&present[e >> 5], 1u << (e & 31));
+    sel_l[tid] = e < n_experts ? e : ~0u;
+  }
+  __syncthreads();
+  if (tid < R) {
+    const uint32_t e = sel_l[tid];
+    bool dup = false;
+    for (uint32_t j = 0; j < tid; ++j) dup = dup || sel_l[j] == e;
+    first_l[tid] = e != ~0u && !dup;
   }
   __syncthreads();
   if (tid == 0) {
-    uint32_t s = 0;
-    for (int i = 0; i < AFFX_MAX_EXPERTS / 32; ++i) { prefix[i] = s; s += __popc(present[i]); }
-    prefix[AFFX_MAX_EXPERTS / 32] = s;
-    plan->n_slots = s;
+    uint32_t ns = 0;
+    for (uint32_t r = 0; r < R; ++r)
+      if (first_l[r]) { first_slot[r] = ns; slot_expert[ns] = sel_l[r]; ++ns; }
+    ns_l = ns;
+    plan->n_slots = ns;
     plan->m_tokens = M;
   }
   __syncthreads();
-  for (uint32_t e = tid; e < n_experts; e += 256) {
-    const uint32_t word = present[e >> 5];
-    if ((word >> (e & 31)) & 1u) {
-      const uint32_t slot = prefix[e >> 5] + __popc(word & ((1u << (e & 31)) - 1u));
-      slot_expert[slot] = e;
-      plan->expert[slot] = e;
-    }
+  if (tid < R) {
+    // a repeated expert takes the slot of its first occurrence
+    const uint32_t e = sel_l[tid];
+    uint32_t s = ~0u;
+    for (uint32_t j = 0; j <= tid && e != ~0u; ++j)
+      if (first_l[j] && sel_l[j] == e) s = first_slot[j];
+    rank_l[tid] = s;
   }
   __syncthreads();
   // one thread per slot: which tokens it serves, with the summed weight of every route to it
   // (a repeated expert counts once per route, summed in route order)
-  const uint32_t ns = prefix[AFFX_MAX_EXPERTS / 32];
+  const uint32_t ns = ns_l;
   if (tid < ns) {
-    const uint32_t e = slot_expert[tid];
+    plan->expert[tid] = slot_expert[tid];
     uint32_t mask = 0;
     for (uint32_t t = 0; t < kMaxTok; ++t) {
       float ws = 0.f;
       if (t < M)
         for (uint32_t j = 0; j < K; ++j)
-          if (sel[t * K + j] == e) { ws += w[t * K + j]; mask |= 1u << t; }
+          if (rank_l[t * K + j] == tid) { ws += w[t * K + j]; mask |= 1u << t; }
       plan->w[tid][t] = ws;
     }
     plan->tok_mask[tid] = mask;
@@ -373,12 +384,12 @@ __global__ void __launch_bounds__(kDownWaves * 64) decode_down_kernel(DecodeArgs
 
 static uint64_t align256(uint64_t v) { return (v + 255) / 256 * 256; }
 
-// Workspace: [sync 256 B: fused-decode counters, zero on first use][plan][zeros][xq][aq]
+// Workspace: [sync: fused-decode counters and flags, zero on first use][plan][zeros][xq][aq]
 DecodeWs decode_ws(uint32_t M, uint32_t K, uint32_t hidden, uint32_t inter) {
   DecodeWs w;
   const uint64_t slots = (uint64_t)M * K;
   w.sync = 0;
-  w.plan = 256;
+  w.plan = align256(kSyncBytes);
   w.zeros = w.plan + align256(sizeof(DecodePlan));
   w.xq = w.zeros + 256;
   w.aq = w.xq + align256((uint64_t)M * kTerms * hidden);

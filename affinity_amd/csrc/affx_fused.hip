@@ -44,7 +44,7 @@ struct FusedArgs {
   const float* w;
   uint8_t* aq;          // [slot][M][3][inter]
   const uint8_t* zeros; // 256 zero bytes (B source of unused down columns)
-  uint32_t* sync;       // [0] gate/up items published, [1] workgroups finished, [2] error bits
+  uint32_t* sync;       // [0] gate/up items published, [2] error bits; release flags from byte 256
   float* y;
   uint64_t yts, yds;
   int accumulate;
@@ -52,16 +52,16 @@ struct FusedArgs {
   int32_t sigma_a;
 };
 
-// LDS layout in bytes (host and device agree): codebook copies, activation terms, zero run,
-// partial sums, plan.
+// Dynamic LDS layout in bytes (host and device agree): activation terms, zero run, partial sums,
+// plan. The codebook copies are the kernel's one static LDS array (at address 0, so a table
+// address needs no base add).
 struct FusedLds {
-  uint32_t tbl, xq, zero, part, plan, total;
+  uint32_t xq, zero, part, plan, total;
 };
 
-__host__ __device__ inline FusedLds fused_lds(uint32_t kc, uint32_t M) {
+__host__ __device__ inline FusedLds fused_lds(uint32_t M) {
   FusedLds L;
-  L.tbl = 0;
-  L.xq = kc * 2048u * 4u;
+  L.xq = 0;
   L.zero = L.xq + 3u * M * kXqRow;
   L.part = L.zero + 256u;
   const uint32_t part_bytes = (uint32_t)kFW * 2u * 16u * M * 4u;  // gate/up [wave][mat][row][tok]
@@ -83,11 +83,12 @@ struct Lut {
   static constexpr int kVarSh = kCodeSh + 10;    // byte-address bit of the variant
 };
 
+// (thread tid: entries tid, tid + 768, tid + 1536)
 template <int KC>
-__device__ __forceinline__ void build_lut(uint32_t* tbl, const uint32_t (&cbv)[3], uint32_t tid) {
+__device__ __forceinline__ void build_lut(uint32_t* tbl, const uint32_t (&cbv)[3], uint32_t i0) {
 #pragma unroll
   for (int i = 0; i < 3; ++i) {
-    const uint32_t e = tid + (uint32_t)i * kFT;
+    const uint32_t e = i0 + (uint32_t)i * kFT;
     if (e >= 2048u) break;
     const uint32_t d = cbv[i];
     const u32x4 v = {d, d, d, d};
@@ -141,7 +142,9 @@ __device__ __forceinline__ v8i lut_finish(const uint32_t (&raw)[8], const uint32
   v8i a;
 #pragma unroll
   for (int b = 0; b < 2; ++b) {
-    const uint32_t rsh = fb[b] & 16u, xm = block_xor(fb[b]), ad = (fb[b] & 7u) * 0x08080808u;
+    // exponent add s << 3 replicated into the four bytes (v_perm: no 32-bit multiply)
+    const uint32_t rsh = fb[b] & 16u, xm = block_xor(fb[b]);
+    const uint32_t ad = __builtin_amdgcn_perm(0u, (fb[b] << 3) & 0x38u, 0u);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t r = __builtin_amdgcn_alignbit(raw[4 * b + i], raw[4 * b + i], rsh);
@@ -290,12 +293,15 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   AFFX_DYN_LDS(lds);
   // the first down unit is loaded while gate/up runs (one column group leaves the registers)
   constexpr bool PREF = CG == 1;
+  // the down phase loads its whole B operand at once (one column group fits the registers)
+  constexpr bool BPRE = CG == 1;
   const uint32_t tid = threadIdx.x, lane = tid & 63, g = blockIdx.x;
   const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar registers
   const uint32_t M = A.M, K = A.K, R = M * K;
   const uint32_t nst = A.hidden / kTileCols, nsi = A.inter / kTileCols;
-  const FusedLds L = fused_lds(KC, M);
-  uint32_t* tbl = reinterpret_cast<uint32_t*>(lds + L.tbl);
+  const FusedLds L = fused_lds(M);
+  __shared__ __align__(16) uint32_t lut_s[KC * 2048];
+  const uint8_t* lut = reinterpret_cast<const uint8_t*>(lut_s);
   uint8_t* xq = lds + L.xq;
   uint8_t* zero_l = lds + L.zero;
   float* part = reinterpret_cast<float*>(lds + L.part);
@@ -310,18 +316,29 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   uint32_t* misc = prefix_l + 16;
   float* slot_w = reinterpret_cast<float*>(misc + 4);
 
+  AFFX_TRACE_INIT;
   AFFX_TRACE(0);
-  // ---- 1. small loads first (codebook, activation, routes: their waits never queue behind the
-  // weight stream, loads complete in issue order); per-quarter activation maxima; plan by wave 0
+  // ---- 1. the small loads first (routes, then codebook and activation: loads complete in issue
+  // order, so waiting for them never waits for the weight stream issued after them); every wave
+  // dedupes the routes itself (registers only) so that it can issue its weight loads as soon as
+  // the routes arrive, with no barrier in between.
+  // Routes r = lane + 64 h. Slots are the distinct experts in order of first occurrence.
+  uint32_t e[2];
+  float wr[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t r = lane + 64u * h, rr = r < R ? r : 0u;
+    e[h] = A.sel[rr];
+    wr[h] = A.w[rr];
+  }
+  // codebook entries tid, tid + 768, tid + 1536; activation pairs p = wv + 12 j (token p / nst,
+  // 1024-column segment p % nst; an absent pair reloads pair 0, unused)
   uint32_t cbv[3];
 #pragma unroll
   for (int i = 0; i < 3; ++i) {
-    const uint32_t e = tid + (uint32_t)i * kFT;
-    cbv[i] = e < 2048u ? A.codebook[e] : 0u;
+    const uint32_t ce = tid + (uint32_t)i * kFT;
+    cbv[i] = A.codebook[ce < 2048u ? ce : 0u];
   }
-  // activation: pair p = wv + 12 j is (token p / nst, 1024-column segment p % nst); its 1024
-  // values are loaded now (an absent pair loads pair 0 again, unused), split after the weight
-  // loads are issued
   constexpr int NP = (MAXM * 4 + kFW - 1) / kFW;
   float4 xr[NP][4];
   {
@@ -342,86 +359,44 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
       }
     }
   }
-  // routes of the batch, loaded by every wave (no loads inside the plan's branch: the wait
-  // tracking then stays exact for the weight loads that follow)
-  uint32_t e[2];
-  float wr[2];
+  AFFX_TRACE(8);
+  // dedupe: a route is the first occurrence of its expert if no earlier route names it (ids
+  // outside the layer are ignored, as in the staged path)
+  bool first[2];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    const uint32_t r = lane + 64u * h, rr = r < R ? r : 0u;
-    e[h] = A.sel[rr];
-    wr[h] = A.w[rr];
+    const uint32_t r = lane + 64u * h;
+    e[h] = (r < R && e[h] < A.n_experts) ? e[h] : ~0u;
   }
-  if (wv == 0) {
-    // ids outside the layer are ignored, as in the staged path
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const uint32_t r = lane + 64u * h;
-      if (r < R) {
-        e[h] = e[h] < A.n_experts ? e[h] : ~0u;
-        w_l[r] = wr[h];
-      } else {
-        e[h] = ~0u;
-      }
+  {
+    bool dup0 = false, dup1 = false;
+    for (uint32_t j = 0; j < R; ++j) {
+      const uint32_t ej = j < 64 ? __builtin_amdgcn_readlane(e[0], j) : __builtin_amdgcn_readlane(e[1], j - 64);
+      dup0 = dup0 || (j < lane && ej == e[0]);
+      dup1 = dup1 || (j < lane + 64 && ej == e[1]);
     }
-    AFFX_TRACE(8);
-    if (lane < 16) present[lane] = 0;
-    slot_mask[lane] = 0;
-    slot_mask[lane + 64] = 0;
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-      if (e[h] != ~0u) atomicOr(&present[e[h] >> 5], 1u << (e[h] & 31));
-    __builtin_amdgcn_wave_barrier();
-    // experts present in the words below each word (sixteen independent reads per lane)
-    if (lane < 16) {
-      uint32_t pre = 0;
-#pragma unroll
-      for (uint32_t j = 0; j < 16; ++j) {
-        const uint32_t c = __popc(present[j]);
-        pre += j < lane ? c : 0u;
-      }
-      prefix_l[lane] = pre;
-      if (lane == 15) misc[0] = pre + __popc(present[15]);
-    }
-    __builtin_amdgcn_wave_barrier();
-    // slot of a route: experts present below it, ascending ids
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const uint32_t r = lane + 64u * h;
-      if (r < R) {
-        uint32_t s = ~0u;
-        if (e[h] != ~0u) {
-          s = prefix_l[e[h] >> 5] + __popc(present[e[h] >> 5] & ((1u << (e[h] & 31)) - 1u));
-          slot_expert[s] = e[h];
-        }
-        rank_l[r] = s;
-      }
-    }
-    __builtin_amdgcn_wave_barrier();
-    // per (slot, token): summed weight of its routes in route order, and the token masks
-    const uint32_t ns0 = misc[0];
-    for (uint32_t p = lane; p < ns0 * M; p += 64) {
-      const uint32_t s = p / M, t = p % M;
-      float ws = 0.f;
-      bool hit = false;
-#pragma unroll
-      for (uint32_t j = 0; j < (uint32_t)AFFX_MAX_TOPK; ++j) {
-        const uint32_t jj = j < K ? j : K - 1;  // in bounds; j >= K contributes nothing
-        const bool m = j < K && rank_l[t * K + jj] == s;
-        const float wj = w_l[t * K + jj];
-        ws += m ? wj : 0.f;
-        hit = hit || m;
-      }
-      slot_w[p] = ws;
-      if (hit) atomicOr(&slot_mask[s], 1u << t);
-    }
-    AFFX_TRACE(9);
+    first[0] = e[0] != ~0u && !dup0;
+    first[1] = e[1] != ~0u && !dup1;
   }
-  __syncthreads();  // the plan is visible
-  AFFX_TRACE(1);
+  const uint64_t fb0 = __ballot(first[0]), fb1 = __ballot(first[1]);
+  AFFX_TRACE(12);
+  const uint32_t nf0 = __popcll(fb0);
+  const uint32_t ns = nf0 + (uint32_t)__popcll(fb1);
+  // slot of a first-occurrence route: first-occurrence routes before it
+  const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
+  const uint32_t fslot0 = (uint32_t)__popcll(fb0 & below), fslot1 = nf0 + (uint32_t)__popcll(fb1 & below);
+  // expert of slot s (s wave-uniform): the route that is its first occurrence
+  auto slot_expert_of = [&](uint32_t s) -> uint32_t {
+    if (s < nf0) {
+      uint64_t m = fb0;
+      for (uint32_t i = 0; i < s; ++i) m &= m - 1;  // drop the s lowest first-occurrence routes
+      return __builtin_amdgcn_readlane(e[0], (uint32_t)__builtin_ctzll(m));
+    }
+    uint64_t m = fb1;
+    for (uint32_t i = nf0; i < s; ++i) m &= m - 1;
+    return __builtin_amdgcn_readlane(e[1], (uint32_t)__builtin_ctzll(m));
+  };
 
-  const uint32_t ns = __builtin_amdgcn_readfirstlane(misc[0]);
   const uint32_t rt_per = A.inter / kTileRows;          // gate/up row tiles per expert
   const uint32_t NI = ns * rt_per;                      // gate/up items of the layer
   const uint32_t groups = kFW / nst;                    // items in flight per workgroup
@@ -446,7 +421,7 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   auto load_gu = [&](uint32_t item) {
     const bool ok = item != ~0u;
     const uint32_t slot = ok ? item / rt_per : 0u, rt = ok ? item % rt_per : 0u;
-    const uint32_t e = ok ? __builtin_amdgcn_readfirstlane(slot_expert[slot]) : 0u;
+    const uint32_t e = ok ? slot_expert_of(slot) : 0u;
     const uint8_t* ex = A.base + (uint64_t)e * A.stride;
     const uint64_t tile = ok ? (uint64_t)rt * nst + S : 0u;
     load_pair(ug, uu, ex + A.off[kGateCodes], ex + A.off[kGateFields], ex + A.off[kUpCodes],
@@ -456,7 +431,7 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   };
   auto load_down = [&](bool ok, uint32_t td, uint32_t u) {
     const uint32_t slot = ok ? u / nsi : 0u, S2 = ok ? u % nsi : 0u;
-    const uint32_t e = ok ? __builtin_amdgcn_readfirstlane(slot_expert[slot]) : 0u;
+    const uint32_t e = ok ? slot_expert_of(slot) : 0u;
     const uint8_t* ex = A.base + (uint64_t)e * A.stride;
     const uint32_t tdd = ok ? td : 0u;
     load_unit_ordered(ud, ex + A.off[kDownCodes], ex + A.off[kDownFields], (uint64_t)tdd * nsi + S2, lane);
@@ -467,11 +442,56 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   // the waves that write the SwiGLU output drain their memory counter before the release
   const uint32_t epi_waves = (groups * 16 * M + 63) / 64;
   load_gu(rounds > 0 ? gu_item(0) : ~0u);
+  AFFX_TRACE(13);
   // (SINGLE: rounds <= 1 always, so no branch around the load for the wait tracking to merge)
   if (PREF && (SINGLE || rounds <= 1)) load_down(has_down, g, wv);
   AFFX_TRACE(2);
 
-  // ---- 3. activation terms and codebook copies into LDS, from the registers loaded up front
+  if (wv == 0) {
+    // (after this wave's loads are out) the plan for the epilogue and the down phase: slot of every route (that of its expert's
+    // first occurrence), expert of every slot, per (slot, token) summed weights and token masks
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t r = lane + 64u * h;
+      uint32_t rank = ~0u;
+      for (uint32_t j = 0; j < R; ++j) {  // all lanes (cross-lane reads in uniform control flow)
+        const uint32_t ej = j < 64 ? __builtin_amdgcn_readlane(e[0], j) : __builtin_amdgcn_readlane(e[1], j - 64);
+        const uint32_t fj = j < 64 ? __builtin_amdgcn_readlane((uint32_t)first[0], j)
+                                   : __builtin_amdgcn_readlane((uint32_t)first[1], j - 64);
+        const uint32_t sj = j < 64 ? __builtin_amdgcn_readlane(fslot0, j) : __builtin_amdgcn_readlane(fslot1, j - 64);
+        rank = (fj && e[h] != ~0u && ej == e[h]) ? sj : rank;
+      }
+      if (r < R) {
+        rank_l[r] = rank;
+        w_l[r] = wr[h];
+      }
+      if (first[h]) slot_expert[h ? fslot1 : fslot0] = e[h];
+    }
+    slot_mask[lane] = 0;
+    slot_mask[lane + 64] = 0;
+    if (lane == 0) misc[0] = ns;
+    __builtin_amdgcn_wave_barrier();
+    // per (slot, token): summed weight of its routes in route order, and the token masks
+    for (uint32_t p = lane; p < ns * M; p += 64) {
+      const uint32_t s = p / M, t = p % M;
+      float ws = 0.f;
+      bool hit = false;
+#pragma unroll
+      for (uint32_t j = 0; j < (uint32_t)AFFX_MAX_TOPK; ++j) {
+        const uint32_t jj = j < K ? j : K - 1;  // in bounds; j >= K contributes nothing
+        const bool m = j < K && rank_l[t * K + jj] == s;
+        const float wj = w_l[t * K + jj];
+        ws += m ? wj : 0.f;
+        hit = hit || m;
+      }
+      slot_w[p] = ws;
+      if (hit) atomicOr(&slot_mask[s], 1u << t);
+    }
+    AFFX_TRACE(9);
+  }
+
+  // ---- 3. activation terms and codebook copies into LDS, from the registers loaded up front:
+  // a pair's maximum (wave reduction) fixes its exponent, then three E4M3 terms per element
 #pragma unroll
   for (int j = 0; j < NP; ++j) {
     const uint32_t p = wv + (uint32_t)j * kFW;
@@ -497,9 +517,10 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
       }
     }
   }
+  build_lut<KC>(lut_s, cbv, tid);
   if (tid < 64) reinterpret_cast<uint32_t*>(zero_l)[tid] = 0u;
-  build_lut<KC>(tbl, cbv, tid);
-  __syncthreads();  // activation terms and codebook copies visible
+  __syncthreads();  // plan, activation terms and codebook copies visible
+  AFFX_TRACE(1);
 
   // B source of this lane for gate/up: its (token, term) row at this wave's segment
   const uint32_t c = lane & 15, kg = lane >> 4;
@@ -532,8 +553,8 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
       uint32_t bg[2], bu[2];
       pin_step(ug, 0);
       pin_step(uu, 0);
-      lut_lookup_step<KC>(ug, lds, copy4, 0, rg, bg);
-      lut_lookup_step<KC>(uu, lds, copy4, 0, ru, bu);
+      lut_lookup_step<KC>(ug, lut, copy4, 0, rg, bg);
+      lut_lookup_step<KC>(uu, lut, copy4, 0, ru, bu);
       v8i bc[CG];
 #pragma unroll
       for (int cg = 0; cg < CG; ++cg) bc[cg] = b_step_lds(bsrc[cg], 0);
@@ -547,8 +568,8 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
           for (int cg = 0; cg < CG; ++cg) { AFFX_PIN(acc[0][cg]); AFFX_PIN(acc[1][cg]); }
           pin_step(ug, m + 1);
           pin_step(uu, m + 1);
-          lut_lookup_step<KC>(ug, lds, copy4, m + 1, ng, nbg);
-          lut_lookup_step<KC>(uu, lds, copy4, m + 1, nu, nbu);
+          lut_lookup_step<KC>(ug, lut, copy4, m + 1, ng, nbg);
+          lut_lookup_step<KC>(uu, lut, copy4, m + 1, nu, nbu);
 #pragma unroll
           for (int cg = 0; cg < CG; ++cg) bn[cg] = b_step_lds(bsrc[cg], m + 1);
         }
@@ -590,6 +611,7 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
             part[((wv * 2 + mm) * 16 + 4 * kg + v) * M + t] = ldexpf(val, -sigma_l[t * 4 + S]);
         }
     __syncthreads();
+    AFFX_TRACE(11);
 
     // epilogue: thread (group, row, token) sums the group's segments in order, SwiGLU, E4M3 terms
     // (up to 12 groups x 16 rows x 8 tokens: two passes of the workgroup)
@@ -638,25 +660,45 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
     // L2 write-back, once per workgroup and serialised per L2, costs microseconds, and nothing
     // else written here is read by other workgroups.
     if (wv < epi_waves) __builtin_amdgcn_s_waitcnt(0);
+    AFFX_TRACE(10);
     __syncthreads();
-    if (tid == 0) {
+    if (wv == 0) {
       const uint32_t done = my_items - rho * groups < groups ? my_items - rho * groups : groups;
-      __hip_atomic_fetch_add(&A.sync[0], done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (rho + 1 < n_rounds) {
+        if (lane == 0) __hip_atomic_fetch_add(&A.sync[0], done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        // this workgroup's last round: the add that completes the count (necessarily a last
+        // round's) finds every other add performed, hence every activation store complete. Its
+        // wave clears the count for the next launch and raises the flag of each waiting workgroup
+        // (one line each: the waiters poll without contending for one address).
+        uint32_t old = 0;
+        if (lane == 0) old = __hip_atomic_fetch_add(&A.sync[0], done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        old = __builtin_amdgcn_readlane(old, 0);
+        if (old + done == NI) {
+          if (lane == 0) __hip_atomic_store(&A.sync[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          const uint32_t nwait = A.n_wg < dtiles ? A.n_wg : dtiles;
+          for (uint32_t i = lane; i < nwait; i += 64)
+            __hip_atomic_store(A.sync + (kSyncHeader + i * kSyncFlagStride) / 4, 1u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
     }
   }
 
   AFFX_TRACE(4);
-  // ---- 5. wait for every gate/up item, then the down tiles ----------------------------------------
+  // ---- 5. wait for every gate/up item (this workgroup's flag), then the down tiles -------------
   if (g < dtiles) {
-    if (tid == 0) {
+    if (tid == 0 && NI > 0) {
+      uint32_t* flag = A.sync + (kSyncHeader + g * kSyncFlagStride) / 4;
       uint32_t n = 0;
-      while (__hip_atomic_load(&A.sync[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < NI) {
+      while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) {
         if (++n > kSpinLimit) {
           __hip_atomic_fetch_or(&A.sync[2], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           break;
         }
         __builtin_amdgcn_s_sleep(2);
       }
+      __hip_atomic_store(flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // for the next launch
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     }
     __syncthreads();
@@ -685,13 +727,22 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
         v4f acc[CG];
 #pragma unroll
         for (int cg = 0; cg < CG; ++cg) acc[cg] = v4f{0.f, 0.f, 0.f, 0.f};
+        // B: one column group (64 registers) is loaded whole up front, so the eight steps wait
+        // for one round trip; two column groups are loaded one step ahead
+        v8i bpre[BPRE ? 8 : 1];
+        v8i bc[CG];
+        if constexpr (BPRE) {
+#pragma unroll
+          for (int m = 0; m < 8; ++m) bpre[m] = b_step(b.p[0], m);
+          __builtin_amdgcn_sched_barrier(0);
+        } else {
+#pragma unroll
+          for (int cg = 0; cg < CG; ++cg) bc[cg] = b_step(b.p[cg], 0);
+        }
         uint32_t raw[8];
         uint32_t bv[2];
         pin_step(ud, 0);
-        lut_lookup_step<KC>(ud, lds, copy4, 0, raw, bv);
-        v8i bc[CG];
-#pragma unroll
-        for (int cg = 0; cg < CG; ++cg) bc[cg] = b_step(b.p[cg], 0);
+        lut_lookup_step<KC>(ud, lut, copy4, 0, raw, bv);
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
           uint32_t nraw[8];
@@ -703,20 +754,28 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
 #pragma unroll
             for (int cg = 0; cg < CG; ++cg) AFFX_PIN(acc[cg]);
             pin_step(ud, m + 1);
-            lut_lookup_step<KC>(ud, lds, copy4, m + 1, nraw, nbv);
+            lut_lookup_step<KC>(ud, lut, copy4, m + 1, nraw, nbv);
+            if constexpr (!BPRE) {
 #pragma unroll
-            for (int cg = 0; cg < CG; ++cg) bn[cg] = b_step(b.p[cg], m + 1);
+              for (int cg = 0; cg < CG; ++cg) bn[cg] = b_step(b.p[cg], m + 1);
+            }
           }
           const v8i a = lut_finish(raw, bv);
+          if constexpr (BPRE) {
+            acc[0] = mfma(a, bpre[m], acc[0]);
+          } else {
 #pragma unroll
-          for (int cg = 0; cg < CG; ++cg) acc[cg] = mfma(a, bc[cg], acc[cg]);
+            for (int cg = 0; cg < CG; ++cg) acc[cg] = mfma(a, bc[cg], acc[cg]);
+          }
           __builtin_amdgcn_sched_barrier(0);
           if (m < 7) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) raw[i] = nraw[i];
             bv[0] = nbv[0]; bv[1] = nbv[1];
+            if constexpr (!BPRE) {
 #pragma unroll
-            for (int cg = 0; cg < CG; ++cg) bc[cg] = bn[cg];
+              for (int cg = 0; cg < CG; ++cg) bc[cg] = bn[cg];
+            }
           }
         }
         const float rs[4] = {__uint_as_float(rsv.x << 16), __uint_as_float(rsv.x & 0xFFFF0000u),
@@ -757,15 +816,6 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   }
 
   AFFX_TRACE(7);
-  // ---- 6. the last workgroup out resets the counters for the next launch ---------------------------
-  if (tid == 0) {
-    // (every workgroup got here after its own wait on sync[0]: the last one may clear it)
-    const uint32_t old = __hip_atomic_fetch_add(&A.sync[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (old == A.n_wg - 1) {
-      __hip_atomic_store(&A.sync[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&A.sync[1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
 }
 
 }  // namespace affx
@@ -804,7 +854,7 @@ int fused_prepare(int dev, int v, FusedVariant* out) {
     f.fn = fns[v];
     f.kc = kcs[v];
     f.maxm = maxms[v];
-    const uint32_t lds = fused_lds(f.kc, f.maxm).total;
+    const uint32_t lds = fused_lds(f.maxm).total;  // dynamic part (the codebook copies are static)
     int rc = check_hip(hipFuncSetAttribute(f.fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
                        "hipFuncSetAttribute(fused decode)");
     if (rc) return rc;
@@ -885,7 +935,7 @@ extern "C" int affx_expert_ffn_decode(const affx_layer* L, const float* x, uint6
   A.accumulate = accumulate;
   A.limit = L->swiglu_limit;
   A.sigma_a = 7 - ilogbf(L->swiglu_limit * L->swiglu_limit);
-  const uint32_t lds = fused_lds(f.kc, M).total;
+  const uint32_t lds = fused_lds(M).total;
   hipStream_t st = (hipStream_t)stream;
   // the down B operand's unused columns read the workspace's zero run: zero in a zero-filled
   // workspace and only ever rewritten with zeros (by the staged prep kernel)

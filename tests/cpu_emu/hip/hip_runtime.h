@@ -30,6 +30,7 @@
 #define __launch_bounds__(...)
 #define __restrict__
 #define __shared__ static
+#define __align__(x) __attribute__((aligned(x)))
 
 struct emu_dim3 { uint32_t x = 1, y = 1, z = 1; };
 struct dim3 { uint32_t x, y, z; dim3(uint32_t a = 1, uint32_t b = 1, uint32_t c = 1) : x(a), y(b), z(c) {} };
@@ -120,6 +121,7 @@ inline T emu_exchange(T v, uint32_t src) {
   T r; memcpy(&r, &got, sizeof(T)); return r;
 }
 template <typename T> inline T __shfl_xor(T v, int o, int width = 64) { return emu_exchange(v, emu_lane() ^ o); }
+template <typename T> inline T __builtin_amdgcn_readlane(T v, uint32_t l) { return emu_exchange(v, l); }
 template <typename T> inline T __shfl_down(T v, int d, int width = 64) {
   uint32_t l = emu_lane(); uint32_t src = ((l % width) + d < (uint32_t)width) ? l + d : l;
   return emu_exchange(v, src);

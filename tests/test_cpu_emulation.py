@@ -55,6 +55,12 @@ def test_decode_emulated_m1(emu):
     assert "identical to staged=1" in run(emu, "decode", 1024, 1024, 7, 1, 6, 1)
 
 
+def test_decode_emulated_all_padding(emu):
+    # no route names an expert of the layer: nothing to wait for, y written as zeros
+    out = run(emu, "decode", 1024, 1024, 5, 2, 3, 4, "allpad", cus=3)
+    assert "identical to staged=1" in out and "rel_l2=0.000e+00" in out
+
+
 def test_decode_emulated_m1_single_pass(emu):
     # 6 workgroups hold all 64 gate/up items: the straight-line batch-1 variant
     assert "identical to staged=1" in run(emu, "decode", 1024, 1024, 5, 1, 1, 9, cus=6)
