@@ -42,13 +42,38 @@ uint64_t a256(uint64_t v) { return (v + 255) / 256 * 256; }
 
 extern "C" {
 
+// Hook workspace. Decode: [decode workspace][routes][weights]; the decode workspace starts at
+// offset 0, so its sync run (counter and release flags, which persist between calls and must stay
+// zero) is at the same bytes in every call whatever the batch. Prefill: [sync run, untouched]
+// [routes][weights][x hi][x lo][y][grouped workspace], so a prefill call never writes those bytes.
+namespace {
+struct HookWs {
+  uint64_t sel, w, hi, lo, y, inner, need;
+};
+HookWs hook_ws(uint32_t nb, uint32_t k, uint32_t n_experts, uint32_t hidden, uint32_t inter) {
+  HookWs h{};
+  const uint64_t pairs = (uint64_t)nb * k;
+  if (nb <= AFFX_MAX_DECODE_TOKENS) {
+    h.inner = 0;
+    h.sel = a256(affx_decode_workspace_size(nb, k, hidden, inter));
+    h.w = h.sel + a256(4 * pairs);
+    h.need = h.w + a256(4 * pairs);
+  } else {
+    h.sel = a256(kSyncBytes);
+    h.w = h.sel + a256(4 * pairs);
+    h.hi = h.w + a256(4 * pairs);
+    h.lo = h.hi + a256(2ull * nb * hidden);
+    h.y = h.lo + a256(2ull * nb * hidden);
+    h.inner = h.y + a256(4ull * nb * hidden);
+    h.need = h.inner + affx_grouped_workspace_size(nb, k, n_experts, hidden, inter);
+  }
+  return h;
+}
+}  // namespace
+
 size_t affx_batch_workspace_size(uint32_t nb, uint32_t k, uint32_t n_experts, uint32_t hidden,
                                  uint32_t inter) {
-  const uint64_t pairs = (uint64_t)nb * k;
-  uint64_t need = 2 * a256(4 * pairs);
-  if (nb <= AFFX_MAX_DECODE_TOKENS) return (size_t)(need + affx_decode_workspace_size(nb, k, hidden, inter));
-  need += 2 * a256(2ull * nb * hidden) + a256(4ull * nb * hidden);
-  return (size_t)(need + affx_grouped_workspace_size(nb, k, n_experts, hidden, inter));
+  return (size_t)hook_ws(nb, k, n_experts, hidden, inter).need;
 }
 
 uint32_t affx_expert_ffn_batch(void* ctx_, uint32_t layer, const uint32_t* sel, const float* w,
@@ -66,22 +91,12 @@ uint32_t affx_expert_ffn_batch(void* ctx_, uint32_t layer, const uint32_t* sel, 
   hipStream_t s = (hipStream_t)ctx->stream;
   uint8_t* ws = (uint8_t*)ctx->workspace;
   const uint64_t pairs = (uint64_t)nb * k;
-  const uint64_t o_sel = 0, o_w = a256(4 * pairs), o_rest = o_w + a256(4 * pairs);
-  uint64_t need = o_rest;
   const bool decode = nb <= AFFX_MAX_DECODE_TOKENS;
-  uint64_t o_hi = 0, o_lo = 0, o_y = 0, o_inner = o_rest;
-  if (decode) {
-    need += affx_decode_workspace_size(nb, k, L->hidden, L->inter);
-  } else {
-    o_hi = o_rest;
-    o_lo = o_hi + a256(2ull * nb * L->hidden);
-    o_y = o_lo + a256(2ull * nb * L->hidden);
-    o_inner = o_y + a256(4ull * nb * L->hidden);
-    need = o_inner + affx_grouped_workspace_size(nb, k, L->n_experts, L->hidden, L->inter);
-  }
-  if (ctx->workspace_bytes < need) {
+  const HookWs h = hook_ws(nb, k, L->n_experts, L->hidden, L->inter);
+  const uint64_t o_sel = h.sel, o_w = h.w, o_hi = h.hi, o_lo = h.lo, o_y = h.y, o_inner = h.inner;
+  if (ctx->workspace_bytes < h.need) {
     set_error(AFFX_ERR_ARG, "ffn_batch: workspace %zu < %llu bytes", ctx->workspace_bytes,
-              (unsigned long long)need);
+              (unsigned long long)h.need);
     return 0;
   }
   if (check_hip(hipMemcpyAsync(ws + o_sel, sel, 4 * pairs, hipMemcpyHostToDevice, s), "routes H2D") ||
@@ -91,7 +106,7 @@ uint32_t affx_expert_ffn_batch(void* ctx_, uint32_t layer, const uint32_t* sel, 
   if (decode) {
     rc = affx_expert_ffn_decode(L, ctx->d_x, 1, ctx->nb_stride, nb, (const uint32_t*)(ws + o_sel),
                                 (const float*)(ws + o_w), k, ctx->d_block, 1, ctx->nb_stride, 1,
-                                ws + o_rest, ctx->workspace_bytes - o_rest, s);
+                                ws + o_inner, o_sel, s);
   } else {
     const uint64_t tot = (uint64_t)nb * L->hidden;
     hipLaunchKernelGGL(split_bf16_kernel, dim3((uint32_t)((tot + 255) / 256)), dim3(256), 0, s, ctx->d_x,

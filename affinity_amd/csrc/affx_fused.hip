@@ -11,10 +11,12 @@
 //      over the 64 banks instead of colliding at random),
 //   4. computes its gate/up items (16 rows x all columns of one expert; wave = 1024-column
 //      segment), sums the segments in fixed order, applies SwiGLU and writes the result as E4M3
-//      terms (aq) to global memory, then publishes its item count with an agent-scope release,
-//   5. waits (bounded spin) until every workgroup's items are published, then computes one
-//      16-row tile of the output from its (expert, segment) down units and writes y.
-// The last workgroup to finish resets the counters, so the workspace is reusable by the next
+//      terms (aq) to global memory with device-coherent stores, drains them, and adds its item
+//      count to one agent-scope counter; the add that completes the count clears it and raises
+//      one release flag per down-phase workgroup (a 128-byte line each),
+//   5. waits (bounded spin) on its own flag, clears it, then computes one 16-row tile of the
+//      output from its (expert, segment) down units and writes y.
+// Counter and flags are zero again when the launch ends, so the workspace is reusable by the next
 // launch on the stream without a memset (graph-capture safe).
 //
 // Reference counterparts: the decode branch of ExpertFfnBatch (src/engine/model.cpp:6045-6121)

@@ -128,8 +128,8 @@ class DecodeWorkspace:
     def __init__(self, m_tokens: int, top_k: int, hidden: int = HIDDEN, inter: int = INTER,
                  device="cuda"):
         self.bytes = int(lib().affx_decode_workspace_size(m_tokens, top_k, hidden, inter))
-        # zero-filled: the fused decode keeps its cross-workgroup counters in the first 256 bytes
-        # and expects them zero on first use (each launch leaves them zero again)
+        # zero-filled: the fused decode keeps its cross-workgroup counter and release flags at the
+        # start of the workspace and expects them zero on first use (each launch leaves them zero)
         self.buf = torch.zeros(self.bytes, dtype=torch.uint8, device=device)
 
     def error_flags(self) -> int:

@@ -192,11 +192,15 @@ def main() -> int:
     fu_bytes = K * STRIDE
     fu_achieved = fu_bytes / (fu_us * 1e-6) / 1e9
     log(f"decode_fused_kernel: {fu_us:.2f} us/launch avg, {fu_bytes} B -> {fu_achieved:.0f} GB/s")
+    # HBM bytes per launch from the committed counter summary (FETCH_SIZE + WRITE_SIZE passes,
+    # each scaled by what the counter reads for a plain copy of known size)
     traffic = None
-    tpath = os.path.join(HERE, "profiles", "decode_fused_c5_traffic.json")
+    tpath = os.path.join(HERE, "profiles", "decode_fused_c5_traffic.txt")
     if os.path.exists(tpath):
         with open(tpath) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+            for line in f:
+                if line.startswith("hbm_bytes_per_launch:"):
+                    traffic = int(line.split(":")[1])
 
     if args.staged:
         def staged_step():

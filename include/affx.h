@@ -113,10 +113,12 @@ int affx_dequant_matrix(const affx_matrix* m, const void* codebook, float* out, 
 /* ---- decode: M <= 8 tokens, fused gate/up -> SwiGLU -> down -> weighted combine ------------- */
 
 /* Workspace bytes affx_expert_ffn_decode needs for m tokens with top-k routing. The workspace
- * must be zero-filled before its first use: its first 256 bytes hold the fused decode's
- * cross-workgroup counters, which every launch leaves zero again (no memset per call, safe under
- * graph capture). Word 2 (bytes 8..11) becomes nonzero if a launch ever gave up waiting for the
- * other workgroups (its output is then invalid); it is sticky until the caller clears it. */
+ * must be zero-filled before its first use: its first 33,024 bytes hold the fused decode's
+ * cross-workgroup state (a 256-byte header with the publish counter, then one 128-byte release
+ * flag per waiting workgroup), which every launch leaves zero again (no memset per call, safe
+ * under graph capture). Word 2 (bytes 8..11) becomes nonzero if a launch ever gave up waiting
+ * for the other workgroups (its output is then invalid); it is sticky until the caller clears it
+ * (and the workspace should then be zero-filled again). */
 size_t affx_decode_workspace_size(uint32_t m_tokens, uint32_t top_k, uint32_t hidden,
                                   uint32_t inter);
 
@@ -130,7 +132,8 @@ size_t affx_decode_workspace_size(uint32_t m_tokens, uint32_t top_k, uint32_t hi
  * Replaces the batch-1 GPU FFN expert_ffn_hip (src/gpu/expert_kernel.hip:2737-2808,
  * expert_kernel_hip.h:273) and the narrow NT=1 arm of the W8A8 GEMM that the engine's decode uses
  * (expert_kernel.hip:3049-3058). One persistent launch (routing plan, activation split, gate/up +
- * SwiGLU, down + combine, with one agent-scope counter between gate/up and down); it needs every
+ * SwiGLU, down + combine; between gate/up and down, an agent-scope publish counter whose last
+ * adder raises one release flag per down-phase workgroup); it needs every
  * workgroup of its grid resident at once, so the grid is sized to the device, and it falls back to
  * the staged launches below when the device cannot hold it. No host synchronisation. */
 int affx_expert_ffn_decode(const affx_layer* layer, const float* x, uint64_t x_tok_stride,
@@ -196,7 +199,8 @@ typedef struct affx_engine_ctx {
   const float* d_x;         /* f32 [hidden][nb_stride], dim-major (the engine's d_x) */
   float* d_block;           /* f32 [hidden][nb_stride], accumulated into */
   uint32_t nb_stride;
-  void* workspace;          /* device */
+  void* workspace;          /* device, zero-filled before first use (its first bytes hold the
+                               decode's persistent counter and flags; no call disturbs them) */
   size_t workspace_bytes;
   void* stream;
 } affx_engine_ctx;

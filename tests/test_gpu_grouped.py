@@ -88,43 +88,47 @@ def test_grouped_is_deterministic(ax, layer):
     np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
-@pytest.mark.parametrize("nb", [3, 12])
-def test_engine_hook_dim_major_arenas(ax, orc, c1_codebook, layer, nb):
+def test_engine_hook_dim_major_arenas(ax, orc, c1_codebook, layer):
     """affx_expert_ffn_batch with host routes, d_x/d_block f32 [hidden][nb_stride] (accumulated),
-    marks every non-padding pair handled and returns their count."""
+    marks every non-padding pair handled and returns their count. One context serves a decode
+    batch, a prefill batch, then the decode batch again: the prefill arm must leave the decode's
+    persistent counter and flags (at the start of the workspace) zero."""
     from affinity_amd._lib import AffxEngineCtx, lib
     ex, pool, hidden, inter = layer
-    rng = np.random.default_rng(nb)
     k, nbs = 6, 16
-    x = rng.standard_normal((nb, hidden)).astype(np.float32)
-    sel, w = _routes(rng, nb, k, ex.shape[0])
-    sel[0, 2] = 4000
-    y0 = rng.standard_normal((nb, hidden)).astype(np.float32)
-    dx = torch.zeros((hidden, nbs), device="cuda")
-    dx[:, :nb] = torch.from_numpy(x.T.copy()).cuda()
-    db = torch.zeros((hidden, nbs), device="cuda")
-    db[:, :nb] = torch.from_numpy(y0.T.copy()).cuda()
-    wsb = lib().affx_batch_workspace_size(nb, k, pool.n_experts, hidden, inter)
-    ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+    wsb = max(lib().affx_batch_workspace_size(nb, k, pool.n_experts, hidden, inter) for nb in (3, 12))
+    ws = torch.zeros(wsb, dtype=torch.uint8, device="cuda")
+    sync_bytes = 256 + 256 * 128
     L = pool.layer()
-    ctx = AffxEngineCtx(C.pointer(L), 1, dx.data_ptr(), db.data_ptr(), nbs, ws.data_ptr(), wsb,
-                        torch.cuda.current_stream().cuda_stream)
-    handled = np.zeros(nb * k, np.uint8)
-    sel_c = np.ascontiguousarray(sel, np.uint32)
-    w_c = np.ascontiguousarray(w, np.float32)
-    n = lib().affx_expert_ffn_batch(C.addressof(ctx), 0, sel_c.ctypes.data, w_c.ctypes.data, nb, k,
-                                    handled.ctypes.data)
-    assert n == nb * k - 1, _lib_err()
-    assert handled.reshape(nb, k)[0, 2] == 0 and handled.sum() == n
-    got = db.cpu().numpy()
-    xr = x
-    if nb > 8:  # the grouped arm carries x as a bf16 hi/lo pair
-        hi = bf16_bits(x)
-        hv = (hi.astype(np.uint32) << 16).view(np.float32)
-        xr = hv + (bf16_bits(x - hv).astype(np.uint32) << 16).view(np.float32)
-    ref = y0 + _oracle(orc, ex, orc.unpack_codebook(c1_codebook), xr, sel, w, hidden, inter)
-    assert rel_l2(got[:, :nb].T, ref) <= TOL
-    np.testing.assert_array_equal(got[:, nb:], 0.0)
+    for call, nb in enumerate((3, 12, 3)):
+        rng = np.random.default_rng(nb + 100 * call)
+        x = rng.standard_normal((nb, hidden)).astype(np.float32)
+        sel, w = _routes(rng, nb, k, ex.shape[0])
+        sel[0, 2] = 4000
+        y0 = rng.standard_normal((nb, hidden)).astype(np.float32)
+        dx = torch.zeros((hidden, nbs), device="cuda")
+        dx[:, :nb] = torch.from_numpy(x.T.copy()).cuda()
+        db = torch.zeros((hidden, nbs), device="cuda")
+        db[:, :nb] = torch.from_numpy(y0.T.copy()).cuda()
+        ctx = AffxEngineCtx(C.pointer(L), 1, dx.data_ptr(), db.data_ptr(), nbs, ws.data_ptr(), wsb,
+                            torch.cuda.current_stream().cuda_stream)
+        handled = np.zeros(nb * k, np.uint8)
+        sel_c = np.ascontiguousarray(sel, np.uint32)
+        w_c = np.ascontiguousarray(w, np.float32)
+        n = lib().affx_expert_ffn_batch(C.addressof(ctx), 0, sel_c.ctypes.data, w_c.ctypes.data, nb, k,
+                                        handled.ctypes.data)
+        assert n == nb * k - 1, _lib_err()
+        assert handled.reshape(nb, k)[0, 2] == 0 and handled.sum() == n
+        got = db.cpu().numpy()
+        xr = x
+        if nb > 8:  # the grouped arm carries x as a bf16 hi/lo pair
+            hi = bf16_bits(x)
+            hv = (hi.astype(np.uint32) << 16).view(np.float32)
+            xr = hv + (bf16_bits(x - hv).astype(np.uint32) << 16).view(np.float32)
+        ref = y0 + _oracle(orc, ex, orc.unpack_codebook(c1_codebook), xr, sel, w, hidden, inter)
+        assert rel_l2(got[:, :nb].T, ref) <= TOL, (call, nb)
+        np.testing.assert_array_equal(got[:, nb:], 0.0)
+        assert int(torch.count_nonzero(ws[:sync_bytes])) == 0, (call, nb)
 
 
 def _lib_err():
