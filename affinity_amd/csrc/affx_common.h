@@ -39,8 +39,8 @@ enum Plane : int {
   kDownCodes = 6, kDownFields = 7, kDownRs = 8
 };
 
-inline uint64_t code_row_bytes(uint64_t cols) { return cols * 10 / 32; }
-inline uint64_t field_row_bytes(uint64_t cols) { return cols * 6 / 128; }
+__host__ __device__ inline uint64_t code_row_bytes(uint64_t cols) { return cols * 10 / 32; }
+__host__ __device__ inline uint64_t field_row_bytes(uint64_t cols) { return cols * 6 / 128; }
 
 // ---- activations as exact fp8 sums -------------------------------------------------------------
 // An activation v is fed to the fp8 MFMA as kTerms E4M3 values: v * 2^sigma ~= t0 + t1/16 +

@@ -17,11 +17,10 @@
 // 1348-1964): moe_plan_kernel (src/gpu/moe_plan.hip:116-380), batch_quant_fp8_kernel
 // (src/gpu/batch_kernels.hip:146-211), expert_gemm_wmma_kernel (src/gpu/expert_kernel.hip:
 // 364-825), expert_swiglu_quant_kernel (862-931), expert_scatter_slots_kernel (935-947).
-#include "affx_tile.h"
+#include "affx_lut.h"
 
 namespace affx {
 
-constexpr int kGroups = 8;         // token groups per tile (one MFMA column block each)
 constexpr int kPlanThreads = 1024;
 
 struct Tile {
@@ -32,28 +31,6 @@ struct GroupedHdr {
   uint32_t n_slots;
   uint32_t n_tiles1, n_tiles2;
   uint32_t tx;                     // activation terms of the gate/up input (2 or 3)
-};
-
-struct GroupedArgs {
-  const uint8_t* base;
-  uint64_t stride;
-  uint64_t off[9];
-  uint32_t hidden, inter, n_experts, n_tok, top_k;
-  const uint32_t* codebook;
-  const GroupedHdr* hdr;
-  const uint32_t* offsets;         // [E+1]
-  const uint32_t* slot_tok;        // [T*K]
-  const int32_t* slot_of;          // [T*K]
-  const Tile* tiles1;
-  const Tile* tiles2;
-  const int32_t* x_sigma;          // [T]
-  const uint8_t* xq;               // [T][tx][hidden]
-  uint8_t* aq;                     // [slots][3][inter]
-  float* z;                        // [slots][hidden]
-  const uint8_t* zeros;
-  float limit;
-  int32_t sigma_a;
-  uint32_t tx, tpg1, tpg2;         // terms and tokens per group, gate/up and down
 };
 
 // ------------------------------------------------------------------------------------------------
@@ -137,16 +114,28 @@ __global__ void __launch_bounds__(256) grouped_place_kernel(
 }
 
 // ------------------------------------------------------------------------------------------------
-// activation terms
+// K order of the B rows
+// ------------------------------------------------------------------------------------------------
+// Activation rows (x terms for gate/up, SwiGLU terms for down) are stored in MFMA-step order:
+// column col = 1024 s + 256 kg + 32 m + i (super-step s, lane group kg, step m, i < 32) sits at
+// byte (8 s + m) * 128 + 32 kg + i, so the 128 bytes one MFMA step needs from a row are one run.
+__host__ __device__ inline uint32_t kperm(uint32_t col) {
+  return ((col >> 10) * 8u + ((col >> 5) & 7u)) * 128u + ((col >> 8) & 3u) * 32u + (col & 31u);
+}
+
+// ------------------------------------------------------------------------------------------------
+// activation terms: per token an exponent and tx E4M3 terms of every element, in step order
 // ------------------------------------------------------------------------------------------------
 __global__ void __launch_bounds__(256) grouped_prep_x_kernel(const uint16_t* __restrict__ x,
                                                              const uint16_t* __restrict__ xlo,
                                                              uint32_t hidden, uint32_t tx,
                                                              int32_t* __restrict__ sigma_out,
                                                              uint8_t* __restrict__ xq,
-                                                             uint32_t* __restrict__ zeros) {
+                                                             uint32_t* __restrict__ zeros,
+                                                             uint32_t zero_words) {
   const uint32_t t = blockIdx.x, tid = threadIdx.x;
-  if (t == 0 && tid < 64) zeros[tid] = 0u;  // the B source of unused columns
+  if (t == 0)  // the B row of unused columns
+    for (uint32_t i = tid; i < zero_words; i += 256) zeros[i] = 0u;
   __shared__ float red[4];
   const uint16_t* xr = x + (uint64_t)t * hidden;
   const uint16_t* lr = xlo ? xlo + (uint64_t)t * hidden : nullptr;
@@ -174,187 +163,386 @@ __global__ void __launch_bounds__(256) grouped_prep_x_kernel(const uint16_t* __r
       q[1] |= b1 << (8 * i);
       q[2] |= b2 << (8 * i);
     }
-    uint32_t* dst = reinterpret_cast<uint32_t*>(xq + (uint64_t)t * tx * hidden + h4);
-    for (uint32_t k = 0; k < tx; ++k) dst[k * (hidden / 4)] = q[k];
+    uint8_t* row = xq + (uint64_t)t * tx * hidden + kperm(h4);
+    for (uint32_t k = 0; k < tx; ++k) *reinterpret_cast<uint32_t*>(row + (uint64_t)k * hidden) = q[k];
   }
 }
 
 // ------------------------------------------------------------------------------------------------
-// GEMM pieces
+// grouped GEMM: one workgroup = one (expert, token tile) x one row block
 // ------------------------------------------------------------------------------------------------
+// 4 waves, one per SIMD. A wave owns 64 weight rows (four 16-row tiles: gate/up = two gate and the
+// same two up tiles, down = four tiles) against all 256 B columns of the tile (16 MFMA column
+// tiles; a token is TX adjacent columns, 16 / TX tokens per column tile), so the 256 accumulators
+// live in the AGPRs. Per MFMA step (128 of K):
+//   - each wave decodes its own rows' A fragments in registers: one codebook lookup per quad
+//     code, reused by 16 MFMAs;
+//   - B (256 columns x 128 bytes) sits in LDS, written by direct global->LDS loads one step ahead
+//     (double buffer), read by all four waves; 16-byte chunks are swizzled by column so that the
+//     fragment reads of 16 lanes hit 16 distinct bank groups;
+//   - the packed weights of the next 1024 columns stream into a register ring, each chunk
+//     reloaded as soon as the lookups of the current 1024 columns are past it.
+constexpr int kGW = 4;                      // waves per workgroup
+constexpr int kGT = kGW * 64;
+constexpr int kGKC = 8;                     // codebook copies
+constexpr int kGCT = 12;                    // 16-column tiles of B per wave
+constexpr int kGCols = kGCT * 16;           // B columns per workgroup
+constexpr uint32_t kGBuf = kGCols * 128;    // bytes of one B buffer (one MFMA step)
+constexpr int kGDma = kGCols / 8 / kGW;     // direct-load instructions per wave per step (8 columns each)
 
-// B source of group g for this lane: column c = token (c / tx) of the group, term c % tx.
-__device__ __forceinline__ const u32x4* group_b(const GroupedArgs& A, const uint8_t* src,
-                                                uint32_t row_bytes, uint32_t tx, uint32_t tpg,
-                                                uint32_t slot0, uint32_t n, uint32_t g,
-                                                uint32_t lane, uint64_t col0, bool by_token) {
-  const uint32_t c = lane & 15, kg = lane >> 4;
-  const uint32_t j = g * tpg + c / tx, tau = c % tx;
-  if (c >= tx * tpg || j >= n) return reinterpret_cast<const u32x4*>(A.zeros);
-  const uint32_t slot = slot0 + j;
-  const uint32_t row = by_token ? A.slot_tok[slot] : slot;
-  return reinterpret_cast<const u32x4*>(src + ((uint64_t)row * tx + tau) * row_bytes + col0 +
-                                        kg * kSegCols);
+struct GemmArgs {
+  const uint8_t* base;
+  uint64_t stride;
+  uint64_t off[9];
+  uint32_t hidden, inter;
+  const uint32_t* codebook;
+  const GroupedHdr* hdr;
+  const Tile* tiles;
+  const uint32_t* slot_tok;
+  const int32_t* x_sigma;
+  const uint8_t* ws;        // B rows and the zero row, addressed by 32-bit offsets from here
+  uint64_t b_off, zero_off;
+  uint8_t* aq;              // gate/up output [slot][3][inter], step order
+  float* z;                 // down output [slot][hidden]
+  float limit;
+  int32_t sigma_a;
+};
+
+// waitcnt immediate for "at most n vector memory operations outstanding" (gfx9 encoding; the
+// other counters left at their maxima)
+#define AFFX_VMCNT(n) ((((n) & 15) | (((n) >> 4) << 14)) | (0x7 << 4) | (0xF << 8))
+
+// Buffer resource over `bytes` bytes at p (raw buffer, no swizzle; reads past the end return 0).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+constexpr int kNT = 2;  // cache policy of streamed weights: non-temporal
+
+// One unit in full (fields first, then the code chunks in order): tile t of the code and field
+// planes cr, fr.
+__device__ __forceinline__ void load_unit_buf(Unit& u, __amdgpu_buffer_rsrc_t cr, __amdgpu_buffer_rsrc_t fr,
+                                              uint32_t t, uint32_t lane) {
+#pragma unroll
+  for (int q = 0; q < 3; ++q)
+    u.f[q] = __builtin_amdgcn_raw_buffer_load_b32(fr, lane * 12u, t * kTileFieldBytes + 4u * q, kNT);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < 5; ++j) {
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(cr, lane * 16u, t * kTileCodeBytes + 1024u * j, kNT);
+    u.c[4 * j] = v[0]; u.c[4 * j + 1] = v[1]; u.c[4 * j + 2] = v[2]; u.c[4 * j + 3] = v[3];
+    __builtin_amdgcn_sched_barrier(0);
+  }
 }
 
-// Sum of the tx term columns starting at this lane's column (row group of 16 lanes).
-__device__ __forceinline__ float combine_cols(float d, uint32_t tx) {
-  const float d1 = __shfl_down(d, 1, 16), d2 = __shfl_down(d, 2, 16);
-  return tx == 2 ? d + d1 * 0.0625f : d + d1 * 0.0625f + d2 * 0.00390625f;
+// Registers of a unit that the ring reloads at step M (for the next 1024 columns). Step M's
+// reloads come before its table reads (those of step M + 1), so a register is reloaded at the
+// first step after the last step whose table reads use it: code chunk j = c[4j..4j+3] (chunk 0
+// at step 1, 1 at 3, 2 at 4, 3 at 6, 4 at 7) and field dword q (f0 at 2, f1 at 5, f2 at 7). One
+// load instruction each: steps 1-6 issue one per unit, step 7 two, step 0 none.
+template <int M>
+__device__ __forceinline__ void ring_load(Unit& u, __amdgpu_buffer_rsrc_t cr, __amdgpu_buffer_rsrc_t fr, uint32_t t,
+                                          uint32_t lane) {
+  auto chunk = [&](int j) {
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(cr, lane * 16u, t * kTileCodeBytes + 1024u * j, kNT);
+    u.c[4 * j] = v[0]; u.c[4 * j + 1] = v[1]; u.c[4 * j + 2] = v[2]; u.c[4 * j + 3] = v[3];
+  };
+  auto field = [&](int q) {
+    u.f[q] = __builtin_amdgcn_raw_buffer_load_b32(fr, lane * 12u, t * kTileFieldBytes + 4u * q, kNT);
+  };
+  if constexpr (M == 1) chunk(0);
+  if constexpr (M == 2) field(0);
+  if constexpr (M == 3) chunk(1);
+  if constexpr (M == 4) chunk(2);
+  if constexpr (M == 5) field(1);
+  if constexpr (M == 6) chunk(3);
+  if constexpr (M == 7) { chunk(4); field(2); }
 }
 
-// ------------------------------------------------------------------------------------------------
-// gate/up + SwiGLU
-// ------------------------------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) grouped_gateup_kernel(GroupedArgs A) {
-  const uint32_t tile_id = blockIdx.y;
-  if (tile_id >= A.hdr->n_tiles1) return;
-  const Tile tl = A.tiles1[tile_id];
-  const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const uint32_t rt = blockIdx.x * 4 + wv;  // 16-row tile of the inter dimension
-  const uint32_t nst = A.hidden / kTileCols, tx = A.tx, tpg = A.tpg1;
-  const uint32_t ng = (tl.n + tpg - 1) / tpg;
+template <int PH, int TX>
+__global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
+  constexpr int TPG = 16 / TX;  // tokens per 16-column tile
+  // XCD-aware order: the device hands consecutive workgroups to its 8 XCDs in turn, so workgroup
+  // w runs on XCD w % 8. All row blocks of one token tile go to the same XCD (its L2 then holds
+  // the tile's activations for all of them), consecutive tiles to different XCDs.
+  const uint32_t nrb = PH == 0 ? A.inter / 128u : A.hidden / 256u;  // row blocks
+  const uint32_t w = blockIdx.x, xcd = w & 7u, l = w >> 3;
+  const uint32_t rb = l % nrb, tile_id = (l / nrb) * 8u + xcd;
+  const uint32_t n_tiles = PH == 0 ? A.hdr->n_tiles1 : A.hdr->n_tiles2;
+  if (tile_id >= n_tiles) return;
+  const Tile tl = A.tiles[tile_id];
+  const uint32_t tid = threadIdx.x, lane = tid & 63;
+  const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t K = PH == 0 ? A.hidden : A.inter;
+  const uint32_t nst = K / kTileCols;
   const uint8_t* ex = A.base + (uint64_t)tl.expert * A.stride;
 
-  __shared__ uint32_t tbl[4 * kLut];
-  Unit ug, uu;
-  load_unit(ug, ex + A.off[kGateCodes], ex + A.off[kGateFields], (uint64_t)rt * nst, lane);
-  load_unit(uu, ex + A.off[kUpCodes], ex + A.off[kUpFields], (uint64_t)rt * nst, lane);
-  build_table(tbl, A.codebook);
-  __syncthreads();
+  __shared__ __align__(16) uint32_t lut_s[kGKC * 2048];
+  // B of step t in buffer t % 4, written three steps ahead (four separate arrays: the compiler
+  // can then tell the buffer being read from the ones being written)
+  __shared__ __align__(16) uint8_t buf0[kGBuf];
+  __shared__ __align__(16) uint8_t buf1[kGBuf];
+  __shared__ __align__(16) uint8_t buf2[kGBuf];
+  __shared__ __align__(16) uint8_t buf3[kGBuf];
+  uint32_t* rowoff = reinterpret_cast<uint32_t*>(buf3);  // set-up only, before buffer 3 is written
+  const uint8_t* lut = reinterpret_cast<const uint8_t*>(lut_s);
 
-  v4f acc[2][kGroups];
+  // ---- set-up: codebook copies, B row of every column, first step of B, first units ----------
+  {
+    uint32_t cbv[8];
 #pragma unroll
-  for (int g = 0; g < kGroups; ++g) acc[0][g] = acc[1][g] = v4f{0.f, 0.f, 0.f, 0.f};
-
-  for (uint32_t S = 0; S < nst; ++S) {
-    if (S > 0) {
-      load_unit(ug, ex + A.off[kGateCodes], ex + A.off[kGateFields], (uint64_t)rt * nst + S, lane);
-      load_unit(uu, ex + A.off[kUpCodes], ex + A.off[kUpFields], (uint64_t)rt * nst + S, lane);
-    }
-    const u32x4* bp[kGroups];
-#pragma unroll
-    for (int g = 0; g < kGroups; ++g)
-      bp[g] = group_b(A, A.xq, A.hidden, tx, tpg, tl.slot0, tl.n, g, lane, (uint64_t)S * kTileCols, true);
-#pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      pin(ug);
-      pin(uu);
-      const v8i ag = decode_step(ug, tbl, m), au = decode_step(uu, tbl, m);
-#pragma unroll
-      for (int g = 0; g < kGroups; ++g) {
-        if ((uint32_t)g < ng) {
-          const v8i b = b_step(bp[g], m);
-          acc[0][g] = mfma(ag, b, acc[0][g]);
-          acc[1][g] = mfma(au, b, acc[1][g]);
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
+    for (int i = 0; i < 8; ++i) cbv[i] = A.codebook[tid + 256u * i];
+    build_lut<kGKC, kGT, 8>(lut_s, cbv, tid);
   }
-
-  // epilogue: lane (col c, row group q) holds rows 16*rt + 4q + v
-  const uint32_t c = lane & 15, q = lane >> 4;
-  const uint32_t row0 = rt * 16 + 4 * q;
-  const uint2 rgv = *reinterpret_cast<const uint2*>(ex + A.off[kGateRs] + (uint64_t)row0 * 2);
-  const uint2 ruv = *reinterpret_cast<const uint2*>(ex + A.off[kUpRs] + (uint64_t)row0 * 2);
-  const float rg[4] = {__uint_as_float(rgv.x << 16), __uint_as_float(rgv.x & 0xFFFF0000u),
-                       __uint_as_float(rgv.y << 16), __uint_as_float(rgv.y & 0xFFFF0000u)};
-  const float ru[4] = {__uint_as_float(ruv.x << 16), __uint_as_float(ruv.x & 0xFFFF0000u),
-                       __uint_as_float(ruv.y << 16), __uint_as_float(ruv.y & 0xFFFF0000u)};
-  const float L = A.limit;
-#pragma unroll
-  for (int g = 0; g < kGroups; ++g) {
-    float sg[4], su[4];
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      sg[v] = combine_cols(acc[0][g][v], tx);
-      su[v] = combine_cols(acc[1][g][v], tx);
-    }
-    const uint32_t j = g * tpg + c / tx;
-    if ((uint32_t)g < ng && c % tx == 0 && c < tx * tpg && j < tl.n) {
+  if (tid < kGCols) {
+    const uint32_t col = tid, cc = col & 15;
+    const uint32_t j = (col >> 4) * TPG + cc / TX, tau = cc % TX;
+    uint64_t off = A.zero_off;
+    if (cc < TX * TPG && j < tl.n) {
       const uint32_t slot = tl.slot0 + j;
-      const int sig = A.x_sigma[A.slot_tok[slot]];
-      uint32_t o0 = 0, o1 = 0, o2 = 0;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        float gv = ldexpf(sg[v], -sig) * rg[v];
-        float uv = ldexpf(su[v], -sig) * ru[v];
-        gv = (L < gv) ? L : gv;  // SwiGLU with the asymmetric clamp: src/engine/ops.cpp:47-60
-        const float lo = (-L < uv) ? uv : -L;
-        uv = (lo < L) ? lo : L;
-        const float a = (gv / (1.0f + expf(-gv))) * uv;
-        uint32_t b0, b1, b2;
-        split3(ldexpf(a, A.sigma_a), b0, b1, b2);
-        o0 |= b0 << (8 * v);
-        o1 |= b1 << (8 * v);
-        o2 |= b2 << (8 * v);
-      }
-      uint8_t* dst = A.aq + (uint64_t)slot * 3 * A.inter + row0;
-      *reinterpret_cast<uint32_t*>(dst) = o0;
-      *reinterpret_cast<uint32_t*>(dst + A.inter) = o1;
-      *reinterpret_cast<uint32_t*>(dst + 2 * (uint64_t)A.inter) = o2;
+      const uint32_t row = PH == 0 ? A.slot_tok[slot] : slot;
+      off = A.b_off + ((uint64_t)row * TX + tau) * K;
     }
+    rowoff[col] = (uint32_t)off;
   }
-}
-
-// ------------------------------------------------------------------------------------------------
-// down: z[slot][row] = rs_d[row] * sum_k W_d[row][k] * a[slot][k]
-// ------------------------------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) grouped_down_kernel(GroupedArgs A) {
-  const uint32_t tile_id = blockIdx.y;
-  if (tile_id >= A.hdr->n_tiles2) return;
-  const Tile tl = A.tiles2[tile_id];
-  const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const uint32_t rt = blockIdx.x * 4 + wv;  // 16-row tile of the hidden dimension
-  const uint32_t nst = A.inter / kTileCols, tpg = A.tpg2;
-  const uint32_t ng = (tl.n + tpg - 1) / tpg;
-  const uint8_t* ex = A.base + (uint64_t)tl.expert * A.stride;
-
-  __shared__ uint32_t tbl[4 * kLut];
-  Unit ud;
-  load_unit(ud, ex + A.off[kDownCodes], ex + A.off[kDownFields], (uint64_t)rt * nst, lane);
-  build_table(tbl, A.codebook);
   __syncthreads();
-
-  v4f acc[kGroups];
+  // DMA lane map: instruction i of wave w writes columns 8b..8b+7 (b = kGDma w + i), lane l to
+  // LDS slot l & 7 of column 8b + (l >> 3); slot p of column col holds global chunk p ^ f(col),
+  // f(col) = (col >> 1) & 7.
+  uint32_t roff[kGDma];
 #pragma unroll
-  for (int g = 0; g < kGroups; ++g) acc[g] = v4f{0.f, 0.f, 0.f, 0.f};
-  for (uint32_t S = 0; S < nst; ++S) {
-    if (S > 0) load_unit(ud, ex + A.off[kDownCodes], ex + A.off[kDownFields], (uint64_t)rt * nst + S, lane);
-    const u32x4* bp[kGroups];
-#pragma unroll
-    for (int g = 0; g < kGroups; ++g)
-      bp[g] = group_b(A, A.aq, A.inter, 3, tpg, tl.slot0, tl.n, g, lane, (uint64_t)S * kTileCols, false);
-#pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      pin(ud);
-      const v8i a = decode_step(ud, tbl, m);
-#pragma unroll
-      for (int g = 0; g < kGroups; ++g)
-        if ((uint32_t)g < ng) acc[g] = mfma(a, b_step(bp[g], m), acc[g]);
-      __builtin_amdgcn_sched_barrier(0);
-    }
+  for (int i = 0; i < kGDma; ++i) {
+    const uint32_t col = 8u * (kGDma * wv + i) + (lane >> 3);
+    const uint32_t q = (lane & 7u) ^ ((col >> 1) & 7u);
+    roff[i] = rowoff[col] + (q << 4);
   }
-  const uint32_t c = lane & 15, q = lane >> 4;
-  const uint32_t row0 = rt * 16 + 4 * q;
-  const uint2 rdv = *reinterpret_cast<const uint2*>(ex + A.off[kDownRs] + (uint64_t)row0 * 2);
-  const float rd[4] = {__uint_as_float(rdv.x << 16), __uint_as_float(rdv.x & 0xFFFF0000u),
-                       __uint_as_float(rdv.y << 16), __uint_as_float(rdv.y & 0xFFFF0000u)};
+  const __amdgpu_buffer_rsrc_t wsr = buffer_rsrc(A.ws, 0xFFFFFFFFu);
+  auto dma = [&](uint8_t* buf, uint32_t step) {
 #pragma unroll
-  for (int g = 0; g < kGroups; ++g) {
-    float s[4];
+    for (int i = 0; i < kGDma; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(wsr, AFFX_LDS_PTR(buf + (kGDma * wv + i) * 1024u), 16, roff[i],
+                                               step * 128u, 0, 0);
+  };
+
+  // the wave's four 16-row tiles: gate/up = gate rt0, rt0 + 1 (units 0, 1) and the same rows of
+  // up (units 2, 3); down = four consecutive tiles. Unit r's code/field planes: (c0, f0) for
+  // r < 2 or down, (c1, f1) for the up units.
+  const uint64_t cbytes = (uint64_t)(PH == 0 ? A.inter : A.hidden) * code_row_bytes(K);
+  const uint64_t fbytes = (uint64_t)(PH == 0 ? A.inter : A.hidden) * field_row_bytes(K);
+  const __amdgpu_buffer_rsrc_t c0 = buffer_rsrc(ex + A.off[PH == 0 ? kGateCodes : kDownCodes], (uint32_t)cbytes);
+  const __amdgpu_buffer_rsrc_t f0 = buffer_rsrc(ex + A.off[PH == 0 ? kGateFields : kDownFields], (uint32_t)fbytes);
+  const __amdgpu_buffer_rsrc_t c1 = buffer_rsrc(ex + A.off[PH == 0 ? kUpCodes : kDownCodes], (uint32_t)cbytes);
+  const __amdgpu_buffer_rsrc_t f1 = buffer_rsrc(ex + A.off[PH == 0 ? kUpFields : kDownFields], (uint32_t)fbytes);
+  const uint32_t rt0 = PH == 0 ? rb * 8u + 2u * wv : rb * 16u + 4u * wv;
+  auto rt_of = [&](int r) -> uint32_t { return PH == 0 ? rt0 + (r & 1) : rt0 + r; };
+  const uint32_t nsteps = nst * 8u;
+  dma(buf0, 0);
+  dma(buf1, 1);
+  dma(buf2, 2);
+  Unit u[4];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) s[v] = combine_cols(acc[g][v], 3);
-    const uint32_t j = g * tpg + c / 3;
-    if ((uint32_t)g < ng && c % 3 == 0 && c < 3 * tpg && j < tl.n) {
-      float4 o;
-      o.x = ldexpf(s[0], -A.sigma_a) * rd[0];
-      o.y = ldexpf(s[1], -A.sigma_a) * rd[1];
-      o.z = ldexpf(s[2], -A.sigma_a) * rd[2];
-      o.w = ldexpf(s[3], -A.sigma_a) * rd[3];
-      *reinterpret_cast<float4*>(A.z + (uint64_t)(tl.slot0 + j) * A.hidden + row0) = o;
+  for (int r = 0; r < 4; ++r)
+    load_unit_buf(u[r], PH == 0 && r >= 2 ? c1 : c0, PH == 0 && r >= 2 ? f1 : f0, rt_of(r) * nst, lane);
+  __builtin_amdgcn_s_waitcnt(AFFX_VMCNT(0));
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+
+  const uint32_t copy4 = ((lane >> 1) & (kGKC - 1)) * 4u;
+  const uint32_t c = lane & 15, kg = lane >> 4;
+  const uint32_t bo0 = c * 128u + (((2u * kg) ^ (c >> 1)) << 4);
+  const uint32_t bo1 = c * 128u + (((2u * kg + 1u) ^ (c >> 1)) << 4);
+
+  v8i a_cur[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    uint32_t raw[8], fb[2];
+    lut_lookup_step<kGKC>(u[r], lut, copy4, 0, raw, fb);
+    a_cur[r] = lut_finish(raw, fb);
+  }
+  v4f acc[4][kGCT];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int ct = 0; ct < kGCT; ++ct) acc[r][ct] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  // ---- main loop: 1024 columns of K per iteration, eight MFMA steps ---------------------------
+  // (each step is instantiated with its index as a constant: the ring loads, the code positions
+  // and the wait counts of a step are all fixed at compile time)
+  auto bufsel = [&](int i) -> uint8_t* { return i == 0 ? buf0 : i == 1 ? buf1 : i == 2 ? buf2 : buf3; };
+  auto step = [&](auto mc, uint32_t s, bool more) {
+    constexpr int m = decltype(mc)::value;
+    const uint8_t* bcur = bufsel(m & 3);
+    // B of step t + 3, issued every step (past the last step it reloads the last step's B into
+    // a buffer nobody reads again: the count of loads in flight stays the same every step)
+    const uint32_t t3 = s * 8u + m + 3u;
+    dma(bufsel((m + 3) & 3), t3 < nsteps ? t3 : nsteps - 1u);
+    __builtin_amdgcn_sched_barrier(0);
+    // ring loads for the next 1024 columns; after the last ones, the same loads of tile 0 (hot
+    // in the cache, read by every workgroup): their registers are not read again, and issuing
+    // them keeps the count of loads in flight the same on every path
+    if constexpr (m != 0) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        ring_load<m>(u[r], PH == 0 && r >= 2 ? c1 : c0, PH == 0 && r >= 2 ? f1 : f0,
+                     more ? rt_of(r) * nst + s + 1 : 0u, lane);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    // The step is 12 groups, one per B column tile: the tile's two fragment reads go out two
+    // groups ahead, its four MFMAs are each followed by a share of the VALU work of the next step
+    // (groups 0-3: code addresses and table reads of unit g; groups 6-9: the sign/scale finish of
+    // unit g - 6, whose reads were issued four groups earlier), so that with one wave per SIMD
+    // the VALU runs while the matrix core works through the MFMAs. (Step 0 of the next 1024
+    // columns after step 7: the ring has reloaded every register those reads use.)
+    constexpr int mn = (m + 1) & 7;
+    uint32_t rawn[4][8], fbn[4][2];
+    v8i a_next[4];
+    auto bread = [&](int ct) -> v8i {
+      const u32x4 lo = *reinterpret_cast<const u32x4*>(bcur + ct * 2048 + bo0);
+      const u32x4 hi = *reinterpret_cast<const u32x4*>(bcur + ct * 2048 + bo1);
+      v8i b;
+      b[0] = (int)lo[0]; b[1] = (int)lo[1]; b[2] = (int)lo[2]; b[3] = (int)lo[3];
+      b[4] = (int)hi[0]; b[5] = (int)hi[1]; b[6] = (int)hi[2]; b[7] = (int)hi[3];
+      return b;
+    };
+    v8i bq0 = bread(0), bq1 = bread(1);
+    static_for<0, kGCT>([&](auto cc) {
+      constexpr int ct = decltype(cc)::value;
+      v8i bq2;
+      if constexpr (ct + 2 < kGCT) bq2 = bread(ct + 2);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r][ct] = mfma(a_cur[r], bq0, acc[r][ct]);
+      if constexpr (ct < 4) {
+        pin_step<mn>(u[ct]);
+        lut_lookup<kGKC, mn>(u[ct], lut, copy4, rawn[ct], fbn[ct]);
+      } else if constexpr (ct >= 6 && ct < 10) {
+        a_next[ct - 6] = lut_finish(rawn[ct - 6], fbn[ct - 6]);
+        AFFX_PIN(a_next[ct - 6]);  // computed here, not sunk into the next step
+      }
+      // four times {one MFMA, then VALU}, then the LDS reads
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x100, 10, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      bq0 = bq1;
+      if constexpr (ct + 2 < kGCT) bq1 = bq2;
+    });
+    // the accumulators are materialised here, in the AGPRs (else the compiler sinks every MFMA
+    // below all eight steps' table reads and holds those in registers)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int ct = 0; ct < kGCT; ++ct) AFFX_PIN_ACC(acc[r][ct]);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) a_cur[r] = a_next[r];
+    // The next step's B (issued at the top of step t - 2) is in LDS once every wave's loads up to
+    // it have landed: loads complete in issue order, so at most the loads issued after it may
+    // still be outstanding: two B loads and the ring loads of steps t - 2 .. t (4 units x
+    // {0,1,1,1,1,1,1,2} by step). (In the first two steps more were issued after it: waiting for
+    // fewer is then only stricter.)
+    {
+      constexpr int c[8] = {0, 1, 1, 1, 1, 1, 1, 2};
+      constexpr int k = 2 * kGDma + 4 * (c[(m + 6) & 7] + c[(m + 7) & 7] + c[m]);
+      __builtin_amdgcn_s_waitcnt(AFFX_VMCNT(k));
+    }
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  for (uint32_t s = 0; s < nst; ++s) {
+    const bool more = s + 1 < nst;
+    step(IConst<0>{}, s, more);
+    step(IConst<1>{}, s, more);
+    step(IConst<2>{}, s, more);
+    step(IConst<3>{}, s, more);
+    step(IConst<4>{}, s, more);
+    step(IConst<5>{}, s, more);
+    step(IConst<6>{}, s, more);
+    step(IConst<7>{}, s, more);
+  }
+  __builtin_amdgcn_s_waitcnt(AFFX_VMCNT(0));  // no direct-to-LDS load outlives the loop
+
+  // ---- epilogue ---------------------------------------------------------------------------------
+  // accumulator lane (c, kg), element v = D[4 kg + v][c]: row 4 kg + v of the row tile, column c.
+  // (Every accumulator index is a compile-time constant: a runtime index would put the whole
+  // accumulator array in scratch memory.)
+  auto terms = [&](float d) -> float {
+    const float d1 = __shfl_down(d, 1, 16);
+    if constexpr (TX == 2) {
+      return d + d1 * 0.0625f;
+    } else {
+      const float d2 = __shfl_down(d, 2, 16);
+      return d + d1 * 0.0625f + d2 * 0.00390625f;
+    }
+  };
+  auto bf16x4 = [](uint2 v, float (&o)[4]) {
+    o[0] = __uint_as_float(v.x << 16);
+    o[1] = __uint_as_float(v.x & 0xFFFF0000u);
+    o[2] = __uint_as_float(v.y << 16);
+    o[3] = __uint_as_float(v.y & 0xFFFF0000u);
+  };
+  if constexpr (PH == 0) {
+    const float L = A.limit;
+    static_for<0, 2>([&](auto pc) {
+      constexpr int p = decltype(pc)::value;
+      const uint32_t row0 = rt_of(p) * 16u + 4u * kg;
+      float rg[4], ru[4];
+      bf16x4(*reinterpret_cast<const uint2*>(ex + A.off[kGateRs] + (uint64_t)row0 * 2), rg);
+      bf16x4(*reinterpret_cast<const uint2*>(ex + A.off[kUpRs] + (uint64_t)row0 * 2), ru);
+      const uint32_t prow = kperm(row0);
+      static_for<0, kGCT>([&](auto cc) {
+        constexpr int ct = decltype(cc)::value;
+        float sg[4], su[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          sg[v] = terms(acc[p][ct][v]);
+          su[v] = terms(acc[p + 2][ct][v]);
+        }
+        const uint32_t j = ct * TPG + c / TX;
+        if (c % TX == 0 && c < TX * TPG && j < tl.n) {
+          const uint32_t slot = tl.slot0 + j;
+          const int sig = A.x_sigma[A.slot_tok[slot]];
+          float a[4];
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            float gv = ldexpf(sg[v], -sig) * rg[v];
+            float uv = ldexpf(su[v], -sig) * ru[v];
+            gv = (L < gv) ? L : gv;  // SwiGLU with the asymmetric clamp: src/engine/ops.cpp:47-60
+            const float lo = (-L < uv) ? uv : -L;
+            uv = (lo < L) ? lo : L;
+            a[v] = ldexpf((gv / (1.0f + expf(-gv))) * uv, A.sigma_a);
+          }
+          uint32_t o0, o1, o2;
+          split3x4(a[0], a[1], a[2], a[3], o0, o1, o2);
+          uint8_t* dst = A.aq + (uint64_t)slot * 3 * A.inter + prow;
+          *reinterpret_cast<uint32_t*>(dst) = o0;
+          *reinterpret_cast<uint32_t*>(dst + A.inter) = o1;
+          *reinterpret_cast<uint32_t*>(dst + 2 * (uint64_t)A.inter) = o2;
+        }
+      });
+    });
+  } else {
+    static_for<0, 4>([&](auto rc) {
+      constexpr int r = decltype(rc)::value;
+      const uint32_t row0 = rt_of(r) * 16u + 4u * kg;
+      float rd[4];
+      bf16x4(*reinterpret_cast<const uint2*>(ex + A.off[kDownRs] + (uint64_t)row0 * 2), rd);
+      static_for<0, kGCT>([&](auto cc) {
+        constexpr int ct = decltype(cc)::value;
+        float sd[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) sd[v] = terms(acc[r][ct][v]);
+        const uint32_t j = ct * TPG + c / TX;
+        if (c % TX == 0 && c < TX * TPG && j < tl.n) {
+          float4 o;
+          o.x = ldexpf(sd[0], -A.sigma_a) * rd[0];
+          o.y = ldexpf(sd[1], -A.sigma_a) * rd[1];
+          o.z = ldexpf(sd[2], -A.sigma_a) * rd[2];
+          o.w = ldexpf(sd[3], -A.sigma_a) * rd[3];
+          *reinterpret_cast<float4*>(A.z + (uint64_t)(tl.slot0 + j) * A.hidden + row0) = o;
+        }
+      });
+    });
   }
 }
 
@@ -395,10 +583,13 @@ struct GroupedWs {
   uint32_t max_tiles1, max_tiles2;
 };
 
-GroupedWs grouped_ws(uint32_t T, uint32_t K, uint32_t E, uint32_t hidden, uint32_t inter,
-                     uint32_t tt1, uint32_t tt2) {
+// tokens per workgroup tile: 16 column tiles of 16 / terms tokens each
+uint32_t tile_tokens(uint32_t terms) { return kGCT * (16 / terms); }
+
+GroupedWs grouped_ws(uint32_t T, uint32_t K, uint32_t E, uint32_t hidden, uint32_t inter, uint32_t tx) {
   GroupedWs w;
   const uint64_t P = (uint64_t)T * K;
+  const uint32_t tt1 = tile_tokens(tx), tt2 = tile_tokens(3);
   w.max_tiles1 = (uint32_t)(P / tt1 + E + 1);
   w.max_tiles2 = (uint32_t)(P / tt2 + E + 1);
   uint64_t o = 0;
@@ -409,16 +600,13 @@ GroupedWs grouped_ws(uint32_t T, uint32_t K, uint32_t E, uint32_t hidden, uint32
   w.tiles1 = o; o += a256(sizeof(Tile) * w.max_tiles1);
   w.tiles2 = o; o += a256(sizeof(Tile) * w.max_tiles2);
   w.sigma = o; o += a256(4ull * T);
-  w.zeros = o; o += 256;
-  w.xq = o; o += a256((uint64_t)T * 3 * hidden);
+  w.zeros = o; o += a256(hidden > inter ? hidden : inter);
+  w.xq = o; o += a256((uint64_t)T * tx * hidden);
   w.aq = o; o += a256(P * 3 * inter);
   w.z = o; o += a256(P * 4 * hidden);
   w.total = o;
   return w;
 }
-
-// tokens per tile: kGroups column blocks of 16/terms tokens each
-uint32_t tpg_of(uint32_t terms) { return 16 / terms; }
 
 }  // namespace
 
@@ -426,9 +614,8 @@ extern "C" {
 
 size_t affx_grouped_workspace_size(uint32_t n_tok, uint32_t top_k, uint32_t n_experts,
                                    uint32_t hidden, uint32_t inter) {
-  // sized for the 3-term gate/up input, which needs the most tiles
-  return (size_t)grouped_ws(n_tok, top_k, n_experts, hidden, inter, kGroups * tpg_of(3),
-                            kGroups * tpg_of(3)).total;
+  // sized for the 3-term gate/up input (x with a low part), the larger layout
+  return (size_t)grouped_ws(n_tok, top_k, n_experts, hidden, inter, 3).total;
 }
 
 int affx_expert_ffn_grouped(const affx_layer* L, const void* x, const void* x_lo, uint32_t T,
@@ -440,15 +627,16 @@ int affx_expert_ffn_grouped(const affx_layer* L, const void* x, const void* x_lo
   if (K == 0 || K > AFFX_MAX_TOPK || L->n_experts == 0 || L->n_experts > AFFX_MAX_EXPERTS)
     return set_error(AFFX_DECLINED, "ffn_grouped: top_k must be 1..%d and n_experts 1..%d",
                      AFFX_MAX_TOPK, AFFX_MAX_EXPERTS);
-  if (L->hidden % kTileCols || L->inter % kTileCols || L->hidden % 64 || L->inter % 64 ||
-      L->hidden == 0 || L->inter == 0)
-    return set_error(AFFX_DECLINED, "ffn_grouped: hidden and inter must be multiples of 1024");
+  if (L->hidden % kTileCols || L->inter % kTileCols || L->hidden == 0 || L->inter == 0 ||
+      L->hidden > 8192 || L->inter > 8192)
+    return set_error(AFFX_DECLINED, "ffn_grouped: hidden and inter must be multiples of 1024, at most 8192");
   if (!(L->swiglu_limit > 0.f) || L->swiglu_limit > 1e6f)
     return set_error(AFFX_DECLINED, "ffn_grouped: needs a SwiGLU clamp limit in (0, 1e6]");
-  if ((uint64_t)T * K > (1ull << 31)) return set_error(AFFX_DECLINED, "ffn_grouped: batch too large");
   const uint32_t tx = x_lo ? 3 : 2;
-  const uint32_t tt1 = kGroups * tpg_of(tx), tt2 = kGroups * tpg_of(3);
-  const GroupedWs lay = grouped_ws(T, K, L->n_experts, L->hidden, L->inter, tt1, tt2);
+  const GroupedWs lay = grouped_ws(T, K, L->n_experts, L->hidden, L->inter, tx);
+  // the GEMM addresses its B rows with 32-bit offsets into the workspace
+  if ((uint64_t)T * K > (1ull << 31) || lay.aq + (uint64_t)T * K * 3 * L->inter > (1ull << 32))
+    return set_error(AFFX_DECLINED, "ffn_grouped: batch too large (split it)");
   if (ws_bytes < lay.total)
     return set_error(AFFX_ERR_ARG, "ffn_grouped: workspace %zu < %llu bytes", ws_bytes,
                      (unsigned long long)lay.total);
@@ -458,34 +646,25 @@ int affx_expert_ffn_grouped(const affx_layer* L, const void* x, const void* x_lo
 
   uint8_t* b = (uint8_t*)ws;
   hipStream_t s = (hipStream_t)stream;
-  GroupedArgs A;
+  GemmArgs A;
   A.base = (const uint8_t*)L->base;
   A.stride = L->stride;
   for (int i = 0; i < 9; ++i) A.off[i] = off9[i];
   A.hidden = L->hidden;
   A.inter = L->inter;
-  A.n_experts = L->n_experts;
-  A.n_tok = T;
-  A.top_k = K;
   A.codebook = (const uint32_t*)L->codebook;
   A.hdr = (const GroupedHdr*)(b + lay.hdr);
-  A.offsets = (const uint32_t*)(b + lay.offsets);
   A.slot_tok = (const uint32_t*)(b + lay.slot_tok);
-  A.slot_of = (const int32_t*)(b + lay.slot_of);
-  A.tiles1 = (const Tile*)(b + lay.tiles1);
-  A.tiles2 = (const Tile*)(b + lay.tiles2);
   A.x_sigma = (const int32_t*)(b + lay.sigma);
-  A.xq = b + lay.xq;
+  A.ws = b;
+  A.zero_off = lay.zeros;
   A.aq = b + lay.aq;
   A.z = (float*)(b + lay.z);
-  A.zeros = b + lay.zeros;
   A.limit = L->swiglu_limit;
   A.sigma_a = 7 - ilogbf(L->swiglu_limit * L->swiglu_limit);
-  A.tx = tx;
-  A.tpg1 = tpg_of(tx);
-  A.tpg2 = tpg_of(3);
 
   const uint32_t P = T * K;
+  const uint32_t tt1 = tile_tokens(tx), tt2 = tile_tokens(3);
   hipLaunchKernelGGL(grouped_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, sel, P, L->n_experts,
                      tt1, tt2, tx, (GroupedHdr*)(b + lay.hdr), (uint32_t*)(b + lay.offsets),
                      (Tile*)(b + lay.tiles1), (Tile*)(b + lay.tiles2));
@@ -495,14 +674,26 @@ int affx_expert_ffn_grouped(const affx_layer* L, const void* x, const void* x_lo
                      L->n_experts, (const uint32_t*)(b + lay.offsets), (uint32_t*)(b + lay.slot_tok),
                      (int32_t*)(b + lay.slot_of));
   if ((rc = check_launch("grouped_place_kernel"))) return rc;
+  const uint32_t zmax = L->hidden > L->inter ? L->hidden : L->inter;
   hipLaunchKernelGGL(grouped_prep_x_kernel, dim3(T), dim3(256), 0, s, (const uint16_t*)x,
                      (const uint16_t*)x_lo, L->hidden, tx, (int32_t*)(b + lay.sigma), b + lay.xq,
-                     (uint32_t*)(b + lay.zeros));
+                     (uint32_t*)(b + lay.zeros), zmax / 4);
   if ((rc = check_launch("grouped_prep_x_kernel"))) return rc;
-  hipLaunchKernelGGL(grouped_gateup_kernel, dim3(L->inter / 64, lay.max_tiles1), dim3(256), 0, s, A);
-  if ((rc = check_launch("grouped_gateup_kernel"))) return rc;
-  hipLaunchKernelGGL(grouped_down_kernel, dim3(L->hidden / 64, lay.max_tiles2), dim3(256), 0, s, A);
-  if ((rc = check_launch("grouped_down_kernel"))) return rc;
+  // gate/up: 128 gate + 128 up rows per workgroup; down: 256 rows. One workgroup per (row
+  // block, tile), the tile count rounded up to a multiple of the 8 XCDs (see the kernel's order)
+  const uint32_t g1 = (L->inter / 128) * ((lay.max_tiles1 + 7) / 8 * 8);
+  const uint32_t g2 = (L->hidden / 256) * ((lay.max_tiles2 + 7) / 8 * 8);
+  A.tiles = (const Tile*)(b + lay.tiles1);
+  A.b_off = lay.xq;
+  if (tx == 2)
+    hipLaunchKernelGGL((grouped_gemm_kernel<0, 2>), dim3(g1), dim3(kGT), 0, s, A);
+  else
+    hipLaunchKernelGGL((grouped_gemm_kernel<0, 3>), dim3(g1), dim3(kGT), 0, s, A);
+  if ((rc = check_launch("grouped_gemm_kernel (gate/up)"))) return rc;
+  A.tiles = (const Tile*)(b + lay.tiles2);
+  A.b_off = lay.aq;
+  hipLaunchKernelGGL((grouped_gemm_kernel<1, 3>), dim3(g2), dim3(kGT), 0, s, A);
+  if ((rc = check_launch("grouped_gemm_kernel (down)"))) return rc;
   hipLaunchKernelGGL(grouped_combine_kernel, dim3((L->hidden / 4 + 255) / 256, T), dim3(256), 0, s,
                      (const float*)(b + lay.z), (const int32_t*)(b + lay.slot_of), w, K, L->hidden,
                      y, accumulate);

@@ -1,0 +1,185 @@
+// The replicated LDS codebook and the A-fragment decode shared by the one-launch decode and the
+// grouped prefill GEMM: a lane's unit (one row's 256-column segment) is looked up code by code in
+// one of KC interleaved copies of the codebook and turned into an E4M3 MFMA A fragment.
+#pragma once
+
+#include "affx_tile.h"
+
+namespace affx {
+
+// ---- replicated codebook -------------------------------------------------------------------------
+// KC interleaved copies of the 2 x 1024 codebook dwords: entry (variant v, code c) of copy j at
+// dword ((v << 10 | c) * KC + j). A lane reads copy (lane >> 1) % KC, so the 64 gathers of one
+// instruction spread over the banks by lane instead of colliding at random.
+template <int KC>
+struct Lut {
+  static constexpr int kLog = KC == 16 ? 4 : KC == 8 ? 3 : 2;
+  static constexpr int kCodeSh = kLog + 2;       // byte-address bit of code bit 0
+  static constexpr int kVarSh = kCodeSh + 10;    // byte-address bit of the variant
+};
+
+// (thread i0 of NT: entries i0 + NT * i, i < N; cbv[i] = codebook dword of that entry)
+template <int KC, int NT, int N>
+__device__ __forceinline__ void build_lut(uint32_t* tbl, const uint32_t (&cbv)[N], uint32_t i0) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const uint32_t e = i0 + (uint32_t)i * NT;
+    if (e >= 2048u) break;
+    const uint32_t d = cbv[i];
+    const u32x4 v = {d, d, d, d};
+    u32x4* dst = reinterpret_cast<u32x4*>(tbl + e * KC);
+#pragma unroll
+    for (int q = 0; q < KC / 4; ++q) dst[q] = v;
+  }
+}
+
+// LDS byte address of code I (0..63) of the unit: the code's ten bits are brought to bit kCodeSh
+// of an alignbit window and inserted into vb (the block's variant and the lane's copy; bits
+// outside the code field come from vb).
+template <int KC, int I>
+__device__ __forceinline__ uint32_t code_addr(const uint32_t (&c)[20], uint32_t vb) {
+  constexpr int S = Lut<KC>::kCodeSh;
+  constexpr int q = 10 * I - S;
+  uint32_t x;
+  if constexpr (q < 0) {
+    x = __builtin_amdgcn_alignbit(c[0], c[0], q + 32);
+  } else {
+    constexpr int lo = q >> 5, sh = q & 31;
+    constexpr int hi = (sh + S + 10 > 32 && lo + 1 < 20) ? lo + 1 : lo;
+    x = sh == 0 ? c[lo] : __builtin_amdgcn_alignbit(c[hi], c[lo], sh);
+  }
+  return (x & (0x3FFu << S)) | vb;
+}
+
+// The eight table reads of MFMA step MSTEP (blocks 2m, 2m+1) and the two blocks' 6-bit fields
+// (bits 0-2 exponent add s, 3 sign, 4 rotation, 5 variant).
+template <int KC, int MSTEP>
+__device__ __forceinline__ void lut_lookup(const Unit& u, const uint8_t* lds, uint32_t copy4,
+                                           uint32_t (&raw)[8], uint32_t (&fb)[2]) {
+  fb[0] = stream_bits<3>(u.f, 12 * MSTEP, 6);
+  fb[1] = stream_bits<3>(u.f, 12 * MSTEP + 6, 6);
+  const uint32_t vb0 = ((fb[0] >> 5) << Lut<KC>::kVarSh) | copy4;
+  const uint32_t vb1 = ((fb[1] >> 5) << Lut<KC>::kVarSh) | copy4;
+  constexpr int I = 8 * MSTEP;
+  raw[0] = *reinterpret_cast<const uint32_t*>(lds + code_addr<KC, I + 0>(u.c, vb0));
+  raw[1] = *reinterpret_cast<const uint32_t*>(lds + code_addr<KC, I + 1>(u.c, vb0));
+  raw[2] = *reinterpret_cast<const uint32_t*>(lds + code_addr<KC, I + 2>(u.c, vb0));
+  raw[3] = *reinterpret_cast<const uint32_t*>(lds + code_addr<KC, I + 3>(u.c, vb0));
+  raw[4] = *reinterpret_cast<const uint32_t*>(lds + code_addr<KC, I + 4>(u.c, vb1));
+  raw[5] = *reinterpret_cast<const uint32_t*>(lds + code_addr<KC, I + 5>(u.c, vb1));
+  raw[6] = *reinterpret_cast<const uint32_t*>(lds + code_addr<KC, I + 6>(u.c, vb1));
+  raw[7] = *reinterpret_cast<const uint32_t*>(lds + code_addr<KC, I + 7>(u.c, vb1));
+}
+
+// A fragment from the table reads: rotation by table-entry halves, sign flip, exponent add
+// (src/gpu/expert_kernel.hip:594-617; rotation src/quant/blockquant.cpp:826-828).
+__device__ __forceinline__ v8i lut_finish(const uint32_t (&raw)[8], const uint32_t (&fb)[2]) {
+  v8i a;
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    // exponent add s << 3 replicated into the four bytes (v_perm: no 32-bit multiply)
+    const uint32_t rsh = fb[b] & 16u, xm = block_xor(fb[b]);
+    const uint32_t ad = __builtin_amdgcn_perm(0u, (fb[b] << 3) & 0x38u, 0u);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t r = __builtin_amdgcn_alignbit(raw[4 * b + i], raw[4 * b + i], rsh);
+      a[4 * b + i] = (int)((r ^ xm) + ad);
+    }
+  }
+  return a;
+}
+
+template <int KC>
+__device__ __forceinline__ void lut_lookup_step(const Unit& u, const uint8_t* lds, uint32_t copy4,
+                                                int m, uint32_t (&raw)[8], uint32_t (&fb)[2]) {
+  switch (m) {
+    case 0: lut_lookup<KC, 0>(u, lds, copy4, raw, fb); break;
+    case 1: lut_lookup<KC, 1>(u, lds, copy4, raw, fb); break;
+    case 2: lut_lookup<KC, 2>(u, lds, copy4, raw, fb); break;
+    case 3: lut_lookup<KC, 3>(u, lds, copy4, raw, fb); break;
+    case 4: lut_lookup<KC, 4>(u, lds, copy4, raw, fb); break;
+    case 5: lut_lookup<KC, 5>(u, lds, copy4, raw, fb); break;
+    case 6: lut_lookup<KC, 6>(u, lds, copy4, raw, fb); break;
+    default: lut_lookup<KC, 7>(u, lds, copy4, raw, fb); break;
+  }
+}
+
+// Makes opaque, at the top of MFMA step MSTEP, only the registers that step reads (the code
+// dwords of codes 8m..8m+7 with their alignbit neighbours, the field dwords of blocks 2m, 2m+1):
+// the step's extraction cannot be hoisted above it, and the step waits only for the load chunks
+// it needs (chunk j = code dwords 4j..4j+3; loads complete in issue order).
+template <int MSTEP>
+__device__ __forceinline__ void pin_step(Unit& u) {
+  constexpr int k0 = (80 * MSTEP - 6) < 0 ? 0 : (80 * MSTEP - 6) >> 5;
+  constexpr int k1 = (80 * MSTEP + 79) >> 5 > 19 ? 19 : (80 * MSTEP + 79) >> 5;
+#pragma unroll
+  for (int k = k0; k <= k1; ++k) AFFX_PIN(u.c[k]);
+  AFFX_PIN(u.f[(12 * MSTEP) >> 5]);
+  if constexpr (((12 * MSTEP + 11) >> 5) != ((12 * MSTEP) >> 5)) AFFX_PIN(u.f[(12 * MSTEP + 11) >> 5]);
+}
+
+__device__ __forceinline__ void pin_step(Unit& u, int m) {
+  switch (m) {
+    case 0: pin_step<0>(u); break;
+    case 1: pin_step<1>(u); break;
+    case 2: pin_step<2>(u); break;
+    case 3: pin_step<3>(u); break;
+    case 4: pin_step<4>(u); break;
+    case 5: pin_step<5>(u); break;
+    case 6: pin_step<6>(u); break;
+    default: pin_step<7>(u); break;
+  }
+}
+
+// One unit, fields first, then the code chunks in order.
+__device__ __forceinline__ void load_unit_ordered(Unit& u, const uint8_t* codes, const uint8_t* fields,
+                                                  uint64_t tile, uint32_t lane) {
+  const uint32_t* fp = reinterpret_cast<const uint32_t*>(fields + tile * kTileFieldBytes + lane * 12);
+  u.f[0] = __builtin_nontemporal_load(fp);
+  u.f[1] = __builtin_nontemporal_load(fp + 1);
+  u.f[2] = __builtin_nontemporal_load(fp + 2);
+  __builtin_amdgcn_sched_barrier(0);
+  const uint8_t* cp = codes + tile * kTileCodeBytes + lane * 16;
+#pragma unroll
+  for (int j = 0; j < 5; ++j) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(cp + j * 1024));
+    u.c[4 * j] = v[0]; u.c[4 * j + 1] = v[1]; u.c[4 * j + 2] = v[2]; u.c[4 * j + 3] = v[3];
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// Three E4M3 terms of four values (|v| < 256) with the hardware conversion (round to nearest
+// even, identical to f32_to_e4m3 in this range): returns the packed bytes of each term.
+__device__ __forceinline__ void split3x4(float v0, float v1, float v2, float v3, uint32_t& q0,
+                                         uint32_t& q1, uint32_t& q2) {
+  typedef float v2f __attribute__((ext_vector_type(2)));
+  uint32_t t = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v0, v1, 0, false);
+  t = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v2, v3, (int)t, true);
+  q0 = t;
+  v2f a = __builtin_amdgcn_cvt_pk_f32_fp8((int)t, false), b = __builtin_amdgcn_cvt_pk_f32_fp8((int)t, true);
+  v0 = (v0 - a.x) * 16.0f; v1 = (v1 - a.y) * 16.0f; v2 = (v2 - b.x) * 16.0f; v3 = (v3 - b.y) * 16.0f;
+  t = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v0, v1, 0, false);
+  t = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v2, v3, (int)t, true);
+  q1 = t;
+  a = __builtin_amdgcn_cvt_pk_f32_fp8((int)t, false);
+  b = __builtin_amdgcn_cvt_pk_f32_fp8((int)t, true);
+  v0 = (v0 - a.x) * 16.0f; v1 = (v1 - a.y) * 16.0f; v2 = (v2 - b.x) * 16.0f; v3 = (v3 - b.y) * 16.0f;
+  t = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v0, v1, 0, false);
+  t = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v2, v3, (int)t, true);
+  q2 = t;
+}
+
+// Calls f(IConst<I>{}) for I = B .. E-1: a loop whose index is a compile-time constant in the body.
+template <int N>
+struct IConst {
+  static constexpr int value = N;
+};
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(IConst<B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+}  // namespace affx

@@ -85,6 +85,7 @@ inline uint32_t __builtin_amdgcn_perm(uint32_t s0, uint32_t s1, uint32_t sel) {
   return out;
 }
 #define __builtin_amdgcn_sched_barrier(x) ((void)0)
+#define __builtin_amdgcn_sched_group_barrier(m, n, id) ((void)0)
 #define __builtin_amdgcn_s_sleep(x) std::this_thread::yield()
 #define __builtin_amdgcn_s_waitcnt(x) std::atomic_thread_fence(std::memory_order_seq_cst)
 // __hip_atomic_* are clang builtins on the host too; their scope constants are clang's
@@ -104,6 +105,7 @@ struct EmuBlock {
 };
 extern thread_local EmuBlock* emu_blk;
 inline void __syncthreads() { emu_blk->block_bar->arrive_and_wait(); }
+inline void __builtin_amdgcn_s_barrier() { __syncthreads(); }
 inline uint32_t emu_lane() { return threadIdx.x & 63; }
 inline uint32_t emu_wave() { return threadIdx.x >> 6; }
 inline void emu_wave_sync() { emu_blk->wave_bar[emu_wave()]->arrive_and_wait(); }
@@ -137,6 +139,31 @@ inline uint64_t __ballot(int pred) {
 inline uint32_t atomicOr(uint32_t* p, uint32_t v) { return __atomic_fetch_or(p, v, __ATOMIC_SEQ_CST); }
 inline uint32_t atomicAdd(uint32_t* p, uint32_t v) { return __atomic_fetch_add(p, v, __ATOMIC_SEQ_CST); }
 inline uint32_t min(uint32_t a, uint32_t b) { return a < b ? a : b; }
+
+// ---- buffer resources and direct global->LDS loads ----
+// A raw buffer resource is a base and a byte count; a read past the count returns zeros, as on
+// the device. A direct-to-LDS load writes lane l's `size` bytes at lds + off + l * size.
+struct emu_rsrc { const uint8_t* base; uint32_t n; };
+#define __amdgpu_buffer_rsrc_t emu_rsrc
+inline emu_rsrc __builtin_amdgcn_make_buffer_rsrc(void* p, short, int n, int) { return {(const uint8_t*)p, (uint32_t)n}; }
+template <typename T> inline T emu_buf_load(emu_rsrc r, uint32_t voff, uint32_t soff) {
+  T v;
+  const uint64_t o = (uint64_t)voff + soff;
+  if (o + sizeof(T) > r.n) { memset(&v, 0, sizeof(T)); return v; }
+  memcpy(&v, r.base + o, sizeof(T));
+  return v;
+}
+typedef uint32_t emu_u32x4 __attribute__((ext_vector_type(4)));
+inline uint32_t __builtin_amdgcn_raw_buffer_load_b32(emu_rsrc r, uint32_t v, uint32_t s, int) { return emu_buf_load<uint32_t>(r, v, s); }
+inline emu_u32x4 __builtin_amdgcn_raw_buffer_load_b128(emu_rsrc r, uint32_t v, uint32_t s, int) { return emu_buf_load<emu_u32x4>(r, v, s); }
+inline void __builtin_amdgcn_raw_ptr_buffer_load_lds(emu_rsrc r, void* lds, int size, uint32_t v, uint32_t s, int off, int) {
+  const uint64_t o = (uint64_t)v + s;
+  uint8_t* dst = (uint8_t*)lds + off + (threadIdx.x & 63) * size;
+  if (o + size > r.n) memset(dst, 0, size); else memcpy(dst, r.base + o, size);
+}
+#define AFFX_LDS_PTR(p) ((void*)(p))
+#define AFFX_PIN_ACC(x) ((void)0)
+inline void __builtin_amdgcn_s_barrier();
 
 // ---- MFMA 16x16x128 fp8 x fp8 -> f32, lane layout as on gfx950 ----
 typedef int emu_v8i __attribute__((ext_vector_type(8)));
