@@ -71,6 +71,10 @@ struct DecodePlan {
 #define AFFX_TRACE_INIT ((void)0)
 #endif
 
+// waitcnt immediate for "at most n vector memory operations outstanding" (gfx9 encoding; the
+// other counters left at their maxima)
+#define AFFX_VMCNT(n) ((((n) & 15) | (((n) >> 4) << 14)) | (0x7 << 4) | (0xF << 8))
+
 // Dynamic LDS of a kernel (one byte array; the kernel carves it up).
 #ifndef AFFX_DYN_LDS
 #define AFFX_DYN_LDS(name) extern __shared__ __align__(16) uint8_t name[]

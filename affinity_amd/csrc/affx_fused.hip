@@ -68,9 +68,8 @@ __host__ __device__ inline FusedLds fused_lds(uint32_t M) {
   L.part = L.zero + 256u;
   const uint32_t part_bytes = (uint32_t)kFW * 2u * 16u * M * 4u;  // gate/up [wave][mat][row][tok]
   L.plan = L.part + part_bytes;
-  // rank[128] w[128] slot_expert[128] slot_mask[128] rs[12][32] sigma[32] present[16] prefix[16]
-  // misc[4] slot_w[128][M]
-  L.total = L.plan + (4u * kPlanRoutes + kFW * 32u + 32u + 16u + 16u + 4u) * 4u + kPlanRoutes * M * 4u;
+  // slot_expert[128] slot_mask[128] rs[12][32] sigma[32] slot_w[128][M]
+  L.total = L.plan + (2u * kPlanRoutes + kFW * 32u + 32u) * 4u + kPlanRoutes * M * 4u;
   return L;
 }
 
@@ -125,11 +124,12 @@ __device__ __forceinline__ float wave_max(float v) {
 // ------------------------------------------------------------------------------------------------
 // The kernel. CG: 16-column groups of the MFMA B operand (5 tokens each). KC: codebook copies.
 // MAXM: largest M this instantiation serves (sizes the per-thread activation registers).
-// The down weights of the first unit are prefetched during gate/up when CG = 1. SINGLE: at most
+// The down weights of the first unit are prefetched before the wait when CG = 1. SINGLE: at most
 // one gate/up item and one down unit (per output tile) per wave, which keeps those two phases
-// loop-free (batch 1).
+// loop-free (batch 1). ROT: the codebook copies include the rotated tables (one VALU op less
+// per code, twice the LDS).
 // ------------------------------------------------------------------------------------------------
-template <int CG, int KC, int MAXM, bool SINGLE>
+template <int CG, int KC, int MAXM, bool SINGLE, bool ROT>
 __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   AFFX_DYN_LDS(lds);
   // the first down unit is loaded while gate/up runs (one column group leaves the registers)
@@ -141,21 +141,16 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   const uint32_t M = A.M, K = A.K, R = M * K;
   const uint32_t nst = A.hidden / kTileCols, nsi = A.inter / kTileCols;
   const FusedLds L = fused_lds(M);
-  __shared__ __align__(16) uint32_t lut_s[KC * 2048];
+  __shared__ __align__(16) uint32_t lut_s[Lut<KC, ROT>::kDwords];
   const uint8_t* lut = reinterpret_cast<const uint8_t*>(lut_s);
   uint8_t* xq = lds + L.xq;
   uint8_t* zero_l = lds + L.zero;
   float* part = reinterpret_cast<float*>(lds + L.part);
-  uint32_t* rank_l = reinterpret_cast<uint32_t*>(lds + L.plan);
-  float* w_l = reinterpret_cast<float*>(rank_l + kPlanRoutes);
-  uint32_t* slot_expert = reinterpret_cast<uint32_t*>(w_l + kPlanRoutes);
+  uint32_t* slot_expert = reinterpret_cast<uint32_t*>(lds + L.plan);
   uint32_t* slot_mask = slot_expert + kPlanRoutes;
   float* rs_l = reinterpret_cast<float*>(slot_mask + kPlanRoutes);  // [group][gate 16 | up 16]
   int32_t* sigma_l = reinterpret_cast<int32_t*>(rs_l + kFW * 32);
-  uint32_t* present = reinterpret_cast<uint32_t*>(sigma_l + 32);
-  uint32_t* prefix_l = present + 16;
-  uint32_t* misc = prefix_l + 16;
-  float* slot_w = reinterpret_cast<float*>(misc + 4);
+  float* slot_w = reinterpret_cast<float*>(sigma_l + 32);
 
   AFFX_TRACE_INIT;
   AFFX_TRACE(0);
@@ -284,52 +279,35 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   const uint32_t epi_waves = (groups * 16 * M + 63) / 64;
   load_gu(rounds > 0 ? gu_item(0) : ~0u);
   AFFX_TRACE(13);
-  // (SINGLE: rounds <= 1 always, so no branch around the load for the wait tracking to merge)
-  if (PREF && (SINGLE || rounds <= 1)) load_down(has_down, g, wv);
   AFFX_TRACE(2);
 
-  if (wv == 0) {
-    // (after this wave's loads are out) the plan for the epilogue and the down phase: slot of every route (that of its expert's
-    // first occurrence), expert of every slot, per (slot, token) summed weights and token masks
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const uint32_t r = lane + 64u * h;
-      uint32_t rank = ~0u;
-      for (uint32_t j = 0; j < R; ++j) {  // all lanes (cross-lane reads in uniform control flow)
-        const uint32_t ej = j < 64 ? __builtin_amdgcn_readlane(e[0], j) : __builtin_amdgcn_readlane(e[1], j - 64);
-        const uint32_t fj = j < 64 ? __builtin_amdgcn_readlane((uint32_t)first[0], j)
-                                   : __builtin_amdgcn_readlane((uint32_t)first[1], j - 64);
-        const uint32_t sj = j < 64 ? __builtin_amdgcn_readlane(fslot0, j) : __builtin_amdgcn_readlane(fslot1, j - 64);
-        rank = (fj && e[h] != ~0u && ej == e[h]) ? sj : rank;
-      }
-      if (r < R) {
-        rank_l[r] = rank;
-        w_l[r] = wr[h];
-      }
-      if (first[h]) slot_expert[h ? fslot1 : fslot0] = e[h];
+  // ---- the plan for the epilogue and the down phase, spread over the waves (slot s by wave
+  // s % 12, registers and cross-lane reads only): expert of the slot, token mask, and per token
+  // the summed weight of its routes to the slot, added in route order (as the staged plan does)
+  for (uint32_t sl = wv; sl < ns; sl += kFW) {
+    const uint32_t ex = slot_expert_of(sl);
+    // lane t < M sums the weights of routes t*K .. t*K + K - 1 that name this expert
+    float ws = 0.f;
+    bool hit = false;
+    for (uint32_t j = 0; j < K; ++j) {
+      const uint32_t r = lane * K + j;                       // route of token `lane`
+      const uint32_t src = (r & 63u) * 4u;                   // bpermute byte index
+      const uint32_t e0 = (uint32_t)__builtin_amdgcn_ds_bpermute((int)src, (int)e[0]);
+      const uint32_t e1 = (uint32_t)__builtin_amdgcn_ds_bpermute((int)src, (int)e[1]);
+      const float w0 = __int_as_float(__builtin_amdgcn_ds_bpermute((int)src, __float_as_int(wr[0])));
+      const float w1 = __int_as_float(__builtin_amdgcn_ds_bpermute((int)src, __float_as_int(wr[1])));
+      const bool m = lane < M && (r < 64u ? e0 : e1) == ex;
+      ws += m ? (r < 64u ? w0 : w1) : 0.f;
+      hit = hit || m;
     }
-    slot_mask[lane] = 0;
-    slot_mask[lane + 64] = 0;
-    if (lane == 0) misc[0] = ns;
-    __builtin_amdgcn_wave_barrier();
-    // per (slot, token): summed weight of its routes in route order, and the token masks
-    for (uint32_t p = lane; p < ns * M; p += 64) {
-      const uint32_t s = p / M, t = p % M;
-      float ws = 0.f;
-      bool hit = false;
-#pragma unroll
-      for (uint32_t j = 0; j < (uint32_t)AFFX_MAX_TOPK; ++j) {
-        const uint32_t jj = j < K ? j : K - 1;  // in bounds; j >= K contributes nothing
-        const bool m = j < K && rank_l[t * K + jj] == s;
-        const float wj = w_l[t * K + jj];
-        ws += m ? wj : 0.f;
-        hit = hit || m;
-      }
-      slot_w[p] = ws;
-      if (hit) atomicOr(&slot_mask[s], 1u << t);
+    const uint32_t mk = (uint32_t)__ballot(hit);  // bit t: token t has a route to this expert
+    if (lane == 0) {
+      slot_expert[sl] = ex;
+      slot_mask[sl] = mk;
     }
-    AFFX_TRACE(9);
+    if (lane < M) slot_w[sl * M + lane] = ws;
   }
+  AFFX_TRACE(9);
 
   // ---- 3. activation terms and codebook copies into LDS, from the registers loaded up front:
   // a pair's maximum (wave reduction) fixes its exponent, then three E4M3 terms per element
@@ -358,7 +336,7 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
       }
     }
   }
-  build_lut<KC, kFT, 3>(lut_s, cbv, tid);
+  build_lut<KC, kFT, 3, ROT>(lut_s, cbv, tid);
   if (tid < 64) reinterpret_cast<uint32_t*>(zero_l)[tid] = 0u;
   __syncthreads();  // plan, activation terms and codebook copies visible
   AFFX_TRACE(1);
@@ -371,10 +349,7 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   const uint32_t n_rounds = SINGLE ? (rounds > 0 ? 1u : 0u) : rounds;
   for (uint32_t rho = 0; rho < n_rounds; ++rho) {
     const uint32_t item = gu_item(rho);
-    if (rho > 0) {
-      load_gu(item);
-      if (PREF && rho == rounds - 1) load_down(has_down, g, wv);
-    }
+    if (rho > 0) load_gu(item);
     v4f acc[2][CG];
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm)
@@ -394,8 +369,8 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
       uint32_t bg[2], bu[2];
       pin_step(ug, 0);
       pin_step(uu, 0);
-      lut_lookup_step<KC>(ug, lut, copy4, 0, rg, bg);
-      lut_lookup_step<KC>(uu, lut, copy4, 0, ru, bu);
+      lut_lookup_step<KC, ROT>(ug, lut, copy4, 0, rg, bg);
+      lut_lookup_step<KC, ROT>(uu, lut, copy4, 0, ru, bu);
       v8i bc[CG];
 #pragma unroll
       for (int cg = 0; cg < CG; ++cg) bc[cg] = b_step_lds(bsrc[cg], 0);
@@ -409,12 +384,12 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
           for (int cg = 0; cg < CG; ++cg) { AFFX_PIN(acc[0][cg]); AFFX_PIN(acc[1][cg]); }
           pin_step(ug, m + 1);
           pin_step(uu, m + 1);
-          lut_lookup_step<KC>(ug, lut, copy4, m + 1, ng, nbg);
-          lut_lookup_step<KC>(uu, lut, copy4, m + 1, nu, nbu);
+          lut_lookup_step<KC, ROT>(ug, lut, copy4, m + 1, ng, nbg);
+          lut_lookup_step<KC, ROT>(uu, lut, copy4, m + 1, nu, nbu);
 #pragma unroll
           for (int cg = 0; cg < CG; ++cg) bn[cg] = b_step_lds(bsrc[cg], m + 1);
         }
-        const v8i ag = lut_finish(rg, bg), au = lut_finish(ru, bu);
+        const v8i ag = lut_finish<ROT>(rg, bg), au = lut_finish<ROT>(ru, bu);
 #pragma unroll
         for (int cg = 0; cg < CG; ++cg) {
           acc[0][cg] = mfma(ag, bc[cg], acc[0][cg]);
@@ -496,11 +471,20 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
     } else {
       for (uint32_t et = et0; et < groups * 16 * M; et += kFT) epilogue(et);
     }
-    // publish: every wave that stored drains its memory counter (its device-coherent stores have
-    // completed), the barrier orders that before thread 0's counter update. No release fence: its
-    // L2 write-back, once per workgroup and serialised per L2, costs microseconds, and nothing
-    // else written here is read by other workgroups.
-    if (wv < epi_waves) __builtin_amdgcn_s_waitcnt(0);
+    // The first down unit's weights are loaded now, after this workgroup's gate/up data has
+    // arrived (issued earlier they would share the HBM stream with it and delay gate/up), so
+    // they stream in while the layer publishes and waits. Publish: every wave that stored drains
+    // its device-coherent stores (loads and stores complete in issue order: at most the 7 or more
+    // down-unit loads issued after them may stay outstanding), the barrier orders that before
+    // thread 0's counter update. No release fence: its L2 write-back, once per workgroup and
+    // serialised per L2, costs microseconds, and nothing else written here is read by other
+    // workgroups.
+    if (PREF && rho + 1 == n_rounds) {
+      load_down(has_down, g, wv);
+      if (wv < epi_waves) __builtin_amdgcn_s_waitcnt(AFFX_VMCNT(7));
+    } else {
+      if (wv < epi_waves) __builtin_amdgcn_s_waitcnt(0);
+    }
     AFFX_TRACE(10);
     __syncthreads();
     if (wv == 0) {
@@ -526,6 +510,7 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
     }
   }
 
+  if (PREF && n_rounds == 0) load_down(has_down, g, wv);  // no gate/up item here
   AFFX_TRACE(4);
   // ---- 5. wait for every gate/up item (this workgroup's flag), then the down tiles -------------
   if (g < dtiles) {
@@ -554,7 +539,7 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
         for (int v = 0; v < 4; ++v) yacc[cg][v] = 0.f;
 #pragma unroll 1
       for (uint32_t u = wv; u < (SINGLE ? (wv < NU ? wv + 1 : 0u) : NU); u += kFW) {
-        if (!(PREF && td == g && u == wv)) load_down(true, td, u);  // else loaded during gate/up
+        if (!(PREF && td == g && u == wv)) load_down(true, td, u);  // else loaded before the wait
         const uint32_t slot = u / nsi, S2 = u % nsi;
         const uint32_t e = __builtin_amdgcn_readfirstlane(slot_expert[slot]);
         const uint32_t mask = __builtin_amdgcn_readfirstlane(slot_mask[slot]);
@@ -583,7 +568,7 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
         uint32_t raw[8];
         uint32_t bv[2];
         pin_step(ud, 0);
-        lut_lookup_step<KC>(ud, lut, copy4, 0, raw, bv);
+        lut_lookup_step<KC, ROT>(ud, lut, copy4, 0, raw, bv);
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
           uint32_t nraw[8];
@@ -595,13 +580,13 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
 #pragma unroll
             for (int cg = 0; cg < CG; ++cg) AFFX_PIN(acc[cg]);
             pin_step(ud, m + 1);
-            lut_lookup_step<KC>(ud, lut, copy4, m + 1, nraw, nbv);
+            lut_lookup_step<KC, ROT>(ud, lut, copy4, m + 1, nraw, nbv);
             if constexpr (!BPRE) {
 #pragma unroll
               for (int cg = 0; cg < CG; ++cg) bn[cg] = b_step(b.p[cg], m + 1);
             }
           }
-          const v8i a = lut_finish(raw, bv);
+          const v8i a = lut_finish<ROT>(raw, bv);
           if constexpr (BPRE) {
             acc[0] = mfma(a, bpre[m], acc[0]);
           } else {
@@ -679,7 +664,7 @@ constexpr int kMaxDev = 64;
 std::mutex g_fused_mu;
 FusedVariant g_fused[kMaxDev][4];
 
-// variants: 0 M = 1 in one pass (16 codebook copies), 1 M = 1 in rounds, 2 M <= 5 (8 copies),
+// variants: 0 M = 1 in one pass (8 codebook copies with rotated tables), 1 M = 1 in rounds, 2 M <= 5 (8 copies),
 // 3 M <= 8 (4 copies, 2 column groups)
 int fused_variant(uint32_t M, bool single) { return M == 1 ? (single ? 0 : 1) : M <= 5 ? 2 : 3; }
 
@@ -687,11 +672,11 @@ int fused_prepare(int dev, int v, FusedVariant* out) {
   std::lock_guard<std::mutex> lk(g_fused_mu);
   FusedVariant& f = g_fused[dev][v];
   if (!f.ready) {
-    static const void* fns[4] = {(const void*)decode_fused_kernel<1, 16, 1, true>,
-                                 (const void*)decode_fused_kernel<1, 16, 1, false>,
-                                 (const void*)decode_fused_kernel<1, 8, 5, false>,
-                                 (const void*)decode_fused_kernel<2, 4, 8, false>};
-    static const uint32_t kcs[4] = {16, 16, 8, 4}, maxms[4] = {1, 1, 5, 8};
+    static const void* fns[4] = {(const void*)decode_fused_kernel<1, 8, 1, true, true>,
+                                 (const void*)decode_fused_kernel<1, 8, 1, false, true>,
+                                 (const void*)decode_fused_kernel<1, 8, 5, false, false>,
+                                 (const void*)decode_fused_kernel<2, 4, 8, false, false>};
+    static const uint32_t kcs[4] = {8, 8, 8, 4}, maxms[4] = {1, 1, 5, 8};
     f.fn = fns[v];
     f.kc = kcs[v];
     f.maxm = maxms[v];
@@ -781,10 +766,10 @@ extern "C" int affx_expert_ffn_decode(const affx_layer* L, const float* x, uint6
   // the down B operand's unused columns read the workspace's zero run: zero in a zero-filled
   // workspace and only ever rewritten with zeros (by the staged prep kernel)
   switch (v) {
-    case 0: hipLaunchKernelGGL((decode_fused_kernel<1, 16, 1, true>), dim3(n_wg), dim3(kFT), lds, st, A); break;
-    case 1: hipLaunchKernelGGL((decode_fused_kernel<1, 16, 1, false>), dim3(n_wg), dim3(kFT), lds, st, A); break;
-    case 2: hipLaunchKernelGGL((decode_fused_kernel<1, 8, 5, false>), dim3(n_wg), dim3(kFT), lds, st, A); break;
-    default: hipLaunchKernelGGL((decode_fused_kernel<2, 4, 8, false>), dim3(n_wg), dim3(kFT), lds, st, A); break;
+    case 0: hipLaunchKernelGGL((decode_fused_kernel<1, 8, 1, true, true>), dim3(n_wg), dim3(kFT), lds, st, A); break;
+    case 1: hipLaunchKernelGGL((decode_fused_kernel<1, 8, 1, false, true>), dim3(n_wg), dim3(kFT), lds, st, A); break;
+    case 2: hipLaunchKernelGGL((decode_fused_kernel<1, 8, 5, false, false>), dim3(n_wg), dim3(kFT), lds, st, A); break;
+    default: hipLaunchKernelGGL((decode_fused_kernel<2, 4, 8, false, false>), dim3(n_wg), dim3(kFT), lds, st, A); break;
   }
   return check_launch("decode_fused_kernel");
 }

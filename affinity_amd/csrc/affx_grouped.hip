@@ -208,9 +208,6 @@ struct GemmArgs {
   int32_t sigma_a;
 };
 
-// waitcnt immediate for "at most n vector memory operations outstanding" (gfx9 encoding; the
-// other counters left at their maxima)
-#define AFFX_VMCNT(n) ((((n) & 15) | (((n) >> 4) << 14)) | (0x7 << 4) | (0xF << 8))
 
 // Buffer resource over `bytes` bytes at p (raw buffer, no swizzle; reads past the end return 0).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uint32_t bytes) {

@@ -10,26 +10,44 @@ namespace affx {
 // ---- replicated codebook -------------------------------------------------------------------------
 // KC interleaved copies of the 2 x 1024 codebook dwords: entry (variant v, code c) of copy j at
 // dword ((v << 10 | c) * KC + j). A lane reads copy (lane >> 1) % KC, so the 64 gathers of one
-// instruction spread over the banks by lane instead of colliding at random.
-template <int KC>
+// instruction spread over the banks by lane instead of colliding at random. With ROT the table
+// also holds every dword pre-rotated (the block rotation of blockquant.cpp:826-828): table
+// t = 2v + rot, entry (t, c) of copy j at dword ((t << 10 | c) * KC + j), so a lookup needs no
+// rotate (twice the LDS).
+template <int KC, bool ROT = false>
 struct Lut {
-  static constexpr int kLog = KC == 16 ? 4 : KC == 8 ? 3 : 2;
+  static constexpr int kLog = KC == 16 ? 4 : KC == 8 ? 3 : KC == 4 ? 2 : 1;
   static constexpr int kCodeSh = kLog + 2;       // byte-address bit of code bit 0
-  static constexpr int kVarSh = kCodeSh + 10;    // byte-address bit of the variant
+  static constexpr int kVarSh = kCodeSh + 10;    // byte-address bit of the table index
+  static constexpr int kDwords = KC * (ROT ? 4096 : 2048);
 };
 
 // (thread i0 of NT: entries i0 + NT * i, i < N; cbv[i] = codebook dword of that entry)
-template <int KC, int NT, int N>
+template <int KC, int NT, int N, bool ROT = false>
 __device__ __forceinline__ void build_lut(uint32_t* tbl, const uint32_t (&cbv)[N], uint32_t i0) {
 #pragma unroll
   for (int i = 0; i < N; ++i) {
     const uint32_t e = i0 + (uint32_t)i * NT;
     if (e >= 2048u) break;
     const uint32_t d = cbv[i];
-    const u32x4 v = {d, d, d, d};
-    u32x4* dst = reinterpret_cast<u32x4*>(tbl + e * KC);
+    auto put = [&](uint32_t idx, uint32_t val) {
+      if constexpr (KC >= 4) {
+        const u32x4 v = {val, val, val, val};
+        u32x4* dst = reinterpret_cast<u32x4*>(tbl + idx * KC);
 #pragma unroll
-    for (int q = 0; q < KC / 4; ++q) dst[q] = v;
+        for (int q = 0; q < KC / 4; ++q) dst[q] = v;
+      } else {
+#pragma unroll
+        for (int q = 0; q < KC; ++q) tbl[idx * KC + q] = val;
+      }
+    };
+    if constexpr (ROT) {
+      const uint32_t v = e >> 10, c = e & 1023u;
+      put((2u * v) << 10 | c, d);
+      put((2u * v + 1u) << 10 | c, __builtin_amdgcn_alignbit(d, d, 16));
+    } else {
+      put(e, d);
+    }
   }
 }
 
@@ -38,7 +56,7 @@ __device__ __forceinline__ void build_lut(uint32_t* tbl, const uint32_t (&cbv)[N
 // outside the code field come from vb).
 template <int KC, int I>
 __device__ __forceinline__ uint32_t code_addr(const uint32_t (&c)[20], uint32_t vb) {
-  constexpr int S = Lut<KC>::kCodeSh;
+  constexpr int S = Lut<KC>::kCodeSh;  // (the same with or without rotated tables)
   constexpr int q = 10 * I - S;
   uint32_t x;
   if constexpr (q < 0) {
@@ -53,13 +71,14 @@ __device__ __forceinline__ uint32_t code_addr(const uint32_t (&c)[20], uint32_t 
 
 // The eight table reads of MFMA step MSTEP (blocks 2m, 2m+1) and the two blocks' 6-bit fields
 // (bits 0-2 exponent add s, 3 sign, 4 rotation, 5 variant).
-template <int KC, int MSTEP>
+template <int KC, int MSTEP, bool ROT = false>
 __device__ __forceinline__ void lut_lookup(const Unit& u, const uint8_t* lds, uint32_t copy4,
                                            uint32_t (&raw)[8], uint32_t (&fb)[2]) {
   fb[0] = stream_bits<3>(u.f, 12 * MSTEP, 6);
   fb[1] = stream_bits<3>(u.f, 12 * MSTEP + 6, 6);
-  const uint32_t vb0 = ((fb[0] >> 5) << Lut<KC>::kVarSh) | copy4;
-  const uint32_t vb1 = ((fb[1] >> 5) << Lut<KC>::kVarSh) | copy4;
+  // table: variant (field bit 5), or 2 * variant + rotation (bits 4-5) with rotated tables
+  const uint32_t vb0 = ((ROT ? (fb[0] >> 4) & 3u : fb[0] >> 5) << Lut<KC>::kVarSh) | copy4;
+  const uint32_t vb1 = ((ROT ? (fb[1] >> 4) & 3u : fb[1] >> 5) << Lut<KC>::kVarSh) | copy4;
   constexpr int I = 8 * MSTEP;
   raw[0] = *reinterpret_cast<const uint32_t*>(lds + code_addr<KC, I + 0>(u.c, vb0));
   raw[1] = *reinterpret_cast<const uint32_t*>(lds + code_addr<KC, I + 1>(u.c, vb0));
@@ -73,34 +92,36 @@ __device__ __forceinline__ void lut_lookup(const Unit& u, const uint8_t* lds, ui
 
 // A fragment from the table reads: rotation by table-entry halves, sign flip, exponent add
 // (src/gpu/expert_kernel.hip:594-617; rotation src/quant/blockquant.cpp:826-828).
+// (ROT: the reads came from pre-rotated tables)
+template <bool ROT = false>
 __device__ __forceinline__ v8i lut_finish(const uint32_t (&raw)[8], const uint32_t (&fb)[2]) {
   v8i a;
 #pragma unroll
   for (int b = 0; b < 2; ++b) {
     // exponent add s << 3 replicated into the four bytes (v_perm: no 32-bit multiply)
-    const uint32_t rsh = fb[b] & 16u, xm = block_xor(fb[b]);
+    const uint32_t xm = block_xor(fb[b]);
     const uint32_t ad = __builtin_amdgcn_perm(0u, (fb[b] << 3) & 0x38u, 0u);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint32_t r = __builtin_amdgcn_alignbit(raw[4 * b + i], raw[4 * b + i], rsh);
+      const uint32_t r = ROT ? raw[4 * b + i] : __builtin_amdgcn_alignbit(raw[4 * b + i], raw[4 * b + i], fb[b] & 16u);
       a[4 * b + i] = (int)((r ^ xm) + ad);
     }
   }
   return a;
 }
 
-template <int KC>
+template <int KC, bool ROT = false>
 __device__ __forceinline__ void lut_lookup_step(const Unit& u, const uint8_t* lds, uint32_t copy4,
                                                 int m, uint32_t (&raw)[8], uint32_t (&fb)[2]) {
   switch (m) {
-    case 0: lut_lookup<KC, 0>(u, lds, copy4, raw, fb); break;
-    case 1: lut_lookup<KC, 1>(u, lds, copy4, raw, fb); break;
-    case 2: lut_lookup<KC, 2>(u, lds, copy4, raw, fb); break;
-    case 3: lut_lookup<KC, 3>(u, lds, copy4, raw, fb); break;
-    case 4: lut_lookup<KC, 4>(u, lds, copy4, raw, fb); break;
-    case 5: lut_lookup<KC, 5>(u, lds, copy4, raw, fb); break;
-    case 6: lut_lookup<KC, 6>(u, lds, copy4, raw, fb); break;
-    default: lut_lookup<KC, 7>(u, lds, copy4, raw, fb); break;
+    case 0: lut_lookup<KC, 0, ROT>(u, lds, copy4, raw, fb); break;
+    case 1: lut_lookup<KC, 1, ROT>(u, lds, copy4, raw, fb); break;
+    case 2: lut_lookup<KC, 2, ROT>(u, lds, copy4, raw, fb); break;
+    case 3: lut_lookup<KC, 3, ROT>(u, lds, copy4, raw, fb); break;
+    case 4: lut_lookup<KC, 4, ROT>(u, lds, copy4, raw, fb); break;
+    case 5: lut_lookup<KC, 5, ROT>(u, lds, copy4, raw, fb); break;
+    case 6: lut_lookup<KC, 6, ROT>(u, lds, copy4, raw, fb); break;
+    default: lut_lookup<KC, 7, ROT>(u, lds, copy4, raw, fb); break;
   }
 }
 

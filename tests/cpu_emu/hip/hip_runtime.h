@@ -61,6 +61,8 @@ inline float4 make_float4(float a, float b, float c, float d) { return {a, b, c,
 
 inline float __uint_as_float(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
 inline uint32_t __float_as_uint(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+inline float __int_as_float(int u) { float f; memcpy(&f, &u, 4); return f; }
+inline int __float_as_int(float f) { int u; memcpy(&u, &f, 4); return u; }
 inline int __popc(uint32_t v) { return __builtin_popcount(v); }
 inline int __popcll(uint64_t v) { return __builtin_popcountll(v); }
 inline float __fsub_rn(float a, float b) { volatile float r = a - b; return r; }
@@ -124,6 +126,7 @@ inline T emu_exchange(T v, uint32_t src) {
 }
 template <typename T> inline T __shfl_xor(T v, int o, int width = 64) { return emu_exchange(v, emu_lane() ^ o); }
 template <typename T> inline T __builtin_amdgcn_readlane(T v, uint32_t l) { return emu_exchange(v, l); }
+inline int __builtin_amdgcn_ds_bpermute(int addr, int v) { return emu_exchange(v, ((uint32_t)addr >> 2) & 63); }
 template <typename T> inline T __shfl_down(T v, int d, int width = 64) {
   uint32_t l = emu_lane(); uint32_t src = ((l % width) + d < (uint32_t)width) ? l + d : l;
   return emu_exchange(v, src);
