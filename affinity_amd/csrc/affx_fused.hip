@@ -196,41 +196,36 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
     }
   }
   AFFX_TRACE(8);
-  // dedupe: a route is the first occurrence of its expert if no earlier route names it (ids
-  // outside the layer are ignored, as in the staged path)
-  bool first[2];
+  // dedupe: slots are the distinct experts in order of first occurrence (ids outside the layer
+  // are ignored, as in the staged path). One pass per distinct expert over the wave's routes
+  // (route r = lane + 64 h): the lowest route not yet assigned names the next slot's expert, a
+  // ballot finds all its routes. Lane s of se[0] (se[1]) then holds the expert of slot s
+  // (s + 64).
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const uint32_t r = lane + 64u * h;
     e[h] = (r < R && e[h] < A.n_experts) ? e[h] : ~0u;
   }
+  uint32_t se[2] = {~0u, ~0u};
+  uint32_t ns = 0;
   {
-    bool dup0 = false, dup1 = false;
-    for (uint32_t j = 0; j < R; ++j) {
-      const uint32_t ej = j < 64 ? __builtin_amdgcn_readlane(e[0], j) : __builtin_amdgcn_readlane(e[1], j - 64);
-      dup0 = dup0 || (j < lane && ej == e[0]);
-      dup1 = dup1 || (j < lane + 64 && ej == e[1]);
+    uint64_t pend0 = __ballot(e[0] != ~0u), pend1 = __ballot(e[1] != ~0u);
+    while (pend0 | pend1) {
+      const uint32_t ex = pend0 ? __builtin_amdgcn_readlane(e[0], (uint32_t)__builtin_ctzll(pend0))
+                                : __builtin_amdgcn_readlane(e[1], (uint32_t)__builtin_ctzll(pend1));
+      pend0 &= ~__ballot(e[0] == ex);
+      pend1 &= ~__ballot(e[1] == ex);
+      if (lane == (ns & 63u)) {
+        if (ns < 64u) se[0] = ex;
+        else se[1] = ex;
+      }
+      ++ns;
     }
-    first[0] = e[0] != ~0u && !dup0;
-    first[1] = e[1] != ~0u && !dup1;
   }
-  const uint64_t fb0 = __ballot(first[0]), fb1 = __ballot(first[1]);
   AFFX_TRACE(12);
-  const uint32_t nf0 = __popcll(fb0);
-  const uint32_t ns = nf0 + (uint32_t)__popcll(fb1);
-  // slot of a first-occurrence route: first-occurrence routes before it
-  const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
-  const uint32_t fslot0 = (uint32_t)__popcll(fb0 & below), fslot1 = nf0 + (uint32_t)__popcll(fb1 & below);
-  // expert of slot s (s wave-uniform): the route that is its first occurrence
+  // expert of slot s (s wave-uniform)
   auto slot_expert_of = [&](uint32_t s) -> uint32_t {
-    if (s < nf0) {
-      uint64_t m = fb0;
-      for (uint32_t i = 0; i < s; ++i) m &= m - 1;  // drop the s lowest first-occurrence routes
-      return __builtin_amdgcn_readlane(e[0], (uint32_t)__builtin_ctzll(m));
-    }
-    uint64_t m = fb1;
-    for (uint32_t i = nf0; i < s; ++i) m &= m - 1;
-    return __builtin_amdgcn_readlane(e[1], (uint32_t)__builtin_ctzll(m));
+    return s < 64u ? __builtin_amdgcn_readlane(se[0], s) : __builtin_amdgcn_readlane(se[1], s - 64u);
   };
 
   const uint32_t rt_per = A.inter / kTileRows;          // gate/up row tiles per expert
@@ -349,7 +344,6 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   const uint32_t n_rounds = SINGLE ? (rounds > 0 ? 1u : 0u) : rounds;
   for (uint32_t rho = 0; rho < n_rounds; ++rho) {
     const uint32_t item = gu_item(rho);
-    if (rho > 0) load_gu(item);
     v4f acc[2][CG];
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm)
@@ -413,6 +407,11 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
       AFFX_PIN(rv);
       rs_l[q * 32 + lane] = __uint_as_float(rv << 16);
     }
+    // the next round's weights go out now (this round's are consumed), so their latency is
+    // spent on this round's epilogue
+    if constexpr (!SINGLE) {
+      if (rho + 1 < n_rounds) load_gu(gu_item(rho + 1));
+    }
     // partial sums of this wave's segment, term-combined, at the segment's exponent:
     // part[wave][mat][row][token]. Accumulator lane l, element v = D[4(l/16)+v][l%16].
 #pragma unroll
@@ -471,46 +470,42 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
     } else {
       for (uint32_t et = et0; et < groups * 16 * M; et += kFT) epilogue(et);
     }
-    // The first down unit's weights are loaded now, after this workgroup's gate/up data has
-    // arrived (issued earlier they would share the HBM stream with it and delay gate/up), so
-    // they stream in while the layer publishes and waits. Publish: every wave that stored drains
-    // its device-coherent stores (loads and stores complete in issue order: at most the 7 or more
-    // down-unit loads issued after them may stay outstanding), the barrier orders that before
-    // thread 0's counter update. No release fence: its L2 write-back, once per workgroup and
-    // serialised per L2, costs microseconds, and nothing else written here is read by other
-    // workgroups.
-    if (PREF && rho + 1 == n_rounds) {
-      load_down(has_down, g, wv);
-      if (wv < epi_waves) __builtin_amdgcn_s_waitcnt(AFFX_VMCNT(7));
-    } else {
-      if (wv < epi_waves) __builtin_amdgcn_s_waitcnt(0);
-    }
-    AFFX_TRACE(10);
-    __syncthreads();
-    if (wv == 0) {
-      const uint32_t done = my_items - rho * groups < groups ? my_items - rho * groups : groups;
-      if (rho + 1 < n_rounds) {
-        if (lane == 0) __hip_atomic_fetch_add(&A.sync[0], done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      } else {
-        // this workgroup's last round: the add that completes the count (necessarily a last
-        // round's) finds every other add performed, hence every activation store complete. Its
-        // wave clears the count for the next launch and raises the flag of each waiting workgroup
-        // (one line each: the waiters poll without contending for one address).
-        uint32_t old = 0;
-        if (lane == 0) old = __hip_atomic_fetch_add(&A.sync[0], done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        old = __builtin_amdgcn_readlane(old, 0);
-        if (old + done == NI) {
-          if (lane == 0) __hip_atomic_store(&A.sync[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          const uint32_t nwait = A.n_wg < dtiles ? A.n_wg : dtiles;
-          for (uint32_t i = lane; i < nwait; i += 64)
-            __hip_atomic_store(A.sync + (kSyncHeader + i * kSyncFlagStride) / 4, 1u, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-        }
-      }
+    if constexpr (!SINGLE) {
+      if (rho + 1 < n_rounds) __syncthreads();  // this round's partial sums read before they are rewritten
     }
   }
 
-  if (PREF && n_rounds == 0) load_down(has_down, g, wv);  // no gate/up item here
+  // The first down unit's weights are loaded now, after this workgroup's gate/up data has arrived
+  // (issued earlier they would share the HBM stream with it and delay gate/up), so they stream in
+  // while the layer publishes and waits. Publish (once, all rounds): every wave that stored
+  // drains its device-coherent stores (loads and stores complete in issue order: at most the 7
+  // or more down-unit loads issued after them may stay outstanding), the barrier orders that
+  // before thread 0's counter update. No release fence: its L2 write-back, once per workgroup
+  // and serialised per L2, costs microseconds, and nothing else written here is read by other
+  // workgroups.
+  if (PREF) {
+    load_down(has_down, g, wv);
+    if (n_rounds > 0 && wv < epi_waves) __builtin_amdgcn_s_waitcnt(AFFX_VMCNT(7));
+  } else {
+    if (n_rounds > 0 && wv < epi_waves) __builtin_amdgcn_s_waitcnt(0);
+  }
+  AFFX_TRACE(10);
+  __syncthreads();
+  if (wv == 0 && n_rounds > 0) {
+    // the add that completes the count finds every other add performed, hence every activation
+    // store complete. Its wave clears the count for the next launch and raises the flag of each
+    // waiting workgroup (one line each: the waiters poll without contending for one address).
+    uint32_t old = 0;
+    if (lane == 0) old = __hip_atomic_fetch_add(&A.sync[0], my_items, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __builtin_amdgcn_readlane(old, 0);
+    if (old + my_items == NI) {
+      if (lane == 0) __hip_atomic_store(&A.sync[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t nwait = A.n_wg < dtiles ? A.n_wg : dtiles;
+      for (uint32_t i = lane; i < nwait; i += 64)
+        __hip_atomic_store(A.sync + (kSyncHeader + i * kSyncFlagStride) / 4, 1u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
   AFFX_TRACE(4);
   // ---- 5. wait for every gate/up item (this workgroup's flag), then the down tiles -------------
   if (g < dtiles) {
