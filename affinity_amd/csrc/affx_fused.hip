@@ -207,6 +207,7 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
     e[h] = (r < R && e[h] < A.n_experts) ? e[h] : ~0u;
   }
   uint32_t se[2] = {~0u, ~0u};
+  uint32_t rslot[2] = {~0u, ~0u};  // slot of route lane + 64 h
   uint32_t ns = 0;
   {
     uint64_t pend0 = __ballot(e[0] != ~0u), pend1 = __ballot(e[1] != ~0u);
@@ -215,6 +216,8 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
                                 : __builtin_amdgcn_readlane(e[1], (uint32_t)__builtin_ctzll(pend1));
       pend0 &= ~__ballot(e[0] == ex);
       pend1 &= ~__ballot(e[1] == ex);
+      rslot[0] = e[0] == ex ? ns : rslot[0];
+      rslot[1] = e[1] == ex ? ns : rslot[1];
       if (lane == (ns & 63u)) {
         if (ns < 64u) se[0] = ex;
         else se[1] = ex;
@@ -276,31 +279,29 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   AFFX_TRACE(13);
   AFFX_TRACE(2);
 
-  // ---- the plan for the epilogue and the down phase, spread over the waves (slot s by wave
-  // s % 12, registers and cross-lane reads only): expert of the slot, token mask, and per token
-  // the summed weight of its routes to the slot, added in route order (as the staged plan does)
-  for (uint32_t sl = wv; sl < ns; sl += kFW) {
-    const uint32_t ex = slot_expert_of(sl);
-    // lane t < M sums the weights of routes t*K .. t*K + K - 1 that name this expert
-    float ws = 0.f;
-    bool hit = false;
+  // ---- the plan for the epilogue and the down phase (wave 0): expert of every slot, token
+  // masks, and per (slot, token) the summed weight of the token's routes to the slot, added in
+  // route order as the staged plan does (lane t walks token t's routes; no two lanes touch the
+  // same entry)
+  if (wv == 0) {
+    if (lane < ns) slot_expert[lane] = se[0];
+    if (lane + 64u < ns) slot_expert[lane + 64u] = se[1];
+    for (uint32_t i = lane; i < ns * M; i += 64u) slot_w[i] = 0.f;
+    for (uint32_t i = lane; i < ns; i += 64u) slot_mask[i] = 0u;
+    __builtin_amdgcn_wave_barrier();
     for (uint32_t j = 0; j < K; ++j) {
-      const uint32_t r = lane * K + j;                       // route of token `lane`
-      const uint32_t src = (r & 63u) * 4u;                   // bpermute byte index
-      const uint32_t e0 = (uint32_t)__builtin_amdgcn_ds_bpermute((int)src, (int)e[0]);
-      const uint32_t e1 = (uint32_t)__builtin_amdgcn_ds_bpermute((int)src, (int)e[1]);
+      const uint32_t r = lane * K + j;              // route j of token `lane`
+      const uint32_t src = (r & 63u) * 4u;          // bpermute byte index
+      const uint32_t s0 = (uint32_t)__builtin_amdgcn_ds_bpermute((int)src, (int)rslot[0]);
+      const uint32_t s1 = (uint32_t)__builtin_amdgcn_ds_bpermute((int)src, (int)rslot[1]);
       const float w0 = __int_as_float(__builtin_amdgcn_ds_bpermute((int)src, __float_as_int(wr[0])));
       const float w1 = __int_as_float(__builtin_amdgcn_ds_bpermute((int)src, __float_as_int(wr[1])));
-      const bool m = lane < M && (r < 64u ? e0 : e1) == ex;
-      ws += m ? (r < 64u ? w0 : w1) : 0.f;
-      hit = hit || m;
+      const uint32_t sl = r < 64u ? s0 : s1;
+      if (lane < M && sl != ~0u) {
+        slot_w[sl * M + lane] += r < 64u ? w0 : w1;
+        atomicOr(&slot_mask[sl], 1u << lane);
+      }
     }
-    const uint32_t mk = (uint32_t)__ballot(hit);  // bit t: token t has a route to this expert
-    if (lane == 0) {
-      slot_expert[sl] = ex;
-      slot_mask[sl] = mk;
-    }
-    if (lane < M) slot_w[sl * M + lane] = ws;
   }
   AFFX_TRACE(9);
 
@@ -435,7 +436,8 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
     // (a loop header here would make every wave with loads in flight wait for all of them, the
     // down prefetch included: SINGLE, with at most 12 x 16 threads busy, takes one pass)
     auto epilogue = [&](uint32_t et) {
-      const uint32_t qq = et / (16 * M), r = (et / M) % 16, t = et % M;
+      // (row fastest: the stores of 16 neighbouring lanes form one 16-byte run per term)
+      const uint32_t qq = et / (16 * M), t = (et / 16) % M, r = et % 16;
       const uint32_t k = rho * groups + qq;
       if (k < my_items) {
         const uint32_t it = g + A.n_wg * k, slot = it / rt_per, rt = it % rt_per;
