@@ -6,11 +6,12 @@
 //                    so every slot and every output sum has a fixed order
 //   grouped_prep_x   per token: exponent and E4M3 terms of the activation (2 terms are exact for
 //                    bf16 input; 3 when a low bf16 term is given)
-//   grouped_gateup   (row block of 64 inter rows, token tile): 4 waves x 16 rows of gate and up,
-//                    K = hidden in 128-column MFMA steps, 8 token groups per A fragment; epilogue
-//                    combines terms, applies row scales, SwiGLU, writes the activation as terms
-//   grouped_down     (row block of 64 hidden rows, slot tile): same structure over K = inter,
-//                    writes each slot's unweighted down output z[slot]
+//   grouped_gemm<0>  gate/up: (row block of 128 inter rows, token tile): 8 waves x 16 rows of
+//                    gate and the same 16 of up, K = hidden in 128-column MFMA steps, 12 column
+//                    tiles per A fragment; epilogue combines terms, applies row scales, SwiGLU,
+//                    writes the activation as terms
+//   grouped_gemm<1>  down: (row block of 256 hidden rows, slot tile): 8 waves x 32 rows, same
+//                    structure over K = inter, writes each slot's unweighted down output z[slot]
 //   grouped_combine  y[t] (+)= sum_j w[t][j] * z[slot(t, j)] in route order
 //
 // Reference counterparts: run_batch_device's prefill arm (src/gpu/static_placement.hip:
@@ -129,7 +130,9 @@ __host__ __device__ inline uint32_t kperm(uint32_t col) {
 __global__ void __launch_bounds__(256) grouped_prep_x_kernel(const uint16_t* __restrict__ x,
                                                              const uint16_t* __restrict__ xlo,
                                                              uint32_t hidden, uint32_t tx,
-                                                             int32_t* __restrict__ sigma_out,
+                                                             const int32_t* __restrict__ slot_of,
+                                                             uint32_t top_k,
+                                                             int32_t* __restrict__ slot_sigma,
                                                              uint8_t* __restrict__ xq,
                                                              uint32_t* __restrict__ zeros,
                                                              uint32_t zero_words) {
@@ -150,7 +153,10 @@ __global__ void __launch_bounds__(256) grouped_prep_x_kernel(const uint16_t* __r
   __syncthreads();
   amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const int sigma = amax > 0.f ? 7 - ilogbf(amax) : 0;
-  if (tid == 0) sigma_out[t] = sigma;
+  if (tid < top_k) {  // the exponent goes to each of the token's slots, for the gate/up epilogue
+    const int32_t sl = slot_of[t * top_k + tid];
+    if (sl >= 0) slot_sigma[sl] = sigma;
+  }
   for (uint32_t h4 = tid * 4; h4 < hidden; h4 += 1024) {
     uint32_t q[3] = {0, 0, 0};
 #pragma unroll
@@ -171,18 +177,20 @@ __global__ void __launch_bounds__(256) grouped_prep_x_kernel(const uint16_t* __r
 // ------------------------------------------------------------------------------------------------
 // grouped GEMM: one workgroup = one (expert, token tile) x one row block
 // ------------------------------------------------------------------------------------------------
-// 4 waves, one per SIMD. A wave owns 64 weight rows (four 16-row tiles: gate/up = two gate and the
-// same two up tiles, down = four tiles) against all 256 B columns of the tile (16 MFMA column
-// tiles; a token is TX adjacent columns, 16 / TX tokens per column tile), so the 256 accumulators
-// live in the AGPRs. Per MFMA step (128 of K):
+// 8 waves, two per SIMD: on gfx950 one wave's VALU work does not overlap its own MFMAs, but it
+// does overlap the other wave's. A wave owns 32 weight rows (two 16-row tiles: gate/up = one gate
+// tile and the same rows of up, down = two tiles) against all 192 B columns of the tile (12 MFMA
+// column tiles; a token is TX adjacent columns, 16 / TX tokens per column tile). Per MFMA step
+// (128 of K):
 //   - each wave decodes its own rows' A fragments in registers: one codebook lookup per quad
 //     code, reused by 16 MFMAs;
-//   - B (256 columns x 128 bytes) sits in LDS, written by direct global->LDS loads one step ahead
-//     (double buffer), read by all four waves; 16-byte chunks are swizzled by column so that the
-//     fragment reads of 16 lanes hit 16 distinct bank groups;
+//   - B (192 columns x 128 bytes) sits in LDS, written by direct global->LDS loads three steps
+//     ahead (four buffers), read by all eight waves; 16-byte chunks are swizzled by column so that
+//     the fragment reads of 16 lanes hit 16 distinct bank groups;
 //   - the packed weights of the next 1024 columns stream into a register ring, each chunk
 //     reloaded as soon as the lookups of the current 1024 columns are past it.
-constexpr int kGW = 4;                      // waves per workgroup
+constexpr int kGW = 8;                      // waves per workgroup (two per SIMD)
+constexpr int kGRT = 16 / kGW;              // 16-row tiles per wave (a workgroup covers 256 rows)
 constexpr int kGT = kGW * 64;
 constexpr int kGKC = 8;                     // codebook copies
 constexpr int kGCT = 12;                    // 16-column tiles of B per wave
@@ -199,7 +207,7 @@ struct GemmArgs {
   const GroupedHdr* hdr;
   const Tile* tiles;
   const uint32_t* slot_tok;
-  const int32_t* x_sigma;
+  const int32_t* slot_sigma;  // activation exponent of the slot's token
   const uint8_t* ws;        // B rows and the zero row, addressed by 32-bit offsets from here
   uint64_t b_off, zero_off;
   uint8_t* aq;              // gate/up output [slot][3][inter], step order
@@ -285,10 +293,11 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
 
   // ---- set-up: codebook copies, B row of every column, first step of B, first units ----------
   {
-    uint32_t cbv[8];
+    constexpr int kPer = 2048 / kGT;
+    uint32_t cbv[kPer];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) cbv[i] = A.codebook[tid + 256u * i];
-    build_lut<kGKC, kGT, 8>(lut_s, cbv, tid);
+    for (int i = 0; i < kPer; ++i) cbv[i] = A.codebook[tid + (uint32_t)kGT * i];
+    build_lut<kGKC, kGT, kPer>(lut_s, cbv, tid);
   }
   if (tid < kGCols) {
     const uint32_t col = tid, cc = col & 15;
@@ -304,12 +313,14 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
   __syncthreads();
   // DMA lane map: instruction i of wave w writes columns 8b..8b+7 (b = kGDma w + i), lane l to
   // LDS slot l & 7 of column 8b + (l >> 3); slot p of column col holds global chunk p ^ f(col),
-  // f(col) = (col >> 1) & 7.
+  // f(col) = (c ^ (c >> 3)) & 7 with c = col & 15 (the column within its 16-column tile), that
+  // is (col & 7) ^ ((col >> 3) & 1). A fragment read (lane = column c + 16 k-group) then puts lanes
+  // 0-7, 8-15 (and so on) on 8 distinct 16-byte bank groups, and lanes 0-15 on 16.
   uint32_t roff[kGDma];
 #pragma unroll
   for (int i = 0; i < kGDma; ++i) {
     const uint32_t col = 8u * (kGDma * wv + i) + (lane >> 3);
-    const uint32_t q = (lane & 7u) ^ ((col >> 1) & 7u);
+    const uint32_t q = (lane & 7u) ^ ((col & 7u) ^ ((col >> 3) & 1u));
     roff[i] = rowoff[col] + (q << 4);
   }
   const __amdgpu_buffer_rsrc_t wsr = buffer_rsrc(A.ws, 0xFFFFFFFFu);
@@ -320,44 +331,45 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
                                                step * 128u, 0, 0);
   };
 
-  // the wave's four 16-row tiles: gate/up = gate rt0, rt0 + 1 (units 0, 1) and the same rows of
-  // up (units 2, 3); down = four consecutive tiles. Unit r's code/field planes: (c0, f0) for
-  // r < 2 or down, (c1, f1) for the up units.
+  // the wave's 16-row tiles: gate/up = gate tile rt0 (unit 0) and the same rows of up (unit 1);
+  // down = two consecutive tiles. Unit r's code/field planes: (c0, f0) for the gate unit or down,
+  // (c1, f1) for the up unit.
   const uint64_t cbytes = (uint64_t)(PH == 0 ? A.inter : A.hidden) * code_row_bytes(K);
   const uint64_t fbytes = (uint64_t)(PH == 0 ? A.inter : A.hidden) * field_row_bytes(K);
   const __amdgpu_buffer_rsrc_t c0 = buffer_rsrc(ex + A.off[PH == 0 ? kGateCodes : kDownCodes], (uint32_t)cbytes);
   const __amdgpu_buffer_rsrc_t f0 = buffer_rsrc(ex + A.off[PH == 0 ? kGateFields : kDownFields], (uint32_t)fbytes);
   const __amdgpu_buffer_rsrc_t c1 = buffer_rsrc(ex + A.off[PH == 0 ? kUpCodes : kDownCodes], (uint32_t)cbytes);
   const __amdgpu_buffer_rsrc_t f1 = buffer_rsrc(ex + A.off[PH == 0 ? kUpFields : kDownFields], (uint32_t)fbytes);
-  const uint32_t rt0 = PH == 0 ? rb * 8u + 2u * wv : rb * 16u + 4u * wv;
-  auto rt_of = [&](int r) -> uint32_t { return PH == 0 ? rt0 + (r & 1) : rt0 + r; };
+  constexpr int kHalf = kGRT / 2;  // gate/up: units [0, kHalf) gate, [kHalf, kGRT) the same rows of up
+  const uint32_t rt0 = PH == 0 ? rb * 8u + kHalf * wv : rb * 16u + kGRT * wv;
+  auto rt_of = [&](int r) -> uint32_t { return PH == 0 ? rt0 + (r % kHalf) : rt0 + r; };
   const uint32_t nsteps = nst * 8u;
   dma(buf0, 0);
   dma(buf1, 1);
   dma(buf2, 2);
-  Unit u[4];
+  Unit u[kGRT];
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
-    load_unit_buf(u[r], PH == 0 && r >= 2 ? c1 : c0, PH == 0 && r >= 2 ? f1 : f0, rt_of(r) * nst, lane);
+  for (int r = 0; r < kGRT; ++r)
+    load_unit_buf(u[r], PH == 0 && r >= kHalf ? c1 : c0, PH == 0 && r >= kHalf ? f1 : f0, rt_of(r) * nst, lane);
   __builtin_amdgcn_s_waitcnt(AFFX_VMCNT(0));
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
 
   const uint32_t copy4 = ((lane >> 1) & (kGKC - 1)) * 4u;
   const uint32_t c = lane & 15, kg = lane >> 4;
-  const uint32_t bo0 = c * 128u + (((2u * kg) ^ (c >> 1)) << 4);
-  const uint32_t bo1 = c * 128u + (((2u * kg + 1u) ^ (c >> 1)) << 4);
+  const uint32_t bo0 = c * 128u + (((2u * kg) ^ ((c ^ (c >> 3)) & 7u)) << 4);
+  const uint32_t bo1 = c * 128u + (((2u * kg + 1u) ^ ((c ^ (c >> 3)) & 7u)) << 4);
 
-  v8i a_cur[4];
+  v8i a_cur[kGRT];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
+  for (int r = 0; r < kGRT; ++r) {
     uint32_t raw[8], fb[2];
     lut_lookup_step<kGKC>(u[r], lut, copy4, 0, raw, fb);
     a_cur[r] = lut_finish(raw, fb);
   }
-  v4f acc[4][kGCT];
+  v4f acc[kGRT][kGCT];
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
+  for (int r = 0; r < kGRT; ++r)
 #pragma unroll
     for (int ct = 0; ct < kGCT; ++ct) acc[r][ct] = v4f{0.f, 0.f, 0.f, 0.f};
 
@@ -378,20 +390,23 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
     // them keeps the count of loads in flight the same on every path
     if constexpr (m != 0) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        ring_load<m>(u[r], PH == 0 && r >= 2 ? c1 : c0, PH == 0 && r >= 2 ? f1 : f0,
+      for (int r = 0; r < kGRT; ++r)
+        ring_load<m>(u[r], PH == 0 && r >= kHalf ? c1 : c0, PH == 0 && r >= kHalf ? f1 : f0,
                      more ? rt_of(r) * nst + s + 1 : 0u, lane);
     }
     __builtin_amdgcn_sched_barrier(0);
     // The step is 12 groups, one per B column tile: the tile's two fragment reads go out two
-    // groups ahead, its four MFMAs are each followed by a share of the VALU work of the next step
-    // (groups 0-3: code addresses and table reads of unit g; groups 6-9: the sign/scale finish of
-    // unit g - 6, whose reads were issued four groups earlier), so that with one wave per SIMD
-    // the VALU runs while the matrix core works through the MFMAs. (Step 0 of the next 1024
-    // columns after step 7: the ring has reloaded every register those reads use.)
+    // groups ahead, its MFMAs (one per row tile) are each followed by a share of the VALU work of
+    // the next step (groups 4-5: code addresses and table reads of unit g - 4; groups 8-9: the
+    // sign/scale finish of unit g - 8, whose reads were issued four groups earlier). The VALU of
+    // one wave runs while the matrix core works through the other wave's MFMAs. The groups are
+    // placed so that the table reads and the next A fragments are live for a third of the step
+    // only: with two waves per SIMD a wave has 256 registers, accumulators included. (Step 0 of
+    // the next 1024 columns after step 7: the ring has reloaded every register those reads use.)
     constexpr int mn = (m + 1) & 7;
-    uint32_t rawn[4][8], fbn[4][2];
-    v8i a_next[4];
+    constexpr int kLook = 4, kFin = 8;
+    uint32_t rawn[kGRT][8], fbn[kGRT][2];
+    v8i a_next[kGRT];
     auto bread = [&](int ct) -> v8i {
       const u32x4 lo = *reinterpret_cast<const u32x4*>(bcur + ct * 2048 + bo0);
       const u32x4 hi = *reinterpret_cast<const u32x4*>(bcur + ct * 2048 + bo1);
@@ -406,17 +421,17 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
       v8i bq2;
       if constexpr (ct + 2 < kGCT) bq2 = bread(ct + 2);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[r][ct] = mfma(a_cur[r], bq0, acc[r][ct]);
-      if constexpr (ct < 4) {
-        pin_step<mn>(u[ct]);
-        lut_lookup<kGKC, mn>(u[ct], lut, copy4, rawn[ct], fbn[ct]);
-      } else if constexpr (ct >= 6 && ct < 10) {
-        a_next[ct - 6] = lut_finish(rawn[ct - 6], fbn[ct - 6]);
-        AFFX_PIN(a_next[ct - 6]);  // computed here, not sunk into the next step
+      for (int r = 0; r < kGRT; ++r) acc[r][ct] = mfma(a_cur[r], bq0, acc[r][ct]);
+      if constexpr (ct >= kLook && ct < kLook + kGRT) {
+        pin_step<mn>(u[ct - kLook]);
+        lut_lookup<kGKC, mn>(u[ct - kLook], lut, copy4, rawn[ct - kLook], fbn[ct - kLook]);
+      } else if constexpr (ct >= kFin && ct < kFin + kGRT) {
+        a_next[ct - kFin] = lut_finish(rawn[ct - kFin], fbn[ct - kFin]);
+        AFFX_PIN(a_next[ct - kFin]);  // computed here, not sunk into the next step
       }
-      // four times {one MFMA, then VALU}, then the LDS reads
+      // {one MFMA, then VALU} per row tile, then the LDS reads
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < kGRT; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
       }
@@ -425,22 +440,24 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
       bq0 = bq1;
       if constexpr (ct + 2 < kGCT) bq1 = bq2;
     });
-    // the accumulators are materialised here, in the AGPRs (else the compiler sinks every MFMA
-    // below all eight steps' table reads and holds those in registers)
+    // the accumulators are materialised here (else the compiler sinks every MFMA below all
+    // eight steps' table reads and holds those in registers). They stay in VGPRs: a kernel that
+    // names no AGPR gets its whole register budget as VGPRs, where one that does is split half
+    // and half, and the other half is then too small for the rest of the step.
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
+    for (int r = 0; r < kGRT; ++r)
 #pragma unroll
-      for (int ct = 0; ct < kGCT; ++ct) AFFX_PIN_ACC(acc[r][ct]);
+      for (int ct = 0; ct < kGCT; ++ct) AFFX_PIN(acc[r][ct]);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) a_cur[r] = a_next[r];
+    for (int r = 0; r < kGRT; ++r) a_cur[r] = a_next[r];
     // The next step's B (issued at the top of step t - 2) is in LDS once every wave's loads up to
     // it have landed: loads complete in issue order, so at most the loads issued after it may
-    // still be outstanding: two B loads and the ring loads of steps t - 2 .. t (4 units x
-    // {0,1,1,1,1,1,1,2} by step). (In the first two steps more were issued after it: waiting for
+    // still be outstanding: the B loads of two steps and the ring loads of steps t - 2 .. t
+    // (2 units x {0,1,1,1,1,1,1,2} by step). (In the first two steps more were issued after it: waiting for
     // fewer is then only stricter.)
     {
       constexpr int c[8] = {0, 1, 1, 1, 1, 1, 1, 2};
-      constexpr int k = 2 * kGDma + 4 * (c[(m + 6) & 7] + c[(m + 7) & 7] + c[m]);
+      constexpr int k = 2 * kGDma + kGRT * (c[(m + 6) & 7] + c[(m + 7) & 7] + c[m]);
       __builtin_amdgcn_s_waitcnt(AFFX_VMCNT(k));
     }
     __builtin_amdgcn_s_barrier();
@@ -480,12 +497,28 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
   };
   if constexpr (PH == 0) {
     const float L = A.limit;
-    static_for<0, 2>([&](auto pc) {
+    // Every input of the epilogue is requested before the first one is used: the activation
+    // exponent of the lane's token in each column tile (columns past the tile's tokens read its
+    // last token and store nothing), then the row scales.
+    int sig[kGCT];
+#pragma unroll
+    for (int ct = 0; ct < kGCT; ++ct) {
+      const uint32_t j = ct * TPG + c / TX;
+      sig[ct] = A.slot_sigma[tl.slot0 + (j < tl.n ? j : tl.n - 1u)];
+    }
+    uint2 rgw[kHalf], ruw[kHalf];
+#pragma unroll
+    for (int p = 0; p < kHalf; ++p) {
+      const uint32_t row0 = rt_of(p) * 16u + 4u * kg;
+      rgw[p] = *reinterpret_cast<const uint2*>(ex + A.off[kGateRs] + (uint64_t)row0 * 2);
+      ruw[p] = *reinterpret_cast<const uint2*>(ex + A.off[kUpRs] + (uint64_t)row0 * 2);
+    }
+    static_for<0, kHalf>([&](auto pc) {
       constexpr int p = decltype(pc)::value;
       const uint32_t row0 = rt_of(p) * 16u + 4u * kg;
       float rg[4], ru[4];
-      bf16x4(*reinterpret_cast<const uint2*>(ex + A.off[kGateRs] + (uint64_t)row0 * 2), rg);
-      bf16x4(*reinterpret_cast<const uint2*>(ex + A.off[kUpRs] + (uint64_t)row0 * 2), ru);
+      bf16x4(rgw[p], rg);
+      bf16x4(ruw[p], ru);
       const uint32_t prow = kperm(row0);
       static_for<0, kGCT>([&](auto cc) {
         constexpr int ct = decltype(cc)::value;
@@ -493,17 +526,16 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           sg[v] = terms(acc[p][ct][v]);
-          su[v] = terms(acc[p + 2][ct][v]);
+          su[v] = terms(acc[p + kHalf][ct][v]);
         }
         const uint32_t j = ct * TPG + c / TX;
         if (c % TX == 0 && c < TX * TPG && j < tl.n) {
           const uint32_t slot = tl.slot0 + j;
-          const int sig = A.x_sigma[A.slot_tok[slot]];
           float a[4];
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
-            float gv = ldexpf(sg[v], -sig) * rg[v];
-            float uv = ldexpf(su[v], -sig) * ru[v];
+            float gv = ldexpf(sg[v], -sig[ct]) * rg[v];
+            float uv = ldexpf(su[v], -sig[ct]) * ru[v];
             gv = (L < gv) ? L : gv;  // SwiGLU with the asymmetric clamp: src/engine/ops.cpp:47-60
             const float lo = (-L < uv) ? uv : -L;
             uv = (lo < L) ? lo : L;
@@ -519,11 +551,15 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
       });
     });
   } else {
-    static_for<0, 4>([&](auto rc) {
+    uint2 rdw[kGRT];  // row scales, all requested before the first is used
+#pragma unroll
+    for (int r = 0; r < kGRT; ++r)
+      rdw[r] = *reinterpret_cast<const uint2*>(ex + A.off[kDownRs] + (uint64_t)(rt_of(r) * 16u + 4u * kg) * 2);
+    static_for<0, kGRT>([&](auto rc) {
       constexpr int r = decltype(rc)::value;
       const uint32_t row0 = rt_of(r) * 16u + 4u * kg;
       float rd[4];
-      bf16x4(*reinterpret_cast<const uint2*>(ex + A.off[kDownRs] + (uint64_t)row0 * 2), rd);
+      bf16x4(rdw[r], rd);
       static_for<0, kGCT>([&](auto cc) {
         constexpr int ct = decltype(cc)::value;
         float sd[4];
@@ -580,7 +616,7 @@ struct GroupedWs {
   uint32_t max_tiles1, max_tiles2;
 };
 
-// tokens per workgroup tile: 16 column tiles of 16 / terms tokens each
+// tokens per workgroup tile: kGCT column tiles of 16 / terms tokens each
 uint32_t tile_tokens(uint32_t terms) { return kGCT * (16 / terms); }
 
 GroupedWs grouped_ws(uint32_t T, uint32_t K, uint32_t E, uint32_t hidden, uint32_t inter, uint32_t tx) {
@@ -596,7 +632,7 @@ GroupedWs grouped_ws(uint32_t T, uint32_t K, uint32_t E, uint32_t hidden, uint32
   w.slot_of = o; o += a256(4 * P);
   w.tiles1 = o; o += a256(sizeof(Tile) * w.max_tiles1);
   w.tiles2 = o; o += a256(sizeof(Tile) * w.max_tiles2);
-  w.sigma = o; o += a256(4ull * T);
+  w.sigma = o; o += a256(4 * P);  // per slot
   w.zeros = o; o += a256(hidden > inter ? hidden : inter);
   w.xq = o; o += a256((uint64_t)T * tx * hidden);
   w.aq = o; o += a256(P * 3 * inter);
@@ -652,7 +688,7 @@ int affx_expert_ffn_grouped(const affx_layer* L, const void* x, const void* x_lo
   A.codebook = (const uint32_t*)L->codebook;
   A.hdr = (const GroupedHdr*)(b + lay.hdr);
   A.slot_tok = (const uint32_t*)(b + lay.slot_tok);
-  A.x_sigma = (const int32_t*)(b + lay.sigma);
+  A.slot_sigma = (const int32_t*)(b + lay.sigma);
   A.ws = b;
   A.zero_off = lay.zeros;
   A.aq = b + lay.aq;
@@ -673,7 +709,8 @@ int affx_expert_ffn_grouped(const affx_layer* L, const void* x, const void* x_lo
   if ((rc = check_launch("grouped_place_kernel"))) return rc;
   const uint32_t zmax = L->hidden > L->inter ? L->hidden : L->inter;
   hipLaunchKernelGGL(grouped_prep_x_kernel, dim3(T), dim3(256), 0, s, (const uint16_t*)x,
-                     (const uint16_t*)x_lo, L->hidden, tx, (int32_t*)(b + lay.sigma), b + lay.xq,
+                     (const uint16_t*)x_lo, L->hidden, tx, (const int32_t*)(b + lay.slot_of), K,
+                     (int32_t*)(b + lay.sigma), b + lay.xq,
                      (uint32_t*)(b + lay.zeros), zmax / 4);
   if ((rc = check_launch("grouped_prep_x_kernel"))) return rc;
   // gate/up: 128 gate + 128 up rows per workgroup; down: 256 rows. One workgroup per (row

@@ -41,10 +41,6 @@ __device__ __forceinline__ void load_unit(Unit& u, const uint8_t* codes, const u
 #ifndef AFFX_PIN
 #define AFFX_PIN(x) asm volatile("" : "+v"(x))
 #endif
-// The same for an MFMA accumulator held in the AGPRs.
-#ifndef AFFX_PIN_ACC
-#define AFFX_PIN_ACC(x) asm volatile("" : "+a"(x))
-#endif
 // LDS pointer operand of a direct global->LDS load.
 #ifndef AFFX_LDS_PTR
 #define AFFX_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))

@@ -165,7 +165,6 @@ inline void __builtin_amdgcn_raw_ptr_buffer_load_lds(emu_rsrc r, void* lds, int 
   if (o + size > r.n) memset(dst, 0, size); else memcpy(dst, r.base + o, size);
 }
 #define AFFX_LDS_PTR(p) ((void*)(p))
-#define AFFX_PIN_ACC(x) ((void)0)
 inline void __builtin_amdgcn_s_barrier();
 
 // ---- MFMA 16x16x128 fp8 x fp8 -> f32, lane layout as on gfx950 ----
