@@ -401,6 +401,11 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
       }
     }
     AFFX_TRACE(3);
+    // one pass: a wave that stores no SwiGLU output issues its down unit now (its gate/up data is
+    // in), so that it has arrived when the wave decodes it during the publish and wait
+    if constexpr (SINGLE && PREF) {
+      if (wv >= epi_waves) load_down(has_down, g, wv);
+    }
     if (item != ~0u && S == 0 && lane < 32) {
       // opaque at the use: no conversion is hoisted next to the load (its wait would then cover
       // every weight load issued before it)
@@ -486,7 +491,7 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   // and serialised per L2, costs microseconds, and nothing else written here is read by other
   // workgroups.
   if (PREF) {
-    load_down(has_down, g, wv);
+    if (!SINGLE || n_rounds == 0 || wv < epi_waves) load_down(has_down, g, wv);
     if (n_rounds > 0 && wv < epi_waves) __builtin_amdgcn_s_waitcnt(AFFX_VMCNT(7));
   } else {
     if (n_rounds > 0 && wv < epi_waves) __builtin_amdgcn_s_waitcnt(0);
@@ -509,6 +514,27 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
     }
   }
   AFFX_TRACE(4);
+  // ---- 4b. one pass (batch 1): the A fragments of this wave's first down unit (the one loaded
+  // before the publish) do not depend on the activations, so they are decoded now, while the
+  // layer publishes and this workgroup waits; after the release only the activation loads and
+  // eight MFMAs remain for it
+  // (the first kPreSteps of the eight steps: with the activation operand loaded whole after the
+  // wait, all eight would not fit the registers; the last steps are decoded after the wait)
+  static_assert(!SINGLE || (CG == 1 && BPRE), "the one-pass down phase holds one column group");
+  constexpr int kPreSteps = 6;
+  v8i ad[SINGLE ? kPreSteps : 1];
+  if constexpr (SINGLE) {
+    if (has_down) {
+#pragma unroll
+      for (int m = 0; m < kPreSteps; ++m) {
+        uint32_t raw[8], bv[2];
+        pin_step(ud, m);
+        lut_lookup_step<KC, ROT>(ud, lut, copy4, m, raw, bv);
+        ad[m] = lut_finish<ROT>(raw, bv);
+      }
+    }
+  }
+  AFFX_TRACE(14);
   // ---- 5. wait for every gate/up item (this workgroup's flag), then the down tiles -------------
   if (g < dtiles) {
     if (tid == 0 && NI > 0) {
@@ -528,7 +554,10 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
     AFFX_TRACE(5);
 
     const uint32_t rg4 = lane >> 4;
-    for (uint32_t td = g; td < dtiles; td += A.n_wg) {
+    // one output tile; PRE: its first unit per wave was decoded before the wait (a separate
+    // instantiation, so that those fragments are not live across the loop over further tiles)
+    auto down_tile = [&](uint32_t td, auto prec) {
+      constexpr bool PRE = decltype(prec)::value;
       float yacc[CG][4];
 #pragma unroll
       for (int cg = 0; cg < CG; ++cg)
@@ -536,7 +565,7 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
         for (int v = 0; v < 4; ++v) yacc[cg][v] = 0.f;
 #pragma unroll 1
       for (uint32_t u = wv; u < (SINGLE ? (wv < NU ? wv + 1 : 0u) : NU); u += kFW) {
-        if (!(PREF && td == g && u == wv)) load_down(true, td, u);  // else loaded before the wait
+        if (!(PRE || (PREF && td == g && u == wv))) load_down(true, td, u);  // else loaded before the wait
         const uint32_t slot = u / nsi, S2 = u % nsi;
         const uint32_t e = __builtin_amdgcn_readfirstlane(slot_expert[slot]);
         const uint32_t mask = __builtin_amdgcn_readfirstlane(slot_mask[slot]);
@@ -562,42 +591,50 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
 #pragma unroll
           for (int cg = 0; cg < CG; ++cg) bc[cg] = b_step(b.p[cg], 0);
         }
-        uint32_t raw[8];
-        uint32_t bv[2];
-        pin_step(ud, 0);
-        lut_lookup_step<KC, ROT>(ud, lut, copy4, 0, raw, bv);
+        // steps [m0, 8) decode their A fragments here (PRE: the first kPreSteps are in ad)
+        constexpr int m0 = PRE ? kPreSteps : 0;
+        if constexpr (PRE) {
 #pragma unroll
-        for (int m = 0; m < 8; ++m) {
-          uint32_t nraw[8];
-          uint32_t nbv[2];
-          v8i bn[CG];
-          if (m < 7) {
-            // the previous step's MFMA stays ahead of these reads (else the compiler sinks every
-            // MFMA below all eight steps' table reads and holds them all in registers)
+          for (int m = 0; m < m0; ++m) acc[0] = mfma(ad[SINGLE ? m : 0], bpre[BPRE ? m : 0], acc[0]);
+        }
+        {
+          uint32_t raw[8];
+          uint32_t bv[2];
+          pin_step(ud, m0);
+          lut_lookup_step<KC, ROT>(ud, lut, copy4, m0, raw, bv);
 #pragma unroll
-            for (int cg = 0; cg < CG; ++cg) AFFX_PIN(acc[cg]);
-            pin_step(ud, m + 1);
-            lut_lookup_step<KC, ROT>(ud, lut, copy4, m + 1, nraw, nbv);
-            if constexpr (!BPRE) {
+          for (int m = m0; m < 8; ++m) {
+            uint32_t nraw[8];
+            uint32_t nbv[2];
+            v8i bn[CG];
+            if (m < 7) {
+              // the previous step's MFMA stays ahead of these reads (else the compiler sinks every
+              // MFMA below all eight steps' table reads and holds them all in registers)
 #pragma unroll
-              for (int cg = 0; cg < CG; ++cg) bn[cg] = b_step(b.p[cg], m + 1);
+              for (int cg = 0; cg < CG; ++cg) AFFX_PIN(acc[cg]);
+              pin_step(ud, m + 1);
+              lut_lookup_step<KC, ROT>(ud, lut, copy4, m + 1, nraw, nbv);
+              if constexpr (!BPRE) {
+#pragma unroll
+                for (int cg = 0; cg < CG; ++cg) bn[cg] = b_step(b.p[cg], m + 1);
+              }
             }
-          }
-          const v8i a = lut_finish<ROT>(raw, bv);
-          if constexpr (BPRE) {
-            acc[0] = mfma(a, bpre[m], acc[0]);
-          } else {
+            const v8i a = lut_finish<ROT>(raw, bv);
+            if constexpr (BPRE) {
+              acc[0] = mfma(a, bpre[m], acc[0]);
+            } else {
 #pragma unroll
-            for (int cg = 0; cg < CG; ++cg) acc[cg] = mfma(a, bc[cg], acc[cg]);
-          }
-          __builtin_amdgcn_sched_barrier(0);
-          if (m < 7) {
+              for (int cg = 0; cg < CG; ++cg) acc[cg] = mfma(a, bc[cg], acc[cg]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (m < 7) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) raw[i] = nraw[i];
-            bv[0] = nbv[0]; bv[1] = nbv[1];
-            if constexpr (!BPRE) {
+              for (int i = 0; i < 8; ++i) raw[i] = nraw[i];
+              bv[0] = nbv[0]; bv[1] = nbv[1];
+              if constexpr (!BPRE) {
 #pragma unroll
-              for (int cg = 0; cg < CG; ++cg) bc[cg] = bn[cg];
+                for (int cg = 0; cg < CG; ++cg) bc[cg] = bn[cg];
+              }
             }
           }
         }
@@ -635,7 +672,13 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
         *dst = A.accumulate ? *dst + sum : sum;
       }
       __syncthreads();
+    };
+    uint32_t td0 = g;
+    if constexpr (SINGLE) {
+      down_tile(g, std::true_type{});
+      td0 += A.n_wg;
     }
+    for (uint32_t td = td0; td < dtiles; td += A.n_wg) down_tile(td, std::false_type{});
   }
 
   AFFX_TRACE(7);
