@@ -539,7 +539,11 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
             gv = (L < gv) ? L : gv;  // SwiGLU with the asymmetric clamp: src/engine/ops.cpp:47-60
             const float lo = (-L < uv) ? uv : -L;
             uv = (lo < L) ? lo : L;
-            a[v] = ldexpf((gv / (1.0f + expf(-gv))) * uv, A.sigma_a);
+            // (hardware exp2 and reciprocal: a few ulp, far inside the path's tolerance, against
+            // some thirty VALU ops per element for expf and an IEEE division; gv -> -inf gives
+            // exp -> inf, reciprocal 0, a signed zero)
+            const float e = __builtin_amdgcn_exp2f(-gv * 1.44269504f);
+            a[v] = ldexpf(gv * __builtin_amdgcn_rcpf(1.0f + e) * uv, A.sigma_a);
           }
           uint32_t o0, o1, o2;
           split3x4(a[0], a[1], a[2], a[3], o0, o1, o2);

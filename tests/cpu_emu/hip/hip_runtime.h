@@ -72,6 +72,9 @@ inline float __fdiv_rn(float a, float b) { volatile float r = a / b; return r; }
 inline double __dmul_rn(double a, double b) { volatile double r = a * b; return r; }
 inline double __ddiv_rn(double a, double b) { volatile double r = a / b; return r; }
 
+// v_exp_f32 / v_rcp_f32: the library uses them where a few ulp are within its tolerance
+inline float __builtin_amdgcn_exp2f(float x) { return exp2f(x); }
+inline float __builtin_amdgcn_rcpf(float x) { return 1.0f / x; }
 inline uint32_t __builtin_amdgcn_alignbit(uint32_t hi, uint32_t lo, uint32_t s) {
   return (uint32_t)((((uint64_t)hi << 32) | lo) >> (s & 31));
 }
