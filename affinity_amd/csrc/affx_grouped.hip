@@ -37,50 +37,82 @@ struct GroupedHdr {
 // ------------------------------------------------------------------------------------------------
 // plan
 // ------------------------------------------------------------------------------------------------
+// Exclusive scan over the workgroup (kPlanThreads threads, thread i holds v[i]) of three counts
+// at once; returns thread i's prefixes and writes the totals to tot.
+__device__ __forceinline__ void plan_scan3(uint32_t (&v)[3], uint32_t* wsum, uint32_t (&tot)[3]) {
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  constexpr uint32_t kW = kPlanThreads / 64;
+  uint32_t inc[3] = {v[0], v[1], v[2]};
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1)
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      const uint32_t n = __shfl_up(inc[q], o);
+      if (lane >= (uint32_t)o) inc[q] += n;
+    }
+  if (lane == 63)
+#pragma unroll
+    for (int q = 0; q < 3; ++q) wsum[q * kW + wv] = inc[q];
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < 3; ++q) {
+    uint32_t before = 0, all = 0;
+    for (uint32_t w = 0; w < kW; ++w) {
+      const uint32_t x = wsum[q * kW + w];
+      before += w < wv ? x : 0u;
+      all += x;
+    }
+    v[q] = before + inc[q] - v[q];
+    tot[q] = all;
+  }
+}
+
 __global__ void __launch_bounds__(kPlanThreads) grouped_plan_kernel(
     const uint32_t* __restrict__ sel, uint32_t n_pairs, uint32_t n_experts, uint32_t tt1,
     uint32_t tt2, uint32_t tx, GroupedHdr* __restrict__ hdr, uint32_t* __restrict__ offsets,
     Tile* __restrict__ tiles1, Tile* __restrict__ tiles2) {
+  static_assert(AFFX_MAX_EXPERTS <= kPlanThreads, "one thread per expert in the scan");
   __shared__ uint32_t cnt[AFFX_MAX_EXPERTS];
-  __shared__ uint32_t off[AFFX_MAX_EXPERTS + 1], t1[AFFX_MAX_EXPERTS + 1], t2[AFFX_MAX_EXPERTS + 1];
+  __shared__ uint32_t wsum[3 * (kPlanThreads / 64)];
   const uint32_t tid = threadIdx.x;
   for (uint32_t e = tid; e < AFFX_MAX_EXPERTS; e += kPlanThreads) cnt[e] = 0;
   __syncthreads();
-  for (uint32_t i = tid; i < n_pairs; i += kPlanThreads) {
-    const uint32_t e = sel[i];
-    if (e < n_experts) atomicAdd(&cnt[e], 1u);
+  // counts per expert: eight routes per thread in flight at a time
+  constexpr uint32_t kU = 8;
+  for (uint32_t i0 = 0; i0 < n_pairs; i0 += kU * kPlanThreads) {
+    uint32_t ev[kU];
+#pragma unroll
+    for (uint32_t u = 0; u < kU; ++u) {
+      const uint32_t i = i0 + u * kPlanThreads + tid;
+      ev[u] = i < n_pairs ? sel[i] : ~0u;
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < kU; ++u)
+      if (ev[u] < n_experts) atomicAdd(&cnt[ev[u]], 1u);
   }
   __syncthreads();
+  // slot offsets and tile offsets: one exclusive scan (expert order) of count and tiles
+  const uint32_t c = tid < n_experts ? cnt[tid] : 0u;
+  uint32_t v[3] = {c, (c + tt1 - 1) / tt1, (c + tt2 - 1) / tt2}, tot[3];
+  plan_scan3(v, wsum, tot);
+  if (tid < n_experts) {
+    offsets[tid] = v[0];
+    for (uint32_t k = 0; k * tt1 < c; ++k) tiles1[v[1] + k] = Tile{tid, v[0] + k * tt1, min(tt1, c - k * tt1)};
+    for (uint32_t k = 0; k * tt2 < c; ++k) tiles2[v[2] + k] = Tile{tid, v[0] + k * tt2, min(tt2, c - k * tt2)};
+  }
   if (tid == 0) {
-    uint32_t s = 0, a = 0, b = 0;
-    for (uint32_t e = 0; e < n_experts; ++e) {
-      off[e] = s; t1[e] = a; t2[e] = b;
-      s += cnt[e];
-      a += (cnt[e] + tt1 - 1) / tt1;
-      b += (cnt[e] + tt2 - 1) / tt2;
-    }
-    off[n_experts] = s; t1[n_experts] = a; t2[n_experts] = b;
-    hdr->n_slots = s;
-    hdr->n_tiles1 = a;
-    hdr->n_tiles2 = b;
+    offsets[n_experts] = tot[0];
+    hdr->n_slots = tot[0];
+    hdr->n_tiles1 = tot[1];
+    hdr->n_tiles2 = tot[2];
     hdr->tx = tx;
-  }
-  __syncthreads();
-  for (uint32_t e = tid; e <= n_experts; e += kPlanThreads) offsets[e] = off[e];
-  for (uint32_t e = tid; e < n_experts; e += kPlanThreads) {
-    for (uint32_t k = 0; k < t1[e + 1] - t1[e]; ++k) {
-      const uint32_t s0 = off[e] + k * tt1, n = min(tt1, off[e] + cnt[e] - s0);
-      tiles1[t1[e] + k] = Tile{e, s0, n};
-    }
-    for (uint32_t k = 0; k < t2[e + 1] - t2[e]; ++k) {
-      const uint32_t s0 = off[e] + k * tt2, n = min(tt2, off[e] + cnt[e] - s0);
-      tiles2[t2[e] + k] = Tile{e, s0, n};
-    }
   }
 }
 
 // One workgroup per expert (plus the padding pass in workgroup n_experts): walks all pairs in
-// order and gives this expert's pairs consecutive slots.
+// order and gives this expert's pairs consecutive slots. Thread tid takes 8 consecutive pairs of
+// each 2048-pair block (so thread order is pair order), an exclusive scan of the match counts
+// places them; the next block's routes are loaded before this block is placed.
 __global__ void __launch_bounds__(256) grouped_place_kernel(
     const uint32_t* __restrict__ sel, uint32_t n_pairs, uint32_t top_k, uint32_t n_experts,
     const uint32_t* __restrict__ offsets, uint32_t* __restrict__ slot_tok,
@@ -91,26 +123,49 @@ __global__ void __launch_bounds__(256) grouped_place_kernel(
       if (sel[i] >= n_experts) slot_of[i] = -1;
     return;
   }
-  __shared__ uint32_t wsum[4];
   uint32_t base = offsets[e];
-  if (offsets[e + 1] == base) return;
-  for (uint32_t c0 = 0; c0 < n_pairs; c0 += 256) {
-    const uint32_t i = c0 + tid;
-    const bool mine = i < n_pairs && sel[i] == e;
-    const uint64_t bal = __ballot(mine);
-    const uint32_t before = __popcll(bal & ((1ull << lane) - 1ull));
-    if (lane == 0) wsum[wv] = __popcll(bal);
-    __syncthreads();
-    uint32_t wofs = 0;
-    for (uint32_t q = 0; q < wv; ++q) wofs += wsum[q];
-    const uint32_t total = wsum[0] + wsum[1] + wsum[2] + wsum[3];
-    if (mine) {
-      const uint32_t pos = base + wofs + before;
-      slot_tok[pos] = i / top_k;
-      slot_of[i] = (int32_t)pos;
+  const uint32_t end = offsets[e + 1];
+  if (end == base) return;
+  __shared__ uint32_t wsum[2][4];
+  constexpr uint32_t kPer = 8, kBlock = 256 * kPer;
+  auto load = [&](uint32_t i0, uint32_t (&v)[kPer]) {
+#pragma unroll
+    for (uint32_t k = 0; k < kPer; ++k) {
+      const uint32_t i = i0 + tid * kPer + k;
+      v[k] = i < n_pairs ? sel[i] : ~0u;
     }
-    base += total;
+  };
+  uint32_t cur[kPer], nxt[kPer];
+  load(0, cur);
+  for (uint32_t i0 = 0, it = 0; i0 < n_pairs && base < end; i0 += kBlock, ++it) {
+    if (i0 + kBlock < n_pairs) load(i0 + kBlock, nxt);
+    uint32_t m = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < kPer; ++k) m |= (cur[k] == e ? 1u : 0u) << k;
+    const uint32_t cnt = __popc(m);
+    uint32_t inc = cnt;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t n = __shfl_up(inc, o);
+      if (lane >= (uint32_t)o) inc += n;
+    }
+    uint32_t* ws = wsum[it & 1];  // alternating: a wave may run one block ahead of a slow one
+    if (lane == 63) ws[wv] = inc;
     __syncthreads();
+    uint32_t pos = base + inc - cnt;
+    for (uint32_t q = 0; q < wv; ++q) pos += ws[q];
+    const uint32_t total = ws[0] + ws[1] + ws[2] + ws[3];
+#pragma unroll
+    for (uint32_t k = 0; k < kPer; ++k)
+      if ((m >> k) & 1u) {
+        const uint32_t i = i0 + tid * kPer + k;
+        slot_tok[pos] = i / top_k;
+        slot_of[i] = (int32_t)pos;
+        ++pos;
+      }
+    base += total;
+#pragma unroll
+    for (uint32_t k = 0; k < kPer; ++k) cur[k] = nxt[k];
   }
 }
 
@@ -136,17 +191,33 @@ __global__ void __launch_bounds__(256) grouped_prep_x_kernel(const uint16_t* __r
                                                              uint8_t* __restrict__ xq,
                                                              uint32_t* __restrict__ zeros,
                                                              uint32_t zero_words) {
-  const uint32_t t = blockIdx.x, tid = threadIdx.x;
+  // thread tid holds the 8-element chunks tid + 256 i (hidden <= 8192: at most 4), loaded once
+  constexpr int kMaxChunks = 4;
+  const uint32_t t = blockIdx.x, tid = threadIdx.x, nch = hidden / 8;
   if (t == 0)  // the B row of unused columns
     for (uint32_t i = tid; i < zero_words; i += 256) zeros[i] = 0u;
   __shared__ float red[4];
-  const uint16_t* xr = x + (uint64_t)t * hidden;
-  const uint16_t* lr = xlo ? xlo + (uint64_t)t * hidden : nullptr;
+  const uint4* xr = reinterpret_cast<const uint4*>(x + (uint64_t)t * hidden);
+  const uint4* lr = xlo ? reinterpret_cast<const uint4*>(xlo + (uint64_t)t * hidden) : nullptr;
+  uint4 hv[kMaxChunks], lv[kMaxChunks];
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; ++i) {
+    const uint32_t ch = tid + 256u * i;
+    hv[i] = ch < nch ? xr[ch] : uint4{0u, 0u, 0u, 0u};
+    lv[i] = (lr && ch < nch) ? lr[ch] : uint4{0u, 0u, 0u, 0u};
+  }
+  float v[kMaxChunks][8];
   float amax = 0.f;
-  for (uint32_t h = tid; h < hidden; h += 256) {
-    float v = __uint_as_float((uint32_t)xr[h] << 16);
-    if (lr) v += __uint_as_float((uint32_t)lr[h] << 16);
-    amax = fmaxf(amax, fabsf(v));
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; ++i) {
+    const uint32_t hw[4] = {hv[i].x, hv[i].y, hv[i].z, hv[i].w}, lw[4] = {lv[i].x, lv[i].y, lv[i].z, lv[i].w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      v[i][2 * k] = __uint_as_float(hw[k] << 16) + __uint_as_float(lw[k] << 16);
+      v[i][2 * k + 1] = __uint_as_float(hw[k] & 0xFFFF0000u) + __uint_as_float(lw[k] & 0xFFFF0000u);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) amax = fmaxf(amax, fabsf(v[i][k]));
   }
   for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
   if ((tid & 63) == 0) red[tid >> 6] = amax;
@@ -157,20 +228,22 @@ __global__ void __launch_bounds__(256) grouped_prep_x_kernel(const uint16_t* __r
     const int32_t sl = slot_of[t * top_k + tid];
     if (sl >= 0) slot_sigma[sl] = sigma;
   }
-  for (uint32_t h4 = tid * 4; h4 < hidden; h4 += 1024) {
-    uint32_t q[3] = {0, 0, 0};
+  // E4M3 terms, 8 bytes per term and chunk (8 consecutive columns stay consecutive in step order)
+  uint8_t* row = xq + (uint64_t)t * tx * hidden;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float v = __uint_as_float((uint32_t)xr[h4 + i] << 16);
-      if (lr) v += __uint_as_float((uint32_t)lr[h4 + i] << 16);
-      uint32_t b0, b1, b2;
-      split3(ldexpf(v, sigma), b0, b1, b2);
-      q[0] |= b0 << (8 * i);
-      q[1] |= b1 << (8 * i);
-      q[2] |= b2 << (8 * i);
+  for (int i = 0; i < kMaxChunks; ++i) {
+    const uint32_t ch = tid + 256u * i;
+    if (ch < nch) {
+      uint32_t a0, a1, a2, b0, b1, b2;
+      split3x4(ldexpf(v[i][0], sigma), ldexpf(v[i][1], sigma), ldexpf(v[i][2], sigma), ldexpf(v[i][3], sigma),
+               a0, a1, a2);
+      split3x4(ldexpf(v[i][4], sigma), ldexpf(v[i][5], sigma), ldexpf(v[i][6], sigma), ldexpf(v[i][7], sigma),
+               b0, b1, b2);
+      uint8_t* dst = row + kperm(8 * ch);
+      *reinterpret_cast<uint2*>(dst) = uint2{a0, b0};
+      *reinterpret_cast<uint2*>(dst + hidden) = uint2{a1, b1};
+      if (tx == 3) *reinterpret_cast<uint2*>(dst + 2 * (uint64_t)hidden) = uint2{a2, b2};
     }
-    uint8_t* row = xq + (uint64_t)t * tx * hidden + kperm(h4);
-    for (uint32_t k = 0; k < tx; ++k) *reinterpret_cast<uint32_t*>(row + (uint64_t)k * hidden) = q[k];
   }
 }
 
@@ -669,6 +742,8 @@ int affx_expert_ffn_grouped(const affx_layer* L, const void* x, const void* x_lo
     return set_error(AFFX_DECLINED, "ffn_grouped: hidden and inter must be multiples of 1024, at most 8192");
   if (!(L->swiglu_limit > 0.f) || L->swiglu_limit > 1e6f)
     return set_error(AFFX_DECLINED, "ffn_grouped: needs a SwiGLU clamp limit in (0, 1e6]");
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(x_lo)) & 15u)
+    return set_error(AFFX_ERR_ARG, "ffn_grouped: x and x_lo must be 16-byte aligned");
   const uint32_t tx = x_lo ? 3 : 2;
   const GroupedWs lay = grouped_ws(T, K, L->n_experts, L->hidden, L->inter, tx);
   // the GEMM addresses its B rows with 32-bit offsets into the workspace

@@ -174,9 +174,10 @@ size_t affx_grouped_workspace_size(uint32_t n_tok, uint32_t top_k, uint32_t n_ex
                                    uint32_t hidden, uint32_t inter);
 
 /* y[t] (+)= sum_j w[t][j] * FFN_{sel[t][j]}(x[t]) for all n_tok tokens, grouped by expert:
- * every expert's weights are decoded once per 128-row tile and reused for all of its tokens.
+ * every expert's weights are decoded once per tile of its tokens (96 tokens for gate/up with a
+ * bf16 x, 60 otherwise) and reused for all of the tile's tokens.
  *  x: device bf16 [n_tok][hidden] (token-major); x_lo: optional second bf16 term (x = x + x_lo)
- *  for f32 activations split hi/lo, or NULL.
+ *  for f32 activations split hi/lo, or NULL. Both 16-byte aligned (else AFFX_ERR_ARG).
  *  sel/w: device [n_tok][top_k]; padding ids >= n_experts skipped.
  *  y: device f32 [n_tok][hidden] (token-major).
  * Replaces run_batch_device's prefill sequence (src/gpu/static_placement.hip:1348-1964):

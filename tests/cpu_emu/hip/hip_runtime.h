@@ -134,6 +134,10 @@ template <typename T> inline T __shfl_down(T v, int d, int width = 64) {
   uint32_t l = emu_lane(); uint32_t src = ((l % width) + d < (uint32_t)width) ? l + d : l;
   return emu_exchange(v, src);
 }
+template <typename T> inline T __shfl_up(T v, int d, int width = 64) {
+  uint32_t l = emu_lane(); uint32_t src = (l % width) >= (uint32_t)d ? l - d : l;
+  return emu_exchange(v, src);
+}
 inline uint64_t __ballot(int pred) {
   emu_blk->xfer[emu_wave()][emu_lane()][0] = pred ? 1 : 0;
   emu_wave_sync();
