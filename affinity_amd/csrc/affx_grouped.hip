@@ -256,7 +256,11 @@ __global__ void __launch_bounds__(256) grouped_prep_x_kernel(const uint16_t* __r
 // column tiles; a token is TX adjacent columns, 16 / TX tokens per column tile). Per MFMA step
 // (128 of K):
 //   - each wave decodes its own rows' A fragments in registers: one codebook lookup per quad
-//     code, reused by 16 MFMAs;
+//     code, reused by 12 MFMAs. The table holds each codebook dword and its half-rotated form
+//     (the rotation field of a block selects the table), so a code costs two VALU ops for its
+//     address and one for sign and scale. Two interleaved copies (lane parity): on this kernel
+//     the VALU, not the LDS bank conflicts, sets the pace, and fewer copies measured as fast as
+//     four or eight;
 //   - B (192 columns x 128 bytes) sits in LDS, written by direct global->LDS loads three steps
 //     ahead (four buffers), read by all eight waves; 16-byte chunks are swizzled by column so that
 //     the fragment reads of 16 lanes hit 16 distinct bank groups;
@@ -265,7 +269,7 @@ __global__ void __launch_bounds__(256) grouped_prep_x_kernel(const uint16_t* __r
 constexpr int kGW = 8;                      // waves per workgroup (two per SIMD)
 constexpr int kGRT = 16 / kGW;              // 16-row tiles per wave (a workgroup covers 256 rows)
 constexpr int kGT = kGW * 64;
-constexpr int kGKC = 8;                     // codebook copies
+constexpr int kGKC = 2;                     // codebook copies (pre-rotated tables)
 constexpr int kGCT = 12;                    // 16-column tiles of B per wave
 constexpr int kGCols = kGCT * 16;           // B columns per workgroup
 constexpr uint32_t kGBuf = kGCols * 128;    // bytes of one B buffer (one MFMA step)
@@ -354,7 +358,7 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
   const uint32_t nst = K / kTileCols;
   const uint8_t* ex = A.base + (uint64_t)tl.expert * A.stride;
 
-  __shared__ __align__(16) uint32_t lut_s[kGKC * 2048];
+  __shared__ __align__(16) uint32_t lut_s[Lut<kGKC, true>::kDwords];
   // B of step t in buffer t % 4, written three steps ahead (four separate arrays: the compiler
   // can then tell the buffer being read from the ones being written)
   __shared__ __align__(16) uint8_t buf0[kGBuf];
@@ -370,7 +374,7 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
     uint32_t cbv[kPer];
 #pragma unroll
     for (int i = 0; i < kPer; ++i) cbv[i] = A.codebook[tid + (uint32_t)kGT * i];
-    build_lut<kGKC, kGT, kPer>(lut_s, cbv, tid);
+    build_lut<kGKC, kGT, kPer, true>(lut_s, cbv, tid);
   }
   if (tid < kGCols) {
     const uint32_t col = tid, cc = col & 15;
@@ -428,7 +432,7 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
 
-  const uint32_t copy4 = ((lane >> 1) & (kGKC - 1)) * 4u;
+  const uint32_t copy4 = (lane & (kGKC - 1)) * 4u;
   const uint32_t c = lane & 15, kg = lane >> 4;
   const uint32_t bo0 = c * 128u + (((2u * kg) ^ ((c ^ (c >> 3)) & 7u)) << 4);
   const uint32_t bo1 = c * 128u + (((2u * kg + 1u) ^ ((c ^ (c >> 3)) & 7u)) << 4);
@@ -437,8 +441,8 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
 #pragma unroll
   for (int r = 0; r < kGRT; ++r) {
     uint32_t raw[8], fb[2];
-    lut_lookup_step<kGKC>(u[r], lut, copy4, 0, raw, fb);
-    a_cur[r] = lut_finish(raw, fb);
+    lut_lookup_step<kGKC, true>(u[r], lut, copy4, 0, raw, fb);
+    a_cur[r] = lut_finish<true>(raw, fb);
   }
   v4f acc[kGRT][kGCT];
 #pragma unroll
@@ -497,9 +501,9 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
       for (int r = 0; r < kGRT; ++r) acc[r][ct] = mfma(a_cur[r], bq0, acc[r][ct]);
       if constexpr (ct >= kLook && ct < kLook + kGRT) {
         pin_step<mn>(u[ct - kLook]);
-        lut_lookup<kGKC, mn>(u[ct - kLook], lut, copy4, rawn[ct - kLook], fbn[ct - kLook]);
+        lut_lookup<kGKC, mn, true>(u[ct - kLook], lut, copy4, rawn[ct - kLook], fbn[ct - kLook]);
       } else if constexpr (ct >= kFin && ct < kFin + kGRT) {
-        a_next[ct - kFin] = lut_finish(rawn[ct - kFin], fbn[ct - kFin]);
+        a_next[ct - kFin] = lut_finish<true>(rawn[ct - kFin], fbn[ct - kFin]);
         AFFX_PIN(a_next[ct - kFin]);  // computed here, not sunk into the next step
       }
       // {one MFMA, then VALU} per row tile, then the LDS reads
