@@ -704,8 +704,9 @@ constexpr int kMaxDev = 64;
 std::mutex g_fused_mu;
 FusedVariant g_fused[kMaxDev][4];
 
-// variants: 0 M = 1 in one pass (8 codebook copies with rotated tables), 1 M = 1 in rounds, 2 M <= 5 (8 copies),
-// 3 M <= 8 (4 copies, 2 column groups)
+// variants (all with the rotated tables): 0 M = 1 in one pass (8 codebook copies), 1 M = 1 in
+// rounds, 2 M <= 5 (4 copies), 3 M <= 8 (2 copies, 2 column groups). The larger M, the more LDS
+// the activation terms take; the copies fill what is left.
 int fused_variant(uint32_t M, bool single) { return M == 1 ? (single ? 0 : 1) : M <= 5 ? 2 : 3; }
 
 int fused_prepare(int dev, int v, FusedVariant* out) {
@@ -714,8 +715,8 @@ int fused_prepare(int dev, int v, FusedVariant* out) {
   if (!f.ready) {
     static const void* fns[4] = {(const void*)decode_fused_kernel<1, 8, 1, true, true>,
                                  (const void*)decode_fused_kernel<1, 8, 1, false, true>,
-                                 (const void*)decode_fused_kernel<1, 8, 5, false, false>,
-                                 (const void*)decode_fused_kernel<2, 4, 8, false, false>};
+                                 (const void*)decode_fused_kernel<1, 4, 5, false, true>,
+                                 (const void*)decode_fused_kernel<2, 2, 8, false, true>};
     static const uint32_t kcs[4] = {8, 8, 8, 4}, maxms[4] = {1, 1, 5, 8};
     f.fn = fns[v];
     f.kc = kcs[v];
@@ -808,8 +809,8 @@ extern "C" int affx_expert_ffn_decode(const affx_layer* L, const float* x, uint6
   switch (v) {
     case 0: hipLaunchKernelGGL((decode_fused_kernel<1, 8, 1, true, true>), dim3(n_wg), dim3(kFT), lds, st, A); break;
     case 1: hipLaunchKernelGGL((decode_fused_kernel<1, 8, 1, false, true>), dim3(n_wg), dim3(kFT), lds, st, A); break;
-    case 2: hipLaunchKernelGGL((decode_fused_kernel<1, 8, 5, false, false>), dim3(n_wg), dim3(kFT), lds, st, A); break;
-    default: hipLaunchKernelGGL((decode_fused_kernel<2, 4, 8, false, false>), dim3(n_wg), dim3(kFT), lds, st, A); break;
+    case 2: hipLaunchKernelGGL((decode_fused_kernel<1, 4, 5, false, true>), dim3(n_wg), dim3(kFT), lds, st, A); break;
+    default: hipLaunchKernelGGL((decode_fused_kernel<2, 2, 8, false, true>), dim3(n_wg), dim3(kFT), lds, st, A); break;
   }
   return check_launch("decode_fused_kernel");
 }
