@@ -143,6 +143,9 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   const FusedLds L = fused_lds(M);
   __shared__ __align__(16) uint32_t lut_s[Lut<KC, ROT>::kDwords];
   const uint8_t* lut = reinterpret_cast<const uint8_t*>(lut_s);
+  // (the finish computes each block's sign mask and exponent add itself: two registers fewer per
+  // block in flight than the block table's, which this kernel's register budget needs)
+  const uint8_t* btbl = nullptr;
   uint8_t* xq = lds + L.xq;
   uint8_t* zero_l = lds + L.zero;
   float* part = reinterpret_cast<float*>(lds + L.part);
@@ -364,8 +367,8 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
       uint32_t bg[2], bu[2];
       pin_step(ug, 0);
       pin_step(uu, 0);
-      lut_lookup_step<KC, ROT>(ug, lut, copy4, 0, rg, bg);
-      lut_lookup_step<KC, ROT>(uu, lut, copy4, 0, ru, bu);
+      lut_lookup_step<KC, ROT>(ug, lut, btbl, copy4, 0, rg, bg);
+      lut_lookup_step<KC, ROT>(uu, lut, btbl, copy4, 0, ru, bu);
       v8i bc[CG];
 #pragma unroll
       for (int cg = 0; cg < CG; ++cg) bc[cg] = b_step_lds(bsrc[cg], 0);
@@ -379,12 +382,12 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
           for (int cg = 0; cg < CG; ++cg) { AFFX_PIN(acc[0][cg]); AFFX_PIN(acc[1][cg]); }
           pin_step(ug, m + 1);
           pin_step(uu, m + 1);
-          lut_lookup_step<KC, ROT>(ug, lut, copy4, m + 1, ng, nbg);
-          lut_lookup_step<KC, ROT>(uu, lut, copy4, m + 1, nu, nbu);
+          lut_lookup_step<KC, ROT>(ug, lut, btbl, copy4, m + 1, ng, nbg);
+          lut_lookup_step<KC, ROT>(uu, lut, btbl, copy4, m + 1, nu, nbu);
 #pragma unroll
           for (int cg = 0; cg < CG; ++cg) bn[cg] = b_step_lds(bsrc[cg], m + 1);
         }
-        const v8i ag = lut_finish<ROT>(rg, bg), au = lut_finish<ROT>(ru, bu);
+        const v8i ag = lut_finish(rg, bg), au = lut_finish(ru, bu);
 #pragma unroll
         for (int cg = 0; cg < CG; ++cg) {
           acc[0][cg] = mfma(ag, bc[cg], acc[0][cg]);
@@ -529,8 +532,8 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
       for (int m = 0; m < kPreSteps; ++m) {
         uint32_t raw[8], bv[2];
         pin_step(ud, m);
-        lut_lookup_step<KC, ROT>(ud, lut, copy4, m, raw, bv);
-        ad[m] = lut_finish<ROT>(raw, bv);
+        lut_lookup_step<KC, ROT>(ud, lut, btbl, copy4, m, raw, bv);
+        ad[m] = lut_finish(raw, bv);
       }
     }
   }
@@ -601,7 +604,7 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
           uint32_t raw[8];
           uint32_t bv[2];
           pin_step(ud, m0);
-          lut_lookup_step<KC, ROT>(ud, lut, copy4, m0, raw, bv);
+          lut_lookup_step<KC, ROT>(ud, lut, btbl, copy4, m0, raw, bv);
 #pragma unroll
           for (int m = m0; m < 8; ++m) {
             uint32_t nraw[8];
@@ -613,13 +616,13 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
 #pragma unroll
               for (int cg = 0; cg < CG; ++cg) AFFX_PIN(acc[cg]);
               pin_step(ud, m + 1);
-              lut_lookup_step<KC, ROT>(ud, lut, copy4, m + 1, nraw, nbv);
+              lut_lookup_step<KC, ROT>(ud, lut, btbl, copy4, m + 1, nraw, nbv);
               if constexpr (!BPRE) {
 #pragma unroll
                 for (int cg = 0; cg < CG; ++cg) bn[cg] = b_step(b.p[cg], m + 1);
               }
             }
-            const v8i a = lut_finish<ROT>(raw, bv);
+            const v8i a = lut_finish(raw, bv);
             if constexpr (BPRE) {
               acc[0] = mfma(a, bpre[m], acc[0]);
             } else {

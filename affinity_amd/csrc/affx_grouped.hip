@@ -359,6 +359,8 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
   const uint8_t* ex = A.base + (uint64_t)tl.expert * A.stride;
 
   __shared__ __align__(16) uint32_t lut_s[Lut<kGKC, true>::kDwords];
+  __shared__ __align__(16) uint2 blk_s[16];
+  const uint8_t* btbl = reinterpret_cast<const uint8_t*>(blk_s);
   // B of step t in buffer t % 4, written three steps ahead (four separate arrays: the compiler
   // can then tell the buffer being read from the ones being written)
   __shared__ __align__(16) uint8_t buf0[kGBuf];
@@ -375,6 +377,7 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
 #pragma unroll
     for (int i = 0; i < kPer; ++i) cbv[i] = A.codebook[tid + (uint32_t)kGT * i];
     build_lut<kGKC, kGT, kPer, true>(lut_s, cbv, tid);
+    build_blk_tbl(blk_s, tid);
   }
   if (tid < kGCols) {
     const uint32_t col = tid, cc = col & 15;
@@ -440,9 +443,9 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
   v8i a_cur[kGRT];
 #pragma unroll
   for (int r = 0; r < kGRT; ++r) {
-    uint32_t raw[8], fb[2];
-    lut_lookup_step<kGKC, true>(u[r], lut, copy4, 0, raw, fb);
-    a_cur[r] = lut_finish<true>(raw, fb);
+    uint32_t raw[8], sx[4];
+    lut_lookup_step<kGKC, true>(u[r], lut, btbl, copy4, 0, raw, sx);
+    a_cur[r] = lut_finish(raw, sx);
   }
   v4f acc[kGRT][kGCT];
 #pragma unroll
@@ -482,7 +485,7 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
     // the next 1024 columns after step 7: the ring has reloaded every register those reads use.)
     constexpr int mn = (m + 1) & 7;
     constexpr int kLook = 4, kFin = 8;
-    uint32_t rawn[kGRT][8], fbn[kGRT][2];
+    uint32_t rawn[kGRT][8], sxn[kGRT][4];
     v8i a_next[kGRT];
     auto bread = [&](int ct) -> v8i {
       const u32x4 lo = *reinterpret_cast<const u32x4*>(bcur + ct * 2048 + bo0);
@@ -501,9 +504,9 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
       for (int r = 0; r < kGRT; ++r) acc[r][ct] = mfma(a_cur[r], bq0, acc[r][ct]);
       if constexpr (ct >= kLook && ct < kLook + kGRT) {
         pin_step<mn>(u[ct - kLook]);
-        lut_lookup<kGKC, mn, true>(u[ct - kLook], lut, copy4, rawn[ct - kLook], fbn[ct - kLook]);
+        lut_lookup<kGKC, mn, true>(u[ct - kLook], lut, btbl, copy4, rawn[ct - kLook], sxn[ct - kLook]);
       } else if constexpr (ct >= kFin && ct < kFin + kGRT) {
-        a_next[ct - kFin] = lut_finish<true>(rawn[ct - kFin], fbn[ct - kFin]);
+        a_next[ct - kFin] = lut_finish(rawn[ct - kFin], sxn[ct - kFin]);
         AFFX_PIN(a_next[ct - kFin]);  // computed here, not sunk into the next step
       }
       // {one MFMA, then VALU} per row tile, then the LDS reads

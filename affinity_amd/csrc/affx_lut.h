@@ -69,16 +69,30 @@ __device__ __forceinline__ uint32_t code_addr(const uint32_t (&c)[20], uint32_t 
   return (x & (0x3FFu << S)) | vb;
 }
 
-// The eight table reads of MFMA step MSTEP (blocks 2m, 2m+1) and the two blocks' 6-bit fields
-// (bits 0-2 exponent add s, 3 sign, 4 rotation, 5 variant).
-template <int KC, int MSTEP, bool ROT = false>
-__device__ __forceinline__ void lut_lookup(const Unit& u, const uint8_t* lds, uint32_t copy4,
-                                           uint32_t (&raw)[8], uint32_t (&fb)[2]) {
-  fb[0] = stream_bits<3>(u.f, 12 * MSTEP, 6);
-  fb[1] = stream_bits<3>(u.f, 12 * MSTEP + 6, 6);
-  // table: variant (field bit 5), or 2 * variant + rotation (bits 4-5) with rotated tables
-  const uint32_t vb0 = ((ROT ? (fb[0] >> 4) & 3u : fb[0] >> 5) << Lut<KC>::kVarSh) | copy4;
-  const uint32_t vb1 = ((ROT ? (fb[1] >> 4) & 3u : fb[1] >> 5) << Lut<KC>::kVarSh) | copy4;
+// Sign mask and exponent add of a block by the low four bits of its field (bits 0-2 exponent add
+// s, bit 3 sign): entry f = {sign ? 0x80808080 : 0, (s << 3) in each of the four bytes}
+// (block_xor, block_add). One 8-byte LDS read per block replaces five VALU ops; the 16 entries
+// occupy 32 distinct banks, so the reads of a wave never conflict.
+constexpr int kBlkTblBytes = 16 * 8;
+__device__ __forceinline__ void build_blk_tbl(uint2* t, uint32_t tid) {
+  if (tid < 16) t[tid] = uint2{block_xor(tid), block_add(tid)};
+}
+
+// The eight table reads of MFMA step MSTEP (blocks 2m, 2m+1) and what the finish needs of the two
+// blocks: NS = 4, their sign masks and exponent adds read from the block table btbl (sx = {xor
+// 2m, add 2m, xor 2m+1, add 2m+1}: fewer VALU ops); NS = 2, their fields (sx = {field 2m, field
+// 2m+1}: fewer registers held until the finish). Block fields: bits 0-2 exponent add s, 3 sign,
+// 4 rotation, 5 variant. The codebook table is the rotated one (both halves of each entry; field
+// bits 4-5 select the table).
+template <int KC, int MSTEP, bool ROT = true, int NS>
+__device__ __forceinline__ void lut_lookup(const Unit& u, const uint8_t* lds, const uint8_t* btbl,
+                                           uint32_t copy4, uint32_t (&raw)[8], uint32_t (&sx)[NS]) {
+  static_assert(ROT, "the finish applies no rotation: the rotated tables are required");
+  static_assert(NS == 2 || NS == 4, "");
+  const uint32_t fb0 = stream_bits<3>(u.f, 12 * MSTEP, 6);
+  const uint32_t fb1 = stream_bits<3>(u.f, 12 * MSTEP + 6, 6);
+  const uint32_t vb0 = (((fb0 >> 4) & 3u) << Lut<KC>::kVarSh) | copy4;
+  const uint32_t vb1 = (((fb1 >> 4) & 3u) << Lut<KC>::kVarSh) | copy4;
   constexpr int I = 8 * MSTEP;
   raw[0] = *reinterpret_cast<const uint32_t*>(lds + code_addr<KC, I + 0>(u.c, vb0));
   raw[1] = *reinterpret_cast<const uint32_t*>(lds + code_addr<KC, I + 1>(u.c, vb0));
@@ -88,40 +102,44 @@ __device__ __forceinline__ void lut_lookup(const Unit& u, const uint8_t* lds, ui
   raw[5] = *reinterpret_cast<const uint32_t*>(lds + code_addr<KC, I + 5>(u.c, vb1));
   raw[6] = *reinterpret_cast<const uint32_t*>(lds + code_addr<KC, I + 6>(u.c, vb1));
   raw[7] = *reinterpret_cast<const uint32_t*>(lds + code_addr<KC, I + 7>(u.c, vb1));
+  if constexpr (NS == 4) {
+    const uint2 t0 = *reinterpret_cast<const uint2*>(btbl + ((fb0 << 3) & 0x78u));
+    const uint2 t1 = *reinterpret_cast<const uint2*>(btbl + ((fb1 << 3) & 0x78u));
+    sx[0] = t0.x; sx[1] = t0.y; sx[2] = t1.x; sx[3] = t1.y;
+  } else {
+    sx[0] = fb0;
+    sx[1] = fb1;
+  }
 }
 
-// A fragment from the table reads: rotation by table-entry halves, sign flip, exponent add
-// (src/gpu/expert_kernel.hip:594-617; rotation src/quant/blockquant.cpp:826-828).
-// (ROT: the reads came from pre-rotated tables)
-template <bool ROT = false>
-__device__ __forceinline__ v8i lut_finish(const uint32_t (&raw)[8], const uint32_t (&fb)[2]) {
+// A fragment from the table reads: sign flip, exponent add, one v_xad per dword
+// (src/gpu/expert_kernel.hip:594-617; the rotation, src/quant/blockquant.cpp:826-828, is in the
+// table).
+template <int NS>
+__device__ __forceinline__ v8i lut_finish(const uint32_t (&raw)[8], const uint32_t (&sx)[NS]) {
   v8i a;
 #pragma unroll
   for (int b = 0; b < 2; ++b) {
-    // exponent add s << 3 replicated into the four bytes (v_perm: no 32-bit multiply)
-    const uint32_t xm = block_xor(fb[b]);
-    const uint32_t ad = __builtin_amdgcn_perm(0u, (fb[b] << 3) & 0x38u, 0u);
+    const uint32_t xm = NS == 4 ? sx[2 * b] : block_xor(sx[b % NS]);
+    const uint32_t ad = NS == 4 ? sx[(2 * b + 1) % NS] : block_add(sx[b % NS]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t r = ROT ? raw[4 * b + i] : __builtin_amdgcn_alignbit(raw[4 * b + i], raw[4 * b + i], fb[b] & 16u);
-      a[4 * b + i] = (int)((r ^ xm) + ad);
-    }
+    for (int i = 0; i < 4; ++i) a[4 * b + i] = (int)((raw[4 * b + i] ^ xm) + ad);
   }
   return a;
 }
 
-template <int KC, bool ROT = false>
-__device__ __forceinline__ void lut_lookup_step(const Unit& u, const uint8_t* lds, uint32_t copy4,
-                                                int m, uint32_t (&raw)[8], uint32_t (&fb)[2]) {
+template <int KC, bool ROT = true, int NS>
+__device__ __forceinline__ void lut_lookup_step(const Unit& u, const uint8_t* lds, const uint8_t* btbl,
+                                                uint32_t copy4, int m, uint32_t (&raw)[8], uint32_t (&sx)[NS]) {
   switch (m) {
-    case 0: lut_lookup<KC, 0, ROT>(u, lds, copy4, raw, fb); break;
-    case 1: lut_lookup<KC, 1, ROT>(u, lds, copy4, raw, fb); break;
-    case 2: lut_lookup<KC, 2, ROT>(u, lds, copy4, raw, fb); break;
-    case 3: lut_lookup<KC, 3, ROT>(u, lds, copy4, raw, fb); break;
-    case 4: lut_lookup<KC, 4, ROT>(u, lds, copy4, raw, fb); break;
-    case 5: lut_lookup<KC, 5, ROT>(u, lds, copy4, raw, fb); break;
-    case 6: lut_lookup<KC, 6, ROT>(u, lds, copy4, raw, fb); break;
-    default: lut_lookup<KC, 7, ROT>(u, lds, copy4, raw, fb); break;
+    case 0: lut_lookup<KC, 0, ROT>(u, lds, btbl, copy4, raw, sx); break;
+    case 1: lut_lookup<KC, 1, ROT>(u, lds, btbl, copy4, raw, sx); break;
+    case 2: lut_lookup<KC, 2, ROT>(u, lds, btbl, copy4, raw, sx); break;
+    case 3: lut_lookup<KC, 3, ROT>(u, lds, btbl, copy4, raw, sx); break;
+    case 4: lut_lookup<KC, 4, ROT>(u, lds, btbl, copy4, raw, sx); break;
+    case 5: lut_lookup<KC, 5, ROT>(u, lds, btbl, copy4, raw, sx); break;
+    case 6: lut_lookup<KC, 6, ROT>(u, lds, btbl, copy4, raw, sx); break;
+    default: lut_lookup<KC, 7, ROT>(u, lds, btbl, copy4, raw, sx); break;
   }
 }
 
