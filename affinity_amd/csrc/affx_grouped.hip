@@ -283,6 +283,7 @@ struct GemmArgs {
   const uint32_t* codebook;
   const GroupedHdr* hdr;
   const Tile* tiles;
+  uint32_t max_tiles;       // entries of tiles (allocated; the header says how many are used)
   const uint32_t* slot_tok;
   const int32_t* slot_sigma;  // activation exponent of the slot's token
   const uint8_t* ws;        // B rows and the zero row, addressed by 32-bit offsets from here
@@ -349,10 +350,18 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
   const uint32_t nrb = PH == 0 ? A.inter / 128u : A.hidden / 256u;  // row blocks
   const uint32_t w = blockIdx.x, xcd = w & 7u, l = w >> 3;
   const uint32_t rb = l % nrb, tile_id = (l / nrb) * 8u + xcd;
-  const uint32_t n_tiles = PH == 0 ? A.hdr->n_tiles1 : A.hdr->n_tiles2;
-  if (tile_id >= n_tiles) return;
-  const Tile tl = A.tiles[tile_id];
   const uint32_t tid = threadIdx.x, lane = tid & 63;
+  // Set-up in three memory round trips: (1) the codebook, the tile count and this tile (read
+  // before it is known to be in use: any index below max_tiles is allocated); (2) the B row of
+  // every column, then the first weights; (3) the first three steps of B.
+  constexpr int kPer = 2048 / kGT;
+  uint32_t cbv[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) cbv[i] = A.codebook[tid + (uint32_t)kGT * i];
+  const uint32_t n_tiles = PH == 0 ? A.hdr->n_tiles1 : A.hdr->n_tiles2;
+  const Tile tl = A.tiles[tile_id < A.max_tiles ? tile_id : 0u];
+  if (tile_id >= n_tiles || tl.n == 0) return;  // (a tile in use has n >= 1: the test only makes
+                                                // both loads precede the branch, in one round trip)
   const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t K = PH == 0 ? A.hidden : A.inter;
   const uint32_t nst = K / kTileCols;
@@ -370,26 +379,37 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
   uint32_t* rowoff = reinterpret_cast<uint32_t*>(buf3);  // set-up only, before buffer 3 is written
   const uint8_t* lut = reinterpret_cast<const uint8_t*>(lut_s);
 
-  // ---- set-up: codebook copies, B row of every column, first step of B, first units ----------
-  {
-    constexpr int kPer = 2048 / kGT;
-    uint32_t cbv[kPer];
+  // ---- set-up (2): B row of every column (its loads first: the set-up waits for them, and loads
+  // complete in issue order), the first weights, the codebook copies ----------------------------
+  const uint32_t bcol_j = (tid >> 4) * TPG + (tid & 15u) / TX;
+  const bool bcol_used = tid < kGCols && (tid & 15u) < TX * TPG && bcol_j < tl.n;
+  // (unconditional: a column past the tile's tokens reads the tile's first slot, unused)
+  const uint32_t bslot = tl.slot0 + (bcol_used ? bcol_j : 0u);
+  const uint32_t brow = PH == 0 ? A.slot_tok[bslot] : bslot;
+  __builtin_amdgcn_sched_barrier(0);
+
+  // the wave's 16-row tiles: gate/up = gate tile rt0 (unit 0) and the same rows of up (unit 1);
+  // down = two consecutive tiles. Unit r's code/field planes: (c0, f0) for the gate unit or down,
+  // (c1, f1) for the up unit.
+  const uint64_t cbytes = (uint64_t)(PH == 0 ? A.inter : A.hidden) * code_row_bytes(K);
+  const uint64_t fbytes = (uint64_t)(PH == 0 ? A.inter : A.hidden) * field_row_bytes(K);
+  const __amdgpu_buffer_rsrc_t c0 = buffer_rsrc(ex + A.off[PH == 0 ? kGateCodes : kDownCodes], (uint32_t)cbytes);
+  const __amdgpu_buffer_rsrc_t f0 = buffer_rsrc(ex + A.off[PH == 0 ? kGateFields : kDownFields], (uint32_t)fbytes);
+  const __amdgpu_buffer_rsrc_t c1 = buffer_rsrc(ex + A.off[PH == 0 ? kUpCodes : kDownCodes], (uint32_t)cbytes);
+  const __amdgpu_buffer_rsrc_t f1 = buffer_rsrc(ex + A.off[PH == 0 ? kUpFields : kDownFields], (uint32_t)fbytes);
+  constexpr int kHalf = kGRT / 2;  // gate/up: units [0, kHalf) gate, [kHalf, kGRT) the same rows of up
+  const uint32_t rt0 = PH == 0 ? rb * 8u + kHalf * wv : rb * 16u + kGRT * wv;
+  auto rt_of = [&](int r) -> uint32_t { return PH == 0 ? rt0 + (r % kHalf) : rt0 + r; };
+  Unit u[kGRT];
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) cbv[i] = A.codebook[tid + (uint32_t)kGT * i];
-    build_lut<kGKC, kGT, kPer, true>(lut_s, cbv, tid);
-    build_blk_tbl(blk_s, tid);
-  }
-  if (tid < kGCols) {
-    const uint32_t col = tid, cc = col & 15;
-    const uint32_t j = (col >> 4) * TPG + cc / TX, tau = cc % TX;
-    uint64_t off = A.zero_off;
-    if (cc < TX * TPG && j < tl.n) {
-      const uint32_t slot = tl.slot0 + j;
-      const uint32_t row = PH == 0 ? A.slot_tok[slot] : slot;
-      off = A.b_off + ((uint64_t)row * TX + tau) * K;
-    }
-    rowoff[col] = (uint32_t)off;
-  }
+  for (int r = 0; r < kGRT; ++r)
+    load_unit_buf(u[r], PH == 0 && r >= kHalf ? c1 : c0, PH == 0 && r >= kHalf ? f1 : f0, rt_of(r) * nst, lane);
+  __builtin_amdgcn_sched_barrier(0);
+
+  build_lut<kGKC, kGT, kPer, true>(lut_s, cbv, tid);
+  build_blk_tbl(blk_s, tid);
+  if (tid < kGCols)
+    rowoff[tid] = bcol_used ? (uint32_t)(A.b_off + ((uint64_t)brow * TX + (tid & 15u) % TX) * K) : (uint32_t)A.zero_off;
   __syncthreads();
   // DMA lane map: instruction i of wave w writes columns 8b..8b+7 (b = kGDma w + i), lane l to
   // LDS slot l & 7 of column 8b + (l >> 3); slot p of column col holds global chunk p ^ f(col),
@@ -410,27 +430,11 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(wsr, AFFX_LDS_PTR(buf + (kGDma * wv + i) * 1024u), 16, roff[i],
                                                step * 128u, 0, 0);
   };
-
-  // the wave's 16-row tiles: gate/up = gate tile rt0 (unit 0) and the same rows of up (unit 1);
-  // down = two consecutive tiles. Unit r's code/field planes: (c0, f0) for the gate unit or down,
-  // (c1, f1) for the up unit.
-  const uint64_t cbytes = (uint64_t)(PH == 0 ? A.inter : A.hidden) * code_row_bytes(K);
-  const uint64_t fbytes = (uint64_t)(PH == 0 ? A.inter : A.hidden) * field_row_bytes(K);
-  const __amdgpu_buffer_rsrc_t c0 = buffer_rsrc(ex + A.off[PH == 0 ? kGateCodes : kDownCodes], (uint32_t)cbytes);
-  const __amdgpu_buffer_rsrc_t f0 = buffer_rsrc(ex + A.off[PH == 0 ? kGateFields : kDownFields], (uint32_t)fbytes);
-  const __amdgpu_buffer_rsrc_t c1 = buffer_rsrc(ex + A.off[PH == 0 ? kUpCodes : kDownCodes], (uint32_t)cbytes);
-  const __amdgpu_buffer_rsrc_t f1 = buffer_rsrc(ex + A.off[PH == 0 ? kUpFields : kDownFields], (uint32_t)fbytes);
-  constexpr int kHalf = kGRT / 2;  // gate/up: units [0, kHalf) gate, [kHalf, kGRT) the same rows of up
-  const uint32_t rt0 = PH == 0 ? rb * 8u + kHalf * wv : rb * 16u + kGRT * wv;
-  auto rt_of = [&](int r) -> uint32_t { return PH == 0 ? rt0 + (r % kHalf) : rt0 + r; };
+  // ---- set-up (3): the first three steps of B ----------------------------------------------
   const uint32_t nsteps = nst * 8u;
   dma(buf0, 0);
   dma(buf1, 1);
   dma(buf2, 2);
-  Unit u[kGRT];
-#pragma unroll
-  for (int r = 0; r < kGRT; ++r)
-    load_unit_buf(u[r], PH == 0 && r >= kHalf ? c1 : c0, PH == 0 && r >= kHalf ? f1 : f0, rt_of(r) * nst, lane);
   __builtin_amdgcn_s_waitcnt(AFFX_VMCNT(0));
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
@@ -804,6 +808,7 @@ int affx_expert_ffn_grouped(const affx_layer* L, const void* x, const void* x_lo
   const uint32_t g1 = (L->inter / 128) * ((lay.max_tiles1 + 7) / 8 * 8);
   const uint32_t g2 = (L->hidden / 256) * ((lay.max_tiles2 + 7) / 8 * 8);
   A.tiles = (const Tile*)(b + lay.tiles1);
+  A.max_tiles = lay.max_tiles1;
   A.b_off = lay.xq;
   if (tx == 2)
     hipLaunchKernelGGL((grouped_gemm_kernel<0, 2>), dim3(g1), dim3(kGT), 0, s, A);
@@ -811,6 +816,7 @@ int affx_expert_ffn_grouped(const affx_layer* L, const void* x, const void* x_lo
     hipLaunchKernelGGL((grouped_gemm_kernel<0, 3>), dim3(g1), dim3(kGT), 0, s, A);
   if ((rc = check_launch("grouped_gemm_kernel (gate/up)"))) return rc;
   A.tiles = (const Tile*)(b + lay.tiles2);
+  A.max_tiles = lay.max_tiles2;
   A.b_off = lay.aq;
   hipLaunchKernelGGL((grouped_gemm_kernel<1, 3>), dim3(g2), dim3(kGT), 0, s, A);
   if ((rc = check_launch("grouped_gemm_kernel (down)"))) return rc;
