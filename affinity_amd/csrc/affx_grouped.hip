@@ -606,6 +606,7 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
       const uint32_t prow = kperm(row0);
       static_for<0, kGCT>([&](auto cc) {
         constexpr int ct = decltype(cc)::value;
+        if (ct * TPG >= tl.n) return;  // no token in this column tile (the same for the whole wave)
         float sg[4], su[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
@@ -650,6 +651,7 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
       bf16x4(rdw[r], rd);
       static_for<0, kGCT>([&](auto cc) {
         constexpr int ct = decltype(cc)::value;
+        if (ct * TPG >= tl.n) return;  // no token in this column tile (the same for the whole wave)
         float sd[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) sd[v] = terms(acc[r][ct][v]);
