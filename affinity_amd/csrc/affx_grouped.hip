@@ -261,8 +261,9 @@ __global__ void __launch_bounds__(256) grouped_prep_x_kernel(const uint16_t* __r
 //     address and one for sign and scale. Two interleaved copies (lane parity): on this kernel
 //     the VALU, not the LDS bank conflicts, sets the pace, and fewer copies measured as fast as
 //     four or eight;
-//   - B (192 columns x 128 bytes) sits in LDS, written by direct global->LDS loads three steps
-//     ahead (four buffers), read by all eight waves; 16-byte chunks are swizzled by column so that
+//   - B (192 columns x 128 bytes) sits in LDS, written by direct global->LDS loads two steps at
+//     a time, two steps ahead (four buffers, one workgroup barrier per two steps), read by all
+//     eight waves; 16-byte chunks are swizzled by column so that
 //     the fragment reads of 16 lanes hit 16 distinct bank groups;
 //   - the packed weights of the next 1024 columns stream into a register ring, each chunk
 //     reloaded as soon as the lookups of the current 1024 columns are past it.
@@ -353,7 +354,7 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
   const uint32_t tid = threadIdx.x, lane = tid & 63;
   // Set-up in three memory round trips: (1) the codebook, the tile count and this tile (read
   // before it is known to be in use: any index below max_tiles is allocated); (2) the B row of
-  // every column, then the first weights; (3) the first three steps of B.
+  // every column, then the first weights; (3) the first two steps of B.
   constexpr int kPer = 2048 / kGT;
   uint32_t cbv[kPer];
 #pragma unroll
@@ -370,8 +371,8 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
   __shared__ __align__(16) uint32_t lut_s[Lut<kGKC, true>::kDwords];
   __shared__ __align__(16) uint2 blk_s[16];
   const uint8_t* btbl = reinterpret_cast<const uint8_t*>(blk_s);
-  // B of step t in buffer t % 4, written three steps ahead (four separate arrays: the compiler
-  // can then tell the buffer being read from the ones being written)
+  // B of step t in buffer t % 4, written two steps at a time, two steps ahead (four separate
+  // arrays: the compiler can then tell the buffers being read from the ones being written)
   __shared__ __align__(16) uint8_t buf0[kGBuf];
   __shared__ __align__(16) uint8_t buf1[kGBuf];
   __shared__ __align__(16) uint8_t buf2[kGBuf];
@@ -430,11 +431,10 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(wsr, AFFX_LDS_PTR(buf + (kGDma * wv + i) * 1024u), 16, roff[i],
                                                step * 128u, 0, 0);
   };
-  // ---- set-up (3): the first three steps of B ----------------------------------------------
+  // ---- set-up (3): the first two steps of B ------------------------------------------------
   const uint32_t nsteps = nst * 8u;
   dma(buf0, 0);
   dma(buf1, 1);
-  dma(buf2, 2);
   __builtin_amdgcn_s_waitcnt(AFFX_VMCNT(0));
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
@@ -464,10 +464,15 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
   auto step = [&](auto mc, uint32_t s, bool more) {
     constexpr int m = decltype(mc)::value;
     const uint8_t* bcur = bufsel(m & 3);
-    // B of step t + 3, issued every step (past the last step it reloads the last step's B into
-    // a buffer nobody reads again: the count of loads in flight stays the same every step)
-    const uint32_t t3 = s * 8u + m + 3u;
-    dma(bufsel((m + 3) & 3), t3 < nsteps ? t3 : nsteps - 1u);
+    // B of steps t + 2 and t + 3, issued at the top of even steps t into the buffers of steps
+    // t - 2 and t - 1 (read before the barrier that ended step t - 1): the workgroup then needs
+    // one barrier per two steps. Past the last step the loads repeat the last step's B into
+    // buffers nobody reads again, so the count of loads in flight is the same on every path.
+    if constexpr ((m & 1) == 0) {
+      const uint32_t t2 = s * 8u + m + 2u, t3 = t2 + 1u;
+      dma(bufsel((m + 2) & 3), t2 < nsteps ? t2 : nsteps - 1u);
+      dma(bufsel((m + 3) & 3), t3 < nsteps ? t3 : nsteps - 1u);
+    }
     __builtin_amdgcn_sched_barrier(0);
     // ring loads for the next 1024 columns; after the last ones, the same loads of tile 0 (hot
     // in the cache, read by every workgroup): their registers are not read again, and issuing
@@ -534,17 +539,16 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
       for (int ct = 0; ct < kGCT; ++ct) AFFX_PIN(acc[r][ct]);
 #pragma unroll
     for (int r = 0; r < kGRT; ++r) a_cur[r] = a_next[r];
-    // The next step's B (issued at the top of step t - 2) is in LDS once every wave's loads up to
-    // it have landed: loads complete in issue order, so at most the loads issued after it may
-    // still be outstanding: the B loads of two steps and the ring loads of steps t - 2 .. t
-    // (2 units x {0,1,1,1,1,1,1,2} by step). (In the first two steps more were issued after it: waiting for
-    // fewer is then only stricter.)
-    {
+    // After an odd step t: the B of steps t + 1 and t + 2 (issued at the top of step t - 1) is in
+    // LDS once every wave's loads up to them have landed. Loads complete in issue order, so at
+    // most the loads issued after them may still be outstanding: the ring loads of steps t - 1
+    // and t (2 units x {0,1,1,1,1,1,1,2} by step).
+    if constexpr ((m & 1) == 1) {
       constexpr int c[8] = {0, 1, 1, 1, 1, 1, 1, 2};
-      constexpr int k = 2 * kGDma + kGRT * (c[(m + 6) & 7] + c[(m + 7) & 7] + c[m]);
+      constexpr int k = kGRT * (c[m - 1] + c[m]);
       __builtin_amdgcn_s_waitcnt(AFFX_VMCNT(k));
+      __builtin_amdgcn_s_barrier();
     }
-    __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
   };
   for (uint32_t s = 0; s < nst; ++s) {
