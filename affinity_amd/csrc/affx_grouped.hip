@@ -345,28 +345,41 @@ __device__ __forceinline__ void ring_load(Unit& u, __amdgpu_buffer_rsrc_t cr, __
 template <int PH, int TX>
 __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
   constexpr int TPG = 16 / TX;  // tokens per 16-column tile
-  // XCD-aware order: the device hands consecutive workgroups to its 8 XCDs in turn, so workgroup
-  // w runs on XCD w % 8. All row blocks of one token tile go to the same XCD (its L2 then holds
-  // the tile's activations for all of them), consecutive tiles to different XCDs.
+  constexpr int kHalf = kGRT / 2;  // gate/up: units [0, kHalf) gate, [kHalf, kGRT) the same rows of up
+  // Persistent: workgroup b runs the items (row block, token tile) w = b, b + G, b + 2G, ... (G =
+  // gridDim.x, a multiple of 8). XCD-aware order: the device hands consecutive workgroups to its
+  // 8 XCDs in turn, so workgroup b runs on XCD b % 8 = w % 8 for all of its items. All row blocks
+  // of one token tile go to the same XCD (its L2 then holds the tile's activations for all of
+  // them), consecutive tiles to different XCDs. Items are in increasing tile order per workgroup,
+  // so the first item past the last tile ends the workgroup.
   const uint32_t nrb = PH == 0 ? A.inter / 128u : A.hidden / 256u;  // row blocks
-  const uint32_t w = blockIdx.x, xcd = w & 7u, l = w >> 3;
-  const uint32_t rb = l % nrb, tile_id = (l / nrb) * 8u + xcd;
+  auto item_of = [&](uint32_t w, uint32_t& rb_, uint32_t& tile_) {
+    const uint32_t l = w >> 3;
+    rb_ = l % nrb;
+    tile_ = (l / nrb) * 8u + (w & 7u);
+  };
   const uint32_t tid = threadIdx.x, lane = tid & 63;
-  // Set-up in three memory round trips: (1) the codebook, the tile count and this tile (read
-  // before it is known to be in use: any index below max_tiles is allocated); (2) the B row of
-  // every column, then the first weights; (3) the first two steps of B.
+  const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t K = PH == 0 ? A.hidden : A.inter;
+  const uint32_t nst = K / kTileCols;
+  const uint32_t nsteps = nst * 8u;
+  // Set-up of the first item in three memory round trips: (1) the codebook, the tile count and
+  // the tile (read before it is known to be in use: any index below max_tiles is allocated);
+  // (2) the B row of every column, then the first weights; (3) the first two steps of B. Later
+  // items request their tile and B rows right after the previous item's steps, so that round
+  // trip is spent on the previous item's epilogue; their weights and first two steps of B follow
+  // the epilogue. (Requesting the weights before the epilogue too was measured slower: the
+  // weights and the accumulators together overflow the registers.)
   constexpr int kPer = 2048 / kGT;
   uint32_t cbv[kPer];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) cbv[i] = A.codebook[tid + (uint32_t)kGT * i];
   const uint32_t n_tiles = PH == 0 ? A.hdr->n_tiles1 : A.hdr->n_tiles2;
-  const Tile tl = A.tiles[tile_id < A.max_tiles ? tile_id : 0u];
+  uint32_t w = blockIdx.x, rb, tile_id;
+  item_of(w, rb, tile_id);
+  Tile tl = A.tiles[tile_id < A.max_tiles ? tile_id : 0u];
   if (tile_id >= n_tiles || tl.n == 0) return;  // (a tile in use has n >= 1: the test only makes
                                                 // both loads precede the branch, in one round trip)
-  const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const uint32_t K = PH == 0 ? A.hidden : A.inter;
-  const uint32_t nst = K / kTileCols;
-  const uint8_t* ex = A.base + (uint64_t)tl.expert * A.stride;
 
   __shared__ __align__(16) uint32_t lut_s[Lut<kGKC, true>::kDwords];
   __shared__ __align__(16) uint2 blk_s[16];
@@ -379,51 +392,58 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
   __shared__ __align__(16) uint8_t buf3[kGBuf];
   uint32_t* rowoff = reinterpret_cast<uint32_t*>(buf3);  // set-up only, before buffer 3 is written
   const uint8_t* lut = reinterpret_cast<const uint8_t*>(lut_s);
+  auto bufsel = [&](int i) -> uint8_t* { return i == 0 ? buf0 : i == 1 ? buf1 : i == 2 ? buf2 : buf3; };
 
-  // ---- set-up (2): B row of every column (its loads first: the set-up waits for them, and loads
-  // complete in issue order), the first weights, the codebook copies ----------------------------
-  const uint32_t bcol_j = (tid >> 4) * TPG + (tid & 15u) / TX;
-  const bool bcol_used = tid < kGCols && (tid & 15u) < TX * TPG && bcol_j < tl.n;
-  // (unconditional: a column past the tile's tokens reads the tile's first slot, unused)
-  const uint32_t bslot = tl.slot0 + (bcol_used ? bcol_j : 0u);
-  const uint32_t brow = PH == 0 ? A.slot_tok[bslot] : bslot;
-  __builtin_amdgcn_sched_barrier(0);
-
+  // ---- per-item state: the expert's planes, this wave's row tiles, the B rows -----------------
   // the wave's 16-row tiles: gate/up = gate tile rt0 (unit 0) and the same rows of up (unit 1);
   // down = two consecutive tiles. Unit r's code/field planes: (c0, f0) for the gate unit or down,
   // (c1, f1) for the up unit.
   const uint64_t cbytes = (uint64_t)(PH == 0 ? A.inter : A.hidden) * code_row_bytes(K);
   const uint64_t fbytes = (uint64_t)(PH == 0 ? A.inter : A.hidden) * field_row_bytes(K);
-  const __amdgpu_buffer_rsrc_t c0 = buffer_rsrc(ex + A.off[PH == 0 ? kGateCodes : kDownCodes], (uint32_t)cbytes);
-  const __amdgpu_buffer_rsrc_t f0 = buffer_rsrc(ex + A.off[PH == 0 ? kGateFields : kDownFields], (uint32_t)fbytes);
-  const __amdgpu_buffer_rsrc_t c1 = buffer_rsrc(ex + A.off[PH == 0 ? kUpCodes : kDownCodes], (uint32_t)cbytes);
-  const __amdgpu_buffer_rsrc_t f1 = buffer_rsrc(ex + A.off[PH == 0 ? kUpFields : kDownFields], (uint32_t)fbytes);
-  constexpr int kHalf = kGRT / 2;  // gate/up: units [0, kHalf) gate, [kHalf, kGRT) the same rows of up
-  const uint32_t rt0 = PH == 0 ? rb * 8u + kHalf * wv : rb * 16u + kGRT * wv;
+  const uint8_t* ex;
+  __amdgpu_buffer_rsrc_t c0, f0, c1, f1;
+  uint32_t rt0;
+  auto set_item = [&](const Tile& t, uint32_t rb_) {
+    ex = A.base + (uint64_t)t.expert * A.stride;
+    c0 = buffer_rsrc(ex + A.off[PH == 0 ? kGateCodes : kDownCodes], (uint32_t)cbytes);
+    f0 = buffer_rsrc(ex + A.off[PH == 0 ? kGateFields : kDownFields], (uint32_t)fbytes);
+    c1 = buffer_rsrc(ex + A.off[PH == 0 ? kUpCodes : kDownCodes], (uint32_t)cbytes);
+    f1 = buffer_rsrc(ex + A.off[PH == 0 ? kUpFields : kDownFields], (uint32_t)fbytes);
+    rt0 = PH == 0 ? rb_ * 8u + kHalf * wv : rb_ * 16u + kGRT * wv;
+  };
   auto rt_of = [&](int r) -> uint32_t { return PH == 0 ? rt0 + (r % kHalf) : rt0 + r; };
   Unit u[kGRT];
+  auto load_units = [&]() {
 #pragma unroll
-  for (int r = 0; r < kGRT; ++r)
-    load_unit_buf(u[r], PH == 0 && r >= kHalf ? c1 : c0, PH == 0 && r >= kHalf ? f1 : f0, rt_of(r) * nst, lane);
-  __builtin_amdgcn_sched_barrier(0);
-
-  build_lut<kGKC, kGT, kPer, true>(lut_s, cbv, tid);
-  build_blk_tbl(blk_s, tid);
-  if (tid < kGCols)
-    rowoff[tid] = bcol_used ? (uint32_t)(A.b_off + ((uint64_t)brow * TX + (tid & 15u) % TX) * K) : (uint32_t)A.zero_off;
-  __syncthreads();
+    for (int r = 0; r < kGRT; ++r)
+      load_unit_buf(u[r], PH == 0 && r >= kHalf ? c1 : c0, PH == 0 && r >= kHalf ? f1 : f0, rt_of(r) * nst, lane);
+  };
+  // B row of column tid (threads below kGCols): a column past the tile's tokens reads the tile's
+  // first slot (unconditional load) and gets the zero row
+  const uint32_t bcol_j = (tid >> 4) * TPG + (tid & 15u) / TX;
+  auto brow_load = [&](const Tile& t) -> uint32_t {
+    const uint32_t bslot = t.slot0 + ((tid < kGCols && (tid & 15u) < TX * TPG && bcol_j < t.n) ? bcol_j : 0u);
+    return PH == 0 ? A.slot_tok[bslot] : bslot;
+  };
+  auto rowoff_store = [&](const Tile& t, uint32_t brow) {
+    const bool used = tid < kGCols && (tid & 15u) < TX * TPG && bcol_j < t.n;
+    if (tid < kGCols)
+      rowoff[tid] = used ? (uint32_t)(A.b_off + ((uint64_t)brow * TX + (tid & 15u) % TX) * K) : (uint32_t)A.zero_off;
+  };
   // DMA lane map: instruction i of wave w writes columns 8b..8b+7 (b = kGDma w + i), lane l to
   // LDS slot l & 7 of column 8b + (l >> 3); slot p of column col holds global chunk p ^ f(col),
   // f(col) = (c ^ (c >> 3)) & 7 with c = col & 15 (the column within its 16-column tile), that
   // is (col & 7) ^ ((col >> 3) & 1). A fragment read (lane = column c + 16 k-group) then puts lanes
   // 0-7, 8-15 (and so on) on 8 distinct 16-byte bank groups, and lanes 0-15 on 16.
   uint32_t roff[kGDma];
+  auto roff_load = [&]() {
 #pragma unroll
-  for (int i = 0; i < kGDma; ++i) {
-    const uint32_t col = 8u * (kGDma * wv + i) + (lane >> 3);
-    const uint32_t q = (lane & 7u) ^ ((col & 7u) ^ ((col >> 3) & 1u));
-    roff[i] = rowoff[col] + (q << 4);
-  }
+    for (int i = 0; i < kGDma; ++i) {
+      const uint32_t col = 8u * (kGDma * wv + i) + (lane >> 3);
+      const uint32_t q = (lane & 7u) ^ ((col & 7u) ^ ((col >> 3) & 1u));
+      roff[i] = rowoff[col] + (q << 4);
+    }
+  };
   const __amdgpu_buffer_rsrc_t wsr = buffer_rsrc(A.ws, 0xFFFFFFFFu);
   auto dma = [&](uint8_t* buf, uint32_t step) {
 #pragma unroll
@@ -431,143 +451,34 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(wsr, AFFX_LDS_PTR(buf + (kGDma * wv + i) * 1024u), 16, roff[i],
                                                step * 128u, 0, 0);
   };
-  // ---- set-up (3): the first two steps of B ------------------------------------------------
-  const uint32_t nsteps = nst * 8u;
-  dma(buf0, 0);
-  dma(buf1, 1);
-  __builtin_amdgcn_s_waitcnt(AFFX_VMCNT(0));
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- set-up of the first item (B row loads first: the set-up waits for them, and loads
+  // complete in issue order; then the weights; the codebook copies while they are in flight) ---
+  {
+    const uint32_t brow = brow_load(tl);
+    __builtin_amdgcn_sched_barrier(0);
+    set_item(tl, rb);
+    load_units();
+    __builtin_amdgcn_sched_barrier(0);
+    build_lut<kGKC, kGT, kPer, true>(lut_s, cbv, tid);
+    build_blk_tbl(blk_s, tid);
+    rowoff_store(tl, brow);
+    __syncthreads();
+    roff_load();
+    dma(buf0, 0);
+    dma(buf1, 1);
+    __builtin_amdgcn_s_waitcnt(AFFX_VMCNT(0));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
   const uint32_t copy4 = (lane & (kGKC - 1)) * 4u;
   const uint32_t c = lane & 15, kg = lane >> 4;
   const uint32_t bo0 = c * 128u + (((2u * kg) ^ ((c ^ (c >> 3)) & 7u)) << 4);
   const uint32_t bo1 = c * 128u + (((2u * kg + 1u) ^ ((c ^ (c >> 3)) & 7u)) << 4);
-
-  v8i a_cur[kGRT];
-#pragma unroll
-  for (int r = 0; r < kGRT; ++r) {
-    uint32_t raw[8], sx[4];
-    lut_lookup_step<kGKC, true>(u[r], lut, btbl, copy4, 0, raw, sx);
-    a_cur[r] = lut_finish(raw, sx);
-  }
-  v4f acc[kGRT][kGCT];
-#pragma unroll
-  for (int r = 0; r < kGRT; ++r)
-#pragma unroll
-    for (int ct = 0; ct < kGCT; ++ct) acc[r][ct] = v4f{0.f, 0.f, 0.f, 0.f};
-
-  // ---- main loop: 1024 columns of K per iteration, eight MFMA steps ---------------------------
-  // (each step is instantiated with its index as a constant: the ring loads, the code positions
-  // and the wait counts of a step are all fixed at compile time)
-  auto bufsel = [&](int i) -> uint8_t* { return i == 0 ? buf0 : i == 1 ? buf1 : i == 2 ? buf2 : buf3; };
-  auto step = [&](auto mc, uint32_t s, bool more) {
-    constexpr int m = decltype(mc)::value;
-    const uint8_t* bcur = bufsel(m & 3);
-    // B of steps t + 2 and t + 3, issued at the top of even steps t into the buffers of steps
-    // t - 2 and t - 1 (read before the barrier that ended step t - 1): the workgroup then needs
-    // one barrier per two steps. Past the last step the loads repeat the last step's B into
-    // buffers nobody reads again, so the count of loads in flight is the same on every path.
-    if constexpr ((m & 1) == 0) {
-      const uint32_t t2 = s * 8u + m + 2u, t3 = t2 + 1u;
-      dma(bufsel((m + 2) & 3), t2 < nsteps ? t2 : nsteps - 1u);
-      dma(bufsel((m + 3) & 3), t3 < nsteps ? t3 : nsteps - 1u);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    // ring loads for the next 1024 columns; after the last ones, the same loads of tile 0 (hot
-    // in the cache, read by every workgroup): their registers are not read again, and issuing
-    // them keeps the count of loads in flight the same on every path
-    if constexpr (m != 0) {
-#pragma unroll
-      for (int r = 0; r < kGRT; ++r)
-        ring_load<m>(u[r], PH == 0 && r >= kHalf ? c1 : c0, PH == 0 && r >= kHalf ? f1 : f0,
-                     more ? rt_of(r) * nst + s + 1 : 0u, lane);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    // The step is 12 groups, one per B column tile: the tile's two fragment reads go out two
-    // groups ahead, its MFMAs (one per row tile) are each followed by a share of the VALU work of
-    // the next step (groups 4-5: code addresses and table reads of unit g - 4; groups 8-9: the
-    // sign/scale finish of unit g - 8, whose reads were issued four groups earlier). The VALU of
-    // one wave runs while the matrix core works through the other wave's MFMAs. The groups are
-    // placed so that the table reads and the next A fragments are live for a third of the step
-    // only: with two waves per SIMD a wave has 256 registers, accumulators included. (Step 0 of
-    // the next 1024 columns after step 7: the ring has reloaded every register those reads use.)
-    constexpr int mn = (m + 1) & 7;
-    constexpr int kLook = 4, kFin = 8;
-    uint32_t rawn[kGRT][8], sxn[kGRT][4];
-    v8i a_next[kGRT];
-    auto bread = [&](int ct) -> v8i {
-      const u32x4 lo = *reinterpret_cast<const u32x4*>(bcur + ct * 2048 + bo0);
-      const u32x4 hi = *reinterpret_cast<const u32x4*>(bcur + ct * 2048 + bo1);
-      v8i b;
-      b[0] = (int)lo[0]; b[1] = (int)lo[1]; b[2] = (int)lo[2]; b[3] = (int)lo[3];
-      b[4] = (int)hi[0]; b[5] = (int)hi[1]; b[6] = (int)hi[2]; b[7] = (int)hi[3];
-      return b;
-    };
-    v8i bq0 = bread(0), bq1 = bread(1);
-    static_for<0, kGCT>([&](auto cc) {
-      constexpr int ct = decltype(cc)::value;
-      v8i bq2;
-      if constexpr (ct + 2 < kGCT) bq2 = bread(ct + 2);
-#pragma unroll
-      for (int r = 0; r < kGRT; ++r) acc[r][ct] = mfma(a_cur[r], bq0, acc[r][ct]);
-      if constexpr (ct >= kLook && ct < kLook + kGRT) {
-        pin_step<mn>(u[ct - kLook]);
-        lut_lookup<kGKC, mn, true>(u[ct - kLook], lut, btbl, copy4, rawn[ct - kLook], sxn[ct - kLook]);
-      } else if constexpr (ct >= kFin && ct < kFin + kGRT) {
-        a_next[ct - kFin] = lut_finish(rawn[ct - kFin], sxn[ct - kFin]);
-        AFFX_PIN(a_next[ct - kFin]);  // computed here, not sunk into the next step
-      }
-      // {one MFMA, then VALU} per row tile, then the LDS reads
-#pragma unroll
-      for (int i = 0; i < kGRT; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x100, 10, 0);
-      __builtin_amdgcn_sched_barrier(0);
-      bq0 = bq1;
-      if constexpr (ct + 2 < kGCT) bq1 = bq2;
-    });
-    // the accumulators are materialised here (else the compiler sinks every MFMA below all
-    // eight steps' table reads and holds those in registers). They stay in VGPRs: a kernel that
-    // names no AGPR gets its whole register budget as VGPRs, where one that does is split half
-    // and half, and the other half is then too small for the rest of the step.
-#pragma unroll
-    for (int r = 0; r < kGRT; ++r)
-#pragma unroll
-      for (int ct = 0; ct < kGCT; ++ct) AFFX_PIN(acc[r][ct]);
-#pragma unroll
-    for (int r = 0; r < kGRT; ++r) a_cur[r] = a_next[r];
-    // After an odd step t: the B of steps t + 1 and t + 2 (issued at the top of step t - 1) is in
-    // LDS once every wave's loads up to them have landed. Loads complete in issue order, so at
-    // most the loads issued after them may still be outstanding: the ring loads of steps t - 1
-    // and t (2 units x {0,1,1,1,1,1,1,2} by step).
-    if constexpr ((m & 1) == 1) {
-      constexpr int c[8] = {0, 1, 1, 1, 1, 1, 1, 2};
-      constexpr int k = kGRT * (c[m - 1] + c[m]);
-      __builtin_amdgcn_s_waitcnt(AFFX_VMCNT(k));
-      __builtin_amdgcn_s_barrier();
-    }
-    __builtin_amdgcn_sched_barrier(0);
-  };
-  for (uint32_t s = 0; s < nst; ++s) {
-    const bool more = s + 1 < nst;
-    step(IConst<0>{}, s, more);
-    step(IConst<1>{}, s, more);
-    step(IConst<2>{}, s, more);
-    step(IConst<3>{}, s, more);
-    step(IConst<4>{}, s, more);
-    step(IConst<5>{}, s, more);
-    step(IConst<6>{}, s, more);
-    step(IConst<7>{}, s, more);
-  }
-  __builtin_amdgcn_s_waitcnt(AFFX_VMCNT(0));  // no direct-to-LDS load outlives the loop
-
-  // ---- epilogue ---------------------------------------------------------------------------------
-  // accumulator lane (c, kg), element v = D[4 kg + v][c]: row 4 kg + v of the row tile, column c.
-  // (Every accumulator index is a compile-time constant: a runtime index would put the whole
-  // accumulator array in scratch memory.)
+  // epilogue helpers: accumulator lane (c, kg), element v = D[4 kg + v][c]: row 4 kg + v of the
+  // row tile, column c. (Every accumulator index is a compile-time constant: a runtime index
+  // would put the whole accumulator array in scratch memory.)
   auto terms = [&](float d) -> float {
     const float d1 = __shfl_down(d, 1, 16);
     if constexpr (TX == 2) {
@@ -583,93 +494,254 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
     o[2] = __uint_as_float(v.y << 16);
     o[3] = __uint_as_float(v.y & 0xFFFF0000u);
   };
-  if constexpr (PH == 0) {
-    const float L = A.limit;
-    // Every input of the epilogue is requested before the first one is used: the activation
-    // exponent of the lane's token in each column tile (columns past the tile's tokens read its
-    // last token and store nothing), then the row scales.
-    int sig[kGCT];
+  const float L = A.limit;
+
+  for (;;) {
+    v8i a_cur[kGRT];
 #pragma unroll
-    for (int ct = 0; ct < kGCT; ++ct) {
-      const uint32_t j = ct * TPG + c / TX;
-      sig[ct] = A.slot_sigma[tl.slot0 + (j < tl.n ? j : tl.n - 1u)];
+    for (int r = 0; r < kGRT; ++r) {
+      uint32_t raw[8], sx[4];
+      lut_lookup_step<kGKC, true>(u[r], lut, btbl, copy4, 0, raw, sx);
+      a_cur[r] = lut_finish(raw, sx);
     }
-    uint2 rgw[kHalf], ruw[kHalf];
-#pragma unroll
-    for (int p = 0; p < kHalf; ++p) {
-      const uint32_t row0 = rt_of(p) * 16u + 4u * kg;
-      rgw[p] = *reinterpret_cast<const uint2*>(ex + A.off[kGateRs] + (uint64_t)row0 * 2);
-      ruw[p] = *reinterpret_cast<const uint2*>(ex + A.off[kUpRs] + (uint64_t)row0 * 2);
-    }
-    static_for<0, kHalf>([&](auto pc) {
-      constexpr int p = decltype(pc)::value;
-      const uint32_t row0 = rt_of(p) * 16u + 4u * kg;
-      float rg[4], ru[4];
-      bf16x4(rgw[p], rg);
-      bf16x4(ruw[p], ru);
-      const uint32_t prow = kperm(row0);
-      static_for<0, kGCT>([&](auto cc) {
-        constexpr int ct = decltype(cc)::value;
-        if (ct * TPG >= tl.n) return;  // no token in this column tile (the same for the whole wave)
-        float sg[4], su[4];
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          sg[v] = terms(acc[p][ct][v]);
-          su[v] = terms(acc[p + kHalf][ct][v]);
-        }
-        const uint32_t j = ct * TPG + c / TX;
-        if (c % TX == 0 && c < TX * TPG && j < tl.n) {
-          const uint32_t slot = tl.slot0 + j;
-          float a[4];
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            float gv = ldexpf(sg[v], -sig[ct]) * rg[v];
-            float uv = ldexpf(su[v], -sig[ct]) * ru[v];
-            gv = (L < gv) ? L : gv;  // SwiGLU with the asymmetric clamp: src/engine/ops.cpp:47-60
-            const float lo = (-L < uv) ? uv : -L;
-            uv = (lo < L) ? lo : L;
-            // (hardware exp2 and reciprocal: a few ulp, far inside the path's tolerance, against
-            // some thirty VALU ops per element for expf and an IEEE division; gv -> -inf gives
-            // exp -> inf, reciprocal 0, a signed zero)
-            const float e = __builtin_amdgcn_exp2f(-gv * 1.44269504f);
-            a[v] = ldexpf(gv * __builtin_amdgcn_rcpf(1.0f + e) * uv, A.sigma_a);
-          }
-          uint32_t o0, o1, o2;
-          split3x4(a[0], a[1], a[2], a[3], o0, o1, o2);
-          uint8_t* dst = A.aq + (uint64_t)slot * 3 * A.inter + prow;
-          *reinterpret_cast<uint32_t*>(dst) = o0;
-          *reinterpret_cast<uint32_t*>(dst + A.inter) = o1;
-          *reinterpret_cast<uint32_t*>(dst + 2 * (uint64_t)A.inter) = o2;
-        }
-      });
-    });
-  } else {
-    uint2 rdw[kGRT];  // row scales, all requested before the first is used
+    v4f acc[kGRT][kGCT];
 #pragma unroll
     for (int r = 0; r < kGRT; ++r)
-      rdw[r] = *reinterpret_cast<const uint2*>(ex + A.off[kDownRs] + (uint64_t)(rt_of(r) * 16u + 4u * kg) * 2);
-    static_for<0, kGRT>([&](auto rc) {
-      constexpr int r = decltype(rc)::value;
-      const uint32_t row0 = rt_of(r) * 16u + 4u * kg;
-      float rd[4];
-      bf16x4(rdw[r], rd);
+#pragma unroll
+      for (int ct = 0; ct < kGCT; ++ct) acc[r][ct] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    // ---- main loop: 1024 columns of K per iteration, eight MFMA steps ---------------------------
+    // (each step is instantiated with its index as a constant: the ring loads, the code positions
+    // and the wait counts of a step are all fixed at compile time)
+    auto step = [&](auto mc, uint32_t s, bool more) {
+      constexpr int m = decltype(mc)::value;
+      const uint8_t* bcur = bufsel(m & 3);
+      // B of steps t + 2 and t + 3, issued at the top of even steps t into the buffers of steps
+      // t - 2 and t - 1 (read before the barrier that ended step t - 1): the workgroup then needs
+      // one barrier per two steps. Past the last step the loads repeat the last step's B into
+      // buffers nobody reads again, so the count of loads in flight is the same on every path.
+      if constexpr ((m & 1) == 0) {
+        const uint32_t t2 = s * 8u + m + 2u, t3 = t2 + 1u;
+        dma(bufsel((m + 2) & 3), t2 < nsteps ? t2 : nsteps - 1u);
+        dma(bufsel((m + 3) & 3), t3 < nsteps ? t3 : nsteps - 1u);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // ring loads for the next 1024 columns; after the last ones, the same loads of tile 0 (hot
+      // in the cache, read by every workgroup): their registers are not read again, and issuing
+      // them keeps the count of loads in flight the same on every path
+      if constexpr (m != 0) {
+#pragma unroll
+        for (int r = 0; r < kGRT; ++r)
+          ring_load<m>(u[r], PH == 0 && r >= kHalf ? c1 : c0, PH == 0 && r >= kHalf ? f1 : f0,
+                       more ? rt_of(r) * nst + s + 1 : 0u, lane);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // The step is 12 groups, one per B column tile: the tile's two fragment reads go out two
+      // groups ahead, its MFMAs (one per row tile) are each followed by a share of the VALU work of
+      // the next step (groups 4-5: code addresses and table reads of unit g - 4; groups 8-9: the
+      // sign/scale finish of unit g - 8, whose reads were issued four groups earlier). The VALU of
+      // one wave runs while the matrix core works through the other wave's MFMAs. The groups are
+      // placed so that the table reads and the next A fragments are live for a third of the step
+      // only: with two waves per SIMD a wave has 256 registers, accumulators included. (Step 0 of
+      // the next 1024 columns after step 7: the ring has reloaded every register those reads use.)
+      constexpr int mn = (m + 1) & 7;
+      constexpr int kLook = 4, kFin = 8;
+      uint32_t rawn[kGRT][8], sxn[kGRT][4];
+      v8i a_next[kGRT];
+      auto bread = [&](int ct) -> v8i {
+        const u32x4 lo = *reinterpret_cast<const u32x4*>(bcur + ct * 2048 + bo0);
+        const u32x4 hi = *reinterpret_cast<const u32x4*>(bcur + ct * 2048 + bo1);
+        v8i b;
+        b[0] = (int)lo[0]; b[1] = (int)lo[1]; b[2] = (int)lo[2]; b[3] = (int)lo[3];
+        b[4] = (int)hi[0]; b[5] = (int)hi[1]; b[6] = (int)hi[2]; b[7] = (int)hi[3];
+        return b;
+      };
+      v8i bq0 = bread(0), bq1 = bread(1);
       static_for<0, kGCT>([&](auto cc) {
         constexpr int ct = decltype(cc)::value;
-        if (ct * TPG >= tl.n) return;  // no token in this column tile (the same for the whole wave)
-        float sd[4];
+        v8i bq2;
+        if constexpr (ct + 2 < kGCT) bq2 = bread(ct + 2);
 #pragma unroll
-        for (int v = 0; v < 4; ++v) sd[v] = terms(acc[r][ct][v]);
-        const uint32_t j = ct * TPG + c / TX;
-        if (c % TX == 0 && c < TX * TPG && j < tl.n) {
-          float4 o;
-          o.x = ldexpf(sd[0], -A.sigma_a) * rd[0];
-          o.y = ldexpf(sd[1], -A.sigma_a) * rd[1];
-          o.z = ldexpf(sd[2], -A.sigma_a) * rd[2];
-          o.w = ldexpf(sd[3], -A.sigma_a) * rd[3];
-          *reinterpret_cast<float4*>(A.z + (uint64_t)(tl.slot0 + j) * A.hidden + row0) = o;
+        for (int r = 0; r < kGRT; ++r) acc[r][ct] = mfma(a_cur[r], bq0, acc[r][ct]);
+        if constexpr (ct >= kLook && ct < kLook + kGRT) {
+          pin_step<mn>(u[ct - kLook]);
+          lut_lookup<kGKC, mn, true>(u[ct - kLook], lut, btbl, copy4, rawn[ct - kLook], sxn[ct - kLook]);
+        } else if constexpr (ct >= kFin && ct < kFin + kGRT) {
+          a_next[ct - kFin] = lut_finish(rawn[ct - kFin], sxn[ct - kFin]);
+          AFFX_PIN(a_next[ct - kFin]);  // computed here, not sunk into the next step
         }
+        // {one MFMA, then VALU} per row tile, then the LDS reads
+#pragma unroll
+        for (int i = 0; i < kGRT; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, 10, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        bq0 = bq1;
+        if constexpr (ct + 2 < kGCT) bq1 = bq2;
       });
-    });
+      // the accumulators are materialised here (else the compiler sinks every MFMA below all
+      // eight steps' table reads and holds those in registers). They stay in VGPRs: a kernel that
+      // names no AGPR gets its whole register budget as VGPRs, where one that does is split half
+      // and half, and the other half is then too small for the rest of the step.
+#pragma unroll
+      for (int r = 0; r < kGRT; ++r)
+#pragma unroll
+        for (int ct = 0; ct < kGCT; ++ct) AFFX_PIN(acc[r][ct]);
+#pragma unroll
+      for (int r = 0; r < kGRT; ++r) a_cur[r] = a_next[r];
+      // After an odd step t: the B of steps t + 1 and t + 2 (issued at the top of step t - 1) is in
+      // LDS once every wave's loads up to them have landed. Loads complete in issue order, so at
+      // most the loads issued after them may still be outstanding: the ring loads of steps t - 1
+      // and t (2 units x {0,1,1,1,1,1,1,2} by step).
+      if constexpr ((m & 1) == 1) {
+        constexpr int c[8] = {0, 1, 1, 1, 1, 1, 1, 2};
+        constexpr int k = kGRT * (c[m - 1] + c[m]);
+        __builtin_amdgcn_s_waitcnt(AFFX_VMCNT(k));
+        __builtin_amdgcn_s_barrier();
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    for (uint32_t s = 0; s < nst; ++s) {
+      const bool more = s + 1 < nst;
+      step(IConst<0>{}, s, more);
+      step(IConst<1>{}, s, more);
+      step(IConst<2>{}, s, more);
+      step(IConst<3>{}, s, more);
+      step(IConst<4>{}, s, more);
+      step(IConst<5>{}, s, more);
+      step(IConst<6>{}, s, more);
+      step(IConst<7>{}, s, more);
+    }
+    // no direct-to-LDS load outlives the steps, and every wave is past its last B read
+    __builtin_amdgcn_s_waitcnt(AFFX_VMCNT(0));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- next item: tile (scalar loads), then, with this item's epilogue inputs, its B rows and
+    // first weights -------------------------------------------------------------------------------
+    uint32_t rb2, tile2;
+    item_of(w + gridDim.x, rb2, tile2);
+    const Tile tl2 = A.tiles[tile2 < A.max_tiles ? tile2 : 0u];
+    const bool next = tile2 < n_tiles && tl2.n != 0;
+
+    // ---- epilogue inputs: every one requested before the first is used ----------------------
+    // (gate/up: the activation exponent of the lane's token in each column tile, columns past the
+    // tile's tokens read its last token and store nothing; the row scales. Down: row scales.)
+    int sig[PH == 0 ? kGCT : 1];
+    uint2 rgw[kHalf], ruw[kHalf], rdw[kGRT];
+    if constexpr (PH == 0) {
+#pragma unroll
+      for (int ct = 0; ct < kGCT; ++ct) {
+        const uint32_t j = ct * TPG + c / TX;
+        sig[ct] = A.slot_sigma[tl.slot0 + (j < tl.n ? j : tl.n - 1u)];
+      }
+#pragma unroll
+      for (int p = 0; p < kHalf; ++p) {
+        const uint32_t row0 = rt_of(p) * 16u + 4u * kg;
+        rgw[p] = *reinterpret_cast<const uint2*>(ex + A.off[kGateRs] + (uint64_t)row0 * 2);
+        ruw[p] = *reinterpret_cast<const uint2*>(ex + A.off[kUpRs] + (uint64_t)row0 * 2);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < kGRT; ++r)
+        rdw[r] = *reinterpret_cast<const uint2*>(ex + A.off[kDownRs] + (uint64_t)(rt_of(r) * 16u + 4u * kg) * 2);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // this item's row tiles and planes, kept for its epilogue (the next item's replace them)
+    const uint32_t rt0_cur = rt0;
+    const Tile tl_cur = tl;
+    uint32_t brow2 = 0;
+    if (next) brow2 = brow_load(tl2);
+    __builtin_amdgcn_sched_barrier(0);
+    auto rt_cur = [&](int r) -> uint32_t { return PH == 0 ? rt0_cur + (r % kHalf) : rt0_cur + r; };
+
+    // ---- epilogue arithmetic and stores ------------------------------------------------------
+    if constexpr (PH == 0) {
+      static_for<0, kHalf>([&](auto pc) {
+        constexpr int p = decltype(pc)::value;
+        const uint32_t row0 = rt_cur(p) * 16u + 4u * kg;
+        float rg[4], ru[4];
+        bf16x4(rgw[p], rg);
+        bf16x4(ruw[p], ru);
+        const uint32_t prow = kperm(row0);
+        static_for<0, kGCT>([&](auto cc) {
+          constexpr int ct = decltype(cc)::value;
+          if (ct * TPG >= tl_cur.n) return;  // no token in this column tile (the same for the whole wave)
+          float sg[4], su[4];
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            sg[v] = terms(acc[p][ct][v]);
+            su[v] = terms(acc[p + kHalf][ct][v]);
+          }
+          const uint32_t j = ct * TPG + c / TX;
+          if (c % TX == 0 && c < TX * TPG && j < tl_cur.n) {
+            const uint32_t slot = tl_cur.slot0 + j;
+            float a[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              float gv = ldexpf(sg[v], -sig[ct]) * rg[v];
+              float uv = ldexpf(su[v], -sig[ct]) * ru[v];
+              gv = (L < gv) ? L : gv;  // SwiGLU with the asymmetric clamp: src/engine/ops.cpp:47-60
+              const float lo = (-L < uv) ? uv : -L;
+              uv = (lo < L) ? lo : L;
+              // (hardware exp2 and reciprocal: a few ulp, far inside the path's tolerance, against
+              // some thirty VALU ops per element for expf and an IEEE division; gv -> -inf gives
+              // exp -> inf, reciprocal 0, a signed zero)
+              const float e = __builtin_amdgcn_exp2f(-gv * 1.44269504f);
+              a[v] = ldexpf(gv * __builtin_amdgcn_rcpf(1.0f + e) * uv, A.sigma_a);
+            }
+            uint32_t o0, o1, o2;
+            split3x4(a[0], a[1], a[2], a[3], o0, o1, o2);
+            uint8_t* dst = A.aq + (uint64_t)slot * 3 * A.inter + prow;
+            *reinterpret_cast<uint32_t*>(dst) = o0;
+            *reinterpret_cast<uint32_t*>(dst + A.inter) = o1;
+            *reinterpret_cast<uint32_t*>(dst + 2 * (uint64_t)A.inter) = o2;
+          }
+        });
+      });
+    } else {
+      static_for<0, kGRT>([&](auto rc) {
+        constexpr int r = decltype(rc)::value;
+        const uint32_t row0 = rt_cur(r) * 16u + 4u * kg;
+        float rd[4];
+        bf16x4(rdw[r], rd);
+        static_for<0, kGCT>([&](auto cc) {
+          constexpr int ct = decltype(cc)::value;
+          if (ct * TPG >= tl_cur.n) return;  // no token in this column tile (the same for the whole wave)
+          float sd[4];
+#pragma unroll
+          for (int v = 0; v < 4; ++v) sd[v] = terms(acc[r][ct][v]);
+          const uint32_t j = ct * TPG + c / TX;
+          if (c % TX == 0 && c < TX * TPG && j < tl_cur.n) {
+            float4 o;
+            o.x = ldexpf(sd[0], -A.sigma_a) * rd[0];
+            o.y = ldexpf(sd[1], -A.sigma_a) * rd[1];
+            o.z = ldexpf(sd[2], -A.sigma_a) * rd[2];
+            o.w = ldexpf(sd[3], -A.sigma_a) * rd[3];
+            *reinterpret_cast<float4*>(A.z + (uint64_t)(tl_cur.slot0 + j) * A.hidden + row0) = o;
+          }
+        });
+      });
+    }
+    if (!next) break;
+
+    // ---- next item's weights and first two steps of B (its B rows have arrived during the
+    // epilogue) ----------------------------------------------------------------------------------
+    set_item(tl2, rb2);
+    load_units();
+    rowoff_store(tl2, brow2);
+    __syncthreads();
+    roff_load();
+    dma(buf0, 0);
+    dma(buf1, 1);
+    w += gridDim.x;
+    rb = rb2;
+    tl = tl2;
+    __builtin_amdgcn_s_waitcnt(AFFX_VMCNT(0));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
@@ -809,10 +881,17 @@ int affx_expert_ffn_grouped(const affx_layer* L, const void* x, const void* x_lo
                      (int32_t*)(b + lay.sigma), b + lay.xq,
                      (uint32_t*)(b + lay.zeros), zmax / 4);
   if ((rc = check_launch("grouped_prep_x_kernel"))) return rc;
-  // gate/up: 128 gate + 128 up rows per workgroup; down: 256 rows. One workgroup per (row
-  // block, tile), the tile count rounded up to a multiple of the 8 XCDs (see the kernel's order)
-  const uint32_t g1 = (L->inter / 128) * ((lay.max_tiles1 + 7) / 8 * 8);
-  const uint32_t g2 = (L->hidden / 256) * ((lay.max_tiles2 + 7) / 8 * 8);
+  // gate/up: 128 gate + 128 up rows per item; down: 256 rows. Items (row block, tile), the tile
+  // count rounded up to a multiple of the 8 XCDs (see the kernel's order), run by a persistent
+  // grid of one workgroup per CU (a multiple of 8), or fewer when there are fewer items
+  int dev = 0, cus = 0;
+  if ((rc = check_hip(hipGetDevice(&dev), "hipGetDevice"))) return rc;
+  if ((rc = check_hip(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "hipDeviceGetAttribute")))
+    return rc;
+  const uint32_t gmax = cus >= 8 ? (uint32_t)cus / 8u * 8u : 8u;
+  const uint32_t i1 = (L->inter / 128) * ((lay.max_tiles1 + 7) / 8 * 8);
+  const uint32_t i2 = (L->hidden / 256) * ((lay.max_tiles2 + 7) / 8 * 8);
+  const uint32_t g1 = i1 < gmax ? i1 : gmax, g2 = i2 < gmax ? i2 : gmax;
   A.tiles = (const Tile*)(b + lay.tiles1);
   A.max_tiles = lay.max_tiles1;
   A.b_off = lay.xq;
