@@ -88,6 +88,26 @@ def test_grouped_is_deterministic(ax, layer):
     np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
+def test_grouped_batch_invariant(ax, layer):
+    """A token's output does not depend on the batch around it: every sum has a fixed order and
+    every MFMA column is computed on its own. 3000 tokens (gate/up: 8 row blocks x ~300 tiles =
+    thousands of items, so each persistent workgroup runs many of them) against slices of the
+    same batch run alone, bit for bit. The slices cover tiles at the start, the middle (an
+    expert's tiles split across the slice boundary) and the end."""
+    ex, pool, hidden, inter = layer
+    rng = np.random.default_rng(5)
+    T, k = 3000, 6
+    xb = torch.from_numpy(bf16_bits(rng.standard_normal((T, hidden)).astype(np.float32)).view(np.int16)).cuda()
+    sel, w = _routes(rng, T, k, ex.shape[0], True)
+    sel[7, 2] = 999  # padding
+    gs, gw = torch.from_numpy(sel.astype(np.int32)).cuda(), torch.from_numpy(w).cuda()
+    full = ax.expert_ffn_grouped(pool, xb.view(torch.bfloat16), gs, gw).cpu().numpy()
+    for a, b in ((0, 37), (1400, 1601), (2950, 3000)):
+        part = ax.expert_ffn_grouped(pool, xb[a:b].contiguous().view(torch.bfloat16), gs[a:b].contiguous(),
+                                     gw[a:b].contiguous()).cpu().numpy()
+        np.testing.assert_array_equal(part.view(np.uint32), full[a:b].view(np.uint32), err_msg=f"tokens {a}:{b}")
+
+
 def test_engine_hook_dim_major_arenas(ax, orc, c1_codebook, layer):
     """affx_expert_ffn_batch with host routes, d_x/d_block f32 [hidden][nb_stride] (accumulated),
     marks every non-padding pair handled and returns their count. One context serves a decode
