@@ -109,6 +109,19 @@ def test_bad_arguments_are_refused(L):
     assert b"bad arguments" in L.affx_last_error()
 
 
+def test_grouped_refuses_misaligned_activations(L):
+    """The grouped prefill reads x with 16-byte loads: a misaligned x or x_lo is an argument error,
+    refused before any device work (so this runs without a GPU)."""
+    from affinity_amd._lib import AffxLayer
+    buf = np.zeros(64, np.uint8)
+    p = buf.ctypes.data
+    lay = AffxLayer(p, 9060352, 256, 4096, 2048, p, 10.0)
+    for x, xlo in ((p + 2, None), (p, p + 8)):
+        rc = L.affx_expert_ffn_grouped(C.byref(lay), x, xlo, 4, p, p, 6, p, 0, p, 1 << 30, None)
+        assert rc == -1, rc  # AFFX_ERR_ARG
+        assert b"16-byte aligned" in L.affx_last_error()
+
+
 def test_decode_workspace_grows_with_batch(L):
     a = L.affx_decode_workspace_size(1, 6, 4096, 2048)
     b = L.affx_decode_workspace_size(8, 6, 4096, 2048)
