@@ -676,7 +676,39 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
             su[v] = terms(acc[p + kHalf][ct][v]);
           }
           const uint32_t j = ct * TPG + c / TX;
-          if (c % TX == 0 && c < TX * TPG && j < tl_cur.n) {
+          if constexpr (TX == 2) {
+            // the lane pair (2i, 2i + 1) shares token i's four rows: the even lane (whose
+            // combined terms these are) keeps rows 0-1 and hands rows 2-3 to the odd lane, so
+            // every lane runs the SwiGLU and the term split on two values
+            const bool odd = (c & 1u) != 0;
+            float g2[2], u2[2];
+#pragma unroll
+            for (int v = 0; v < 2; ++v) {
+              const float gu = __shfl_up(sg[v + 2], 1, 16), uu = __shfl_up(su[v + 2], 1, 16);
+              g2[v] = odd ? gu : sg[v];
+              u2[v] = odd ? uu : su[v];
+            }
+            if (j < tl_cur.n) {
+              const uint32_t slot = tl_cur.slot0 + j;
+              float a2[2];
+#pragma unroll
+              for (int v = 0; v < 2; ++v) {
+                float gv = ldexpf(g2[v], -sig[ct]) * (odd ? rg[v + 2] : rg[v]);
+                float uv = ldexpf(u2[v], -sig[ct]) * (odd ? ru[v + 2] : ru[v]);
+                gv = (L < gv) ? L : gv;  // SwiGLU with the asymmetric clamp: src/engine/ops.cpp:47-60
+                const float lo = (-L < uv) ? uv : -L;
+                uv = (lo < L) ? lo : L;
+                const float e = __builtin_amdgcn_exp2f(-gv * 1.44269504f);
+                a2[v] = ldexpf(gv * __builtin_amdgcn_rcpf(1.0f + e) * uv, A.sigma_a);
+              }
+              uint32_t o0, o1, o2;
+              split3x2(a2[0], a2[1], o0, o1, o2);
+              uint8_t* dst = A.aq + (uint64_t)slot * 3 * A.inter + prow + (odd ? 2u : 0u);
+              *reinterpret_cast<uint16_t*>(dst) = (uint16_t)o0;
+              *reinterpret_cast<uint16_t*>(dst + A.inter) = (uint16_t)o1;
+              *reinterpret_cast<uint16_t*>(dst + 2 * (uint64_t)A.inter) = (uint16_t)o2;
+            }
+          } else if (c % TX == 0 && c < TX * TPG && j < tl_cur.n) {
             const uint32_t slot = tl_cur.slot0 + j;
             float a[4];
 #pragma unroll

@@ -208,6 +208,20 @@ __device__ __forceinline__ void split3x4(float v0, float v1, float v2, float v3,
   q2 = t;
 }
 
+// The same for two values: returns the two bytes of each term in bits 0-15.
+__device__ __forceinline__ void split3x2(float v0, float v1, uint32_t& q0, uint32_t& q1, uint32_t& q2) {
+  typedef float v2f __attribute__((ext_vector_type(2)));
+  uint32_t t = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v0, v1, 0, false);
+  q0 = t & 0xFFFFu;
+  v2f a = __builtin_amdgcn_cvt_pk_f32_fp8((int)t, false);
+  v0 = (v0 - a.x) * 16.0f; v1 = (v1 - a.y) * 16.0f;
+  t = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v0, v1, 0, false);
+  q1 = t & 0xFFFFu;
+  a = __builtin_amdgcn_cvt_pk_f32_fp8((int)t, false);
+  v0 = (v0 - a.x) * 16.0f; v1 = (v1 - a.y) * 16.0f;
+  q2 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v0, v1, 0, false) & 0xFFFFu;
+}
+
 // Calls f(IConst<I>{}) for I = B .. E-1: a loop whose index is a compile-time constant in the body.
 template <int N>
 struct IConst {
