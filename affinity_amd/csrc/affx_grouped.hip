@@ -480,11 +480,11 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
   // row tile, column c. (Every accumulator index is a compile-time constant: a runtime index
   // would put the whole accumulator array in scratch memory.)
   auto terms = [&](float d) -> float {
-    const float d1 = __shfl_down(d, 1, 16);
+    const float d1 = row_shl<1>(d);
     if constexpr (TX == 2) {
       return d + d1 * 0.0625f;
     } else {
-      const float d2 = __shfl_down(d, 2, 16);
+      const float d2 = row_shl<2>(d);
       return d + d1 * 0.0625f + d2 * 0.00390625f;
     }
   };
@@ -684,7 +684,7 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
             float g2[2], u2[2];
 #pragma unroll
             for (int v = 0; v < 2; ++v) {
-              const float gu = __shfl_up(sg[v + 2], 1, 16), uu = __shfl_up(su[v + 2], 1, 16);
+              const float gu = row_shr<1>(sg[v + 2]), uu = row_shr<1>(su[v + 2]);
               g2[v] = odd ? gu : sg[v];
               u2[v] = odd ? uu : su[v];
             }

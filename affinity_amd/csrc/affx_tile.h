@@ -41,6 +41,17 @@ __device__ __forceinline__ void load_unit(Unit& u, const uint8_t* codes, const u
 #ifndef AFFX_PIN
 #define AFFX_PIN(x) asm volatile("" : "+v"(x))
 #endif
+// Cross-lane moves within a row of 16 lanes, as one DPP op (not an LDS permute): lane l gets the
+// value of lane l + N (row_shl) or l - N (row_shr) of its row; a lane whose source is outside
+// the row keeps its own value.
+template <int N>
+__device__ __forceinline__ float row_shl(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x100 + N, 0xF, 0xF, false));
+}
+template <int N>
+__device__ __forceinline__ float row_shr(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x110 + N, 0xF, 0xF, false));
+}
 // LDS pointer operand of a direct global->LDS load.
 #ifndef AFFX_LDS_PTR
 #define AFFX_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))

@@ -138,6 +138,15 @@ template <typename T> inline T __shfl_up(T v, int d, int width = 64) {
   uint32_t l = emu_lane(); uint32_t src = (l % width) >= (uint32_t)d ? l - d : l;
   return emu_exchange(v, src);
 }
+// DPP row shifts (dpp_ctrl 0x101-0x10F row_shl, 0x111-0x11F row_shr; rows of 16 lanes)
+inline int __builtin_amdgcn_update_dpp(int old, int src, int ctrl, int, int, bool bound_ctrl) {
+  const uint32_t l = emu_lane(), rl = l & 15;
+  int from = -1;
+  if (ctrl >= 0x101 && ctrl <= 0x10F && rl + (ctrl - 0x100) < 16) from = (int)l + (ctrl - 0x100);
+  if (ctrl >= 0x111 && ctrl <= 0x11F && (int)rl - (ctrl - 0x110) >= 0) from = (int)l - (ctrl - 0x110);
+  const int v = emu_exchange(src, from < 0 ? l : (uint32_t)from);
+  return from < 0 ? (bound_ctrl ? 0 : old) : v;
+}
 inline uint64_t __ballot(int pred) {
   emu_blk->xfer[emu_wave()][emu_lane()][0] = pred ? 1 : 0;
   emu_wave_sync();
