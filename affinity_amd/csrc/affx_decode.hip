@@ -151,7 +151,7 @@ __global__ void __launch_bounds__(256) decode_prep_kernel(const float* __restric
 // y = x - low terms: the value of three E4M3 terms t0 + t1/16 + t2/256 from a lane's column c
 // and its two right neighbours (same 16-lane row group).
 __device__ __forceinline__ float combine_terms(float d) {
-  const float d1 = __shfl_down(d, 1, 16), d2 = __shfl_down(d, 2, 16);
+  const float d1 = row_shl<1>(d), d2 = row_shl<2>(d);  // (DPP row shifts)
   return d + d1 * 0.0625f + d2 * 0.00390625f;
 }
 

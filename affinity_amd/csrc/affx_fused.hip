@@ -111,7 +111,7 @@ __device__ __forceinline__ void load_pair(Unit& g, Unit& u, const uint8_t* gc, c
 
 // value of the three E4M3 term columns c, c+1, c+2 (valid in lanes whose column is a multiple of 3)
 __device__ __forceinline__ float fused_terms(float d) {
-  const float d1 = __shfl_down(d, 1, 16), d2 = __shfl_down(d, 2, 16);
+  const float d1 = row_shl<1>(d), d2 = row_shl<2>(d);  // (DPP row shifts)
   return d + d1 * 0.0625f + d2 * 0.00390625f;
 }
 
