@@ -570,8 +570,8 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
           a_next[ct - kFin] = lut_finish(rawn[ct - kFin], sxn[ct - kFin]);
           AFFX_PIN(a_next[ct - kFin]);  // computed here, not sunk into the next step
         }
-        // {one MFMA, then up to 12 VALU} per row tile, then the LDS reads (12 measured faster
-        // than 8, 16, 24 or no pattern at all)
+        // {one MFMA, then up to 12 VALU} per row tile, then the LDS reads (8, 12, 16, 24 and no
+        // pattern measured within about 1 % of each other)
 #pragma unroll
         for (int i = 0; i < kGRT; ++i) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
