@@ -67,6 +67,9 @@ struct DecodePlan {
 #ifndef AFFX_TRACE
 #define AFFX_TRACE(k) ((void)0)
 #endif
+#ifndef AFFX_TRACEW
+#define AFFX_TRACEW(k) ((void)0)
+#endif
 #ifndef AFFX_TRACE_INIT
 #define AFFX_TRACE_INIT ((void)0)
 #endif

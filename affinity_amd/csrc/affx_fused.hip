@@ -335,8 +335,11 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
       }
     }
   }
+  AFFX_TRACE(15);
+  AFFX_TRACEW(0);
   build_lut<KC, kFT, 3, ROT>(lut_s, cbv, tid);
   if (tid < 64) reinterpret_cast<uint32_t*>(zero_l)[tid] = 0u;
+  AFFX_TRACEW(1);
   __syncthreads();  // plan, activation terms and codebook copies visible
   AFFX_TRACE(1);
 
