@@ -33,6 +33,17 @@ constexpr int kXqChunk = 272;                // LDS bytes of one 256-column chun
 constexpr int kXqRow = 16 * kXqChunk + 64;   // LDS bytes of one (token, term) row, hidden <= 4096
 constexpr uint32_t kSpinLimit = 1u << 22;    // polls (~2^22 x 128 cycles ~ 0.2 s) before giving up
 constexpr int kPlanRoutes = AFFX_MAX_DECODE_TOKENS * AFFX_MAX_TOPK;  // 128
+// How the kernel reads x (element (t, h) at x[t * xts + h * xds]):
+//  kXStrided     any strides, four loads per four elements;
+//  kXTokenMajor  xds = 1, 16-byte aligned rows: 16-byte loads;
+//  kXDimMajor    xts = 1 (the engine's dim-major batch arena, rows of xds >= M floats), xds a
+//                multiple of 4 and x 16-byte aligned: read one token at a time, a pair's
+//                elements would sit xds * 4 bytes apart and every load instruction would touch
+//                64 cache lines, so the kernel reads whole 16-byte row pieces of 4 tokens.
+// A kernel per form: with the forms as branches of one kernel, the compiler shared the load
+// instructions between them (the token-major form lost its 16-byte loads) or, kept apart, waited
+// for every load in flight where the branches joined.
+enum XForm { kXStrided = 0, kXTokenMajor = 1, kXDimMajor = 2 };
 
 struct FusedArgs {
   const uint8_t* base;
@@ -127,9 +138,9 @@ __device__ __forceinline__ float wave_max(float v) {
 // The down weights of the first unit are prefetched before the wait when CG = 1. SINGLE: at most
 // one gate/up item and one down unit (per output tile) per wave, which keeps those two phases
 // loop-free (batch 1). ROT: the codebook copies include the rotated tables (one VALU op less
-// per code, twice the LDS).
+// per code, twice the LDS). XF: how x is read (an XForm; the host picks it from the strides).
 // ------------------------------------------------------------------------------------------------
-template <int CG, int KC, int MAXM, bool SINGLE, bool ROT>
+template <int CG, int KC, int MAXM, bool SINGLE, bool ROT, int XF>
 __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   AFFX_DYN_LDS(lds);
   // the first down unit is loaded while gate/up runs (one column group leaves the registers)
@@ -179,21 +190,45 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
     cbv[i] = A.codebook[ce < 2048u ? ce : 0u];
   }
   constexpr int NP = (MAXM * 4 + kFW - 1) / kFW;
-  float4 xr[NP][4];
+  // kXDimMajor: each wave takes a unit of four tokens of one 1024-column segment instead of a
+  // (token, segment) pair; each lane reads the 16-byte row pieces (tokens 4 g4 .. 4 g4 + 3) of its
+  // four consecutive rows per 256-column chunk, which leaves it the same four consecutive
+  // columns of each token that a pair gives it.
+  constexpr int NX = XF == kXDimMajor ? 16 : NP * 4;
+  float4 xr[NX];  // pairs: xr[4 j + i]; units: xr[4 i + r]
+  const uint32_t xquads = (M + 3) / 4;
   {
-    const bool xvec = A.xds == 1 && (A.xts & 3u) == 0 && (reinterpret_cast<uintptr_t>(A.x) & 15u) == 0;
+    // element offsets in 32 bits (the host sends larger arenas to the staged launches)
+    const uint32_t xts = (uint32_t)A.xts, xds = (uint32_t)A.xds;
+    if constexpr (XF == kXTokenMajor) {
 #pragma unroll
-    for (int j = 0; j < NP; ++j) {
-      const uint32_t p0 = wv + (uint32_t)j * kFW, p = p0 < M * nst ? p0 : 0u;
-      const uint32_t t = p / nst, Sx = p % nst;
+      for (int j = 0; j < NP; ++j) {
+        const uint32_t p0 = wv + (uint32_t)j * kFW, p = p0 < M * nst ? p0 : 0u;
+        const uint32_t t = p / nst, Sx = p % nst;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t h = Sx * kTileCols + 4 * (lane + 64 * i);
-        if (xvec) {
-          xr[j][i] = *reinterpret_cast<const float4*>(A.x + t * A.xts + h);
-        } else {
-          const float* px = A.x + t * A.xts + h * A.xds;
-          xr[j][i] = make_float4(px[0], px[A.xds], px[2 * A.xds], px[3 * A.xds]);
+        for (int i = 0; i < 4; ++i)
+          xr[4 * j + i] = *reinterpret_cast<const float4*>(A.x + (t * xts + Sx * kTileCols + 4 * (lane + 64 * i)));
+      }
+    } else if constexpr (XF == kXDimMajor) {
+      if (wv < xquads * nst) {
+        const uint32_t g4 = wv / nst, Sx = wv % nst;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const uint32_t h = Sx * kTileCols + 256u * i + 4u * lane + r;
+            xr[4 * i + r] = *reinterpret_cast<const float4*>(A.x + (h * xds + 4u * g4));
+          }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NP; ++j) {
+        const uint32_t p0 = wv + (uint32_t)j * kFW, p = p0 < M * nst ? p0 : 0u;
+        const uint32_t t = p / nst, Sx = p % nst;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t o = t * xts + (Sx * kTileCols + 4 * (lane + 64 * i)) * xds;
+          xr[4 * j + i] = make_float4(A.x[o], A.x[o + xds], A.x[o + 2 * xds], A.x[o + 3 * xds]);
         }
       }
     }
@@ -207,7 +242,10 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const uint32_t r = lane + 64u * h;
-    e[h] = (r < R && e[h] < A.n_experts) ? e[h] : ~0u;
+    // (absent routes OR in all ones: a select on r < R lets the compiler move the route load
+    // into a branch that then waits for every load in flight)
+    const uint32_t v = e[h] | (r < R ? 0u : ~0u);
+    e[h] = v < A.n_experts ? v : ~0u;
   }
   uint32_t se[2] = {~0u, ~0u};
   uint32_t rslot[2] = {~0u, ~0u};  // slot of route lane + 64 h
@@ -310,29 +348,48 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
 
   // ---- 3. activation terms and codebook copies into LDS, from the registers loaded up front:
   // a pair's maximum (wave reduction) fixes its exponent, then three E4M3 terms per element
+  auto stage_pair = [&](uint32_t t, uint32_t Sx, float4 v0, float4 v1, float4 v2, float4 v3) {
+    const float4 v[4] = {v0, v1, v2, v3};
+    float mx = 0.f;
 #pragma unroll
-  for (int j = 0; j < NP; ++j) {
-    const uint32_t p = wv + (uint32_t)j * kFW;
-    if (p < M * nst) {
-      const uint32_t t = p / nst, Sx = p % nst;
-      float mx = 0.f;
+    for (int i = 0; i < 4; ++i)
+      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+    mx = wave_max(mx);
+    // amax * 2^sigma in [128, 256): below E4M3's 448
+    const int sigma = mx > 0.f ? 7 - ilogbf(mx) : 0;
+    if (lane == 0) sigma_l[t * 4 + Sx] = sigma;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(xr[j][i].x), fabsf(xr[j][i].y)), fmaxf(fabsf(xr[j][i].z), fabsf(xr[j][i].w))));
-      mx = wave_max(mx);
-      // amax * 2^sigma in [128, 256): below E4M3's 448
-      const int sigma = mx > 0.f ? 7 - ilogbf(mx) : 0;
-      if (lane == 0) sigma_l[t * 4 + Sx] = sigma;
+    for (int i = 0; i < 4; ++i) {
+      uint32_t q0, q1, q2;
+      split3x4(ldexpf(v[i].x, sigma), ldexpf(v[i].y, sigma), ldexpf(v[i].z, sigma), ldexpf(v[i].w, sigma), q0, q1, q2);
+      const uint32_t col = (Sx * 4 + i) * kXqChunk + 4 * lane;
+      *reinterpret_cast<uint32_t*>(xq + (t * 3 + 0) * kXqRow + col) = q0;
+      *reinterpret_cast<uint32_t*>(xq + (t * 3 + 1) * kXqRow + col) = q1;
+      *reinterpret_cast<uint32_t*>(xq + (t * 3 + 2) * kXqRow + col) = q2;
+    }
+  };
+  if constexpr (XF == kXDimMajor) {
+    if (wv < xquads * nst) {
+      // unit: token 4 g4 + c is component c of the row pieces; its columns 4 lane .. 4 lane + 3
+      // of chunk i are rows r = 0..3 of xr[4 i + r]
+      const uint32_t g4 = wv / nst, Sx = wv % nst;
+      auto comp = [](float4 a, int c) { return c == 0 ? a.x : c == 1 ? a.y : c == 2 ? a.z : a.w; };
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        uint32_t q0, q1, q2;
-        split3x4(ldexpf(xr[j][i].x, sigma), ldexpf(xr[j][i].y, sigma), ldexpf(xr[j][i].z, sigma),
-                 ldexpf(xr[j][i].w, sigma), q0, q1, q2);
-        const uint32_t col = (Sx * 4 + i) * kXqChunk + 4 * lane;
-        *reinterpret_cast<uint32_t*>(xq + (t * 3 + 0) * kXqRow + col) = q0;
-        *reinterpret_cast<uint32_t*>(xq + (t * 3 + 1) * kXqRow + col) = q1;
-        *reinterpret_cast<uint32_t*>(xq + (t * 3 + 2) * kXqRow + col) = q2;
+      for (int c = 0; c < 4; ++c) {
+        if (4 * g4 + c < M) {
+          float4 v[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            v[i] = make_float4(comp(xr[4 * i], c), comp(xr[4 * i + 1], c), comp(xr[4 * i + 2], c), comp(xr[4 * i + 3], c));
+          stage_pair(4 * g4 + c, Sx, v[0], v[1], v[2], v[3]);
+        }
       }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+      const uint32_t p = wv + (uint32_t)j * kFW;
+      if (p < M * nst) stage_pair(p / nst, p % nst, xr[4 * j], xr[4 * j + 1], xr[4 * j + 2], xr[4 * j + 3]);
     }
   }
   AFFX_TRACE(15);
@@ -701,32 +758,61 @@ namespace {
 
 struct FusedVariant {
   const void* fn;
+  void (*launch)(uint32_t n_wg, uint32_t lds, hipStream_t st, const FusedArgs& A);
   uint32_t kc, maxm;
   int max_wg;  // workgroups the device holds at once (0: cannot run)
   bool ready;
 };
 
+template <int CG, int KC, int MAXM, bool SINGLE, int XF>
+void launch_fused(uint32_t n_wg, uint32_t lds, hipStream_t st, const FusedArgs& A) {
+  hipLaunchKernelGGL((decode_fused_kernel<CG, KC, MAXM, SINGLE, true, XF>), dim3(n_wg), dim3(kFT), lds, st, A);
+}
+
+template <int CG, int KC, int MAXM, bool SINGLE, int XF>
+FusedVariant fused_entry() {
+  FusedVariant f{};
+  f.fn = (const void*)decode_fused_kernel<CG, KC, MAXM, SINGLE, true, XF>;
+  f.launch = launch_fused<CG, KC, MAXM, SINGLE, XF>;
+  f.kc = KC;
+  f.maxm = MAXM;
+  return f;
+}
+
 constexpr int kMaxDev = 64;
 std::mutex g_fused_mu;
-FusedVariant g_fused[kMaxDev][4];
+FusedVariant g_fused[kMaxDev][4][3];
 
 // variants (all with the rotated tables): 0 M = 1 in one pass (8 codebook copies), 1 M = 1 in
 // rounds, 2 M <= 5 (4 copies), 3 M <= 8 (2 copies, 2 column groups). The larger M, the more LDS
 // the activation terms take; the copies fill what is left.
 int fused_variant(uint32_t M, bool single) { return M == 1 ? (single ? 0 : 1) : M <= 5 ? 2 : 3; }
 
-int fused_prepare(int dev, int v, FusedVariant* out) {
+// the XForm for these strides
+int fused_xform(const float* x, uint64_t x_ts, uint64_t x_ds, uint32_t M, uint32_t hidden) {
+  const bool al = (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+  if (x_ds == 1 && (M == 1 || (x_ts & 3u) == 0) && al) return kXTokenMajor;
+  const uint32_t quads = (M + 3) / 4, nst = hidden / kTileCols;
+  if (x_ts == 1 && (x_ds & 3u) == 0 && x_ds >= 4u * quads && al && quads * nst <= (uint32_t)kFW)
+    return kXDimMajor;
+  return kXStrided;
+}
+
+int fused_prepare(int dev, int v, int xf, FusedVariant* out) {
   std::lock_guard<std::mutex> lk(g_fused_mu);
-  FusedVariant& f = g_fused[dev][v];
+  FusedVariant& f = g_fused[dev][v][xf];
   if (!f.ready) {
-    static const void* fns[4] = {(const void*)decode_fused_kernel<1, 8, 1, true, true>,
-                                 (const void*)decode_fused_kernel<1, 8, 1, false, true>,
-                                 (const void*)decode_fused_kernel<1, 4, 5, false, true>,
-                                 (const void*)decode_fused_kernel<2, 2, 8, false, true>};
-    static const uint32_t kcs[4] = {8, 8, 8, 4}, maxms[4] = {1, 1, 5, 8};
-    f.fn = fns[v];
-    f.kc = kcs[v];
-    f.maxm = maxms[v];
+    static const FusedVariant table[4][3] = {
+        {fused_entry<1, 8, 1, true, kXStrided>(), fused_entry<1, 8, 1, true, kXTokenMajor>(),
+         fused_entry<1, 8, 1, true, kXDimMajor>()},
+        {fused_entry<1, 8, 1, false, kXStrided>(), fused_entry<1, 8, 1, false, kXTokenMajor>(),
+         fused_entry<1, 8, 1, false, kXDimMajor>()},
+        {fused_entry<1, 4, 5, false, kXStrided>(), fused_entry<1, 4, 5, false, kXTokenMajor>(),
+         fused_entry<1, 4, 5, false, kXDimMajor>()},
+        {fused_entry<2, 2, 8, false, kXStrided>(), fused_entry<2, 2, 8, false, kXTokenMajor>(),
+         fused_entry<2, 2, 8, false, kXDimMajor>()}};
+    if (!table[v][xf].fn) return set_error(AFFX_ERR_ARG, "ffn_decode: no fused kernel for variant %d form %d", v, xf);
+    f = table[v][xf];
     const uint32_t lds = fused_lds(f.maxm).total;  // dynamic part (the codebook copies are static)
     int rc = check_hip(hipFuncSetAttribute(f.fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
                        "hipFuncSetAttribute(fused decode)");
@@ -769,15 +855,18 @@ extern "C" int affx_expert_ffn_decode(const affx_layer* L, const float* x, uint6
   uint32_t want = (items_max + groups - 1) / groups;
   if (want < dtiles) want = dtiles;
   FusedVariant f;
-  rc = fused_prepare(dev, fused_variant(M, false), &f);  // any variant: the grid capacity
+  const int xf = fused_xform(x, x_ts, x_ds, M, L->hidden);
+  rc = fused_prepare(dev, fused_variant(M, false), xf, &f);  // any variant: the grid capacity
   if (rc) return rc;
-  if (f.max_wg <= 0)
+  // the kernel addresses x with 32-bit element offsets; larger arenas take the staged launches
+  const bool x_small = (uint64_t)M * x_ts + (uint64_t)L->hidden * x_ds < (1ull << 30);
+  if (f.max_wg <= 0 || !x_small)
     return affx_decode_staged(L, x, x_ts, x_ds, M, sel, w, K, y, y_ts, y_ds, accumulate, ws, ws_bytes, stream);
   const uint32_t n_wg = want < (uint32_t)f.max_wg ? want : (uint32_t)f.max_wg;
   // one pass: every gate/up item has its own wave group, every down unit of a tile its own wave
   const bool single = items_max <= groups * n_wg && units_max <= (uint32_t)kFW;
   const int v = fused_variant(M, single);
-  rc = fused_prepare(dev, v, &f);
+  rc = fused_prepare(dev, v, xf, &f);
   if (rc) return rc;
 
   FusedArgs A;
@@ -812,11 +901,6 @@ extern "C" int affx_expert_ffn_decode(const affx_layer* L, const float* x, uint6
   hipStream_t st = (hipStream_t)stream;
   // the down B operand's unused columns read the workspace's zero run: zero in a zero-filled
   // workspace and only ever rewritten with zeros (by the staged prep kernel)
-  switch (v) {
-    case 0: hipLaunchKernelGGL((decode_fused_kernel<1, 8, 1, true, true>), dim3(n_wg), dim3(kFT), lds, st, A); break;
-    case 1: hipLaunchKernelGGL((decode_fused_kernel<1, 8, 1, false, true>), dim3(n_wg), dim3(kFT), lds, st, A); break;
-    case 2: hipLaunchKernelGGL((decode_fused_kernel<1, 4, 5, false, true>), dim3(n_wg), dim3(kFT), lds, st, A); break;
-    default: hipLaunchKernelGGL((decode_fused_kernel<2, 2, 8, false, true>), dim3(n_wg), dim3(kFT), lds, st, A); break;
-  }
+  f.launch(n_wg, lds, st, A);
   return check_launch("decode_fused_kernel");
 }

@@ -242,7 +242,7 @@ def main() -> int:
                    "bytes_per_token": bytes_tok},
         "roofline": {"bound": "hbm", "achieved": round(fu_achieved, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                      "frac": round(fu_achieved * 1e9 / HBM_PEAK, 4), "traffic": traffic,
-                     "kernel": "decode_fused_kernel<1,8,1,true,true>", "bytes_per_launch": fu_bytes,
+                     "kernel": "decode_fused_kernel<1,8,1,true,true,1>", "bytes_per_launch": fu_bytes,
                      "us_per_launch": round(fu_us, 3)},
         "c3": {"gb_per_s": round(gbs8, 1), "us_per_step": round(ms8 * 1e3, 2),
                "distinct_experts_per_layer": round(distinct / L, 2)},

@@ -1,7 +1,7 @@
 // Runs libaffx's kernels on the CPU (see hip/hip_runtime.h) against the C oracle.
 // Test infrastructure: built with AddressSanitizer by tests/test_cpu_emulation.py.
 //
-//   emu_main decode  hidden inter n_experts M K seed [staged] -> rel_l2 of the decode FFN (the
+//   emu_main decode  hidden inter n_experts M K seed [staged|allpad|dm<nb>] -> rel_l2 of the decode FFN (the
 //                    fused launch, also checked equal to the staged launches; `staged` alone)
 //   emu_main grouped hidden inter n_experts T K seed lo   -> rel_l2 of the grouped FFN
 //   emu_main quant   rows cols seed                       -> planes bit-exact vs the oracle
@@ -136,9 +136,17 @@ int run_decode(int argc, char** argv) {
   bool same = true;
   if (!staged_only && rc == 0) {
     // twice on one workspace: the second launch relies on the first leaving its counters zero
+    // "dm<nb>": x as the engine's dim-major arena [hidden][nb] (tok stride 1, dim stride nb), the
+    // unused token slots of each row filled with huge values that must not reach the result
+    const uint32_t nb = mode.rfind("dm", 0) == 0 ? (uint32_t)atoi(mode.c_str() + 2) : 0;
+    std::vector<float> xd(nb ? (size_t)hidden * nb : 0, 3e37f);
+    for (uint32_t h = 0; nb && h < hidden; ++h)
+      for (uint32_t t = 0; t < M; ++t) xd[(size_t)h * nb + t] = x[(size_t)t * hidden + h];
     for (int rep = 0; rep < 2 && rc == 0; ++rep)
-      rc = affx_expert_ffn_decode(&abi, x.data(), hidden, 1, M, sel.data(), w.data(), K, y.data(), hidden, 1, 0,
-                                  ws.data(), wsb, nullptr);
+      rc = nb ? affx_expert_ffn_decode(&abi, xd.data(), 1, nb, M, sel.data(), w.data(), K, y.data(), hidden, 1, 0,
+                                       ws.data(), wsb, nullptr)
+              : affx_expert_ffn_decode(&abi, x.data(), hidden, 1, M, sel.data(), w.data(), K, y.data(), hidden, 1, 0,
+                                       ws.data(), wsb, nullptr);
     // the sync run (counters, error bits, release flags: everything before the plan) is zero again
     uint32_t sync[3];
     memcpy(sync, ws.data(), sizeof(sync));

@@ -70,6 +70,12 @@ def test_decode_emulated_m6_two_column_groups(emu):
     assert "identical to staged=1" in run(emu, "decode", 2048, 1024, 5, 6, 2, 2)
 
 
+def test_decode_emulated_m6_dim_major_arena(emu):
+    # the engine's dim-major batch arena at its 16-token stride: whole-row reads of four tokens
+    # per wave (two token quads x two column segments), the second quad half padding slots
+    assert "identical to staged=1" in run(emu, "decode", 2048, 1024, 5, 6, 2, 2, "dm16")
+
+
 def test_decode_emulated_m8_wide_epilogue(emu):
     # 12 gate/up groups x 16 rows x 8 tokens: the epilogue takes two passes of the workgroup
     # (hidden 1024: one column segment, so 12 wave groups; inter 1024 keeps the emulation short)

@@ -249,6 +249,33 @@ def test_fused_decode_identical_to_staged_full_layer(ax, orc, c1_codebook, M, k)
         assert err <= TOL
 
 
+@pytest.mark.parametrize("M,nb", [(1, 16), (3, 16), (6, 16), (8, 16), (8, 8), (7, 12), (6, 10)])
+def test_fused_decode_dim_major_arena(ax, c1_codebook, M, nb):
+    """The engine's dim-major batch arena x[h * nb + t] (16 = the reference's narrow-batch
+    stride, src/gpu/batch_kernels.h:57) at the benchmark layer shape: equal bit for bit to the
+    token-major call and to the staged launches. The arena's unused token slots hold huge values
+    that must not reach the result (the 6-8 token decode reads four tokens of a row at once)."""
+    hidden, inter, n, k = 4096, 2048, 256, 6
+    pool = _random_device_pool(ax, c1_codebook, n, hidden, inter, seed=31 + M)
+    rng = np.random.default_rng(200 + M + nb)
+    xn = (rng.standard_normal((M, hidden)) * 0.7).astype(np.float32)
+    x = torch.from_numpy(xn).cuda()
+    xd = torch.full((hidden, nb), 3e37, device="cuda")
+    xd[:, :M] = x.t()
+    sel = torch.from_numpy(np.stack([rng.choice(n, k, replace=False) for _ in range(M)]).astype(np.int32)).cuda()
+    w = torch.from_numpy(rng.uniform(0.05, 1.0, (M, k)).astype(np.float32)).cuda()
+    ws = ax.DecodeWorkspace(M, k, hidden, inter)
+    yt = ax.expert_ffn_decode(pool, x, sel, w, workspace=ws)
+    ys = ax.expert_ffn_decode(pool, x, sel, w, staged=True, workspace=ax.DecodeWorkspace(M, k, hidden, inter))
+    yd = torch.zeros((hidden, nb), device="cuda")
+    ax.expert_ffn_decode(pool, xd[:, :M], sel, w, y=yd[:, :M], workspace=ws, dim_major=True)
+    torch.cuda.synchronize()
+    assert torch.equal(yt, ys)
+    assert torch.equal(yd[:, :M].t(), yt)
+    assert torch.equal(yd[:, M:], torch.zeros_like(yd[:, M:]))
+    assert ws.error_flags() == 0
+
+
 def test_fused_decode_graph_replays(ax, c1_codebook):
     """Captured in a HIP graph, the persistent decode replays to the eager result every time
     (its counters are reset by the kernel itself, nothing is memset)."""
