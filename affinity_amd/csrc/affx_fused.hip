@@ -127,9 +127,16 @@ __device__ __forceinline__ float fused_terms(float d) {
 }
 
 
+// maximum over the wave, wave-uniform: DPP row shifts leave each 16-lane row's maximum in its
+// last lane, then the four rows' last lanes are combined (no LDS round trips)
 __device__ __forceinline__ float wave_max(float v) {
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
+  v = fmaxf(v, row_shr<1>(v));
+  v = fmaxf(v, row_shr<2>(v));
+  v = fmaxf(v, row_shr<4>(v));
+  v = fmaxf(v, row_shr<8>(v));
+  const int b = __float_as_int(v);
+  return fmaxf(fmaxf(__int_as_float(__builtin_amdgcn_readlane(b, 15)), __int_as_float(__builtin_amdgcn_readlane(b, 31))),
+               fmaxf(__int_as_float(__builtin_amdgcn_readlane(b, 47)), __int_as_float(__builtin_amdgcn_readlane(b, 63))));
 }
 
 // ------------------------------------------------------------------------------------------------
