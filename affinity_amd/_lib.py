@@ -9,6 +9,8 @@ LIB_PATH = os.path.join(HERE, "libaffx.so")
 
 AFFX_OK = 0
 AFFX_DECLINED = 1
+AFFX_ERR_ARG = -1
+AFFX_ERR_DEVICE = -3
 
 _vp = C.c_void_p
 _u32 = C.c_uint32
@@ -50,6 +52,7 @@ _SIGS = {
     "affx_permute_experts": ([_vp, _vp, _u64, _u64, _u64, _vp], C.c_int),
     "affx_dequant_matrix": ([C.POINTER(AffxMatrix), _vp, _vp, _vp], C.c_int),
     "affx_decode_workspace_size": ([_u32, _u32, _u32, _u32], C.c_size_t),
+    "affx_decode_status": ([_vp, C.c_int, _vp], C.c_int),
     "affx_expert_ffn_decode": ([C.POINTER(AffxLayer), _vp, _u64, _u64, _u32, _vp, _vp, _u32, _vp,
                                 _u64, _u64, C.c_int, _vp, C.c_size_t, _vp], C.c_int),
     "affx_decode_prepare": ([C.POINTER(AffxLayer), _vp, _u64, _u64, _u32, _vp, _vp, _u32, _vp, C.c_size_t,

@@ -36,10 +36,6 @@ __global__ void __launch_bounds__(256) add_transposed_kernel(const float* __rest
 
 using namespace affx;
 
-namespace {
-uint64_t a256(uint64_t v) { return (v + 255) / 256 * 256; }
-}  // namespace
-
 extern "C" {
 
 // Hook workspace. Decode: [decode workspace][routes][weights]; the decode workspace starts at
@@ -122,7 +118,18 @@ uint32_t affx_expert_ffn_batch(void* ctx_, uint32_t layer, const uint32_t* sel, 
     }
   }
   if (rc != AFFX_OK) return 0;
+  // the decode's error word comes back with the sync the hook does anyway (routes are host
+  // memory, so the engine waits for the layer regardless): a wait that gave up fails the call
+  uint32_t err = 0;
+  if (decode && check_hip(hipMemcpyAsync(&err, ws + kSyncErrWord * 4, 4, hipMemcpyDeviceToHost, s), "status D2H"))
+    return 0;
   if (check_hip(hipStreamSynchronize(s), "ffn_batch sync")) return 0;
+  if (err) {
+    decode_sync_reset(ws, s);
+    set_error(AFFX_ERR_DEVICE, "ffn_batch: layer %u: the decode's workgroups gave up waiting for each "
+              "other (error bits 0x%x; the device did not hold the grid resident); output invalid", layer, err);
+    return 0;
+  }
   uint32_t taken = 0;
   for (uint64_t i = 0; i < pairs; ++i)
     if (sel[i] < L->n_experts) {
@@ -130,6 +137,21 @@ uint32_t affx_expert_ffn_batch(void* ctx_, uint32_t layer, const uint32_t* sel, 
       ++taken;
     }
   return taken;
+}
+
+int affx_decode_status(void* workspace, int reset, void* stream) {
+  if (!workspace) return set_error(AFFX_ERR_ARG, "decode_status: null workspace");
+  hipStream_t s = (hipStream_t)stream;
+  uint32_t err = 0;
+  int rc = check_hip(hipMemcpyAsync(&err, (uint8_t*)workspace + kSyncErrWord * 4, 4, hipMemcpyDeviceToHost, s),
+                     "decode_status D2H");
+  if (!rc) rc = check_hip(hipStreamSynchronize(s), "decode_status sync");
+  if (rc) return rc;
+  if (!err) return AFFX_OK;
+  if (reset && (rc = decode_sync_reset(workspace, s))) return rc;
+  if (reset && (rc = check_hip(hipStreamSynchronize(s), "decode_status sync"))) return rc;
+  return set_error(AFFX_ERR_DEVICE, "decode_status: a decode launch gave up waiting for its workgroups "
+                   "(error bits 0x%x); its output was invalid%s", err, reset ? " (state reset)" : "");
 }
 
 }  // extern "C"

@@ -39,6 +39,7 @@ enum Plane : int {
   kDownCodes = 6, kDownFields = 7, kDownRs = 8
 };
 
+__host__ __device__ inline uint64_t a256(uint64_t v) { return (v + 255) / 256 * 256; }
 __host__ __device__ inline uint64_t code_row_bytes(uint64_t cols) { return cols * 10 / 32; }
 __host__ __device__ inline uint64_t field_row_bytes(uint64_t cols) { return cols * 6 / 128; }
 
@@ -92,6 +93,10 @@ constexpr uint32_t kSyncHeader = 256;
 constexpr uint32_t kSyncFlagStride = 128;
 constexpr uint32_t kSyncFlags = 256;  // down-phase workgroups: output row tiles, hidden / 16 <= 256
 constexpr uint32_t kSyncBytes = kSyncHeader + kSyncFlags * kSyncFlagStride;
+constexpr uint32_t kSyncErrWord = 2;  // dword of the error bits (bit 0: a waiter gave up)
+// Zeroes the sync run of a decode workspace (stream-ordered; after a wait gave up, the late
+// publisher may have raised flags that a later launch would take for its own).
+int decode_sync_reset(void* ws, hipStream_t s);
 struct DecodeWs {
   uint64_t sync, plan, zeros, xq, aq, total;
 };

@@ -382,18 +382,16 @@ __global__ void __launch_bounds__(kDownWaves * 64) decode_down_kernel(DecodeArgs
   }
 }
 
-static uint64_t align256(uint64_t v) { return (v + 255) / 256 * 256; }
-
 // Workspace: [sync: fused-decode counters and flags, zero on first use][plan][zeros][xq][aq]
 DecodeWs decode_ws(uint32_t M, uint32_t K, uint32_t hidden, uint32_t inter) {
   DecodeWs w;
   const uint64_t slots = (uint64_t)M * K;
   w.sync = 0;
-  w.plan = align256(kSyncBytes);
-  w.zeros = w.plan + align256(sizeof(DecodePlan));
+  w.plan = a256(kSyncBytes);
+  w.zeros = w.plan + a256(sizeof(DecodePlan));
   w.xq = w.zeros + 256;
-  w.aq = w.xq + align256((uint64_t)M * kTerms * hidden);
-  w.total = w.aq + align256(slots * M * kTerms * inter);
+  w.aq = w.xq + a256((uint64_t)M * kTerms * hidden);
+  w.total = w.aq + a256(slots * M * kTerms * inter);
   return w;
 }
 
@@ -434,6 +432,10 @@ int decode_check(const affx_layer* L, uint32_t M, uint32_t K, const void* ws, si
   const uint64_t stride = affx_expert_layout(L->hidden, L->inter, off9, nullptr);
   if (L->stride < stride) return set_error(AFFX_ERR_ARG, "ffn_decode: layer stride below expert size");
   return AFFX_OK;
+}
+
+int decode_sync_reset(void* ws, hipStream_t s) {
+  return check_hip(hipMemsetAsync(ws, 0, kSyncBytes, s), "decode sync reset");
 }
 
 // decode_check, then the staged kernels' arguments.

@@ -63,6 +63,7 @@ struct FusedArgs {
   int accumulate;
   float limit;
   int32_t sigma_a;
+  uint32_t spin_limit;  // polls of the release flag before a waiter gives up (sets error bit 0)
 };
 
 // Dynamic LDS layout in bytes (host and device agree): activation terms, zero run, partial sums,
@@ -554,12 +555,27 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
 
   // The first down unit's weights are loaded now, after this workgroup's gate/up data has arrived
   // (issued earlier they would share the HBM stream with it and delay gate/up), so they stream in
-  // while the layer publishes and waits. Publish (once, all rounds): every wave that stored
-  // drains its device-coherent stores (loads and stores complete in issue order: at most the 7
-  // or more down-unit loads issued after them may stay outstanding), the barrier orders that
-  // before thread 0's counter update. No release fence: its L2 write-back, once per workgroup
-  // and serialised per L2, costs microseconds, and nothing else written here is read by other
-  // workgroups.
+  // while the layer publishes and waits.
+  //
+  // Publish (once, all rounds). Why the SwiGLU output is visible to every down workgroup, on any
+  // XCD, without a release fence (the memory-model argument; a formal agent-scope release here
+  // measured 2.7 to 8.4 us per layer slower: its L2 write-back, and its wait for the down-unit
+  // loads in flight in the releasing wave):
+  //  * every value handed across is written by an agent-scope atomic store, which the compiler
+  //    emits as `global_store ... sc1`; its own mapping of agent-scope atomics treats such a store
+  //    as visible to the whole device once it has completed (it emits no L2 write-back for it:
+  //    the write-back of a release is for non-atomic stores, and there are none to hand over);
+  //  * each storing wave waits for its stores to complete: vector memory operations complete in
+  //    issue order (the property the compiler's own waits rely on when they wait for one load
+  //    among several with vmcnt(N) > 0), and only the nine loads of the down unit were issued
+  //    after the stores, so vmcnt(7) covers them;
+  //  * the barrier orders those waits before thread 0's counter add; the add that completes the
+  //    count is performed after every other add, hence after every workgroup's stores completed;
+  //    its wave reads the old value back before it raises the flags, so the add is performed
+  //    before any flag store is issued;
+  //  * a waiter that sees its flag runs an agent-scope acquire fence (`buffer_inv sc1`) before
+  //    any workgroup thread reads the SwiGLU output, so no stale line of an earlier launch is
+  //    read from its CU's or its XCD's caches.
   if (PREF) {
     if (!SINGLE || n_rounds == 0 || wv < epi_waves) load_down(has_down, g, wv);
     if (n_rounds > 0 && wv < epi_waves) __builtin_amdgcn_s_waitcnt(AFFX_VMCNT(7));
@@ -569,9 +585,8 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   AFFX_TRACE(10);
   __syncthreads();
   if (wv == 0 && n_rounds > 0) {
-    // the add that completes the count finds every other add performed, hence every activation
-    // store complete. Its wave clears the count for the next launch and raises the flag of each
-    // waiting workgroup (one line each: the waiters poll without contending for one address).
+    // the add that completes the count clears it for the next launch and raises the flag of each
+    // waiting workgroup (one line each: the waiters poll without contending for one address)
     uint32_t old = 0;
     if (lane == 0) old = __hip_atomic_fetch_add(&A.sync[0], my_items, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     old = __builtin_amdgcn_readlane(old, 0);
@@ -609,12 +624,13 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   if (g < dtiles) {
     if (tid == 0 && NI > 0) {
       uint32_t* flag = A.sync + (kSyncHeader + g * kSyncFlagStride) / 4;
-      uint32_t n = 0;
-      while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) {
-        if (++n > kSpinLimit) {
-          __hip_atomic_fetch_or(&A.sync[2], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // at most spin_limit polls (none at 0: the give-up path runs deterministically)
+      for (uint32_t n = 0;; ++n) {
+        if (n >= A.spin_limit) {
+          __hip_atomic_fetch_or(&A.sync[kSyncErrWord], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           break;
         }
+        if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) break;
         __builtin_amdgcn_s_sleep(2);
       }
       __hip_atomic_store(flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // for the next launch
@@ -795,6 +811,14 @@ FusedVariant g_fused[kMaxDev][4][3];
 // the activation terms take; the copies fill what is left.
 int fused_variant(uint32_t M, bool single) { return M == 1 ? (single ? 0 : 1) : M <= 5 ? 2 : 3; }
 
+// Polls of a release flag before a waiter gives up: kSpinLimit, or AFFX_DECODE_SPIN_LIMIT from
+// the environment (read at every call; a test makes the wait give up with a small value, so the
+// failure path runs with every kernel still exiting normally).
+uint32_t decode_spin_limit() {
+  const char* e = getenv("AFFX_DECODE_SPIN_LIMIT");
+  return e && *e ? (uint32_t)strtoul(e, nullptr, 10) : kSpinLimit;
+}
+
 // the XForm for these strides
 int fused_xform(const float* x, uint64_t x_ts, uint64_t x_ds, uint32_t M, uint32_t hidden) {
   const bool al = (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
@@ -869,12 +893,24 @@ extern "C" int affx_expert_ffn_decode(const affx_layer* L, const float* x, uint6
   const bool x_small = (uint64_t)M * x_ts + (uint64_t)L->hidden * x_ds < (1ull << 30);
   if (f.max_wg <= 0 || !x_small)
     return affx_decode_staged(L, x, x_ts, x_ds, M, sel, w, K, y, y_ts, y_ds, accumulate, ws, ws_bytes, stream);
-  const uint32_t n_wg = want < (uint32_t)f.max_wg ? want : (uint32_t)f.max_wg;
+  uint32_t n_wg = want < (uint32_t)f.max_wg ? want : (uint32_t)f.max_wg;
   // one pass: every gate/up item has its own wave group, every down unit of a tile its own wave
-  const bool single = items_max <= groups * n_wg && units_max <= (uint32_t)kFW;
+  bool single = items_max <= groups * n_wg && units_max <= (uint32_t)kFW;
   const int v = fused_variant(M, single);
-  rc = fused_prepare(dev, v, xf, &f);
-  if (rc) return rc;
+  if (v != fused_variant(M, false)) {
+    // the one-pass kernel is another instantiation: its own occupancy bounds the grid (every
+    // workgroup must be resident at once), and a smaller grid may no longer hold every item in
+    // one pass, in which case the rounds kernel runs on the grid that its own occupancy allows
+    rc = fused_prepare(dev, v, xf, &f);
+    if (rc) return rc;
+    if (f.max_wg <= 0 || n_wg > (uint32_t)f.max_wg) {
+      rc = fused_prepare(dev, fused_variant(M, false), xf, &f);
+      if (rc) return rc;
+      single = false;
+    }
+  }
+  if (f.max_wg <= 0 || n_wg > (uint32_t)f.max_wg)
+    return affx_decode_staged(L, x, x_ts, x_ds, M, sel, w, K, y, y_ts, y_ds, accumulate, ws, ws_bytes, stream);
 
   FusedArgs A;
   uint64_t off9[9];
@@ -904,6 +940,7 @@ extern "C" int affx_expert_ffn_decode(const affx_layer* L, const float* x, uint6
   A.accumulate = accumulate;
   A.limit = L->swiglu_limit;
   A.sigma_a = 7 - ilogbf(L->swiglu_limit * L->swiglu_limit);
+  A.spin_limit = decode_spin_limit();
   const uint32_t lds = fused_lds(M).total;
   hipStream_t st = (hipStream_t)stream;
   // the down B operand's unused columns read the workspace's zero run: zero in a zero-filled

@@ -4,8 +4,10 @@
 //   grouped_plan     one workgroup: per-expert counts, exclusive scan, tile lists
 //   grouped_place    one workgroup per expert: its (token, route) pairs in token order (stable),
 //                    so every slot and every output sum has a fixed order
-//   grouped_prep_x   per token: exponent and E4M3 terms of the activation (2 terms are exact for
-//                    bf16 input; 3 when a low bf16 term is given)
+//   grouped_prep_x   per token: exponent and E4M3 terms of the activation (2 terms for a bf16
+//                    input: exact for every element of at least 2^-13 of the token's largest
+//                    magnitude, where both terms are normal E4M3 numbers, and within 2^-20 of that
+//                    maximum below it; 3 when a low bf16 term is given)
 //   grouped_gemm<0>  gate/up: (row block of 128 inter rows, token tile): 8 waves x 16 rows of
 //                    gate and the same 16 of up, K = hidden in 128-column MFMA steps, 12 column
 //                    tiles per A fragment; epilogue combines terms, applies row scales, SwiGLU,
@@ -808,7 +810,6 @@ using namespace affx;
 
 namespace {
 
-uint64_t a256(uint64_t v) { return (v + 255) / 256 * 256; }
 
 struct GroupedWs {
   uint64_t hdr, offsets, slot_tok, slot_of, tiles1, tiles2, sigma, zeros, xq, aq, z, total;

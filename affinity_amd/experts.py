@@ -136,6 +136,11 @@ class DecodeWorkspace:
         """Nonzero if a fused decode launch on this workspace gave up waiting (bounded spin)."""
         return int(self.buf[8:12].view(torch.int32).item())
 
+    def status(self, reset: bool = False, stream=None) -> int:
+        """affx_decode_status: 0, or AFFX_ERR_DEVICE (< 0) when a launch on this workspace gave up
+        waiting for its workgroups; reset zeroes the sync run. Synchronises the stream."""
+        return int(lib().affx_decode_status(self.buf.data_ptr(), int(reset), _stream(stream)))
+
 
 def expert_ffn_decode(pool: ExpertPool, x: torch.Tensor, sel: torch.Tensor, w: torch.Tensor,
                       y: torch.Tensor | None = None, accumulate: bool = False,

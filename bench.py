@@ -4,7 +4,8 @@
 Metric: expert-FFN decode GB/s (% of HBM peak) + prefill grouped-GEMM TFLOP/s.
 
 Workloads (synthetic, seeds of the benchmark configs; weights quantised on the GPU by the
-library's own quantiser against the config-1 codebook the reference fitted):
+library's own quantiser against the config-1 codebook the reference fitted; affinity_amd/
+synthetic.py):
   value      C5: batch-1 decode of the config-2 MoE layer (256 experts x 2.875 bpw, top-6 softmax
              routes) through a stack of resident layers (43 by default: 92.9 GiB), one token per
              step, captured in a HIP graph. GB/s counts algorithmic bytes: 6 experts x 9,060,352 B
@@ -16,8 +17,9 @@ library's own quantiser against the config-1 codebook the reference fitted):
              per launch (6 x 9,060,352 B) over its average duration, timed with HIP events on the
              launch stream (the C5 graph holds only these launches); traffic = HBM bytes per
              launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary.
-  cpu_baseline  the reference's own CPU path (oracle/_ref/libaffref.so, else the oracle) on a
-             bounded sample: one token through the 6 routed experts of layer 0.
+  cpu_baseline  the reference's own CPU path (oracle/_ref/libaffref.so, else the oracle that
+             restates it) on bounded samples of every config, on this host's cores; its outputs are
+             also the checker of the GPU results reported under "parity".
 
     python bench.py [--steps K] [--warmup W] [--layers L] [--gpus 1]
 """
@@ -27,6 +29,7 @@ import argparse
 import ctypes as C
 import json
 import os
+import platform
 import sys
 import time
 
@@ -35,8 +38,9 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, HERE)
 
-S_W, S_X, S_R, S_Z = 1000, 7, 11, 13
-H, I, E, K = 4096, 2048, 256, 6
+from affinity_amd import synthetic  # noqa: E402
+from affinity_amd.synthetic import E, H, I, K, S_R, S_X  # noqa: E402
+
 STRIDE = 9_060_352
 HBM_PEAK = 8.0e12               # B/s, MI355X
 BF16_PEAK = 2.5e15              # FLOP/s dense, MI355X
@@ -47,43 +51,14 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def softmax_topk(logits, k):
-    """Top-k by logit (stable: ties -> lower id), weights = softmax renormalised over the k."""
-    import torch
-    order = torch.sort(logits, dim=-1, descending=True, stable=True).indices[..., :k]
-    top = torch.gather(logits, -1, order).double()
-    w = torch.softmax(top, dim=-1).float()
-    return order.to(torch.int32).contiguous(), w.contiguous()
+def rel_l2(got, ref) -> float:
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return float(np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30))
 
 
-def zipf_routes(T, n, k, s=1.1, seed=S_Z):
-    rng = np.random.default_rng(seed)
-    perm = rng.permutation(n)
-    p = 1.0 / np.arange(1, n + 1) ** s
-    p /= p.sum()
-    sel = np.empty((T, k), np.int32)
-    for t in range(T):
-        sel[t] = perm[rng.choice(n, k, replace=False, p=p)]
-    lg = rng.standard_normal((T, k))
-    w = np.exp(lg - lg.max(1, keepdims=True))
-    w = (w / w.sum(1, keepdims=True)).astype(np.float32)
-    return sel, w
-
-
-def build_layer(ax, torch, cb_packed):
-    """The config-2 layer: 256 experts, expert e from seeds S_W + 3e + {0,1,2}, in container layout."""
-    cbf = torch.from_numpy(ax.codebook_floats(cb_packed)).cuda()
-    cont = torch.empty(E * STRIDE, dtype=torch.uint8, device="cuda")
-    t0 = time.time()
-    for e0 in range(0, E, 32):
-        ax.fill_synthetic_experts(cont, e0, 32, cbf, lambda e: S_W + 3 * e)
-        torch.cuda.synchronize()
-        log(f"quantised experts {e0 + 32}/{E} ({time.time() - t0:.1f} s)")
-    return cont
-
-
-def time_graph(torch, fn, steps, warmup, replays_check=True):
-    """Captures fn into a HIP graph, checks a replay against eager, times `steps` replays."""
+def time_graph(torch, fn, steps, warmup):
+    """Captures fn into a HIP graph and times `steps` replays with events on the current stream."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -131,7 +106,7 @@ def main() -> int:
 
     ax.init()
     torch.cuda.set_device(0)
-    cb_packed = np.fromfile(os.path.join(HERE, "tests", "golden", "c1_codebook.bin"), dtype="<u4")
+    cb_packed = synthetic.c1_codebook()
     L = args.layers
 
     if args.calibrate:
@@ -143,10 +118,8 @@ def main() -> int:
         del src, dst
 
     # ---- resident stack ----------------------------------------------------------------------
-    cont = build_layer(ax, torch, cb_packed)
-    pools = []
-    for l in range(L):
-        pools.append(ax.ExpertPool.from_container(cont, cb_packed))
+    cont = synthetic.build_layer_container(ax, torch, log=log)
+    pools = [ax.ExpertPool.from_container(cont, cb_packed) for _ in range(L)]
     torch.cuda.synchronize()
     log(f"{L} layers resident: {L * E * STRIDE / 2**30:.2f} GiB")
     layers = [p.layer() for p in pools]
@@ -157,8 +130,8 @@ def main() -> int:
     routes1, routes8 = [], []
     for l in range(L):
         lg = ax.gen_normal(S_R + l, 8 * E, 1.0, bf16_round=False).view(8, E)
-        routes1.append(softmax_topk(lg[:1], K))
-        routes8.append(softmax_topk(lg, K))
+        routes1.append(synthetic.softmax_topk(lg[:1], K))
+        routes8.append(synthetic.softmax_topk(lg, K))
     ws1 = ax.DecodeWorkspace(1, K)
     ws8 = ax.DecodeWorkspace(8, K)
     y1 = torch.zeros((L, H), device="cuda")
@@ -222,6 +195,12 @@ def main() -> int:
     gbs8 = distinct * STRIDE / (ms8 * 1e-3) / 1e9
     log(f"C3 decode (M=8): {ms8 * 1e3:.1f} us/step, {distinct / L:.1f} experts/layer -> {gbs8:.0f} GB/s")
 
+    # a launch whose workgroups gave up waiting for each other wrote invalid output: fail the run
+    st1, st8 = ws1.status(), ws8.status()
+    if st1 or st8:
+        log(f"decode workspace status {st1}, {st8}: a launch gave up waiting; results invalid")
+        return 3
+
     result = {
         "metric": "expert-FFN decode GB/s (% of HBM peak) + prefill grouped-GEMM TFLOP/s",
         "value": round(gbs, 1),
@@ -245,13 +224,16 @@ def main() -> int:
                      "kernel": "decode_fused_kernel<1,8,1,true,true,1>", "bytes_per_launch": fu_bytes,
                      "us_per_launch": round(fu_us, 3)},
         "c3": {"gb_per_s": round(gbs8, 1), "us_per_step": round(ms8 * 1e3, 2),
+               "us_per_layer": round(ms8 * 1e3 / L, 2), "hbm_fraction": round(gbs8 * 1e9 / HBM_PEAK, 4),
                "distinct_experts_per_layer": round(distinct / L, 2)},
+        "decode_status": {"m1": st1, "m8": st8},
     }
 
     # ---- C4 prefill ------------------------------------------------------------------------------
+    prefill = None
     if args.only == "all":
         T = 4096
-        sel_np, w_np = zipf_routes(T, E, K)
+        sel_np, w_np = synthetic.zipf_routes(T, E, K)
         counts = np.bincount(sel_np.reshape(-1), minlength=E)
         xb = ax.gen_normal(S_X, T * H, 1.0).view(T, H).to(torch.bfloat16)
         sel_t = torch.from_numpy(sel_np).cuda()
@@ -276,75 +258,147 @@ def main() -> int:
                              "tokens_per_s": round(T / (msp * 1e-3), 1), "flop_per_layer": flops,
                              "expert_counts": {"min": int(counts.min()), "median": float(np.median(counts)),
                                                "max": int(counts.max())}}
+        prefill = (sel_np, w_np, xb, yp)
 
-    # ---- CPU baseline ------------------------------------------------------------------------------
+    # ---- CPU baseline (and the checker of the GPU results) ----------------------------------------
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(ax, torch, cont, routes1[0], x1)
+        gpu = {"c1_dequant": [ax.dequant_matrix(pools[0], 0, m).cpu().numpy() for m in range(3)],
+               "x1": x1.cpu().numpy()[0], "x8": x8.cpu().numpy(),
+               "routes1": [(r[0].cpu().numpy(), r[1].cpu().numpy()) for r in routes1],
+               "routes8": (routes8[0][0].cpu().numpy(), routes8[0][1].cpu().numpy()),
+               "y1": y1.cpu().numpy(), "y8": y8[0].cpu().numpy()}
+        if prefill is not None:
+            sel_np, w_np, xb, yp = prefill
+            toks, _, _ = synthetic.prefill_sample(sel_np, E)
+            gpu["c4"] = (sel_np, w_np, xb.float().cpu().numpy()[toks], yp.cpu().numpy()[toks], toks)
+        result["cpu_baseline"], result["parity"] = cpu_baseline(ax, cont, gpu, L)
     print(json.dumps(result), flush=True)
     return 0
 
 
-def cpu_baseline(ax, torch, cont, route, x1):
-    """The reference CPU path (else the oracle restating it) on one token through the 6 routed
-    experts of layer 0: gate/up GEMV, SwiGLU, down GEMV with the route weight."""
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(ax, cont, gpu, L):
+    """The reference's CPU path (else the oracle restating it) on bounded samples of every config
+    timed on this host; returns (cpu_baseline, parity). The samples:
+      C1  dequantize_matrix of the config-1 expert (1 thread); its FFN at 1 and all threads
+      C2  one token through layer 0's 6 routed experts (1 and all threads): the reported value
+      C5  the same for layer L-1; ms per token over L layers = L x the mean token-layer time
+      C3  the 8-token layer 0 (48 routed expert FFNs)
+      C4  64 sampled prefill tokens, extrapolated linearly to the 4096-token layer
+    The same outputs are the checker of the GPU's (rel L2; dequant bit for bit)."""
     from oracle import load_oracle, load_ref, ref_available
-    sel = route[0].cpu().numpy().reshape(-1)
-    w = route[1].cpu().numpy().reshape(-1)
-    experts = [cont[int(e) * STRIDE:(int(e) + 1) * STRIDE].cpu().numpy() for e in sel]
-    x = x1.cpu().numpy().reshape(-1).astype(np.float32)
     _, off, size = ax.expert_layout()
-    cbf = ax.codebook_floats(np.fromfile(os.path.join(HERE, "tests", "golden", "c1_codebook.bin"),
-                                         dtype="<u4")).reshape(-1)
+    cbf = ax.codebook_floats(synthetic.c1_codebook()).reshape(-1)
     kind = "reference" if ref_available() else "port"
     lib = load_ref() if kind == "reference" else load_oracle()
+    if kind == "reference":
+        n_all = lib.pool_threads()
+    else:
+        n_all = min(os.cpu_count() or 1, 16)
+    cache = {}
+
+    def expert(e):
+        e = int(e)
+        if e not in cache:
+            cache[e] = synthetic.expert_bytes(cont, e, STRIDE)
+        return cache[e]
 
     def planes(ex, m):
         return (np.ascontiguousarray(ex[off[3 * m]:off[3 * m] + size[3 * m]]),
                 np.ascontiguousarray(ex[off[3 * m + 1]:off[3 * m + 1] + size[3 * m + 1]]),
                 np.ascontiguousarray(ex[off[3 * m + 2]:off[3 * m + 2] + size[3 * m + 2]]).view(np.uint16))
 
-    def token(mt):
-        y = np.zeros(H, np.float32)
-        for ex, wt in zip(experts, w):
-            if kind == "reference":
-                g = lib.gemv(*planes(ex, 0), I, H, cbf, x, 1.0, mt=mt)
-                u = lib.gemv(*planes(ex, 1), I, H, cbf, x, 1.0, mt=mt)
-                a = lib.swiglu(g, u, 10.0)
-                lib.gemv(*planes(ex, 2), H, I, cbf, a, float(wt), y, mt=mt)
-            else:
-                lib.expert_ffn(ex, cbf, x, float(wt), 10.0, y)
+    def ffn(ex, x, wt, y, mt):
+        """y += wt * FFN(x): src/engine/model.cpp:1187-1198 over the reference's GEMV."""
+        if kind == "reference":
+            g = lib.gemv(*planes(ex, 0), I, H, cbf, x, 1.0, mt=mt)
+            u = lib.gemv(*planes(ex, 1), I, H, cbf, x, 1.0, mt=mt)
+            a = lib.swiglu(g, u, 10.0)
+            lib.gemv(*planes(ex, 2), H, I, cbf, a, float(wt), y, mt=mt)
+        else:
+            lib.set_threads(n_all if mt else 1)
+            lib.expert_ffn(ex, cbf, x, float(wt), 10.0, y)
         return y
 
-    out = {"kind": kind, "sample": "1 token x 6 routed experts of layer 0 (one token-layer)",
-           "unit": "GB/s"}
-    if kind == "port":
+    def token(x, sel, w, mt):
+        y = np.zeros(H, np.float32)
+        for e, wt in zip(sel, w):
+            ffn(expert(e), x, wt, y, mt)
+        return y
+
+    def timed(fn, reps):
+        fn()                                   # warm-up (and the result)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            out = fn()
+        return (time.perf_counter() - t0) / reps, out
+
+    x1 = gpu["x1"]
+    ex0 = expert(0)
+    # C1: dequant (1 thread) and one expert FFN
+    dims = ((I, H), (I, H), (H, I))
+    if kind == "reference":
+        t_deq, deq = timed(lambda: [lib.dequantize(*planes(ex0, m), *dims[m], cbf) for m in range(3)], 3)
+    else:
         lib.set_threads(1)
-    t0 = time.time()
-    token(False)
-    t1 = (time.time() - t0)
-    reps = max(1, min(5, int(10.0 / max(t1, 1e-3))))
-    t0 = time.time()
-    for _ in range(reps):
-        token(False)
-    t_single = (time.time() - t0) / reps
-    cores = os.cpu_count() or 1
-    if kind == "port":
-        lib.set_threads(min(cores, 16))
-        cores = min(cores, 16)
-    token(True)
-    t0 = time.time()
-    for _ in range(reps):
-        token(True)
-    t_multi = (time.time() - t0) / reps
-    b = K * STRIDE
-    out.update({"value": round(b / t_multi / 1e9, 3), "cores": cores,
-                "ms_per_token_layer": round(t_multi * 1e3, 2),
-                "single_thread": {"value": round(b / t_single / 1e9, 4), "cores": 1,
-                                  "ms_per_token_layer": round(t_single * 1e3, 1)},
-                "reps": reps})
-    log(f"CPU baseline ({kind}): {t_single * 1e3:.0f} ms/token-layer at 1 thread, "
-        f"{t_multi * 1e3:.0f} ms at {cores} threads")
-    return out
+        t_deq, deq = timed(lambda: [lib.dequantize(*planes(ex0, m), *dims[m], cbf) for m in range(3)], 3)
+    deq_exact = all(np.array_equal(a.view(np.uint32), b.view(np.uint32)) for a, b in zip(deq, gpu["c1_dequant"]))
+    t_c1_1, _ = timed(lambda: ffn(ex0, x1, 1.0, np.zeros(H, np.float32), False), 5)
+    t_c1_n, _ = timed(lambda: ffn(ex0, x1, 1.0, np.zeros(H, np.float32), True), 5)
+    # C2 (layer 0) at 1 and all threads, C5's last layer
+    s0, w0 = gpu["routes1"][0][0][0], gpu["routes1"][0][1][0]
+    t_c2_1, y_c2 = timed(lambda: token(x1, s0, w0, False), 3)
+    t_c2_n, _ = timed(lambda: token(x1, s0, w0, True), 5)
+    sl, wl = gpu["routes1"][L - 1][0][0], gpu["routes1"][L - 1][1][0]
+    t_c5_n, y_c5 = timed(lambda: token(x1, sl, wl, True), 3)
+    # C3: eight tokens of layer 0
+    s8, w8 = gpu["routes8"]
+    t_c3_n, y_c3 = timed(lambda: np.stack([token(gpu["x8"][t], s8[t], w8[t], True) for t in range(8)]), 2)
+    out = {"kind": kind, "unit": "GB/s",
+           "sample": "C2: 1 token x the 6 routed experts of layer 0 (one token-layer), all threads",
+           "cores": n_all, "cpu_model": cpu_model(), "hardware_concurrency": os.cpu_count(),
+           "value": round(6 * STRIDE / t_c2_n / 1e9, 3),
+           "ms_per_token_layer": round(t_c2_n * 1e3, 2),
+           "single_thread": {"value": round(6 * STRIDE / t_c2_1 / 1e9, 4), "cores": 1,
+                             "ms_per_token_layer": round(t_c2_1 * 1e3, 1)},
+           "c1": {"dequant_ms_1thread": round(t_deq * 1e3, 1),
+                  "dequant_gb_per_s_1thread": round(STRIDE / t_deq / 1e9, 3),
+                  "ffn_ms_1thread": round(t_c1_1 * 1e3, 2), "ffn_ms_all": round(t_c1_n * 1e3, 2),
+                  "ffn_gb_per_s_all": round(STRIDE / t_c1_n / 1e9, 3)},
+           "c3_ms_per_layer_all": round(t_c3_n * 1e3, 1),
+           "c5_ms_per_token_all": round(L * (t_c2_n + t_c5_n) / 2 * 1e3, 1)}
+    parity = {"c1_dequant_bit_exact": deq_exact,
+              "c2_layer0_rel_l2": rel_l2(gpu["y1"][0], y_c2),
+              f"c5_layer{L - 1}_rel_l2": rel_l2(gpu["y1"][L - 1], y_c5),
+              "c3_layer0_rel_l2": rel_l2(gpu["y8"], y_c3)}
+    msg = (f"CPU baseline ({kind}, {n_all} threads): C1 dequant {t_deq * 1e3:.0f} ms, C1 FFN "
+           f"{t_c1_1 * 1e3:.1f} / {t_c1_n * 1e3:.1f} ms; C2 {t_c2_1 * 1e3:.0f} / {t_c2_n * 1e3:.1f} ms per "
+           f"token-layer; C3 {t_c3_n * 1e3:.0f} ms per layer")
+    if "c4" in gpu:
+        sel_np, w_np, xs, yg, toks = gpu["c4"]
+        t0 = time.perf_counter()
+        yc = np.stack([token(xs[i], sel_np[t], w_np[t], True) for i, t in enumerate(toks)])
+        t_c4 = time.perf_counter() - t0
+        out["c4"] = {"tokens_timed": len(toks), "ms_sample": round(t_c4 * 1e3, 1),
+                     "ms_per_layer_extrapolated": round(t_c4 * 4096 / len(toks) * 1e3, 0),
+                     "note": "per-token GEMV path, 64 sampled tokens, extrapolated linearly to 4096"}
+        parity["c4_sample_rel_l2"] = rel_l2(yg, yc)
+        parity["c4_sample_worst_token_rel_l2"] = max(rel_l2(yg[i], yc[i]) for i in range(len(toks)))
+        msg += f"; C4 {len(toks)} tokens {t_c4:.1f} s"
+    parity = {k: (round(v, 9) if isinstance(v, float) else v) for k, v in parity.items()}
+    log(msg)
+    log(f"parity vs the CPU path: {parity}")
+    return out, parity
 
 
 if __name__ == "__main__":

@@ -67,7 +67,11 @@ typedef struct affx_layer {
   uint32_t n_experts;
   uint32_t hidden, inter;
   const void* codebook; /* device: uint32[2048] */
-  float swiglu_limit;   /* src/engine/model.h:52 (10 for V4-Flash); <= 0 disables the clamp */
+  float swiglu_limit;   /* the SwiGLU clamp L of src/engine/model.h:52 (10 for V4-Flash). Must be
+                           in (0, 1e6]: the kernels scale the SwiGLU output by 2^(7 - ilogb(L^2)),
+                           which needs the clamp's bound. The reference's "no clamp" (L <= 0,
+                           src/engine/ops.cpp:47-60) is declined (AFFX_DECLINED, nothing
+                           launched), so a caller without a clamp takes its own path. */
 } affx_layer;
 
 /* ---- library / device --------------------------------------------------------------------- */
@@ -121,6 +125,15 @@ int affx_dequant_matrix(const affx_matrix* m, const void* codebook, float* out, 
  * (and the workspace should then be zero-filled again). */
 size_t affx_decode_workspace_size(uint32_t m_tokens, uint32_t top_k, uint32_t hidden,
                                   uint32_t inter);
+
+/* Status of a decode workspace: AFFX_OK, or AFFX_ERR_DEVICE when a launch of
+ * affx_expert_ffn_decode on it gave up waiting for its workgroups (error word 2 nonzero; that
+ * launch's output was invalid). Copies 4 bytes to the host and synchronises `stream`. reset = 1
+ * also zeroes the workspace's sync run (counter, error bits, release flags), which a timed-out
+ * launch can leave raised. The counterpart of the reference's periodic device-status read that
+ * aborts the process on a bad dispatch (src/gpu/static_placement.hip:1939-1961); the engine hook
+ * affx_expert_ffn_batch makes this check itself after every decode call. */
+int affx_decode_status(void* workspace, int reset, void* stream);
 
 /* y[t] (+)= sum_j w[t][j] * FFN_{sel[t][j]}(x[t]) for t < m_tokens (<= 8), j < top_k.
  *  x: device f32, element (t, h) at x[t*x_tok_stride + h*x_dim_stride]; y likewise with
@@ -210,8 +223,9 @@ typedef struct affx_engine_ctx {
  * host arrays sel/w [nb_tok][k], runs them on the GPU into ctx->d_block, sets handled[b*k+j]=1
  * for each pair taken, returns the count. Padding ids >= n_experts are neither taken nor marked.
  * nb_tok <= 8 runs the decode path, larger batches the grouped path. Returns 0 (nothing taken)
- * on any error; affx_last_error() says why. Synchronises the stream before returning (the
- * routes arrive in host memory). */
+ * on any error, a decode whose workgroups gave up waiting for each other included (the hook
+ * then resets the workspace's sync run); affx_last_error() says why. Synchronises the stream
+ * before returning (the routes arrive in host memory). */
 uint32_t affx_expert_ffn_batch(void* ctx, uint32_t layer, const uint32_t* sel, const float* w,
                                uint32_t nb_tok, uint32_t k, uint8_t* handled);
 

@@ -236,6 +236,7 @@ class RefLib:
         L.affref_float_to_bf16.restype = C.c_uint16
         L.affref_expert_layout.argtypes = [C.c_uint64, C.c_uint64, _u64p, _u64p]
         L.affref_expert_layout.restype = C.c_uint64
+        L.affref_pool_threads.restype = C.c_uint
 
     def collect_samples(self, w: np.ndarray, budget: int) -> np.ndarray:
         rows, cols = w.shape
@@ -294,6 +295,10 @@ class RefLib:
                                            _p(np.ascontiguousarray(x, np.float32), _f32p), float(w),
                                            _p(y, _f32p), int(mt))
         return y
+
+    def pool_threads(self) -> int:
+        """Threads of the reference's global pool (hardware_concurrency), which the _mt GEMV uses."""
+        return int(self.lib.affref_pool_threads())
 
     def swiglu(self, g, u, limit=10.0) -> np.ndarray:
         out = np.empty_like(g, dtype=np.float32)

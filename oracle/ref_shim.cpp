@@ -12,6 +12,7 @@
 #include "format/aff_format.h"
 #include "engine/expert_kernel.h"
 #include "engine/ops.h"
+#include "engine/threadpool.h"
 
 #include <cstring>
 #include <vector>
@@ -153,5 +154,8 @@ uint64_t affref_expert_layout(uint64_t hidden, uint64_t inter, uint64_t* off9, u
   }
   return stride;
 }
+
+// src/engine/threadpool.cpp:122-131: the pool expert_gemv_scaled_mt runs on (hardware_concurrency)
+unsigned affref_pool_threads(void) { return global_pool().size(); }
 
 }  // extern "C"

@@ -6,6 +6,9 @@
 //   emu_main grouped hidden inter n_experts T K seed lo   -> rel_l2 of the grouped FFN
 //   emu_main quant   rows cols seed                       -> planes bit-exact vs the oracle
 //   emu_main dequant hidden inter seed                    -> dequant bit-exact vs the oracle
+//   emu_main timeout hidden inter n_experts M K seed      -> a decode whose waiters give up (spin
+//                    limit 0 from the host) fails the engine hook and affx_decode_status; after
+//                    the reset, the next calls are correct
 //
 // Exit status 0 when the check passes.
 #include <hip/hip_runtime.h>
@@ -20,6 +23,7 @@ thread_local EmuBlock* emu_blk;
 #include "../../affinity_amd/csrc/affx_fused.hip"
 #include "../../affinity_amd/csrc/affx_quant.hip"
 #include "../../affinity_amd/csrc/affx_grouped.hip"
+#include "../../affinity_amd/csrc/affx_api.hip"
 
 extern "C" {
 #include "../../oracle/oracle.h"
@@ -238,6 +242,70 @@ int run_dequant(int argc, char** argv) {
   return ok ? 0 : 1;
 }
 
+// The failure path of the fused decode's bounded wait, forced from the host: with
+// AFFX_DECODE_SPIN_LIMIT=0 every waiting workgroup gives up at once (no poll), sets the error
+// bit and runs on; every kernel still exits normally.
+int run_timeout(int argc, char** argv) {
+  const uint32_t hidden = atoi(argv[2]), inter = atoi(argv[3]), n = atoi(argv[4]), M = atoi(argv[5]),
+                 K = atoi(argv[6]);
+  std::mt19937_64 rng(atoi(argv[7]));
+  Layer L(hidden, inter, n, rng);
+  std::vector<float> x(M * hidden), yref(M * hidden, 0.f), w;
+  std::vector<uint32_t> sel;
+  std::normal_distribution<float> nd;
+  for (auto& v : x) v = 0.5f * nd(rng);
+  routes(rng, M, K, n, sel, w);
+  L.oracle(x.data(), sel.data(), w.data(), M, K, yref.data());
+  affx_layer abi = L.abi();
+  // the engine's arenas: d_x / d_block f32 [hidden][nb], tokens in columns
+  const uint32_t nb = 8;
+  std::vector<float> dx((size_t)hidden * nb, 0.f), db((size_t)hidden * nb, 0.f);
+  for (uint32_t h = 0; h < hidden; ++h)
+    for (uint32_t t = 0; t < M; ++t) dx[(size_t)h * nb + t] = x[(size_t)t * hidden + h];
+  const size_t wsb = affx_batch_workspace_size(M, K, n, hidden, inter);
+  std::vector<uint8_t> ws(wsb, 0);
+  affx_engine_ctx ctx{&abi, 1, dx.data(), db.data(), nb, ws.data(), wsb, nullptr};
+  std::vector<uint8_t> handled(M * K, 0);
+  auto sync_nonzero = [&]() {
+    uint32_t z = 0;
+    for (uint32_t i = 0; i < kSyncBytes; ++i) z += ws[i] != 0;
+    return z;
+  };
+  bool ok = true;
+  // 1. the hook: the wait gives up, the call fails (returns 0, marks nothing), the state is reset
+  setenv("AFFX_DECODE_SPIN_LIMIT", "0", 1);
+  uint32_t got = affx_expert_ffn_batch(&ctx, 0, sel.data(), w.data(), M, K, handled.data());
+  const std::string err = affx_last_error();
+  uint32_t marked = 0;
+  for (auto h : handled) marked += h;
+  printf("hook with spin limit 0: returned %u, marked %u, error \"%s\", sync bytes nonzero after %u\n", got,
+         marked, err.c_str(), sync_nonzero());
+  ok = ok && got == 0 && marked == 0 && err.find("gave up") != std::string::npos && sync_nonzero() == 0;
+  // 2. the direct entry: the launch itself returns OK (nothing is known before the kernel runs);
+  // affx_decode_status reports the failure, resets, then reports OK
+  std::vector<float> y(M * hidden, 0.f);
+  int rc = affx_expert_ffn_decode(&abi, x.data(), hidden, 1, M, sel.data(), w.data(), K, y.data(), hidden, 1, 0,
+                                  ws.data(), wsb, nullptr);
+  const int st1 = affx_decode_status(ws.data(), 1, nullptr);
+  const int st2 = affx_decode_status(ws.data(), 0, nullptr);
+  printf("direct with spin limit 0: rc=%d status=%d then %d\n", rc, st1, st2);
+  ok = ok && rc == 0 && st1 == AFFX_ERR_DEVICE && st2 == AFFX_OK;
+  // 3. normal waits again: the hook takes every pair and the result is right
+  unsetenv("AFFX_DECODE_SPIN_LIMIT");
+  std::fill(db.begin(), db.end(), 0.f);
+  std::fill(handled.begin(), handled.end(), 0);
+  got = affx_expert_ffn_batch(&ctx, 0, sel.data(), w.data(), M, K, handled.data());
+  std::vector<float> yd(M * hidden);
+  for (uint32_t h = 0; h < hidden; ++h)
+    for (uint32_t t = 0; t < M; ++t) yd[(size_t)t * hidden + h] = db[(size_t)h * nb + t];
+  const double e = rel_l2(yd, yref);
+  printf("hook after reset: returned %u of %u, rel_l2=%.3e, sync bytes nonzero %u, status %d\n", got, M * K, e,
+         sync_nonzero(), affx_decode_status(ws.data(), 0, nullptr));
+  ok = ok && got == M * K && e <= 1e-3 && sync_nonzero() == 0;
+  printf("timeout path ok=%d\n", (int)ok);
+  return ok ? 0 : 1;
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -248,6 +316,7 @@ int main(int argc, char** argv) {
   if (cmd == "grouped" && argc >= 8) return run_grouped(argc, argv);
   if (cmd == "quant" && argc >= 5) return run_quant(argc, argv);
   if (cmd == "dequant" && argc >= 5) return run_dequant(argc, argv);
+  if (cmd == "timeout" && argc >= 8) return run_timeout(argc, argv);
   fprintf(stderr, "usage: see header\n");
   return 2;
 }

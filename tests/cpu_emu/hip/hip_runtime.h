@@ -46,6 +46,9 @@ inline int hipGetDevice(int* d) { *d = 0; return 0; }
 struct hipDeviceProp_t { char gcnArchName[64]; int multiProcessorCount; };
 inline int hipGetDeviceProperties(hipDeviceProp_t* p, int) { strcpy(p->gcnArchName, "gfx950"); p->multiProcessorCount = 256; return 0; }
 inline int hipMemsetAsync(void* p, int v, size_t n, hipStream_t) { memset(p, v, n); return 0; }
+enum hipMemcpyKind { hipMemcpyHostToDevice = 1, hipMemcpyDeviceToHost = 2, hipMemcpyDeviceToDevice = 3 };
+inline int hipMemcpyAsync(void* d, const void* s, size_t n, hipMemcpyKind, hipStream_t) { memmove(d, s, n); return 0; }
+inline int hipStreamSynchronize(hipStream_t) { return 0; }  // launches run to completion
 // device shape of the emulation: AFFX_EMU_CUS compute units (default 4), one resident workgroup each
 inline int emu_cus() { const char* e = getenv("AFFX_EMU_CUS"); return e ? atoi(e) : 4; }
 enum { hipDeviceAttributeMultiprocessorCount = 1, hipFuncAttributeMaxDynamicSharedMemorySize = 2 };

@@ -38,3 +38,17 @@ def planes(expert: np.ndarray, layout, which: int):
     f = expert[off[3 * which + 1]:off[3 * which + 1] + size[3 * which + 1]]
     r = expert[off[3 * which + 2]:off[3 * which + 2] + size[3 * which + 2]].view(np.uint16)
     return np.ascontiguousarray(c), np.ascontiguousarray(f), np.ascontiguousarray(r)
+
+
+def oracle_ffn_tokens(orc, experts: dict, cb_f32, x: np.ndarray, sel: np.ndarray, w: np.ndarray,
+                      tokens, hidden: int, inter: int, limit: float = 10.0) -> np.ndarray:
+    """The CPU oracle on the given tokens: y[i] = sum_j w[t][j] FFN_{sel[t][j]}(x[t]) with
+    t = tokens[i]. experts: expert id -> container bytes (host); other ids are padding."""
+    y = np.zeros((len(tokens), hidden), np.float32)
+    for i, t in enumerate(tokens):
+        for j in range(sel.shape[1]):
+            e = int(sel[t, j])
+            if e in experts:
+                orc.expert_ffn(experts[e], cb_f32, np.ascontiguousarray(x[t], np.float32), float(w[t, j]),
+                               limit, y[i], hidden, inter)
+    return y

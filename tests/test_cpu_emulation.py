@@ -88,3 +88,10 @@ def test_quantizer_emulated(emu):
 
 def test_grouped_emulated(emu):
     assert "rel_l2" in run(emu, "grouped", 1024, 1024, 5, 12, 3, 4, 1, timeout=900)
+
+
+def test_decode_wait_give_up_fails_loudly(emu):
+    # the host forces the bounded wait to give up (no polls); the hook returns 0 with an error,
+    # affx_decode_status reports it, and after the reset the next call is right
+    out = run(emu, "timeout", 1024, 1024, 6, 2, 3, 8, cus=4)
+    assert "timeout path ok=1" in out, out

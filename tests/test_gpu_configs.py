@@ -1,0 +1,202 @@
+"""GPU parity on the benchmark configurations themselves, with the reference's own outputs.
+
+* Config 1: the expert the GPU quantiser produces (its planes hash-pinned to the reference's)
+  goes through every entry point of the path: dequant (bit-exact to the reference's hashes),
+  the one-launch decode, the staged decode, the grouped prefill (bf16 and hi/lo inputs) and the
+  engine hook (decode and grouped arms). Each output is compared with c1_ffn_y.bin, which the
+  compiled reference wrote.
+* Config 2 / 3: batch-1 and M = 8 decode on the quantised 256-expert layer with the configs'
+  softmax top-6 routes, against the oracle.
+* Config 4: the full prefill shape (4096 tokens, 256 experts, Zipf(1.1) routes) with a bf16 and
+  with a hi/lo input; a 64-token subsample that covers the head expert's first, middle and last
+  tiles and the 1-token tail tiles is compared with the oracle.
+"""
+import ctypes as C
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+
+from gpu_util import bf16_bits, oracle_ffn_tokens, rel_l2
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+H, I, E, K = 4096, 2048, 256, 6
+
+
+def sha(a) -> str:
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+@pytest.fixture(scope="module")
+def ax():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import affinity_amd.experts as ax
+    ax.init()
+    return ax
+
+
+@pytest.fixture(scope="module")
+def manifest():
+    return json.load(open(os.path.join(GOLDEN, "c1_manifest.json")))
+
+
+@pytest.fixture(scope="module")
+def fixture_y():
+    return np.fromfile(os.path.join(GOLDEN, "c1_ffn_y.bin"), dtype="<f4")
+
+
+@pytest.fixture(scope="module")
+def layer(ax, c1_codebook):
+    """The config-2 layer quantised on the GPU: (container bytes on the device, device pool)."""
+    from affinity_amd import synthetic
+    cont = synthetic.build_layer_container(ax, torch)
+    pool = ax.ExpertPool.from_container(cont, c1_codebook)
+    torch.cuda.synchronize()
+    return cont, pool
+
+
+@pytest.fixture(scope="module")
+def c1_pool(ax, c1_codebook, layer):
+    """Expert 0 of the layer is the config-1 expert (seeds 1000, 1001, 1002)."""
+    cont, _ = layer
+    stride = ax.expert_layout()[0]
+    pool = ax.ExpertPool.from_container(cont[:stride], c1_codebook)
+    torch.cuda.synchronize()
+    return pool
+
+
+def test_config1_planes_are_the_reference_planes(ax, layer, manifest):
+    cont, _ = layer
+    stride, off, size = ax.expert_layout()
+    ex = cont[:stride].cpu().numpy()
+    for m, name in enumerate(("gate", "up", "down")):
+        for p, k in enumerate(("codes", "fields", "rscales")):
+            assert sha(ex[off[3 * m + p]:off[3 * m + p] + size[3 * m + p]]) == manifest["planes"][name][k], (name, k)
+
+
+def test_config1_dequant_bit_exact(ax, c1_pool, manifest):
+    for m, name in enumerate(("gate", "up", "down")):
+        assert sha(ax.dequant_matrix(c1_pool, 0, m).cpu().numpy()) == manifest["dequant"][name], name
+
+
+def _c1_x(ax, manifest):
+    x = ax.gen_normal(7, H, 1.0)
+    assert sha(x.cpu().numpy()) == manifest["inputs"]["x"]
+    return x
+
+
+@pytest.mark.parametrize("staged", [False, True])
+def test_config1_decode_matches_reference_output(ax, c1_pool, manifest, fixture_y, staged):
+    x = _c1_x(ax, manifest).view(1, H)
+    sel = torch.zeros((1, 1), dtype=torch.int32, device="cuda")
+    w = torch.ones((1, 1), device="cuda")
+    ws = ax.DecodeWorkspace(1, 1)
+    y = ax.expert_ffn_decode(c1_pool, x, sel, w, workspace=ws, staged=staged)
+    torch.cuda.synchronize()
+    err = rel_l2(y.cpu().numpy()[0], fixture_y)
+    print(f"config 1 decode (staged={staged}) rel_l2={err:.3e}")
+    assert err <= TOL
+    assert ws.status() == 0
+
+
+@pytest.mark.parametrize("lo", [False, True])
+def test_config1_grouped_matches_reference_output(ax, c1_pool, manifest, fixture_y, lo):
+    """Five copies of the token (one tile), bf16 x exact; with a zero low term the 3-term path."""
+    x = _c1_x(ax, manifest)
+    xb = x.to(torch.bfloat16).view(1, H).repeat(5, 1).contiguous()
+    assert torch.equal(xb.float()[0], x)
+    xl = torch.zeros_like(xb) if lo else None
+    sel = torch.zeros((5, 1), dtype=torch.int32, device="cuda")
+    w = torch.ones((5, 1), device="cuda")
+    y = ax.expert_ffn_grouped(c1_pool, xb, sel, w, x_lo=xl).cpu().numpy()
+    for t in range(5):
+        err = rel_l2(y[t], fixture_y)
+        assert err <= TOL, (t, err)
+    print(f"config 1 grouped (lo={lo}) rel_l2={rel_l2(y[0], fixture_y):.3e}")
+
+
+@pytest.mark.parametrize("nb", [1, 9])
+def test_config1_engine_hook_matches_reference_output(ax, c1_pool, manifest, fixture_y, nb):
+    """The ExpertFfnBatch hook with the engine's dim-major arenas: nb = 1 takes the decode arm,
+    nb = 9 the grouped arm; every token is the config-1 token routed to the config-1 expert."""
+    from affinity_amd._lib import AffxEngineCtx, lib, last_error
+    x = _c1_x(ax, manifest)
+    nbs = 16
+    dx = torch.zeros((H, nbs), device="cuda")
+    dx[:, :nb] = x.view(H, 1)
+    db = torch.zeros((H, nbs), device="cuda")
+    wsb = lib().affx_batch_workspace_size(nb, 1, 1, H, I)
+    ws = torch.zeros(wsb, dtype=torch.uint8, device="cuda")
+    L = c1_pool.layer()
+    ctx = AffxEngineCtx(C.pointer(L), 1, dx.data_ptr(), db.data_ptr(), nbs, ws.data_ptr(), wsb,
+                        torch.cuda.current_stream().cuda_stream)
+    sel = np.zeros(nb, np.uint32)
+    w = np.ones(nb, np.float32)
+    handled = np.zeros(nb, np.uint8)
+    n = lib().affx_expert_ffn_batch(C.addressof(ctx), 0, sel.ctypes.data, w.ctypes.data, nb, 1, handled.ctypes.data)
+    assert n == nb, last_error()
+    got = db.cpu().numpy()
+    for t in range(nb):
+        assert rel_l2(got[:, t], fixture_y) <= TOL, t
+    np.testing.assert_array_equal(got[:, nb:], 0.0)
+
+
+def _container_experts(ax, cont, ids):
+    from affinity_amd import synthetic
+    stride = ax.expert_layout()[0]
+    return {int(e): synthetic.expert_bytes(cont, int(e), stride) for e in sorted(set(int(v) for v in ids))}
+
+
+@pytest.mark.parametrize("M", [1, 8])
+def test_config2_config3_decode_vs_oracle(ax, orc, c1_codebook, layer, M):
+    """Config 2 (M = 1) and config 3 (M = 8): seeded N(0,1) router logits, softmax top-6."""
+    from affinity_amd import synthetic
+    cont, pool = layer
+    x = ax.gen_normal(synthetic.S_X, M * H, 1.0).view(M, H)
+    lg = ax.gen_normal(synthetic.S_R, 8 * E, 1.0, bf16_round=False).view(8, E)[:M]
+    sel, w = synthetic.softmax_topk(lg, K)
+    ws = ax.DecodeWorkspace(M, K)
+    y = ax.expert_ffn_decode(pool, x, sel, w, workspace=ws).cpu().numpy()
+    assert ws.status() == 0
+    sel_np, w_np = sel.cpu().numpy(), w.cpu().numpy()
+    experts = _container_experts(ax, cont, sel_np.reshape(-1))
+    ref = oracle_ffn_tokens(orc, experts, orc.unpack_codebook(c1_codebook), x.cpu().numpy(), sel_np, w_np,
+                            range(M), H, I)
+    err = rel_l2(y, ref)
+    print(f"config {2 if M == 1 else 3}: {len(experts)} distinct experts, rel_l2={err:.3e}")
+    assert err <= TOL
+    for t in range(M):
+        assert rel_l2(y[t], ref[t]) <= TOL, t
+
+
+@pytest.mark.parametrize("lo", [False, True])
+def test_config4_full_shape_subsample_vs_oracle(ax, orc, c1_codebook, layer, lo):
+    """The full prefill: 4096 tokens, Zipf(1.1) top-6 of 256 experts. lo = False: x is bf16
+    N(0,1) (two E4M3 terms); lo = True: x is an f32 N(0,1) carried as a bf16 hi/lo pair (three
+    terms, the engine hook's form). 64 sampled tokens against the oracle, each token and all."""
+    from affinity_amd import synthetic
+    cont, pool = layer
+    T = 4096
+    sel, w = synthetic.zipf_routes(T)
+    xf = ax.gen_normal(synthetic.S_X, T * H, 1.0, bf16_round=not lo).view(T, H)
+    hi = xf.to(torch.bfloat16)
+    xl = (xf - hi.float()).to(torch.bfloat16) if lo else None
+    y = ax.expert_ffn_grouped(pool, hi.contiguous(), torch.from_numpy(sel).cuda(), torch.from_numpy(w).cuda(),
+                              x_lo=xl).cpu().numpy()
+    toks, head, head_n = synthetic.prefill_sample(sel, E)
+    xr = (hi.float() + (xl.float() if lo else 0)).cpu().numpy()
+    experts = _container_experts(ax, cont, sel[toks].reshape(-1))
+    ref = oracle_ffn_tokens(orc, experts, orc.unpack_codebook(c1_codebook), xr, sel, w, toks, H, I)
+    err = rel_l2(y[toks], ref)
+    worst = max(rel_l2(y[t], ref[i]) for i, t in enumerate(toks))
+    print(f"config 4 (lo={lo}): head expert {head} with {head_n} tokens, {len(toks)} sampled tokens, "
+          f"{len(experts)} experts: rel_l2={err:.3e}, worst token {worst:.3e}")
+    assert err <= TOL and worst <= TOL
+    assert np.isfinite(y).all()

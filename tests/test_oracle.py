@@ -291,6 +291,35 @@ def test_config1_dequant_and_ffn_match_reference(orc, c1_planes, manifest):
     np.testing.assert_array_equal(y, np.fromfile(os.path.join(GOLDEN, "c1_ffn_y.bin"), dtype="<f4"))
 
 
+def _c1_container(orc, q):
+    """The config-1 expert in container layout: the nine planes at orc_expert_layout's offsets."""
+    stride, off, size = orc.expert_layout(H, I)
+    ex = np.zeros(stride, np.uint8)
+    for m, name in enumerate(("gate", "up", "down")):
+        for p in range(3):
+            b = np.ascontiguousarray(q[name][p]).view(np.uint8).reshape(-1)
+            assert b.size == size[3 * m + p]
+            ex[off[3 * m + p]:off[3 * m + p] + b.size] = b
+    return ex
+
+
+def test_config1_expert_ffn_matches_reference(orc, c1_planes):
+    """orc_expert_ffn, the checker of every GPU FFN test, reproduces the reference-written config-1
+    output bit for bit from the container expert (plane order, where the route weight is applied,
+    the clamp: src/engine/model.cpp:1187-1198 over expert_gemv_scaled_mt and swiglu). With a
+    route weight w and a nonzero y it adds w * tmp per element, as expert_gemv_scaled does
+    (src/engine/expert_kernel.cpp:126-139)."""
+    cb, q = c1_planes
+    ex = _c1_container(orc, q)
+    x = orc.normal_bf16(7, H, 1.0)
+    fixture = np.fromfile(os.path.join(GOLDEN, "c1_ffn_y.bin"), dtype="<f4")
+    y = orc.expert_ffn(ex, cb, x, 1.0, 10.0)
+    np.testing.assert_array_equal(y.view(np.uint32), fixture.view(np.uint32))
+    y0 = np.linspace(-3, 3, H).astype(np.float32)
+    y2 = orc.expert_ffn(ex, cb, x, 0.375, 10.0, y0.copy())
+    np.testing.assert_array_equal(y2.view(np.uint32), (y0 + np.float32(0.375) * fixture).view(np.uint32))
+
+
 def _numpy_dequant(codes, fields, rs, rows, cols, cb):
     """Independent statement of the format: 10-bit codes and 6-bit fields LSB-first; field bits
     [0..2] s, [3] sign, [4] rotate, [5] variant; w = rs * 2^s * (+-1) * e[v][code][(p+rh)%4]."""
