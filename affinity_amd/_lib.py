@@ -55,6 +55,8 @@ _SIGS = {
     "affx_decode_status": ([_vp, C.c_int, _vp], C.c_int),
     "affx_expert_ffn_decode": ([C.POINTER(AffxLayer), _vp, _u64, _u64, _u32, _vp, _vp, _u32, _vp,
                                 _u64, _u64, C.c_int, _vp, C.c_size_t, _vp], C.c_int),
+    "affx_expert_ffn_decode_noalloc": ([C.POINTER(AffxLayer), _vp, _u64, _u64, _u32, _vp, _vp, _u32, _vp,
+                                        _u64, _u64, C.c_int, _vp], C.c_int),
     "affx_decode_prepare": ([C.POINTER(AffxLayer), _vp, _u64, _u64, _u32, _vp, _vp, _u32, _vp, C.c_size_t,
                              _vp], C.c_int),
     "affx_decode_gateup": ([C.POINTER(AffxLayer), _u32, _u32, _vp, C.c_size_t, _vp], C.c_int),

@@ -104,6 +104,9 @@ DecodeWs decode_ws(uint32_t M, uint32_t K, uint32_t hidden, uint32_t inter);
 int decode_check(const affx_layer* L, uint32_t M, uint32_t K, const void* ws, size_t ws_bytes,
                  DecodeWs* lay);
 
+// Set-up of the allocation-free decode's scratch array on device `dev` (current), from affx_init.
+int noalloc_init_device(int dev);
+
 // ---- status ------------------------------------------------------------------------------------
 int set_error(int code, const char* fmt, ...);
 int check_hip(hipError_t e, const char* what);

@@ -253,7 +253,7 @@ int affx_init(void) {
     return set_error(AFFX_ERR_DEVICE, "device %d is %s, this library is built for gfx950", dev,
                      p.gcnArchName);
   g_cus = p.multiProcessorCount;
-  return AFFX_OK;
+  return noalloc_init_device(dev);
 }
 
 uint64_t affx_expert_layout(uint64_t hidden, uint64_t inter, uint64_t off9[9], uint64_t size9[9]) {

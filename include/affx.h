@@ -155,6 +155,20 @@ int affx_expert_ffn_decode(const affx_layer* layer, const float* x, uint64_t x_t
                            uint64_t y_dim_stride, int accumulate, void* workspace,
                            size_t workspace_bytes, void* stream);
 
+/* affx_expert_ffn_decode for callers that cannot allocate: code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc. No counterpart in the reference (its decode
+ * takes caller-owned scratch). Same arguments without the workspace: the library keeps it in a
+ * static device array of 3.25 MiB per GPU (held until the process ends), set up by affx_init (or
+ * by the first call on a device) and shared by every call on that GPU, so calls that overlap on
+ * one GPU (other streams, other threads) race. Serves m_tokens <= 8, m_tokens * top_k <= 64,
+ * hidden <= 4096, inter <= 2048; larger sizes return AFFX_ERR_ARG with a message. Calls no
+ * hipMalloc, hipFree or allocating routine. affx_decode_status does not see its array: a wait
+ * that gave up is invisible here (the workspace entry reports it). */
+int affx_expert_ffn_decode_noalloc(const affx_layer* layer, const float* x, uint64_t x_tok_stride,
+                                   uint64_t x_dim_stride, uint32_t m_tokens, const uint32_t* sel,
+                                   const float* w, uint32_t top_k, float* y, uint64_t y_tok_stride,
+                                   uint64_t y_dim_stride, int accumulate, void* stream);
+
 /* The same three steps as separate stream-ordered calls (same workspace, same arguments), for
  * callers that interleave other work or time the stages, as the reference's GPU FFN is three
  * launches: activation prep + routing plan (batch_quant_fp8_hip, src/gpu/batch_kernels.h:124;

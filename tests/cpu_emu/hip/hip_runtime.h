@@ -49,6 +49,8 @@ inline int hipMemsetAsync(void* p, int v, size_t n, hipStream_t) { memset(p, v, 
 enum hipMemcpyKind { hipMemcpyHostToDevice = 1, hipMemcpyDeviceToHost = 2, hipMemcpyDeviceToDevice = 3 };
 inline int hipMemcpyAsync(void* d, const void* s, size_t n, hipMemcpyKind, hipStream_t) { memmove(d, s, n); return 0; }
 inline int hipStreamSynchronize(hipStream_t) { return 0; }  // launches run to completion
+#define HIP_SYMBOL(x) (&(x))
+inline int hipGetSymbolAddress(void** p, const void* sym) { *p = const_cast<void*>(sym); return 0; }
 // device shape of the emulation: AFFX_EMU_CUS compute units (default 4), one resident workgroup each
 inline int emu_cus() { const char* e = getenv("AFFX_EMU_CUS"); return e ? atoi(e) : 4; }
 enum { hipDeviceAttributeMultiprocessorCount = 1, hipFuncAttributeMaxDynamicSharedMemorySize = 2 };
