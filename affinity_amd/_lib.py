@@ -9,6 +9,8 @@ LIB_PATH = os.path.join(HERE, "libaffx.so")
 
 AFFX_OK = 0
 AFFX_DECLINED = 1
+AFFX_ROUTE_ENGINE = 0
+AFFX_ROUTE_SOFTMAX = 1
 AFFX_ERR_ARG = -1
 AFFX_ERR_DEVICE = -3
 
@@ -20,6 +22,10 @@ _u64p = C.POINTER(C.c_uint64)
 
 class AffxMatrix(C.Structure):
     _fields_ = [("codes", _vp), ("fields", _vp), ("rscales", _vp), ("rows", _u32), ("cols", _u32)]
+
+
+class AffxDeviceExpert(C.Structure):
+    _fields_ = [("gate", AffxMatrix), ("up", AffxMatrix), ("down", AffxMatrix)]
 
 
 class AffxLayer(C.Structure):
@@ -49,7 +55,16 @@ _SIGS = {
     "affx_codebook_valid": ([_vp], C.c_int),
     "affx_expert_to_device_layout": ([_vp, _vp, _u64, _u64], C.c_int),
     "affx_expert_from_device_layout": ([_vp, _vp, _u64, _u64], C.c_int),
+    "affx_matrix_to_device_layout": ([_vp, _vp, _vp, _vp, _u32, _u32], C.c_int),
+    "affx_expert_ffn": ([C.POINTER(AffxDeviceExpert), _vp, _u32, _vp, _vp, C.c_float, _vp, _vp, _vp], C.c_int),
     "affx_permute_experts": ([_vp, _vp, _u64, _u64, _u64, _vp], C.c_int),
+    "affx_container_open": ([C.c_char_p, C.POINTER(_vp)], C.c_int),
+    "affx_container_close": ([_vp], None),
+    "affx_container_layer_count": ([_vp], _u32),
+    "affx_container_layer": ([_vp, _u32, C.POINTER(_u32), _u64p, _u64p, _u64p], C.c_int),
+    "affx_container_expert_ptr": ([_vp, _u32, _u32], _vp),
+    "affx_container_codebook": ([_vp, _vp], C.c_int),
+    "affx_container_upload_layer": ([_vp, _u32, _vp, _vp, _vp], C.c_int),
     "affx_dequant_matrix": ([C.POINTER(AffxMatrix), _vp, _vp, _vp], C.c_int),
     "affx_decode_workspace_size": ([_u32, _u32, _u32, _u32], C.c_size_t),
     "affx_decode_status": ([_vp, C.c_int, _vp], C.c_int),
@@ -67,6 +82,10 @@ _SIGS = {
     "affx_grouped_workspace_size": ([_u32, _u32, _u32, _u32, _u32], C.c_size_t),
     "affx_expert_ffn_grouped": ([C.POINTER(AffxLayer), _vp, _vp, _u32, _vp, _vp, _u32, _vp, C.c_int,
                                  _vp, C.c_size_t, _vp], C.c_int),
+    "affx_expert_ffn_grouped_slots": ([C.POINTER(AffxLayer), _vp, _vp, _u32, _vp, _vp, _vp, _vp, _vp, _u32, _vp,
+                                       C.c_int, _vp, C.c_size_t, _vp], C.c_int),
+    "affx_route_topk": ([_vp, _u64, _u64, _vp, _u32, _u32, _u32, C.c_int, C.c_int, C.c_float, _vp, _vp, _vp],
+                        C.c_int),
     "affx_expert_ffn_batch": ([_vp, _u32, _vp, _vp, _u32, _u32, _vp], _u32),
     "affx_batch_workspace_size": ([_u32, _u32, _u32, _u32, _u32], C.c_size_t),
     "affx_selftest_mfma_fp8": ([_vp, _vp, _vp, _vp], C.c_int),

@@ -23,10 +23,17 @@
 
 namespace affx {
 
+// Experts of the pointer-table form (the reference's DeviceExpert arrays): at most this many.
+constexpr uint32_t kTblMax = 16;
+
 struct DecodeArgs {
   const uint8_t* base;  // layer expert pool, device layout
   uint64_t stride;
   uint64_t off[9];      // plane offsets inside an expert
+  // Pointer-table form: n_tbl > 0 means expert e's plane p is at tbl[e][p] (any device addresses,
+  // each plane in device layout) instead of base + e * stride + off[p].
+  uint32_t n_tbl;
+  const uint8_t* tbl[kTblMax][9];
   uint32_t hidden, inter, m_tokens;
   const uint32_t* codebook;
   const DecodePlan* plan;
@@ -39,6 +46,12 @@ struct DecodeArgs {
   uint64_t y_ts, y_ds;
   int accumulate;
 };
+
+// Plane p of expert e (e uniform across the wave: a scalar load from the kernel arguments in the
+// pointer-table form).
+__device__ __forceinline__ const uint8_t* plane_ptr(const DecodeArgs& A, uint32_t e, int p) {
+  return A.n_tbl ? A.tbl[e < kTblMax ? e : 0][p] : A.base + (uint64_t)e * A.stride + A.off[p];
+}
 
 // ------------------------------------------------------------------------------------------------
 // prep: blocks 0 .. M*nst-1 split one (token, 1024-column super-segment) of the activation into
@@ -98,7 +111,7 @@ __global__ void __launch_bounds__(256) decode_prep_kernel(const float* __restric
   if (tid < 64) reinterpret_cast<uint32_t*>(zeros)[tid] = 0u;  // the B source of unused columns
   const uint32_t R = M * K;
   if (tid < R) {
-    const uint32_t e = sel[tid];
+    const uint32_t e = sel ? sel[tid] : tid;  // no route list: route j names expert j
     sel_l[tid] = e < n_experts ? e : ~0u;
   }
   __syncthreads();
@@ -164,7 +177,6 @@ __global__ void __launch_bounds__(256) decode_gateup_kernel(DecodeArgs A) {
   if (slot >= A.plan->n_slots) return;
   const uint32_t rt = blockIdx.x, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const uint32_t e = A.plan->expert[slot], mask = A.plan->tok_mask[slot], M = A.m_tokens;
-  const uint8_t* ex = A.base + (uint64_t)e * A.stride;
   const uint32_t nst = A.hidden / kTileCols;
 
   __shared__ uint32_t tbl[4 * kLut];
@@ -182,8 +194,8 @@ __global__ void __launch_bounds__(256) decode_gateup_kernel(DecodeArgs A) {
   Unit ug, uu;
   if (S < nst) {
     const uint64_t tile = (uint64_t)rt * nst + S;
-    load_unit(ug, ex + A.off[kGateCodes], ex + A.off[kGateFields], tile, lane);
-    load_unit(uu, ex + A.off[kUpCodes], ex + A.off[kUpFields], tile, lane);
+    load_unit(ug, plane_ptr(A, e, kGateCodes), plane_ptr(A, e, kGateFields), tile, lane);
+    load_unit(uu, plane_ptr(A, e, kUpCodes), plane_ptr(A, e, kUpFields), tile, lane);
   }
   build_table(tbl, A.codebook);
   __syncthreads();
@@ -254,8 +266,8 @@ __global__ void __launch_bounds__(256) decode_gateup_kernel(DecodeArgs A) {
         s[m] = sum;
       }
       const uint32_t row = rt * 16 + r;
-      const float rg = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(ex + A.off[kGateRs])[row] << 16);
-      const float ru = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(ex + A.off[kUpRs])[row] << 16);
+      const float rg = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(plane_ptr(A, e, kGateRs))[row] << 16);
+      const float ru = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(plane_ptr(A, e, kUpRs))[row] << 16);
       float g = s[0] * rg;
       float u = s[1] * ru;
       // SwiGLU with the asymmetric clamp: src/engine/ops.cpp:47-60
@@ -305,8 +317,8 @@ __global__ void __launch_bounds__(kDownWaves * 64) decode_down_kernel(DecodeArgs
   Unit cur;
   if (wv < units) {
     const uint32_t slot = wv / nst, S = wv % nst;
-    const uint8_t* ex = A.base + (uint64_t)A.plan->expert[slot] * A.stride;
-    load_unit(cur, ex + A.off[kDownCodes], ex + A.off[kDownFields], (uint64_t)rt * nst + S, lane);
+    const uint32_t e0 = A.plan->expert[slot];
+    load_unit(cur, plane_ptr(A, e0, kDownCodes), plane_ptr(A, e0, kDownFields), (uint64_t)rt * nst + S, lane);
   }
   build_table(tbl, A.codebook);
   __syncthreads();
@@ -315,11 +327,11 @@ __global__ void __launch_bounds__(kDownWaves * 64) decode_down_kernel(DecodeArgs
   for (uint32_t u = wv; u < (SINGLE ? (wv < units ? wv + 1 : 0) : units); u += kDownWaves) {
     const uint32_t slot = u / nst, S = u % nst;
     const uint32_t e = A.plan->expert[slot], mask = A.plan->tok_mask[slot];
-    const uint8_t* ex = A.base + (uint64_t)e * A.stride;
-    if (!SINGLE && u != wv) load_unit(cur, ex + A.off[kDownCodes], ex + A.off[kDownFields], (uint64_t)rt * nst + S, lane);
+    if (!SINGLE && u != wv)
+      load_unit(cur, plane_ptr(A, e, kDownCodes), plane_ptr(A, e, kDownFields), (uint64_t)rt * nst + S, lane);
     const BSrc<CG> b = b_source<CG>(A.aq + (uint64_t)slot * M * kTerms * A.inter, A.inter,
                                     (uint64_t)S * kTileCols, lane, M, mask, A.zeros);
-    const uint2 rsv = *reinterpret_cast<const uint2*>(ex + A.off[kDownRs] + (uint64_t)(rt * 16 + 4 * rg) * 2);
+    const uint2 rsv = *reinterpret_cast<const uint2*>(plane_ptr(A, e, kDownRs) + (uint64_t)(rt * 16 + 4 * rg) * 2);
     __builtin_amdgcn_sched_barrier(0);
     v4f acc[CG];
 #pragma unroll
@@ -460,6 +472,7 @@ int decode_setup(const affx_layer* L, uint32_t M, uint32_t K, void* ws, size_t w
   A->limit = L->swiglu_limit;
   // |SwiGLU| <= L * L under the clamp; scale so that it stays below 256 < 448
   A->sigma_a = 7 - ilogbf(L->swiglu_limit * L->swiglu_limit);
+  A->n_tbl = 0;
   A->y = nullptr;
   A->y_ts = A->y_ds = 0;
   A->accumulate = 0;
@@ -533,6 +546,76 @@ int affx_decode_staged(const affx_layer* L, const float* x, uint64_t x_ts, uint6
   rc = affx_decode_gateup(L, M, K, ws, ws_bytes, stream);
   if (rc) return rc;
   return affx_decode_down(L, M, K, y, y_ts, y_ds, accumulate, ws, ws_bytes, stream);
+}
+
+// expert_ffn_hip's arguments (src/gpu/expert_kernel_hip.h:273): one token through n experts given
+// as a host array of per-matrix device pointers, out += sum_k weights[k] * FFN_k(x). The staged
+// kernels with the plane-pointer table in their arguments and route k = expert k; no cross-workgroup
+// state, so the caller's scratch needs no clearing. Its layout: [plan][zeros][xq][aq].
+int affx_expert_ffn(const affx_device_expert* experts, const float* weights, uint32_t n,
+                    const void* codebook, const float* x, float swiglu_limit, float* scratch, float* out,
+                    void* stream) {
+  if (n == 0) return AFFX_OK;
+  if (!experts || !weights || !codebook || !x || !scratch || !out)
+    return set_error(AFFX_ERR_ARG, "expert_ffn: null pointer");
+  if (n > kTblMax) return set_error(AFFX_DECLINED, "expert_ffn: at most %u experts per call (got %u)", kTblMax, n);
+  const uint32_t inter = experts[0].gate.rows, hidden = experts[0].gate.cols;
+  if (hidden % kTileCols || inter % kTileCols || hidden == 0 || inter == 0 || hidden > 4 * kTileCols)
+    return set_error(AFFX_DECLINED, "expert_ffn: hidden must be 1024..4096 and inter a multiple of 1024 "
+                     "(got %u, %u)", hidden, inter);
+  if (!(swiglu_limit > 0.f) || swiglu_limit > 1e6f)
+    return set_error(AFFX_DECLINED, "expert_ffn: needs a SwiGLU clamp limit in (0, 1e6]");
+  DecodeArgs A{};
+  A.n_tbl = n;
+  for (uint32_t k = 0; k < n; ++k) {
+    const affx_matrix* m[3] = {&experts[k].gate, &experts[k].up, &experts[k].down};
+    for (int i = 0; i < 3; ++i) {
+      const uint32_t rows = i < 2 ? inter : hidden, cols = i < 2 ? hidden : inter;
+      if (m[i]->rows != rows || m[i]->cols != cols || !m[i]->codes || !m[i]->fields || !m[i]->rscales)
+        return set_error(AFFX_ERR_ARG, "expert_ffn: expert %u matrix %d is %ux%u, expected %ux%u with planes", k, i,
+                         m[i]->rows, m[i]->cols, rows, cols);
+      A.tbl[k][3 * i + 0] = (const uint8_t*)m[i]->codes;
+      A.tbl[k][3 * i + 1] = (const uint8_t*)m[i]->fields;
+      A.tbl[k][3 * i + 2] = (const uint8_t*)m[i]->rscales;
+    }
+  }
+  // scratch: the reference's contract is 2 * n * inter floats
+  const uint64_t plan = 0, zeros = a256(sizeof(DecodePlan)), xq = zeros + 256, aq = xq + a256(3ull * hidden);
+  const uint64_t need = aq + 3ull * n * inter, have = 8ull * n * inter;
+  if (need > have)
+    return set_error(AFFX_DECLINED, "expert_ffn: needs %llu bytes of scratch, the 2 * n * inter floats hold %llu",
+                     (unsigned long long)need, (unsigned long long)have);
+  uint8_t* ws = (uint8_t*)scratch;
+  A.base = nullptr;
+  A.stride = 0;
+  A.hidden = hidden;
+  A.inter = inter;
+  A.m_tokens = 1;
+  A.codebook = (const uint32_t*)codebook;
+  A.plan = (const DecodePlan*)(ws + plan);
+  A.xq = ws + xq;
+  A.aq = ws + aq;
+  A.zeros = ws + zeros;
+  A.limit = swiglu_limit;
+  A.sigma_a = 7 - ilogbf(swiglu_limit * swiglu_limit);
+  A.y = out;
+  A.y_ts = hidden;
+  A.y_ds = 1;
+  A.accumulate = 1;
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(decode_prep_kernel, dim3(hidden / kTileCols + 1), dim3(256), 0, st, x, (uint64_t)hidden,
+                     (uint64_t)1, 1u, (const uint32_t*)nullptr, weights, n, n, hidden, (DecodePlan*)(ws + plan),
+                     ws + xq, ws + zeros);
+  int rc = check_launch("decode_prep_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL(decode_gateup_kernel<1>, dim3(inter / kTileRows, n), dim3(256), 0, st, A);
+  if ((rc = check_launch("decode_gateup_kernel"))) return rc;
+  const uint32_t units = n * (inter / kTileCols);
+  if (units <= (uint32_t)kDownWaves)
+    hipLaunchKernelGGL((decode_down_kernel<1, true>), dim3(hidden / kTileRows), dim3(kDownWaves * 64), 0, st, A);
+  else
+    hipLaunchKernelGGL((decode_down_kernel<1, false>), dim3(hidden / kTileRows), dim3(kDownWaves * 64), 0, st, A);
+  return check_launch("decode_down_kernel");
 }
 
 }  // extern "C"

@@ -1,9 +1,12 @@
 // Prefill path: the routed experts of a whole chunk, grouped by expert (each expert's weights
 // are decoded once per tile of its tokens), on the fp8 MFMA.
 //
-//   grouped_plan     one workgroup: per-expert counts, exclusive scan, tile lists
+//   grouped_plan     one workgroup: per-expert counts (from the routes, or from a slot list the
+//                    caller built), exclusive scan, tile lists
+//   grouped_run      one workgroup: per-token prefix of valid routes (the slot list's `run`)
 //   grouped_place    one workgroup per expert: its (token, route) pairs in token order (stable),
-//                    so every slot and every output sum has a fixed order
+//                    so every slot and every output sum has a fixed order; writes the slot list
+//                    (token and weight per slot, `ord`: each token's slots in route order)
 //   grouped_prep_x   per token: exponent and E4M3 terms of the activation (2 terms for a bf16
 //                    input: exact for every element of at least 2^-13 of the token's largest
 //                    magnitude, where both terms are normal E4M3 numbers, and within 2^-20 of that
@@ -14,7 +17,7 @@
 //                    writes the activation as terms
 //   grouped_gemm<1>  down: (row block of 256 hidden rows, slot tile): 8 waves x 32 rows, same
 //                    structure over K = inter, writes each slot's unweighted down output z[slot]
-//   grouped_combine  y[t] (+)= sum_j w[t][j] * z[slot(t, j)] in route order
+//   grouped_combine  y[t] (+)= sum over token t's slots in `ord` order of wt[slot] * z[slot]
 //
 // Reference counterparts: run_batch_device's prefill arm (src/gpu/static_placement.hip:
 // 1348-1964): moe_plan_kernel (src/gpu/moe_plan.hip:116-380), batch_quant_fp8_kernel
@@ -34,6 +37,7 @@ struct GroupedHdr {
   uint32_t n_slots;
   uint32_t n_tiles1, n_tiles2;
   uint32_t tx;                     // activation terms of the gate/up input (2 or 3)
+  uint32_t bad;                    // a caller's slot list needed more tiles than it can hold
 };
 
 // ------------------------------------------------------------------------------------------------
@@ -69,14 +73,41 @@ __device__ __forceinline__ void plan_scan3(uint32_t (&v)[3], uint32_t* wsum, uin
   }
 }
 
+// start_in: a caller's slot list, expert e owning slots [start_in[e], start_in[e+1]) of n_slots_in
+// (each bound clamped to n_slots_in; a range that runs backwards is empty); null: count the routes.
 __global__ void __launch_bounds__(kPlanThreads) grouped_plan_kernel(
     const uint32_t* __restrict__ sel, uint32_t n_pairs, uint32_t n_experts, uint32_t tt1,
-    uint32_t tt2, uint32_t tx, GroupedHdr* __restrict__ hdr, uint32_t* __restrict__ offsets,
+    uint32_t tt2, uint32_t tx, const uint32_t* __restrict__ start_in, uint32_t n_slots_in,
+    uint32_t max_tiles1, uint32_t max_tiles2, GroupedHdr* __restrict__ hdr, uint32_t* __restrict__ offsets,
     Tile* __restrict__ tiles1, Tile* __restrict__ tiles2) {
   static_assert(AFFX_MAX_EXPERTS <= kPlanThreads, "one thread per expert in the scan");
   __shared__ uint32_t cnt[AFFX_MAX_EXPERTS];
   __shared__ uint32_t wsum[3 * (kPlanThreads / 64)];
   const uint32_t tid = threadIdx.x;
+  if (start_in) {
+    uint32_t c = 0, b0 = 0;
+    if (tid < n_experts) {
+      const uint32_t a = min(start_in[tid], n_slots_in), b = min(start_in[tid + 1], n_slots_in);
+      c = b > a ? b - a : 0u;
+      b0 = a;
+    }
+    uint32_t v[3] = {c, (c + tt1 - 1) / tt1, (c + tt2 - 1) / tt2}, tot[3];
+    plan_scan3(v, wsum, tot);
+    // overlapping ranges could ask for more tiles than the workspace holds: then no tile at all
+    const bool fits = tot[1] <= max_tiles1 && tot[2] <= max_tiles2;
+    if (fits && tid < n_experts) {
+      for (uint32_t k = 0; k * tt1 < c; ++k) tiles1[v[1] + k] = Tile{tid, b0 + k * tt1, min(tt1, c - k * tt1)};
+      for (uint32_t k = 0; k * tt2 < c; ++k) tiles2[v[2] + k] = Tile{tid, b0 + k * tt2, min(tt2, c - k * tt2)};
+    }
+    if (tid == 0) {
+      hdr->n_slots = n_slots_in;
+      hdr->n_tiles1 = fits ? tot[1] : 0u;
+      hdr->n_tiles2 = fits ? tot[2] : 0u;
+      hdr->tx = tx;
+      hdr->bad = fits ? 0u : 1u;
+    }
+    return;
+  }
   for (uint32_t e = tid; e < AFFX_MAX_EXPERTS; e += kPlanThreads) cnt[e] = 0;
   __syncthreads();
   // counts per expert: eight routes per thread in flight at a time
@@ -108,7 +139,28 @@ __global__ void __launch_bounds__(kPlanThreads) grouped_plan_kernel(
     hdr->n_tiles1 = tot[1];
     hdr->n_tiles2 = tot[2];
     hdr->tx = tx;
+    hdr->bad = 0;
   }
+}
+
+// run[t] = number of routes of tokens before t that name an expert of the layer (run[n_tok] = all
+// of them): one workgroup, each thread a contiguous run of tokens.
+__global__ void __launch_bounds__(kPlanThreads) grouped_run_kernel(const uint32_t* __restrict__ sel,
+                                                                  uint32_t n_tok, uint32_t top_k,
+                                                                  uint32_t n_experts, uint32_t* __restrict__ run) {
+  __shared__ uint32_t wsum[3 * (kPlanThreads / 64)];
+  const uint32_t tid = threadIdx.x, per = (n_tok + kPlanThreads - 1) / kPlanThreads;
+  const uint32_t t0 = tid * per, t1 = min(n_tok, t0 + per);
+  uint32_t c = 0;
+  for (uint32_t i = t0 * top_k; i < t1 * top_k; ++i) c += sel[i] < n_experts ? 1u : 0u;
+  uint32_t v[3] = {c, 0u, 0u}, tot[3];
+  plan_scan3(v, wsum, tot);
+  uint32_t r = v[0];
+  for (uint32_t t = t0; t < t1; ++t) {
+    run[t] = r;
+    for (uint32_t j = 0; j < top_k; ++j) r += sel[t * top_k + j] < n_experts ? 1u : 0u;
+  }
+  if (tid == 0) run[n_tok] = tot[0];
 }
 
 // One workgroup per expert (plus the padding pass in workgroup n_experts): walks all pairs in
@@ -116,15 +168,10 @@ __global__ void __launch_bounds__(kPlanThreads) grouped_plan_kernel(
 // each 2048-pair block (so thread order is pair order), an exclusive scan of the match counts
 // places them; the next block's routes are loaded before this block is placed.
 __global__ void __launch_bounds__(256) grouped_place_kernel(
-    const uint32_t* __restrict__ sel, uint32_t n_pairs, uint32_t top_k, uint32_t n_experts,
-    const uint32_t* __restrict__ offsets, uint32_t* __restrict__ slot_tok,
-    int32_t* __restrict__ slot_of) {
+    const uint32_t* __restrict__ sel, const float* __restrict__ w, uint32_t n_pairs, uint32_t top_k,
+    uint32_t n_experts, const uint32_t* __restrict__ offsets, const uint32_t* __restrict__ run,
+    uint32_t* __restrict__ slot_tok, float* __restrict__ slot_w, uint32_t* __restrict__ ord) {
   const uint32_t e = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  if (e == n_experts) {
-    for (uint32_t i = tid; i < n_pairs; i += 256)
-      if (sel[i] >= n_experts) slot_of[i] = -1;
-    return;
-  }
   uint32_t base = offsets[e];
   const uint32_t end = offsets[e + 1];
   if (end == base) return;
@@ -160,9 +207,13 @@ __global__ void __launch_bounds__(256) grouped_place_kernel(
 #pragma unroll
     for (uint32_t k = 0; k < kPer; ++k)
       if ((m >> k) & 1u) {
-        const uint32_t i = i0 + tid * kPer + k;
-        slot_tok[pos] = i / top_k;
-        slot_of[i] = (int32_t)pos;
+        const uint32_t i = i0 + tid * kPer + k, t = i / top_k;
+        // the route's rank among its token's routes to the layer: its place in ord
+        uint32_t rank = 0;
+        for (uint32_t j = t * top_k; j < i; ++j) rank += sel[j] < n_experts ? 1u : 0u;
+        slot_tok[pos] = t;
+        slot_w[pos] = w[i];
+        ord[run[t] + rank] = pos;
         ++pos;
       }
     base += total;
@@ -187,8 +238,9 @@ __host__ __device__ inline uint32_t kperm(uint32_t col) {
 __global__ void __launch_bounds__(256) grouped_prep_x_kernel(const uint16_t* __restrict__ x,
                                                              const uint16_t* __restrict__ xlo,
                                                              uint32_t hidden, uint32_t tx,
-                                                             const int32_t* __restrict__ slot_of,
-                                                             uint32_t top_k,
+                                                             const uint32_t* __restrict__ ord,
+                                                             const uint32_t* __restrict__ run,
+                                                             uint32_t n_slots,
                                                              int32_t* __restrict__ slot_sigma,
                                                              uint8_t* __restrict__ xq,
                                                              uint32_t* __restrict__ zeros,
@@ -226,9 +278,12 @@ __global__ void __launch_bounds__(256) grouped_prep_x_kernel(const uint16_t* __r
   __syncthreads();
   amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const int sigma = amax > 0.f ? 7 - ilogbf(amax) : 0;
-  if (tid < top_k) {  // the exponent goes to each of the token's slots, for the gate/up epilogue
-    const int32_t sl = slot_of[t * top_k + tid];
-    if (sl >= 0) slot_sigma[sl] = sigma;
+  {  // the exponent goes to each of the token's slots, for the gate/up epilogue
+    const uint32_t r1 = min(run[t + 1], n_slots);
+    for (uint32_t i = min(run[t], r1) + tid; i < r1; i += 256) {
+      const uint32_t sl = ord[i];
+      if (sl < n_slots) slot_sigma[sl] = sigma;
+    }
   }
   // E4M3 terms, 8 bytes per term and chunk (8 consecutive columns stay consecutive in step order)
   uint8_t* row = xq + (uint64_t)t * tx * hidden;
@@ -288,6 +343,7 @@ struct GemmArgs {
   const Tile* tiles;
   uint32_t max_tiles;       // entries of tiles (allocated; the header says how many are used)
   const uint32_t* slot_tok;
+  uint32_t n_tok;             // tokens of the batch (a slot's token id is clamped below it)
   const int32_t* slot_sigma;  // activation exponent of the slot's token
   const uint8_t* ws;        // B rows and the zero row, addressed by 32-bit offsets from here
   uint64_t b_off, zero_off;
@@ -425,7 +481,7 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
   const uint32_t bcol_j = (tid >> 4) * TPG + (tid & 15u) / TX;
   auto brow_load = [&](const Tile& t) -> uint32_t {
     const uint32_t bslot = t.slot0 + ((tid < kGCols && (tid & 15u) < TX * TPG && bcol_j < t.n) ? bcol_j : 0u);
-    return PH == 0 ? A.slot_tok[bslot] : bslot;
+    return PH == 0 ? min(A.slot_tok[bslot], A.n_tok - 1u) : bslot;
   };
   auto rowoff_store = [&](const Tile& t, uint32_t brow) {
     const bool used = tid < kGCols && (tid & 15u) < TX * TPG && bcol_j < t.n;
@@ -780,21 +836,24 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
   }
 }
 
-// y[t][h] (+)= sum_j w[t][j] * z[slot(t,j)][h], j ascending.
+// y[t][h] (+)= sum_i wt[ord[i]] * z[ord[i]][h] over token t's slots i = run[t] .. run[t+1]-1, in
+// that order (the routes-in entry lists a token's slots in route order).
 __global__ void __launch_bounds__(256) grouped_combine_kernel(const float* __restrict__ z,
-                                                              const int32_t* __restrict__ slot_of,
-                                                              const float* __restrict__ w,
-                                                              uint32_t top_k, uint32_t hidden,
+                                                              const uint32_t* __restrict__ ord,
+                                                              const uint32_t* __restrict__ run,
+                                                              const float* __restrict__ slot_w,
+                                                              uint32_t n_slots, uint32_t hidden,
                                                               float* __restrict__ y, int accumulate) {
   const uint32_t t = blockIdx.y;
   const uint32_t h = (blockIdx.x * 256 + threadIdx.x) * 4;
   if (h >= hidden) return;
   float4 acc = accumulate ? *reinterpret_cast<const float4*>(y + (uint64_t)t * hidden + h)
                           : make_float4(0.f, 0.f, 0.f, 0.f);
-  for (uint32_t j = 0; j < top_k; ++j) {
-    const int32_t s = slot_of[t * top_k + j];
-    if (s < 0) continue;
-    const float wt = w[t * top_k + j];
+  const uint32_t r1 = min(run[t + 1], n_slots);
+  for (uint32_t i = min(run[t], r1); i < r1; ++i) {
+    const uint32_t s = ord[i];
+    if (s >= n_slots) continue;
+    const float wt = slot_w[s];
     const float4 v = *reinterpret_cast<const float4*>(z + (uint64_t)s * hidden + h);
     acc.x += wt * v.x;
     acc.y += wt * v.y;
@@ -812,24 +871,26 @@ namespace {
 
 
 struct GroupedWs {
-  uint64_t hdr, offsets, slot_tok, slot_of, tiles1, tiles2, sigma, zeros, xq, aq, z, total;
+  uint64_t hdr, offsets, run, slot_tok, slot_w, ord, tiles1, tiles2, sigma, zeros, xq, aq, z, total;
   uint32_t max_tiles1, max_tiles2;
 };
 
 // tokens per workgroup tile: kGCT column tiles of 16 / terms tokens each
 uint32_t tile_tokens(uint32_t terms) { return kGCT * (16 / terms); }
 
-GroupedWs grouped_ws(uint32_t T, uint32_t K, uint32_t E, uint32_t hidden, uint32_t inter, uint32_t tx) {
+// T tokens, room for P slots (the routes form: T * top_k)
+GroupedWs grouped_ws(uint32_t T, uint64_t P, uint32_t E, uint32_t hidden, uint32_t inter, uint32_t tx) {
   GroupedWs w;
-  const uint64_t P = (uint64_t)T * K;
   const uint32_t tt1 = tile_tokens(tx), tt2 = tile_tokens(3);
   w.max_tiles1 = (uint32_t)(P / tt1 + E + 1);
   w.max_tiles2 = (uint32_t)(P / tt2 + E + 1);
   uint64_t o = 0;
   w.hdr = o; o += a256(sizeof(GroupedHdr));
   w.offsets = o; o += a256(4ull * (AFFX_MAX_EXPERTS + 1));
+  w.run = o; o += a256(4ull * ((uint64_t)T + 1));
   w.slot_tok = o; o += a256(4 * P);
-  w.slot_of = o; o += a256(4 * P);
+  w.slot_w = o; o += a256(4 * P);
+  w.ord = o; o += a256(4 * P);
   w.tiles1 = o; o += a256(sizeof(Tile) * w.max_tiles1);
   w.tiles2 = o; o += a256(sizeof(Tile) * w.max_tiles2);
   w.sigma = o; o += a256(4 * P);  // per slot
@@ -841,46 +902,41 @@ GroupedWs grouped_ws(uint32_t T, uint32_t K, uint32_t E, uint32_t hidden, uint32
   return w;
 }
 
-}  // namespace
-
-extern "C" {
-
-size_t affx_grouped_workspace_size(uint32_t n_tok, uint32_t top_k, uint32_t n_experts,
-                                   uint32_t hidden, uint32_t inter) {
-  // sized for the 3-term gate/up input (x with a low part), the larger layout
-  return (size_t)grouped_ws(n_tok, top_k, n_experts, hidden, inter, 3).total;
-}
-
-int affx_expert_ffn_grouped(const affx_layer* L, const void* x, const void* x_lo, uint32_t T,
-                            const uint32_t* sel, const float* w, uint32_t K, float* y,
-                            int accumulate, void* ws, size_t ws_bytes, void* stream) {
-  if (!L || !x || !sel || !w || !y || !ws || !L->base || !L->codebook)
-    return set_error(AFFX_ERR_ARG, "ffn_grouped: null pointer");
-  if (T == 0) return AFFX_OK;
-  if (K == 0 || K > AFFX_MAX_TOPK || L->n_experts == 0 || L->n_experts > AFFX_MAX_EXPERTS)
-    return set_error(AFFX_DECLINED, "ffn_grouped: top_k must be 1..%d and n_experts 1..%d",
-                     AFFX_MAX_TOPK, AFFX_MAX_EXPERTS);
+// The two entries' shared body. Routes form (sel != null): plan, run and place build the slot list
+// on the device from the routes. Slot-list form: the caller's expert ranges (start), tok, wt, ord
+// and run; only the tiles are built here.
+int grouped_body(const affx_layer* L, const void* x, const void* x_lo, uint32_t T, const uint32_t* sel,
+                 const float* w, uint32_t K, const uint32_t* start, const uint32_t* tok, const float* wt,
+                 const uint32_t* ord, const uint32_t* run, uint32_t n_slots, float* y, int accumulate,
+                 void* ws, size_t ws_bytes, void* stream, const char* what) {
+  if (!L || !x || !y || !ws || !L->base || !L->codebook) return set_error(AFFX_ERR_ARG, "%s: null pointer", what);
+  if (L->n_experts == 0 || L->n_experts > AFFX_MAX_EXPERTS)
+    return set_error(AFFX_DECLINED, "%s: n_experts must be 1..%d", what, AFFX_MAX_EXPERTS);
   if (L->hidden % kTileCols || L->inter % kTileCols || L->hidden == 0 || L->inter == 0 ||
       L->hidden > 8192 || L->inter > 8192)
-    return set_error(AFFX_DECLINED, "ffn_grouped: hidden and inter must be multiples of 1024, at most 8192");
+    return set_error(AFFX_DECLINED, "%s: hidden and inter must be multiples of 1024, at most 8192", what);
   if (!(L->swiglu_limit > 0.f) || L->swiglu_limit > 1e6f)
-    return set_error(AFFX_DECLINED, "ffn_grouped: needs a SwiGLU clamp limit in (0, 1e6]");
+    return set_error(AFFX_DECLINED, "%s: needs a SwiGLU clamp limit in (0, 1e6]", what);
   if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(x_lo)) & 15u)
-    return set_error(AFFX_ERR_ARG, "ffn_grouped: x and x_lo must be 16-byte aligned");
+    return set_error(AFFX_ERR_ARG, "%s: x and x_lo must be 16-byte aligned", what);
   const uint32_t tx = x_lo ? 3 : 2;
-  const GroupedWs lay = grouped_ws(T, K, L->n_experts, L->hidden, L->inter, tx);
+  const uint64_t P = sel ? (uint64_t)T * K : n_slots;
+  const GroupedWs lay = grouped_ws(T, P, L->n_experts, L->hidden, L->inter, tx);
   // the GEMM addresses its B rows with 32-bit offsets into the workspace
-  if ((uint64_t)T * K > (1ull << 31) || lay.aq + (uint64_t)T * K * 3 * L->inter > (1ull << 32))
-    return set_error(AFFX_DECLINED, "ffn_grouped: batch too large (split it)");
+  if (P > (1ull << 31) || lay.aq + P * 3 * L->inter > (1ull << 32))
+    return set_error(AFFX_DECLINED, "%s: batch too large (split it)", what);
   if (ws_bytes < lay.total)
-    return set_error(AFFX_ERR_ARG, "ffn_grouped: workspace %zu < %llu bytes", ws_bytes,
-                     (unsigned long long)lay.total);
+    return set_error(AFFX_ERR_ARG, "%s: workspace %zu < %llu bytes", what, ws_bytes, (unsigned long long)lay.total);
   uint64_t off9[9];
   const uint64_t stride = affx_expert_layout(L->hidden, L->inter, off9, nullptr);
-  if (L->stride < stride) return set_error(AFFX_ERR_ARG, "ffn_grouped: layer stride below expert size");
+  if (L->stride < stride) return set_error(AFFX_ERR_ARG, "%s: layer stride below expert size", what);
 
   uint8_t* b = (uint8_t*)ws;
   hipStream_t s = (hipStream_t)stream;
+  const uint32_t* slot_tok = sel ? (const uint32_t*)(b + lay.slot_tok) : tok;
+  const float* slot_w = sel ? (const float*)(b + lay.slot_w) : wt;
+  const uint32_t* ord_d = sel ? (const uint32_t*)(b + lay.ord) : ord;
+  const uint32_t* run_d = sel ? (const uint32_t*)(b + lay.run) : run;
   GemmArgs A;
   A.base = (const uint8_t*)L->base;
   A.stride = L->stride;
@@ -889,7 +945,8 @@ int affx_expert_ffn_grouped(const affx_layer* L, const void* x, const void* x_lo
   A.inter = L->inter;
   A.codebook = (const uint32_t*)L->codebook;
   A.hdr = (const GroupedHdr*)(b + lay.hdr);
-  A.slot_tok = (const uint32_t*)(b + lay.slot_tok);
+  A.slot_tok = slot_tok;
+  A.n_tok = T;
   A.slot_sigma = (const int32_t*)(b + lay.sigma);
   A.ws = b;
   A.zero_off = lay.zeros;
@@ -898,21 +955,27 @@ int affx_expert_ffn_grouped(const affx_layer* L, const void* x, const void* x_lo
   A.limit = L->swiglu_limit;
   A.sigma_a = 7 - ilogbf(L->swiglu_limit * L->swiglu_limit);
 
-  const uint32_t P = T * K;
   const uint32_t tt1 = tile_tokens(tx), tt2 = tile_tokens(3);
-  hipLaunchKernelGGL(grouped_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, sel, P, L->n_experts,
-                     tt1, tt2, tx, (GroupedHdr*)(b + lay.hdr), (uint32_t*)(b + lay.offsets),
-                     (Tile*)(b + lay.tiles1), (Tile*)(b + lay.tiles2));
+  const uint32_t Pp = sel ? T * K : 0u;
+  hipLaunchKernelGGL(grouped_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, sel, Pp, L->n_experts, tt1, tt2, tx,
+                     sel ? nullptr : start, sel ? 0u : n_slots, lay.max_tiles1, lay.max_tiles2,
+                     (GroupedHdr*)(b + lay.hdr), (uint32_t*)(b + lay.offsets), (Tile*)(b + lay.tiles1),
+                     (Tile*)(b + lay.tiles2));
   int rc = check_launch("grouped_plan_kernel");
   if (rc) return rc;
-  hipLaunchKernelGGL(grouped_place_kernel, dim3(L->n_experts + 1), dim3(256), 0, s, sel, P, K,
-                     L->n_experts, (const uint32_t*)(b + lay.offsets), (uint32_t*)(b + lay.slot_tok),
-                     (int32_t*)(b + lay.slot_of));
-  if ((rc = check_launch("grouped_place_kernel"))) return rc;
+  if (sel) {
+    hipLaunchKernelGGL(grouped_run_kernel, dim3(1), dim3(kPlanThreads), 0, s, sel, T, K, L->n_experts,
+                       (uint32_t*)(b + lay.run));
+    if ((rc = check_launch("grouped_run_kernel"))) return rc;
+    hipLaunchKernelGGL(grouped_place_kernel, dim3(L->n_experts), dim3(256), 0, s, sel, w, Pp, K, L->n_experts,
+                       (const uint32_t*)(b + lay.offsets), (const uint32_t*)(b + lay.run),
+                       (uint32_t*)(b + lay.slot_tok), (float*)(b + lay.slot_w), (uint32_t*)(b + lay.ord));
+    if ((rc = check_launch("grouped_place_kernel"))) return rc;
+  }
+  const uint32_t n_sl = (uint32_t)P;  // slot indices are below this (the routes form's taken slots too)
   const uint32_t zmax = L->hidden > L->inter ? L->hidden : L->inter;
-  hipLaunchKernelGGL(grouped_prep_x_kernel, dim3(T), dim3(256), 0, s, (const uint16_t*)x,
-                     (const uint16_t*)x_lo, L->hidden, tx, (const int32_t*)(b + lay.slot_of), K,
-                     (int32_t*)(b + lay.sigma), b + lay.xq,
+  hipLaunchKernelGGL(grouped_prep_x_kernel, dim3(T), dim3(256), 0, s, (const uint16_t*)x, (const uint16_t*)x_lo,
+                     L->hidden, tx, ord_d, run_d, n_sl, (int32_t*)(b + lay.sigma), b + lay.xq,
                      (uint32_t*)(b + lay.zeros), zmax / 4);
   if ((rc = check_launch("grouped_prep_x_kernel"))) return rc;
   // gate/up: 128 gate + 128 up rows per item; down: 256 rows. Items (row block, tile), the tile
@@ -940,9 +1003,39 @@ int affx_expert_ffn_grouped(const affx_layer* L, const void* x, const void* x_lo
   hipLaunchKernelGGL((grouped_gemm_kernel<1, 3>), dim3(g2), dim3(kGT), 0, s, A);
   if ((rc = check_launch("grouped_gemm_kernel (down)"))) return rc;
   hipLaunchKernelGGL(grouped_combine_kernel, dim3((L->hidden / 4 + 255) / 256, T), dim3(256), 0, s,
-                     (const float*)(b + lay.z), (const int32_t*)(b + lay.slot_of), w, K, L->hidden,
-                     y, accumulate);
+                     (const float*)(b + lay.z), ord_d, run_d, slot_w, n_sl, L->hidden, y, accumulate);
   return check_launch("grouped_combine_kernel");
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t affx_grouped_workspace_size(uint32_t n_tok, uint32_t top_k, uint32_t n_experts,
+                                   uint32_t hidden, uint32_t inter) {
+  // sized for the 3-term gate/up input (x with a low part), the larger layout
+  return (size_t)grouped_ws(n_tok, (uint64_t)n_tok * top_k, n_experts, hidden, inter, 3).total;
+}
+
+int affx_expert_ffn_grouped(const affx_layer* L, const void* x, const void* x_lo, uint32_t T,
+                            const uint32_t* sel, const float* w, uint32_t K, float* y,
+                            int accumulate, void* ws, size_t ws_bytes, void* stream) {
+  if (!sel || !w) return set_error(AFFX_ERR_ARG, "ffn_grouped: null pointer");
+  if (T == 0) return AFFX_OK;
+  if (K == 0 || K > AFFX_MAX_TOPK)
+    return set_error(AFFX_DECLINED, "ffn_grouped: top_k must be 1..%d", AFFX_MAX_TOPK);
+  return grouped_body(L, x, x_lo, T, sel, w, K, nullptr, nullptr, nullptr, nullptr, nullptr, 0, y, accumulate, ws,
+                      ws_bytes, stream, "ffn_grouped");
+}
+
+int affx_expert_ffn_grouped_slots(const affx_layer* L, const void* x, const void* x_lo, uint32_t T,
+                                  const uint32_t* expert_start, const uint32_t* tok, const float* wt,
+                                  const uint32_t* ord, const uint32_t* run, uint32_t n_slots, float* y,
+                                  int accumulate, void* ws, size_t ws_bytes, void* stream) {
+  if (!expert_start || !tok || !wt || !ord || !run) return set_error(AFFX_ERR_ARG, "ffn_grouped_slots: null pointer");
+  if (T == 0) return AFFX_OK;
+  return grouped_body(L, x, x_lo, T, nullptr, nullptr, 0, expert_start, tok, wt, ord, run, n_slots, y, accumulate,
+                      ws, ws_bytes, stream, "ffn_grouped_slots");
 }
 
 }  // extern "C"

@@ -82,32 +82,37 @@ __host__ __device__ inline void unit_dest(uint64_t r, uint64_t u, uint64_t cols,
   *lane = (uint32_t)(r % kTileRows + kTileRows * (u % 4));
 }
 
+// One matrix's code and field planes, container (row-major) <-> device (wave-tile) layout.
+static void permute_matrix_host(const uint8_t* sc, const uint8_t* sf, uint8_t* dc, uint8_t* df, uint64_t rows,
+                                uint64_t cols, bool to_device) {
+  const uint64_t nseg = cols / kSegCols, crow = code_row_bytes(cols), frow = field_row_bytes(cols);
+  for (uint64_t r = 0; r < rows; ++r)
+    for (uint64_t u = 0; u < nseg; ++u) {
+      uint64_t tile;
+      uint32_t lane;
+      unit_dest(r, u, cols, &tile, &lane);
+      const uint64_t c_row = r * crow + u * kUnitCodeBytes;
+      const uint64_t f_row = r * frow + u * kUnitFieldBytes;
+      const uint64_t f_dev = tile * kTileFieldBytes + lane * kUnitFieldBytes;
+      for (int j = 0; j < 5; ++j) {
+        const uint64_t c_dev = tile * kTileCodeBytes + j * 1024 + lane * 16;
+        if (to_device) std::memcpy(dc + c_dev, sc + c_row + 16 * j, 16);
+        else std::memcpy(dc + c_row + 16 * j, sc + c_dev, 16);
+      }
+      if (to_device) std::memcpy(df + f_dev, sf + f_row, kUnitFieldBytes);
+      else std::memcpy(df + f_row, sf + f_dev, kUnitFieldBytes);
+    }
+}
+
 static void permute_host(const uint8_t* src, uint8_t* dst, uint64_t hidden, uint64_t inter,
                          bool to_device) {
   MatPlanes mp[3];
   mats_of(hidden, inter, mp);
   const uint64_t stride = layout(hidden, inter, nullptr, nullptr);
   std::memcpy(dst, src, stride);  // row scales and padding are not permuted
-  for (int m = 0; m < 3; ++m) {
-    const uint64_t cols = mp[m].cols, nseg = cols / kSegCols;
-    const uint64_t crow = code_row_bytes(cols), frow = field_row_bytes(cols);
-    for (uint64_t r = 0; r < mp[m].rows; ++r)
-      for (uint64_t u = 0; u < nseg; ++u) {
-        uint64_t tile;
-        uint32_t lane;
-        unit_dest(r, u, cols, &tile, &lane);
-        const uint64_t c_src = mp[m].code_off + r * crow + u * kUnitCodeBytes;
-        const uint64_t f_src = mp[m].field_off + r * frow + u * kUnitFieldBytes;
-        const uint64_t f_dst = mp[m].field_off + tile * kTileFieldBytes + lane * kUnitFieldBytes;
-        for (int j = 0; j < 5; ++j) {
-          const uint64_t c_dst = mp[m].code_off + tile * kTileCodeBytes + j * 1024 + lane * 16;
-          if (to_device) std::memcpy(dst + c_dst, src + c_src + 16 * j, 16);
-          else std::memcpy(dst + c_src + 16 * j, src + c_dst, 16);
-        }
-        if (to_device) std::memcpy(dst + f_dst, src + f_src, kUnitFieldBytes);
-        else std::memcpy(dst + f_src, src + f_dst, kUnitFieldBytes);
-      }
-  }
+  for (int m = 0; m < 3; ++m)
+    permute_matrix_host(src + mp[m].code_off, src + mp[m].field_off, dst + mp[m].code_off,
+                        dst + mp[m].field_off, mp[m].rows, mp[m].cols, to_device);
 }
 
 // One thread per 16-byte code chunk or 12-byte field run; grid over (expert, matrix, unit).
@@ -281,6 +286,16 @@ int affx_expert_from_device_layout(const void* src, void* dst, uint64_t hidden, 
   if (!src || !dst || src == dst || !shape_ok(hidden, inter))
     return set_error(AFFX_ERR_ARG, "expert_from_device_layout: bad arguments");
   permute_host((const uint8_t*)src, (uint8_t*)dst, hidden, inter, false);
+  return AFFX_OK;
+}
+
+int affx_matrix_to_device_layout(const void* src_codes, const void* src_fields, void* dst_codes,
+                                 void* dst_fields, uint32_t rows, uint32_t cols) {
+  if (!src_codes || !src_fields || !dst_codes || !dst_fields || src_codes == dst_codes ||
+      src_fields == dst_fields || rows == 0 || cols == 0 || rows % kTileRows || cols % kTileCols)
+    return set_error(AFFX_ERR_ARG, "matrix_to_device_layout: bad arguments (rows %% 16, cols %% 1024)");
+  permute_matrix_host((const uint8_t*)src_codes, (const uint8_t*)src_fields, (uint8_t*)dst_codes,
+                      (uint8_t*)dst_fields, rows, cols, true);
   return AFFX_OK;
 }
 

@@ -59,6 +59,13 @@ typedef struct affx_matrix {
   uint32_t rows, cols;
 } affx_matrix;
 
+/* One expert's three matrices, each anywhere in device memory. Mirrors DeviceExpert{gate, up,
+ * down} (src/gpu/expert_kernel_hip.h:259-261); affx_matrix has DeviceMatrix's field order, so an
+ * array of DeviceExpert can be passed as it is (INTEGRATION.md shows the static checks). */
+typedef struct affx_device_expert {
+  affx_matrix gate, up, down;
+} affx_device_expert;
+
 /* Where a layer's experts live: expert e at base + e*stride (device layout), the O(1)
  * addressing of AffReader::expert_ptr (src/format/aff_reader.h:45-48). */
 typedef struct affx_layer {
@@ -101,11 +108,49 @@ int affx_expert_to_device_layout(const void* src_host, void* dst_host, uint64_t 
 int affx_expert_from_device_layout(const void* src_host, void* dst_host, uint64_t hidden,
                                    uint64_t inter);
 
+/* One matrix's code and field planes, container (row-major bit streams) -> device layout (wave
+ * tiles); rows % 16 == 0, cols % 1024 == 0; host pointers, no overlap. Row scales are not
+ * permuted. expert_transpose_plane_host (src/gpu/expert_kernel_hip.h:78-80), the per-matrix upload
+ * step of aff-gpucheck (tools/aff_gpucheck.cpp:54-74). */
+int affx_matrix_to_device_layout(const void* src_codes, const void* src_fields, void* dst_codes,
+                                 void* dst_fields, uint32_t rows, uint32_t cols);
+
 /* The same permutation on the GPU for n experts uploaded in container layout (src and dst are
  * device buffers of n*stride bytes, not overlapping). The upload step of StaticPlacement::init
  * (src/gpu/static_placement.hip:1094-1097), moved onto the device. */
 int affx_permute_experts(const void* src_container, void* dst_device, uint64_t n_experts,
                          uint64_t hidden, uint64_t inter, void* stream);
+
+/* ---- the .aff container ------------------------------------------------------------------- */
+
+/* An open .aff file: one read-only mapping of it, checked. Opaque. */
+typedef struct affx_container affx_container;
+
+/* Maps and checks a container as the reference's AffReader::open does (src/format/aff_reader.cpp:
+ * 56-118: magic "AFFINITY", version 1, file size, every section inside the file, every layer's
+ * experts inside the expert pool) and as its expert tier does at load (src/engine/model.cpp:
+ * 335-357, src/gpu/static_placement.hip:918-951): every layer's matrices in the quad format
+ * (AFF_Q2P875_Q4) with compute_expert_layout's plane geometry, a __codebook tensor of 2048 packed
+ * dwords with every stored exponent in 1..7. AFFX_ERR_ARG with the reason otherwise. */
+int affx_container_open(const char* path, affx_container** out);
+void affx_container_close(affx_container* c);
+uint32_t affx_container_layer_count(const affx_container* c);
+/* A layer's expert count, hidden and intermediate size and the container's expert stride. */
+int affx_container_layer(const affx_container* c, uint32_t layer, uint32_t* n_experts,
+                         uint64_t* hidden, uint64_t* inter, uint64_t* stride);
+/* Host address of expert (layer, expert) in the mapping: pool + base_off + expert * stride, the
+ * O(1) addressing of AffReader::expert_ptr (src/format/aff_reader.h:45-48). NULL if out of range. */
+const void* affx_container_expert_ptr(const affx_container* c, uint32_t layer, uint32_t expert);
+/* The __codebook tensor's 2048 dwords (host out[2048]): what affx_layer.codebook holds once on
+ * the device (src/engine/model.cpp:335-357, tools/aff_quantize.cpp:262-271). */
+int affx_container_codebook(const affx_container* c, uint32_t* out);
+/* Uploads every expert of a layer into the device layout at dst (n_experts * stride bytes with
+ * the library's stride for the layer's shape), through staging (device, the same size): the
+ * experts are copied host -> device as they lie in the file, then permuted on the device
+ * (affx_permute_experts). The upload step of StaticPlacement::init
+ * (src/gpu/static_placement.hip:1000-1100). Stream-ordered. */
+int affx_container_upload_layer(const affx_container* c, uint32_t layer, void* staging, void* dst,
+                                void* stream);
 
 /* ---- dequantisation (validation path) ------------------------------------------------------ */
 
@@ -169,6 +214,20 @@ int affx_expert_ffn_decode_noalloc(const affx_layer* layer, const float* x, uint
                                    const float* w, uint32_t top_k, float* y, uint64_t y_tok_stride,
                                    uint64_t y_dim_stride, int accumulate, void* stream);
 
+/* out[h] += sum_k weights[k] * FFN_k(x)[h] for one token through n_experts experts given as a
+ * host array of per-matrix device pointers (planes in device layout): expert_ffn_hip with its
+ * arguments unchanged (src/gpu/expert_kernel_hip.h:273, expert_kernel.hip:2737-2808), the call
+ * aff-gpucheck makes (tools/aff_gpucheck.cpp:498, 585). weights: device f32[n_experts]; x: device
+ * f32[hidden]; out: device f32[hidden], accumulated; codebook: device uint32[2048] (the packed
+ * quads the reference passes through a float pointer). scratch: device, the reference's
+ * 2 * n_experts * inter floats, no clearing needed. n_experts <= 16 (the reference's 32 matrices
+ * per launch); shapes as the layer entries. Three stream-ordered launches (the staged decode:
+ * routing plan and activation split, gate/up + SwiGLU, down + combine), no synchronisation.
+ * AFFX_DECLINED when a shape or the scratch size is outside this. */
+int affx_expert_ffn(const affx_device_expert* experts, const float* weights, uint32_t n_experts,
+                    const void* codebook, const float* x, float swiglu_limit, float* scratch,
+                    float* out, void* stream);
+
 /* The same three steps as separate stream-ordered calls (same workspace, same arguments), for
  * callers that interleave other work or time the stages, as the reference's GPU FFN is three
  * launches: activation prep + routing plan (batch_quant_fp8_hip, src/gpu/batch_kernels.h:124;
@@ -216,6 +275,47 @@ int affx_expert_ffn_grouped(const affx_layer* layer, const void* x, const void* 
                             uint32_t n_tok, const uint32_t* sel, const float* w, uint32_t top_k,
                             float* y, int accumulate, void* workspace, size_t workspace_bytes,
                             void* stream);
+
+/* The same prefill over a slot list the caller has already built on the device, the shape of the
+ * reference engine's device plan (MoePlanArgs, src/gpu/moe_plan.h:144-170, from moe_plan_kernel,
+ * src/gpu/moe_plan.hip:116-380): slots sorted by expert, expert e owning slots
+ * [expert_start[e], expert_start[e+1]) (n_experts + 1 entries); tok[s] the token of slot s and
+ * wt[s] its router weight; ord the slots sorted by token, token t's being
+ * ord[run[t] .. run[t+1]) (run: n_tok + 1 entries). Token t's output sums its slots in ord order.
+ * x, x_lo, y as affx_expert_ffn_grouped; all arrays device memory. Workspace:
+ * affx_grouped_workspace_size(n_tok, top_k, ...) for any top_k with n_tok * top_k >= n_slots.
+ * The entry trusts the list's consistency but not its bounds: indices are clamped on the device
+ * (a bad list gives wrong output, never an access outside the buffers). affx_expert_ffn_grouped
+ * is this entry after building the list from the routes on the device, a token's slots in route
+ * order. */
+int affx_expert_ffn_grouped_slots(const affx_layer* layer, const void* x, const void* x_lo,
+                                  uint32_t n_tok, const uint32_t* expert_start, const uint32_t* tok,
+                                  const float* wt, const uint32_t* ord, const uint32_t* run,
+                                  uint32_t n_slots, float* y, int accumulate, void* workspace,
+                                  size_t workspace_bytes, void* stream);
+
+/* ---- routing on the device ------------------------------------------------------------------ */
+
+#define AFFX_ROUTE_ENGINE 0  /* the engine router: sqrtsoftplus scores, bias for selection only */
+#define AFFX_ROUTE_SOFTMAX 1 /* the benchmark configs: top-k logits, softmax over the k */
+
+/* Top-k routing of n_tok tokens from their router logits, on the device, writing the
+ * sel/w [n_tok][top_k] (token-major, device) that affx_expert_ffn_decode and
+ * affx_expert_ffn_grouped read, so routes never pass through the host. Logit (t, e) at
+ * logits[t * tok_stride + e * expert_stride]: token-major [n_tok][n_expert] is (n_expert, 1), the
+ * engine's dim-major batch arena [n_expert][nb] is (1, nb).
+ * AFFX_ROUTE_ENGINE: route_topk (src/engine/ops.cpp:62-92; the device form router_topk_kernel,
+ * src/gpu/batch_kernels.hip:2964-3031, called from the layer loop at src/engine/model.cpp:
+ * 1582-1599): score = sqrt(softplus(logit)) (x > 20 taken as is), the top_k largest of
+ * score + bias[e] (bias: device f32[n_expert] or NULL), ties to the lower id; weight = score *
+ * inv * routed_scaling, inv = 1 / max(sum of the k scores in double, 2^-14) if norm_topk_prob,
+ * else 1. The scores are within an ulp of the host's float libm (so the weights within a few).
+ * AFFX_ROUTE_SOFTMAX: the top_k largest logits (ties to the lower id), weights the softmax over
+ * those k in double (bias, norm_topk_prob and routed_scaling unused).
+ * top_k <= min(16, n_expert), n_expert <= 512. One wave per token; no synchronisation. */
+int affx_route_topk(const float* logits, uint64_t tok_stride, uint64_t expert_stride,
+                    const float* bias, uint32_t n_tok, uint32_t n_expert, uint32_t top_k, int rule,
+                    int norm_topk_prob, float routed_scaling, uint32_t* sel, float* w, void* stream);
 
 /* ---- engine hook ---------------------------------------------------------------------------- */
 

@@ -85,6 +85,10 @@ class Oracle:
         L.orc_swiglu.argtypes = [_f32p, _f32p, C.c_uint64, C.c_float, _f32p]
         L.orc_expert_ffn.argtypes = [_u8p, C.c_uint64, C.c_uint64, _f32p, _f32p, C.c_float, C.c_float, _f32p]
         L.orc_route_softmax_topk.argtypes = [_f32p, C.c_uint32, C.c_uint32, _u32p, _f32p]
+        L.orc_sqrtsoftplus.argtypes = [C.c_float]
+        L.orc_sqrtsoftplus.restype = C.c_float
+        L.orc_route_topk.argtypes = [_f32p, _f32p, C.c_uint32, C.c_uint32, C.c_int, C.c_float, _u32p, _f32p]
+        L.orc_route_topk.restype = C.c_uint32
 
     # -- threads ---------------------------------------------------------------------------
     def set_threads(self, n: int) -> None:
@@ -199,6 +203,16 @@ class Oracle:
                                 _p(y, _f32p))
         return y
 
+    def route_topk(self, logits: np.ndarray, bias: np.ndarray | None, k: int = 6, norm: bool = True,
+                   scaling: float = 1.0):
+        """The engine's router (sqrtsoftplus + bias for selection, renormalised, scaled)."""
+        sel = np.zeros(k, np.uint32)
+        w = np.zeros(k, np.float32)
+        lg = np.ascontiguousarray(logits, np.float32)
+        b = None if bias is None else _p(np.ascontiguousarray(bias, np.float32), _f32p)
+        n = self.lib.orc_route_topk(_p(lg, _f32p), b, lg.size, k, int(norm), scaling, _p(sel, _u32p), _p(w, _f32p))
+        return sel[:n], w[:n]
+
     def route(self, logits: np.ndarray, k: int = 6):
         sel = np.zeros(k, np.uint32)
         w = np.zeros(k, np.float32)
@@ -236,7 +250,14 @@ class RefLib:
         L.affref_float_to_bf16.restype = C.c_uint16
         L.affref_expert_layout.argtypes = [C.c_uint64, C.c_uint64, _u64p, _u64p]
         L.affref_expert_layout.restype = C.c_uint64
+        L.affref_route_topk.argtypes = [_f32p, _f32p, C.c_uint32, C.c_uint32, C.c_int, C.c_float, _u32p, _f32p]
+        L.affref_route_topk.restype = C.c_uint32
         L.affref_pool_threads.restype = C.c_uint
+        L.affref_write_container.argtypes = [C.c_char_p, C.c_char_p, C.c_uint32, C.c_uint32, C.c_uint64, C.c_uint64,
+                                             _u32p, _u8p, C.c_uint64, C.c_char_p, C.c_uint64]
+        L.affref_write_container.restype = C.c_int
+        L.affref_expert_offset.argtypes = [C.c_char_p, C.c_uint32, C.c_uint32]
+        L.affref_expert_offset.restype = C.c_int64
 
     def collect_samples(self, w: np.ndarray, budget: int) -> np.ndarray:
         rows, cols = w.shape
@@ -295,6 +316,30 @@ class RefLib:
                                            _p(np.ascontiguousarray(x, np.float32), _f32p), float(w),
                                            _p(y, _f32p), int(mt))
         return y
+
+    def route_topk(self, logits, bias, k=6, norm=True, scaling=1.0):
+        sel = np.zeros(k, np.uint32)
+        w = np.zeros(k, np.float32)
+        lg = np.ascontiguousarray(logits, np.float32)
+        b = None if bias is None else _p(np.ascontiguousarray(bias, np.float32), _f32p)
+        n = self.lib.affref_route_topk(_p(lg, _f32p), b, lg.size, k, int(norm), scaling, _p(sel, _u32p),
+                                       _p(w, _f32p))
+        return sel[:n], w[:n]
+
+    def write_container(self, path: str, meta: str, experts: np.ndarray, codebook: np.ndarray, hidden: int,
+                        inter: int) -> None:
+        """A .aff file through the reference's AffWriter. experts: uint8 [layers][experts][stride]."""
+        n_layers, n_experts, stride = experts.shape
+        err = C.create_string_buffer(512)
+        rc = self.lib.affref_write_container(path.encode(), meta.encode(), n_layers, n_experts, hidden, inter,
+                                             _p(np.ascontiguousarray(codebook, np.uint32), _u32p),
+                                             _p(np.ascontiguousarray(experts), _u8p), stride, err, 512)
+        if rc != 0:
+            raise ValueError("reference AffWriter: " + err.value.decode())
+
+    def expert_offset(self, path: str, layer: int, expert: int) -> int:
+        """File offset of an expert by the reference reader's own addressing."""
+        return int(self.lib.affref_expert_offset(path.encode(), layer, expert))
 
     def pool_threads(self) -> int:
         """Threads of the reference's global pool (hardware_concurrency), which the _mt GEMV uses."""

@@ -636,3 +636,45 @@ void orc_route_softmax_topk(const float* logits, uint32_t n_expert, uint32_t k, 
   for (uint32_t j = 0; j < k; ++j) w[j] = (float)(ex[j] / sum);
   free(taken);
 }
+
+/* The engine's router (src/engine/ops.cpp:30-35 sqrtsoftplus, 62-92 route_topk): score =
+ * sqrt(softplus(logit)) with the x > 20 guard, all in float (expf, log1pf, sqrtf: the float
+ * overloads std::exp/std::log1p/std::sqrt call); selection value = score + bias; the k best by
+ * selection value, ties to the lower id (std::partial_sort with that strict order picks exactly
+ * these, in that order); weights from the scores only: sum in double, floored at the fp16 least
+ * normal, weight = (float)(score * inv * routed_scaling) with inv = 1/sum when norm_topk_prob.
+ * Returns the number of experts chosen (min(k, n_expert)). */
+float orc_sqrtsoftplus(float x) {
+  const float sp = (x > 20.0f) ? x : log1pf(expf(x));
+  return sqrtf(sp);
+}
+
+uint32_t orc_route_topk(const float* logits, const float* bias, uint32_t n_expert, uint32_t k,
+                        int norm_topk_prob, float routed_scaling, uint32_t* sel, float* w) {
+  float* score = (float*)malloc(sizeof(float) * n_expert);
+  float* key = (float*)malloc(sizeof(float) * n_expert);
+  uint8_t* taken = (uint8_t*)calloc(n_expert, 1);
+  for (uint32_t e = 0; e < n_expert; ++e) {
+    score[e] = orc_sqrtsoftplus(logits[e]);
+    key[e] = score[e] + (bias ? bias[e] : 0.0f);
+  }
+  const uint32_t kk = k < n_expert ? k : n_expert;
+  for (uint32_t j = 0; j < kk; ++j) {
+    uint32_t best = UINT32_MAX;
+    for (uint32_t e = 0; e < n_expert; ++e) {
+      if (taken[e]) continue;
+      if (best == UINT32_MAX || key[e] > key[best]) best = e; /* equal keys keep the lower id */
+    }
+    taken[best] = 1;
+    sel[j] = best;
+  }
+  double sum = 0.0;
+  for (uint32_t j = 0; j < kk; ++j) sum += score[sel[j]];
+  if (sum < 6.103515625e-5) sum = 6.103515625e-5;
+  const double inv = norm_topk_prob ? 1.0 / sum : 1.0;
+  for (uint32_t j = 0; j < kk; ++j) w[j] = (float)(score[sel[j]] * inv * routed_scaling);
+  free(score);
+  free(key);
+  free(taken);
+  return kk;
+}

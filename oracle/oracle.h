@@ -77,9 +77,12 @@ void orc_swiglu(const float* gate, const float* up, uint64_t n, float limit, flo
 void orc_expert_ffn(const uint8_t* expert, uint64_t hidden, uint64_t inter, const float* cb,
                     const float* x, float w, float limit, float* y);
 
-/* ---- routing used by the synthetic configs ---- */
+/* ---- routing ---- */
 void orc_route_softmax_topk(const float* logits, uint32_t n_expert, uint32_t k, uint32_t* sel,
                             float* w);
+float orc_sqrtsoftplus(float x);
+uint32_t orc_route_topk(const float* logits, const float* bias, uint32_t n_expert, uint32_t k,
+                        int norm_topk_prob, float routed_scaling, uint32_t* sel, float* w);
 
 #ifdef __cplusplus
 }

@@ -13,6 +13,8 @@
 #include "engine/expert_kernel.h"
 #include "engine/ops.h"
 #include "engine/threadpool.h"
+#include "format/aff_reader.h"
+#include "format/aff_writer.h"
 
 #include <cstring>
 #include <vector>
@@ -157,5 +159,75 @@ uint64_t affref_expert_layout(uint64_t hidden, uint64_t inter, uint64_t* off9, u
 
 // src/engine/threadpool.cpp:122-131: the pool expert_gemv_scaled_mt runs on (hardware_concurrency)
 unsigned affref_pool_threads(void) { return global_pool().size(); }
+
+// src/engine/ops.cpp:62-92 (the engine router). Returns the number of experts chosen.
+uint32_t affref_route_topk(const float* logits, const float* bias, uint32_t n_expert, uint32_t top_k,
+                           int norm_topk_prob, float routed_scaling, uint32_t* sel, float* w) {
+  RouterOut out{};
+  route_topk(logits, bias, n_expert, top_k, norm_topk_prob != 0, routed_scaling, &out);
+  for (uint32_t i = 0; i < out.n; ++i) { sel[i] = out.expert[i]; w[i] = out.weight[i]; }
+  return out.n;
+}
+
+// A container through the reference's own writer (src/format/aff_writer.cpp): n_layers layers of
+// n_experts quad-format experts (container layout, `stride` bytes each, laid out [layer][expert]
+// in `experts`), the packed codebook as the `__codebook` tensor (1 x 2048, f32-declared, the
+// bytes of the dwords: tools/aff_quantize.cpp:262-271, 514-527) and one small bf16 tensor.
+// Returns 0, or -1 with the writer's message in err.
+int affref_write_container(const char* path, const char* meta, uint32_t n_layers, uint32_t n_experts,
+                           uint64_t hidden, uint64_t inter, const uint32_t* codebook, const uint8_t* experts,
+                           uint64_t stride, char* err, uint64_t err_len) {
+  std::vector<LayerDecl> layers(n_layers);
+  for (auto& L : layers) {
+    L.n_experts = n_experts;
+    L.geom = ExpertGeometry{hidden, inter, AFF_Q2P875_Q4, AFF_Q2P875_Q4, AFF_Q2P875_Q4};
+  }
+  std::vector<TensorDecl> tensors(2);
+  tensors[0] = TensorDecl{"__codebook", 1, 2048, AFF_F32};
+  tensors[1] = TensorDecl{"blk.0.norm", 1, 64, AFF_BF16};
+  AffWriter w;
+  std::string e;
+  auto fail = [&]() {
+    std::snprintf(err, err_len, "%s", e.c_str());
+    return -1;
+  };
+  if (!w.begin(path, meta, layers, tensors, &e)) return fail();
+  MatrixData cb;
+  cb.data = codebook;
+  cb.data_size = 2048 * 4;
+  if (!w.write_tensor("__codebook", cb, &e)) return fail();
+  std::vector<uint16_t> norm(64, 0x3F80);
+  MatrixData nm;
+  nm.data = norm.data();
+  nm.data_size = 128;
+  if (!w.write_tensor("blk.0.norm", nm, &e)) return fail();
+  AffMatrixDesc g, u, d;
+  compute_expert_layout(ExpertGeometry{hidden, inter, AFF_Q2P875_Q4, AFF_Q2P875_Q4, AFF_Q2P875_Q4}, g, u, d);
+  for (uint32_t l = 0; l < n_layers; ++l)
+    for (uint32_t x = 0; x < n_experts; ++x) {
+      const uint8_t* p = experts + ((uint64_t)l * n_experts + x) * stride;
+      auto md = [&](const AffMatrixDesc& m) {
+        MatrixData r;
+        r.data = p + m.data_off; r.data_size = m.data_size;
+        r.scales = p + m.scale_off; r.scale_size = m.scale_size;
+        r.rscales = p + m.rscale_off; r.rscale_size = m.rscale_size;
+        return r;
+      };
+      ExpertData ed{md(g), md(u), md(d)};
+      if (!w.write_expert(l, x, ed, &e)) return fail();
+    }
+  if (!w.finalize(&e)) return fail();
+  return 0;
+}
+
+// The reference reader's addressing (src/format/aff_reader.h:45-48): the file offset of expert
+// (layer, expert), or -1 if the file does not open.
+int64_t affref_expert_offset(const char* path, uint32_t layer, uint32_t expert) {
+  AffReader r;
+  std::string e;
+  if (!r.open(path, &e)) return -1;
+  const uint8_t* base = r.expert_ptr(0, 0) - r.header().expert_pool_off - r.layer(0).base_off;
+  return (int64_t)(r.expert_ptr(layer, expert) - base);
+}
 
 }  // extern "C"

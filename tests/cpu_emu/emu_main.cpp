@@ -6,6 +6,11 @@
 //   emu_main grouped hidden inter n_experts T K seed lo   -> rel_l2 of the grouped FFN
 //   emu_main quant   rows cols seed                       -> planes bit-exact vs the oracle
 //   emu_main dequant hidden inter seed                    -> dequant bit-exact vs the oracle
+//   emu_main slots   hidden inter n_experts T K seed      -> the slot-list grouped entry vs the
+//                    routes entry (bit for bit) and, with a reordered list, vs the oracle
+//   emu_main ffnptr  hidden inter n_experts seed          -> affx_expert_ffn (pointer table) vs
+//                    the staged decode (bit for bit) and the oracle
+//   emu_main route   n_tok n_experts top_k seed           -> the device router vs the oracle's
 //   emu_main timeout hidden inter n_experts M K seed      -> a decode whose waiters give up (spin
 //                    limit 0 from the host) fails the engine hook and affx_decode_status; after
 //                    the reset, the next calls are correct
@@ -24,6 +29,8 @@ thread_local EmuBlock* emu_blk;
 #include "../../affinity_amd/csrc/affx_quant.hip"
 #include "../../affinity_amd/csrc/affx_grouped.hip"
 #include "../../affinity_amd/csrc/affx_api.hip"
+#include "../../affinity_amd/csrc/affx_noalloc.hip"
+#include "../../affinity_amd/csrc/affx_route.hip"
 
 extern "C" {
 #include "../../oracle/oracle.h"
@@ -203,6 +210,164 @@ int run_grouped(int argc, char** argv) {
   return rc == 0 && e <= 1e-3 ? 0 : 1;
 }
 
+// The slot-list entry: the host builds the list the routes entry builds on the device (slots
+// sorted by expert, a token's slots in route order): bit-identical to the routes entry; then the
+// same list with each expert's tokens and each token's slots reversed (another valid list): the
+// oracle's tolerance.
+int run_slots(int argc, char** argv) {
+  const uint32_t hidden = atoi(argv[2]), inter = atoi(argv[3]), n = atoi(argv[4]), T = atoi(argv[5]),
+                 K = atoi(argv[6]);
+  std::mt19937_64 rng(atoi(argv[7]));
+  Layer L(hidden, inter, n, rng);
+  std::vector<uint16_t> xb(T * hidden);
+  std::vector<float> x(T * hidden), y1(T * hidden, 0.f), y2(T * hidden, 0.f), y3(T * hidden, 0.f),
+      yref(T * hidden, 0.f), w;
+  std::vector<uint32_t> sel;
+  std::normal_distribution<float> nd;
+  for (size_t i = 0; i < x.size(); ++i) {
+    xb[i] = bf16(nd(rng));
+    x[i] = __uint_as_float((uint32_t)xb[i] << 16);
+  }
+  routes(rng, T, K, n, sel, w);
+  sel[K + 1] = n + 3;  // a padding id
+  affx_layer abi = L.abi();
+  const size_t wsb = affx_grouped_workspace_size(T, K, n, hidden, inter);
+  std::vector<uint8_t> ws(wsb);
+  int rc = affx_expert_ffn_grouped(&abi, xb.data(), nullptr, T, sel.data(), w.data(), K, y1.data(), 0, ws.data(),
+                                   wsb, nullptr);
+  // the canonical list
+  std::vector<uint32_t> start(n + 1, 0), tok, ord, run(T + 1, 0), slot_of(T * K, ~0u);
+  std::vector<float> wt;
+  for (uint32_t e = 0; e < n; ++e) {
+    start[e] = (uint32_t)tok.size();
+    for (uint32_t i = 0; i < T * K; ++i)
+      if (sel[i] == e) { slot_of[i] = (uint32_t)tok.size(); tok.push_back(i / K); wt.push_back(w[i]); }
+  }
+  start[n] = (uint32_t)tok.size();
+  for (uint32_t t = 0; t < T; ++t) {
+    run[t] = (uint32_t)ord.size();
+    for (uint32_t j = 0; j < K; ++j)
+      if (slot_of[t * K + j] != ~0u) ord.push_back(slot_of[t * K + j]);
+  }
+  run[T] = (uint32_t)ord.size();
+  const uint32_t ns = (uint32_t)tok.size();
+  if (rc == 0)
+    rc = affx_expert_ffn_grouped_slots(&abi, xb.data(), nullptr, T, start.data(), tok.data(), wt.data(), ord.data(),
+                                       run.data(), ns, y2.data(), 0, ws.data(), wsb, nullptr);
+  const bool same = memcmp(y1.data(), y2.data(), y1.size() * 4) == 0;
+  // another valid list: each expert's slots in reverse token order, each token's slots reversed
+  std::vector<uint32_t> tok2(ns), ord2(ns), remap(ns);
+  std::vector<float> wt2(ns);
+  for (uint32_t e = 0; e < n; ++e)
+    for (uint32_t s0 = start[e]; s0 < start[e + 1]; ++s0) {
+      const uint32_t s1 = start[e] + start[e + 1] - 1 - s0;
+      remap[s0] = s1;
+      tok2[s1] = tok[s0];
+      wt2[s1] = wt[s0];
+    }
+  for (uint32_t t = 0; t < T; ++t)
+    for (uint32_t i = run[t]; i < run[t + 1]; ++i) ord2[run[t] + run[t + 1] - 1 - i] = remap[ord[i]];
+  if (rc == 0)
+    rc = affx_expert_ffn_grouped_slots(&abi, xb.data(), nullptr, T, start.data(), tok2.data(), wt2.data(),
+                                       ord2.data(), run.data(), ns, y3.data(), 0, ws.data(), wsb, nullptr);
+  L.oracle(x.data(), sel.data(), w.data(), T, K, yref.data());
+  const double e1 = rel_l2(y1, yref), e3 = rel_l2(y3, yref);
+  printf("slots rc=%d slots=%u routes==slots=%d rel_l2 routes=%.3e reordered=%.3e %s\n", rc, ns, (int)same, e1, e3,
+         rc ? affx_last_error() : "");
+  return rc == 0 && same && e1 <= 1e-3 && e3 <= 1e-3 ? 0 : 1;
+}
+
+// affx_expert_ffn (expert_ffn_hip's arguments): each matrix in a buffer of its own, permuted by
+// affx_matrix_to_device_layout; bit-identical to the staged decode over a slab of the same experts.
+int run_ffnptr(int argc, char** argv) {
+  const uint32_t hidden = atoi(argv[2]), inter = atoi(argv[3]), n = atoi(argv[4]);
+  std::mt19937_64 rng(atoi(argv[5]));
+  Layer L(hidden, inter, n, rng);
+  std::vector<std::vector<uint8_t>> bufs;
+  bufs.reserve(9 * n);  // references into it are held while it fills
+  std::vector<affx_device_expert> des(n);
+  for (uint32_t k = 0; k < n; ++k) {
+    for (int i = 0; i < 3; ++i) {
+      const uint32_t rows = i < 2 ? inter : hidden, cols = i < 2 ? hidden : inter;
+      const uint8_t* ex = L.cont.data() + (uint64_t)k * L.stride;
+      bufs.emplace_back(L.size[3 * i]);
+      std::vector<uint8_t>& c = bufs.back();
+      bufs.emplace_back(L.size[3 * i + 1]);
+      std::vector<uint8_t>& f = bufs.back();
+      bufs.emplace_back(ex + L.off[3 * i + 2], ex + L.off[3 * i + 2] + L.size[3 * i + 2]);
+      if (affx_matrix_to_device_layout(ex + L.off[3 * i], ex + L.off[3 * i + 1], c.data(), f.data(), rows, cols))
+        return 3;
+    }
+  }
+  for (uint32_t k = 0; k < n; ++k) {
+    affx_matrix* m[3] = {&des[k].gate, &des[k].up, &des[k].down};
+    for (int i = 0; i < 3; ++i) {
+      const uint32_t rows = i < 2 ? inter : hidden, cols = i < 2 ? hidden : inter;
+      const size_t b = (size_t)(k * 3 + i) * 3;
+      *m[i] = affx_matrix{bufs[b].data(), bufs[b + 1].data(), bufs[b + 2].data(), rows, cols};
+    }
+  }
+  std::vector<float> x(hidden), w(n), y(hidden), ys(hidden), yref(hidden, 0.f);
+  std::vector<uint32_t> sel(n);
+  std::normal_distribution<float> nd;
+  for (auto& v : x) v = nd(rng);
+  for (uint32_t k = 0; k < n; ++k) { w[k] = 0.1f + 0.13f * k; sel[k] = k; }
+  for (uint32_t h = 0; h < hidden; ++h) y[h] = ys[h] = yref[h] = 0.25f * nd(rng);
+  std::vector<float> scratch(2 * n * inter, 1e30f);
+  int rc = affx_expert_ffn(des.data(), w.data(), n, L.cb.data(), x.data(), 10.0f, scratch.data(), y.data(), nullptr);
+  affx_layer abi = L.abi();
+  const size_t wsb = affx_decode_workspace_size(1, n, hidden, inter);
+  std::vector<uint8_t> ws(wsb, 0);
+  if (rc == 0)
+    rc = affx_decode_staged(&abi, x.data(), hidden, 1, 1, sel.data(), w.data(), n, ys.data(), hidden, 1, 1, ws.data(),
+                            wsb, nullptr);
+  L.oracle(x.data(), sel.data(), w.data(), 1, n, yref.data());
+  const bool same = memcmp(y.data(), ys.data(), y.size() * 4) == 0;
+  const double e = rel_l2(y, yref);
+  printf("ffnptr rc=%d identical to staged=%d rel_l2=%.3e %s\n", rc, (int)same, e, rc ? affx_last_error() : "");
+  return rc == 0 && same && e <= 1e-3 ? 0 : 1;
+}
+
+// The device router against the oracle's: token-major and dim-major logits, both rules, a
+// non-multiple-of-64 expert count; ids equal, weights within 2 ulp.
+int run_route(int argc, char** argv) {
+  const uint32_t T = atoi(argv[2]), E = atoi(argv[3]), K = atoi(argv[4]);
+  std::mt19937_64 rng(atoi(argv[5]));
+  std::normal_distribution<float> nd;
+  std::vector<float> lg(T * E), lgd(T * E), bias(E);
+  for (auto& v : lg) v = 2.0f * nd(rng);
+  for (auto& v : bias) v = 0.1f * nd(rng);
+  for (uint32_t t = 0; t < T; ++t)
+    for (uint32_t e = 0; e < E; ++e) lgd[(size_t)e * T + t] = lg[(size_t)t * E + e];
+  lg[3] = lg[7] = 50.0f;  // token 0: two tied past the softplus guard
+  lgd[3 * T] = lgd[7 * T] = 50.0f;
+  bool ok = true;
+  int worst = 0;
+  for (int rule = 0; rule < 2; ++rule)
+    for (int dm = 0; dm < 2; ++dm) {
+      std::vector<uint32_t> sel(T * K);
+      std::vector<float> w(T * K);
+      const int rc = dm ? affx_route_topk(lgd.data(), 1, T, bias.data(), T, E, K, rule, 1, 1.5f, sel.data(), w.data(), nullptr)
+                        : affx_route_topk(lg.data(), E, 1, bias.data(), T, E, K, rule, 1, 1.5f, sel.data(), w.data(), nullptr);
+      ok = ok && rc == 0;
+      for (uint32_t t = 0; t < T; ++t) {
+        uint32_t rs[16];
+        float rw[16];
+        if (rule == AFFX_ROUTE_ENGINE) orc_route_topk(lg.data() + (size_t)t * E, bias.data(), E, K, 1, 1.5f, rs, rw);
+        else orc_route_softmax_topk(lg.data() + (size_t)t * E, E, K, rs, rw);
+        for (uint32_t j = 0; j < K; ++j) {
+          int32_t a, b;
+          memcpy(&a, &w[t * K + j], 4);
+          memcpy(&b, &rw[j], 4);
+          worst = std::max(worst, std::abs(a - b));
+          ok = ok && sel[t * K + j] == rs[j];
+        }
+      }
+    }
+  printf("route ids equal=%d worst weight ulp=%d\n", (int)ok, worst);
+  return ok && worst <= 2 ? 0 : 1;
+}
+
 int run_quant(int argc, char** argv) {
   const uint32_t rows = atoi(argv[2]), cols = atoi(argv[3]);
   std::mt19937_64 rng(atoi(argv[4]));
@@ -317,6 +482,9 @@ int main(int argc, char** argv) {
   if (cmd == "quant" && argc >= 5) return run_quant(argc, argv);
   if (cmd == "dequant" && argc >= 5) return run_dequant(argc, argv);
   if (cmd == "timeout" && argc >= 8) return run_timeout(argc, argv);
+  if (cmd == "slots" && argc >= 8) return run_slots(argc, argv);
+  if (cmd == "ffnptr" && argc >= 6) return run_ffnptr(argc, argv);
+  if (cmd == "route" && argc >= 6) return run_route(argc, argv);
   fprintf(stderr, "usage: see header\n");
   return 2;
 }

@@ -19,6 +19,8 @@ Fixtures (data only: inputs and the reference's outputs):
   small.npz         small matrices (edge rows, importance, odd shapes) with the reference's
                     planes, dequantised values and GEMV outputs
   scalars.npz       E4M3 table, bf16 rounding cases, swiglu cases
+  route.npz         the engine router (route_topk): logits and bias cases with the chosen
+                    experts and weights
 """
 from __future__ import annotations
 
@@ -168,8 +170,39 @@ def make_scalars(O, R):
                         sw_out=sw, sw_out_nolimit=sw0)
 
 
+def make_route(R):
+    """route_topk cases: N(0,1) logits with and without a bias, exact ties (lower id wins), logits
+    past softplus's x > 20 guard, very negative logits (the sum floor), top-6 and top-8, with and
+    without renormalisation, scaling 1 and 1.5."""
+    rng = np.random.default_rng(17)
+    E = 256
+    cases = []
+    for i in range(40):
+        lg = rng.standard_normal(E).astype(np.float32) * (1.0 if i % 4 else 3.0)
+        bias = (rng.standard_normal(E).astype(np.float32) * 0.05) if i % 2 else None
+        if i % 5 == 0:
+            lg[rng.choice(E, 8, replace=False)] = lg.max() + 0.5          # an 8-way tie at the top
+        if i % 7 == 0:
+            lg[rng.choice(E, 3, replace=False)] = 25.0 + i                # past the x > 20 guard
+        if i == 39:
+            lg[:] = -60.0                                                  # sum below the fp16 floor
+        k = 8 if i % 3 == 0 else 6
+        norm = i % 6 != 5
+        scaling = 1.5 if i % 2 else 1.0
+        sel, w = R.route_topk(lg, bias, k, norm, scaling)
+        cases.append((lg, np.zeros(E, np.float32) if bias is None else bias, bias is not None, k, norm, scaling,
+                      np.pad(sel, (0, 8 - sel.size)), np.pad(w, (0, 8 - w.size))))
+    np.savez_compressed(os.path.join(OUT, "route.npz"),
+                        logits=np.stack([c[0] for c in cases]), bias=np.stack([c[1] for c in cases]),
+                        has_bias=np.array([c[2] for c in cases]), k=np.array([c[3] for c in cases], np.uint32),
+                        norm=np.array([c[4] for c in cases]), scaling=np.array([c[5] for c in cases], np.float32),
+                        sel=np.stack([c[6] for c in cases]).astype(np.uint32),
+                        w=np.stack([c[7] for c in cases]).astype(np.float32))
+
+
 def main():
     O, R = load_oracle(), load_ref()
+    make_route(R)
     make_scalars(O, R)
     cb = make_c1(O, R)
     make_small(O, R, cb)
@@ -177,4 +210,7 @@ def main():
 
 
 if __name__ == "__main__":
-    main()
+    if len(sys.argv) > 1 and sys.argv[1] == "route":     # only the router fixture
+        make_route(load_ref())
+    else:
+        main()

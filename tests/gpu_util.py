@@ -52,3 +52,23 @@ def oracle_ffn_tokens(orc, experts: dict, cb_f32, x: np.ndarray, sel: np.ndarray
                 orc.expert_ffn(experts[e], cb_f32, np.ascontiguousarray(x[t], np.float32), float(w[t, j]),
                                limit, y[i], hidden, inter)
     return y
+
+
+def slot_list(sel: np.ndarray, w: np.ndarray, n_experts: int):
+    """The slot list the grouped routes entry builds (the shape of the reference engine's device
+    plan, src/gpu/moe_plan.h:144-170): slots sorted by expert and, within an expert, by token;
+    expert e owns slots [start[e], start[e+1]); a token's slots in ord[run[t]:run[t+1]] in route
+    order. Returns (start, tok, wt, ord, run) as numpy arrays."""
+    T, k = sel.shape
+    flat = sel.reshape(-1).astype(np.int64)
+    valid = (flat >= 0) & (flat < n_experts)
+    pairs = np.nonzero(valid)[0]
+    order = pairs[np.argsort(flat[pairs], kind="stable")]
+    slot_of = np.full(T * k, -1, np.int64)
+    slot_of[order] = np.arange(order.size)
+    start = np.searchsorted(flat[order], np.arange(n_experts + 1)).astype(np.uint32)
+    tok = (order // k).astype(np.uint32)
+    wt = w.reshape(-1)[order].astype(np.float32)
+    ordv = slot_of[pairs].astype(np.uint32)
+    run = np.concatenate([[0], np.cumsum(valid.reshape(T, k).sum(1))]).astype(np.uint32)
+    return start, tok, wt, ordv, run

@@ -102,6 +102,27 @@ def test_host_permutation_is_the_stated_bijection(L, hidden, inter):
     np.testing.assert_array_equal(back, src)
 
 
+@pytest.mark.parametrize("hidden,inter", [(1024, 1024), (4096, 2048)])
+def test_matrix_permutation_composes_to_the_expert_permutation(L, hidden, inter):
+    """affx_matrix_to_device_layout on each matrix's own planes (separate buffers, as aff-gpucheck
+    uploads them) gives the same bytes as the whole-expert permutation at those planes."""
+    rng = np.random.default_rng(4)
+    lay = layout(L, hidden, inter)
+    _, off, size = lay
+    src = random_expert_container(rng, hidden, inter, lay)
+    dev = np.zeros_like(src)
+    assert L.affx_expert_to_device_layout(src.ctypes.data, dev.ctypes.data, hidden, inter) == 0
+    for m, (rows, cols) in enumerate(((inter, hidden), (inter, hidden), (hidden, inter))):
+        c = np.ascontiguousarray(src[off[3 * m]:off[3 * m] + size[3 * m]])
+        f = np.ascontiguousarray(src[off[3 * m + 1]:off[3 * m + 1] + size[3 * m + 1]])
+        dc, df = np.zeros_like(c), np.zeros_like(f)
+        assert L.affx_matrix_to_device_layout(c.ctypes.data, f.ctypes.data, dc.ctypes.data, df.ctypes.data,
+                                              rows, cols) == 0
+        np.testing.assert_array_equal(dc, dev[off[3 * m]:off[3 * m] + size[3 * m]])
+        np.testing.assert_array_equal(df, dev[off[3 * m + 1]:off[3 * m + 1] + size[3 * m + 1]])
+    assert L.affx_matrix_to_device_layout(c.ctypes.data, f.ctypes.data, dc.ctypes.data, df.ctypes.data, 15, 1024) < 0
+
+
 def test_bad_arguments_are_refused(L):
     buf = np.zeros(16, np.uint8)
     assert L.affx_expert_to_device_layout(buf.ctypes.data, buf.ctypes.data, 4096, 2048) < 0

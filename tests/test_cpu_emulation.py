@@ -95,3 +95,20 @@ def test_decode_wait_give_up_fails_loudly(emu):
     # affx_decode_status reports it, and after the reset the next call is right
     out = run(emu, "timeout", 1024, 1024, 6, 2, 3, 8, cus=4)
     assert "timeout path ok=1" in out, out
+
+
+def test_grouped_slot_list_emulated(emu):
+    # the slot-list entry: bit-identical to the routes entry on the list the routes build, and
+    # within tolerance on a reordered list
+    out = run(emu, "slots", 1024, 1024, 4, 6, 2, 9, timeout=900)
+    assert "routes==slots=1" in out, out
+
+
+def test_expert_ffn_pointer_table_emulated(emu):
+    out = run(emu, "ffnptr", 1024, 1024, 3, 12)
+    assert "identical to staged=1" in out, out
+
+
+def test_route_emulated(emu):
+    out = run(emu, "route", 21, 100, 6, 4)
+    assert "route ids equal=1" in out, out

@@ -19,7 +19,7 @@ import os
 import numpy as np
 import pytest
 
-from gpu_util import bf16_bits, oracle_ffn_tokens, rel_l2
+from gpu_util import bf16_bits, oracle_ffn_tokens, rel_l2, slot_list
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -200,3 +200,26 @@ def test_config4_full_shape_subsample_vs_oracle(ax, orc, c1_codebook, layer, lo)
           f"{len(experts)} experts: rel_l2={err:.3e}, worst token {worst:.3e}")
     assert err <= TOL and worst <= TOL
     assert np.isfinite(y).all()
+
+
+def test_config4_slot_list_entry_equals_routes_entry(ax, layer):
+    """The full prefill through the slot-list entry (the list the routes entry builds, given by the
+    caller) gives the routes entry's output bit for bit."""
+    import ctypes as C
+    from affinity_amd import synthetic
+    from affinity_amd._lib import check, lib
+    _, pool = layer
+    T = 4096
+    sel, w = synthetic.zipf_routes(T)
+    xb = ax.gen_normal(synthetic.S_X, T * H, 1.0).view(T, H).to(torch.bfloat16).contiguous()
+    yr = ax.expert_ffn_grouped(pool, xb, torch.from_numpy(sel).cuda(), torch.from_numpy(w).cuda())
+    start, tok, wt, ordv, run = (torch.from_numpy(np.ascontiguousarray(a)).cuda() for a in slot_list(sel, w, E))
+    ys = torch.zeros_like(yr)
+    ws = ax.GroupedWorkspace(T, K, E)
+    L = pool.layer()
+    check(lib().affx_expert_ffn_grouped_slots(C.byref(L), xb.data_ptr(), 0, T, start.data_ptr(), tok.data_ptr(),
+                                              wt.data_ptr(), ordv.data_ptr(), run.data_ptr(), int(tok.numel()),
+                                              ys.data_ptr(), 0, ws.buf.data_ptr(), ws.bytes,
+                                              torch.cuda.current_stream().cuda_stream), "grouped_slots")
+    torch.cuda.synchronize()
+    assert torch.equal(ys, yr)

@@ -390,3 +390,32 @@ def test_route_softmax_topk(orc):
     p = np.exp(lg[order].astype(np.float64) - lg.max())
     np.testing.assert_allclose(w, p / p.sum(), rtol=1e-6)
     assert abs(w.sum() - 1) < 1e-6
+
+
+def test_route_topk_matches_reference(orc):
+    """orc_route_topk (the engine router, src/engine/ops.cpp:62-92) against the reference's own
+    outputs (tests/golden/route.npz: ties, the softplus guard, the sum floor, bias, top-6/8,
+    renormalisation on and off, scaling 1 and 1.5), bit for bit; and the closed form of the
+    score on a grid."""
+    d = np.load(os.path.join(GOLDEN, "route.npz"))
+    for i in range(d["logits"].shape[0]):
+        k = int(d["k"][i])
+        bias = d["bias"][i] if d["has_bias"][i] else None
+        sel, w = orc.route_topk(d["logits"][i], bias, k, bool(d["norm"][i]), float(d["scaling"][i]))
+        np.testing.assert_array_equal(sel, d["sel"][i][:k], err_msg=str(i))
+        np.testing.assert_array_equal(w.view(np.uint32), d["w"][i][:k].view(np.uint32), err_msg=str(i))
+    x = np.linspace(-30, 40, 701).astype(np.float32)
+    got = np.array([orc.lib.orc_sqrtsoftplus(float(v)) for v in x], np.float32)
+    ref = np.sqrt(np.where(x > 20, x.astype(np.float64), np.log1p(np.exp(x.astype(np.float64)))))
+    np.testing.assert_allclose(got, ref, rtol=3e-7, atol=1e-30)
+
+
+def test_route_topk_matches_live_reference(orc, ref):
+    rng = np.random.default_rng(23)
+    for i in range(200):
+        lg = (rng.standard_normal(256) * rng.uniform(0.1, 8)).astype(np.float32)
+        bias = rng.standard_normal(256).astype(np.float32) * 0.1 if i % 2 else None
+        a = orc.route_topk(lg, bias, 6, True, 1.5)
+        b = ref.route_topk(lg, bias, 6, True, 1.5)
+        np.testing.assert_array_equal(a[0], b[0])
+        np.testing.assert_array_equal(a[1].view(np.uint32), b[1].view(np.uint32))
