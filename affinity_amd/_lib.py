@@ -33,6 +33,15 @@ class AffxLayer(C.Structure):
                 ("inter", _u32), ("codebook", _vp), ("swiglu_limit", C.c_float)]
 
 
+class AffxDenseFp8(C.Structure):
+    _fields_ = [("data", _vp), ("scales", _vp), ("rows", _u64), ("cols", _u64)]
+
+
+class AffxSharedExpert(C.Structure):
+    _fields_ = [("gate", AffxDenseFp8), ("up", AffxDenseFp8), ("down", AffxDenseFp8), ("hidden", _u32),
+                ("inter", _u32), ("swiglu_limit", C.c_float)]
+
+
 class AffxEngineCtx(C.Structure):
     _fields_ = [("layers", C.POINTER(AffxLayer)), ("n_layers", _u32), ("d_x", _vp),
                 ("d_block", _vp), ("nb_stride", _u32), ("workspace", _vp),
@@ -86,6 +95,16 @@ _SIGS = {
                                        C.c_int, _vp, C.c_size_t, _vp], C.c_int),
     "affx_route_topk": ([_vp, _u64, _u64, _vp, _u32, _u32, _u32, C.c_int, C.c_int, C.c_float, _vp, _vp, _vp],
                         C.c_int),
+    "affx_shared_decode_workspace_size": ([_u32, _u32, _u32], C.c_size_t),
+    "affx_shared_batch_workspace_size": ([_u32, _u32, _u32], C.c_size_t),
+    "affx_shared_expert_decode": ([C.POINTER(AffxSharedExpert), _vp, _u64, _u64, _u32, _vp, _u64, _u64, C.c_int,
+                                   _vp, C.c_size_t, _vp], C.c_int),
+    "affx_shared_expert_batch": ([C.POINTER(AffxSharedExpert), _vp, _vp, _u32, _vp, C.c_int, _vp, C.c_size_t, _vp],
+                                 C.c_int),
+    "affx_hc_post": ([_vp, _vp, _vp, _vp, _vp, _u32, _u32, C.c_int, _vp], C.c_int),
+    "affx_hc_add": ([_vp, _vp, _u32, C.c_int, _vp], C.c_int),
+    "affx_hc_post_batch": ([_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, C.c_int, _vp], C.c_int),
+    "affx_hc_add_batch": ([_vp, _vp, _u64, C.c_int, _vp], C.c_int),
     "affx_expert_ffn_batch": ([_vp, _u32, _vp, _vp, _u32, _u32, _vp], _u32),
     "affx_batch_workspace_size": ([_u32, _u32, _u32, _u32, _u32], C.c_size_t),
     "affx_selftest_mfma_fp8": ([_vp, _vp, _vp, _vp], C.c_int),

@@ -69,33 +69,7 @@ __global__ void __launch_bounds__(256) decode_prep_kernel(const float* __restric
   if (blockIdx.x < M * nst) {
     const uint32_t t = blockIdx.x / nst, S = blockIdx.x % nst;
     __shared__ float red[4];
-    const uint32_t h0 = S * kTileCols + 4 * tid;
-    float v[4];
-    float amax = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[i] = x[t * xts + (h0 + i) * xds];
-      amax = fmaxf(amax, fabsf(v[i]));
-    }
-    for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
-    if ((tid & 63) == 0) red[tid >> 6] = amax;
-    __syncthreads();
-    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    // amax * 2^sigma in [128, 256): below E4M3's 448, one binade of headroom
-    const int sigma = amax > 0.f ? 7 - ilogbf(amax) : 0;
-    uint32_t q0 = 0, q1 = 0, q2 = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      uint32_t b0, b1, b2;
-      split3(ldexpf(v[i], sigma), b0, b1, b2);
-      q0 |= b0 << (8 * i);
-      q1 |= b1 << (8 * i);
-      q2 |= b2 << (8 * i);
-    }
-    uint32_t* dst = reinterpret_cast<uint32_t*>(xq + (uint64_t)t * kTerms * hidden + h0);
-    dst[0] = q0;
-    dst[hidden / 4] = q1;
-    dst[2 * (hidden / 4)] = q2;
+    const int sigma = segment_terms(x, xts, xds, t, S, hidden, xq, red);
     if (tid == 0) plan->x_sigma[t][S] = sigma;
     return;
   }

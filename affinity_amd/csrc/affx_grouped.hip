@@ -223,16 +223,6 @@ __global__ void __launch_bounds__(256) grouped_place_kernel(
 }
 
 // ------------------------------------------------------------------------------------------------
-// K order of the B rows
-// ------------------------------------------------------------------------------------------------
-// Activation rows (x terms for gate/up, SwiGLU terms for down) are stored in MFMA-step order:
-// column col = 1024 s + 256 kg + 32 m + i (super-step s, lane group kg, step m, i < 32) sits at
-// byte (8 s + m) * 128 + 32 kg + i, so the 128 bytes one MFMA step needs from a row are one run.
-__host__ __device__ inline uint32_t kperm(uint32_t col) {
-  return ((col >> 10) * 8u + ((col >> 5) & 7u)) * 128u + ((col >> 8) & 3u) * 32u + (col & 31u);
-}
-
-// ------------------------------------------------------------------------------------------------
 // activation terms: per token an exponent and tx E4M3 terms of every element, in step order
 // ------------------------------------------------------------------------------------------------
 __global__ void __launch_bounds__(256) grouped_prep_x_kernel(const uint16_t* __restrict__ x,
@@ -245,62 +235,17 @@ __global__ void __launch_bounds__(256) grouped_prep_x_kernel(const uint16_t* __r
                                                              uint8_t* __restrict__ xq,
                                                              uint32_t* __restrict__ zeros,
                                                              uint32_t zero_words) {
-  // thread tid holds the 8-element chunks tid + 256 i (hidden <= 8192: at most 4), loaded once
-  constexpr int kMaxChunks = 4;
-  const uint32_t t = blockIdx.x, tid = threadIdx.x, nch = hidden / 8;
+  const uint32_t t = blockIdx.x, tid = threadIdx.x;
   if (t == 0)  // the B row of unused columns
     for (uint32_t i = tid; i < zero_words; i += 256) zeros[i] = 0u;
   __shared__ float red[4];
-  const uint4* xr = reinterpret_cast<const uint4*>(x + (uint64_t)t * hidden);
-  const uint4* lr = xlo ? reinterpret_cast<const uint4*>(xlo + (uint64_t)t * hidden) : nullptr;
-  uint4 hv[kMaxChunks], lv[kMaxChunks];
-#pragma unroll
-  for (int i = 0; i < kMaxChunks; ++i) {
-    const uint32_t ch = tid + 256u * i;
-    hv[i] = ch < nch ? xr[ch] : uint4{0u, 0u, 0u, 0u};
-    lv[i] = (lr && ch < nch) ? lr[ch] : uint4{0u, 0u, 0u, 0u};
-  }
-  float v[kMaxChunks][8];
-  float amax = 0.f;
-#pragma unroll
-  for (int i = 0; i < kMaxChunks; ++i) {
-    const uint32_t hw[4] = {hv[i].x, hv[i].y, hv[i].z, hv[i].w}, lw[4] = {lv[i].x, lv[i].y, lv[i].z, lv[i].w};
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      v[i][2 * k] = __uint_as_float(hw[k] << 16) + __uint_as_float(lw[k] << 16);
-      v[i][2 * k + 1] = __uint_as_float(hw[k] & 0xFFFF0000u) + __uint_as_float(lw[k] & 0xFFFF0000u);
-    }
-#pragma unroll
-    for (int k = 0; k < 8; ++k) amax = fmaxf(amax, fabsf(v[i][k]));
-  }
-  for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
-  if ((tid & 63) == 0) red[tid >> 6] = amax;
-  __syncthreads();
-  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  const int sigma = amax > 0.f ? 7 - ilogbf(amax) : 0;
-  {  // the exponent goes to each of the token's slots, for the gate/up epilogue
-    const uint32_t r1 = min(run[t + 1], n_slots);
-    for (uint32_t i = min(run[t], r1) + tid; i < r1; i += 256) {
-      const uint32_t sl = ord[i];
-      if (sl < n_slots) slot_sigma[sl] = sigma;
-    }
-  }
-  // E4M3 terms, 8 bytes per term and chunk (8 consecutive columns stay consecutive in step order)
-  uint8_t* row = xq + (uint64_t)t * tx * hidden;
-#pragma unroll
-  for (int i = 0; i < kMaxChunks; ++i) {
-    const uint32_t ch = tid + 256u * i;
-    if (ch < nch) {
-      uint32_t a0, a1, a2, b0, b1, b2;
-      split3x4(ldexpf(v[i][0], sigma), ldexpf(v[i][1], sigma), ldexpf(v[i][2], sigma), ldexpf(v[i][3], sigma),
-               a0, a1, a2);
-      split3x4(ldexpf(v[i][4], sigma), ldexpf(v[i][5], sigma), ldexpf(v[i][6], sigma), ldexpf(v[i][7], sigma),
-               b0, b1, b2);
-      uint8_t* dst = row + kperm(8 * ch);
-      *reinterpret_cast<uint2*>(dst) = uint2{a0, b0};
-      *reinterpret_cast<uint2*>(dst + hidden) = uint2{a1, b1};
-      if (tx == 3) *reinterpret_cast<uint2*>(dst + 2 * (uint64_t)hidden) = uint2{a2, b2};
-    }
+  const int sigma = row_terms<true>(x + (uint64_t)t * hidden, xlo ? xlo + (uint64_t)t * hidden : nullptr, hidden,
+                                    tx, xq + (uint64_t)t * tx * hidden, red);
+  // the exponent goes to each of the token's slots, for the gate/up epilogue
+  const uint32_t r1 = min(run[t + 1], n_slots);
+  for (uint32_t i = min(run[t], r1) + tid; i < r1; i += 256) {
+    const uint32_t sl = ord[i];
+    if (sl < n_slots) slot_sigma[sl] = sigma;
   }
 }
 

@@ -222,6 +222,74 @@ __device__ __forceinline__ void split3x2(float v0, float v1, uint32_t& q0, uint3
   q2 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v0, v1, 0, false) & 0xFFFFu;
 }
 
+// ------------------------------------------------------------------------------------------------
+// K order of the B rows
+// ------------------------------------------------------------------------------------------------
+// The routed GEMM's activation rows (x terms for gate/up, SwiGLU terms for down) are stored in
+// MFMA-step order: column col = 1024 s + 256 kg + 32 m + i (super-step s, lane group kg, step m,
+// i < 32) sits at byte (8 s + m) * 128 + 32 kg + i, so the 128 bytes one MFMA step needs from a
+// row are one run.
+__host__ __device__ inline uint32_t kperm(uint32_t col) {
+  return ((col >> 10) * 8u + ((col >> 5) & 7u)) * 128u + ((col >> 8) & 3u) * 32u + (col & 31u);
+}
+
+// One token's bf16 row x (+ the low part xlo, or null): its exponent sigma (returned: the row's
+// largest magnitude times 2^sigma lies in [128, 256)) and tx (2 or 3) E4M3 terms of every element
+// times 2^sigma, term j at row + j * hidden + pos(col), pos = kperm (KPERM) or the identity. All
+// 256 threads of the workgroup call it (red: 4 floats of LDS). x, xlo 16-byte aligned; hidden a
+// multiple of 8, at most 8192.
+template <bool KPERM>
+__device__ __forceinline__ int row_terms(const uint16_t* __restrict__ x, const uint16_t* __restrict__ xlo,
+                                         uint32_t hidden, uint32_t tx, uint8_t* __restrict__ row, float* red) {
+  // thread tid holds the 8-element chunks tid + 256 i (at most 4), loaded once
+  constexpr int kMaxChunks = 4;
+  const uint32_t tid = threadIdx.x, nch = hidden / 8;
+  const uint4* xr = reinterpret_cast<const uint4*>(x);
+  const uint4* lr = reinterpret_cast<const uint4*>(xlo);
+  uint4 hv[kMaxChunks], lv[kMaxChunks];
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; ++i) {
+    const uint32_t ch = tid + 256u * i;
+    hv[i] = ch < nch ? xr[ch] : uint4{0u, 0u, 0u, 0u};
+    lv[i] = (lr && ch < nch) ? lr[ch] : uint4{0u, 0u, 0u, 0u};
+  }
+  float v[kMaxChunks][8];
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; ++i) {
+    const uint32_t hw[4] = {hv[i].x, hv[i].y, hv[i].z, hv[i].w}, lw[4] = {lv[i].x, lv[i].y, lv[i].z, lv[i].w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      v[i][2 * k] = __uint_as_float(hw[k] << 16) + __uint_as_float(lw[k] << 16);
+      v[i][2 * k + 1] = __uint_as_float(hw[k] & 0xFFFF0000u) + __uint_as_float(lw[k] & 0xFFFF0000u);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) amax = fmaxf(amax, fabsf(v[i][k]));
+  }
+  for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+  if ((tid & 63) == 0) red[tid >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const int sigma = amax > 0.f ? 7 - ilogbf(amax) : 0;
+  // E4M3 terms, 8 bytes per term and chunk (8 consecutive columns stay consecutive in step order)
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; ++i) {
+    const uint32_t ch = tid + 256u * i;
+    if (ch < nch) {
+      uint32_t a0, a1, a2, b0, b1, b2;
+      split3x4(ldexpf(v[i][0], sigma), ldexpf(v[i][1], sigma), ldexpf(v[i][2], sigma), ldexpf(v[i][3], sigma),
+               a0, a1, a2);
+      split3x4(ldexpf(v[i][4], sigma), ldexpf(v[i][5], sigma), ldexpf(v[i][6], sigma), ldexpf(v[i][7], sigma),
+               b0, b1, b2);
+      uint8_t* dst = row + (KPERM ? kperm(8 * ch) : 8 * ch);
+      *reinterpret_cast<uint2*>(dst) = uint2{a0, b0};
+      *reinterpret_cast<uint2*>(dst + hidden) = uint2{a1, b1};
+      if (tx == 3) *reinterpret_cast<uint2*>(dst + 2 * (uint64_t)hidden) = uint2{a2, b2};
+    }
+  }
+  return sigma;
+}
+
 // Calls f(IConst<I>{}) for I = B .. E-1: a loop whose index is a compile-time constant in the body.
 template <int N>
 struct IConst {

@@ -236,3 +236,75 @@ def fill_synthetic_experts(container: torch.Tensor, first: int, count: int, code
         check(lib().affx_fill_expert(container.data_ptr() + e * stride, hidden, inter,
                                      codebook_f32.data_ptr(), int(seed_of(e)), scratch.data_ptr(),
                                      _stream(stream)), "affx_fill_expert")
+
+
+# ---- the step after: shared expert and hyper-connection post ------------------------------------
+
+class SharedExpert:
+    """A layer's FP8 shared expert on the device (the reference's shexp_gate/up/down DenseW,
+    src/engine/model.h:125-127): E4M3 weights [rows x cols] (uint8 tensors) and UE8M0 tile scales
+    [rows / 128][cols / 128]."""
+
+    def __init__(self, gate, gate_s, up, up_s, down, down_s, swiglu_limit: float = SWIGLU_LIMIT):
+        inter, hidden = gate.shape
+        self.tensors = (gate, gate_s, up, up_s, down, down_s)   # keeps the memory alive
+        mk = lambda w, s: _lib.AffxDenseFp8(w.data_ptr(), s.data_ptr(), w.shape[0], w.shape[1])
+        self.abi = _lib.AffxSharedExpert(mk(gate, gate_s), mk(up, up_s), mk(down, down_s), hidden, inter,
+                                         float(swiglu_limit))
+        self.hidden, self.inter = hidden, inter
+
+    def decode(self, x: torch.Tensor, y: torch.Tensor, accumulate: bool = True, stream=None) -> torch.Tensor:
+        """y (+)= W_d . swiglu(W_g x, W_u x) for M <= 8 f32 tokens x [M][hidden] (DenseOps::shexp,
+        src/engine/model.h:314-319)."""
+        M = x.shape[0]
+        ws = torch.empty(lib().affx_shared_decode_workspace_size(M, self.hidden, self.inter), dtype=torch.uint8,
+                         device=x.device)
+        check(lib().affx_shared_expert_decode(C.byref(self.abi), x.data_ptr(), x.stride(0), x.stride(1), M,
+                                              y.data_ptr(), y.stride(0), y.stride(1), int(accumulate),
+                                              ws.data_ptr(), ws.numel(), _stream(stream)), "shared_expert_decode")
+        return y
+
+    def batch(self, x: torch.Tensor, y: torch.Tensor, x_lo: torch.Tensor | None = None, accumulate: bool = True,
+              stream=None) -> torch.Tensor:
+        """y (+)= the shared expert of every bf16 token row of x [T][hidden] (BatchOps::shexp,
+        src/engine/model.h:504-505)."""
+        T = x.shape[0]
+        ws = torch.empty(lib().affx_shared_batch_workspace_size(T, self.hidden, self.inter), dtype=torch.uint8,
+                         device=x.device)
+        check(lib().affx_shared_expert_batch(C.byref(self.abi), x.data_ptr(), 0 if x_lo is None else x_lo.data_ptr(),
+                                             T, y.data_ptr(), int(accumulate), ws.data_ptr(), ws.numel(),
+                                             _stream(stream)), "shared_expert_batch")
+        return y
+
+
+def hc_post(block: torch.Tensor, hc: torch.Tensor, post: torch.Tensor | None, comb: torch.Tensor | None,
+            out_hc: torch.Tensor | None = None, zero_block: bool = True, stream=None) -> torch.Tensor:
+    """The sublayer's hyper-connection post for one token (DenseGpu::hc_post,
+    src/gpu/dense_gpu.hip:2394-2465): with a control (post, comb) the next state
+    [n_hc][n_embd] = block * post[dst] + sum_src comb[dst + src n_hc] * hc[src]; without one,
+    hc[0] += block in place. The block is left zero when zero_block."""
+    n_hc, n = hc.shape
+    s = _stream(stream)
+    if post is None:
+        check(lib().affx_hc_add(hc.data_ptr(), block.data_ptr(), n, int(zero_block), s), "hc_add")
+        return hc
+    out_hc = torch.empty_like(hc) if out_hc is None else out_hc
+    check(lib().affx_hc_post(out_hc.data_ptr(), block.data_ptr(), hc.data_ptr(), post.data_ptr(), comb.data_ptr(),
+                             n, n_hc, int(zero_block), s), "hc_post")
+    return out_hc
+
+
+def hc_post_batch(block: torch.Tensor, hc: torch.Tensor, post: torch.Tensor | None, comb: torch.Tensor | None,
+                  out_hc: torch.Tensor | None = None, zero_block: bool = True, stream=None) -> torch.Tensor:
+    """The batch form over the engine's dim-major arenas (batch_hc_post, src/gpu/dense_gpu.hip:
+    4517-4534): hc bf16 [n_hc][n_embd][nb], block f32 [n_embd][nb], post [n_hc][nb], comb
+    [n_hc * n_hc][nb]; without a control hc lane 0 += block in place."""
+    n_hc, n, nb = hc.shape
+    s = _stream(stream)
+    if post is None:
+        check(lib().affx_hc_add_batch(hc.data_ptr(), block.data_ptr(), n * nb, int(zero_block), s), "hc_add_batch")
+        return hc
+    out_hc = torch.empty_like(hc) if out_hc is None else out_hc
+    check(lib().affx_hc_post_batch(out_hc.data_ptr(), block.data_ptr(), hc.data_ptr(), post.data_ptr(),
+                                   comb.data_ptr(), n, n_hc, nb, int(zero_block), s), "hc_post_batch")
+    return out_hc

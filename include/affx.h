@@ -317,6 +317,79 @@ int affx_route_topk(const float* logits, uint64_t tok_stride, uint64_t expert_st
                     const float* bias, uint32_t n_tok, uint32_t n_expert, uint32_t top_k, int rule,
                     int norm_topk_prob, float routed_scaling, uint32_t* sel, float* w, void* stream);
 
+/* ---- the step after: shared expert and hyper-connection post -------------------------------- */
+
+/* One FP8 dense matrix as the container holds it: the reference's DenseW with quant
+ * AFF_FP8_E4M3 (src/engine/ops.h:142-151; format src/engine/matvec_fp8.inc:8-10). data: device
+ * E4M3 bytes, row-major [rows x cols], 16-byte aligned; scales: device UE8M0 bytes, one per
+ * 128 x 128 tile, row-major [rows / 128][cols / 128], 4-byte aligned. E4M3 0x7F / 0xFF are NaN
+ * (as in the reference's scalar decode, src/quant/source_dtypes.cpp:24-25). */
+typedef struct affx_dense_fp8 {
+  const void* data;
+  const uint8_t* scales;
+  uint64_t rows, cols;
+} affx_dense_fp8;
+
+/* The shared expert of a layer: gate, up [inter x hidden] and down [hidden x inter] (the
+ * reference's shexp_gate/up/down, src/engine/model.h:125-127), hidden and inter multiples of 1024
+ * (inter <= 8192; hidden <= 4096 for decode, 8192 for the batch), the SwiGLU clamp limit in
+ * (0, 1e6] (see affx_layer). */
+typedef struct affx_shared_expert {
+  affx_dense_fp8 gate, up, down;
+  uint32_t hidden, inter;
+  float swiglu_limit;
+} affx_shared_expert;
+
+size_t affx_shared_decode_workspace_size(uint32_t m_tokens, uint32_t hidden, uint32_t inter);
+size_t affx_shared_batch_workspace_size(uint32_t n_tok, uint32_t hidden, uint32_t inter);
+
+/* The shared expert on m_tokens <= 8 tokens: y[t] (+)= W_d . swiglu(W_g x[t], W_u x[t]).
+ * Replaces DenseOps::shexp (src/engine/model.h:314-319; DenseGpu::shexp, src/gpu/dense_gpu.hip:
+ * 2030-2116) for a resident shared expert: accumulate = 1 is its out == nullptr form (added into
+ * the device block the routed experts wrote), 0 stores. x and y as in affx_expert_ffn_decode
+ * (element (t, h) at x[t * x_tok_stride + h * x_dim_stride]). The host composition it matches is
+ * src/engine/model.cpp:1214-1222. Accumulating after the routed experts on the same stream gives
+ * the host's order: block = routed sum, then block += shared. Three launches, no
+ * synchronisation. */
+int affx_shared_expert_decode(const affx_shared_expert* shexp, const float* x, uint64_t x_tok_stride,
+                              uint64_t x_dim_stride, uint32_t m_tokens, float* y, uint64_t y_tok_stride,
+                              uint64_t y_dim_stride, int accumulate, void* workspace, size_t workspace_bytes,
+                              void* stream);
+
+/* The shared expert on a chunk of n_tok tokens: y[t] (+)= W_d . swiglu(W_g x[t], W_u x[t]) for
+ * every token. Replaces BatchOps::shexp (src/engine/model.h:504-505; DenseGpu::batch_shexp,
+ * src/gpu/dense_gpu.hip:4897-4950, which accumulates into the batch block). x (and x_lo, or NULL)
+ * bf16 [n_tok][hidden] as in affx_expert_ffn_grouped (x_lo carries the low part of an f32
+ * input); y f32 [n_tok][hidden]; all 16-byte aligned. Three launches, no synchronisation. */
+int affx_shared_expert_batch(const affx_shared_expert* shexp, const void* x, const void* x_lo, uint32_t n_tok,
+                             float* y, int accumulate, void* workspace, size_t workspace_bytes, void* stream);
+
+/* The sublayer's hyper-connection post for one token, with a control: lane dst of out_hc
+ * [n_hc][n_embd] = block * post[dst] + sum over src in order of comb[dst + src * n_hc] * hc lane
+ * src, bit for bit the host's hc_expand (src/engine/ops.cpp:470-482). Replaces DenseGpu::hc_post's
+ * control arm (src/gpu/dense_gpu.hip:2394-2465, hc_expand_reg_kernel 1703-1710). zero_block = 1
+ * leaves the block zero for the next sublayer, as the reference's kernel does. n_hc in {1, 2, 4,
+ * 8} (the reference silently runs 4 for any other value; this declines it). All f32, device. On
+ * one GPU the block is already whole: the sublayer's block_reduce (model.cpp:1759-1762) is the
+ * identity and there is no exchange to fold in. */
+int affx_hc_post(float* out_hc, float* block, const float* hc, const float* post, const float* comb,
+                 uint32_t n_embd, uint32_t n_hc, int zero_block, void* stream);
+
+/* hc_post for a layer without a control: lane 0 += block (src/engine/model.cpp:1237-1238;
+ * hc_add_kernel, src/gpu/dense_gpu.hip:1717-1724). */
+int affx_hc_add(float* hc, float* block, uint32_t n_embd, int zero_block, void* stream);
+
+/* The batch form over the engine's dim-major arenas of nb tokens (batch_hc_post,
+ * src/gpu/dense_gpu.hip:4517-4534; batch_hc_expand_reg_kernel, src/gpu/batch_kernels.hip:
+ * 1977-2002): hc and out_hc bf16 [n_hc][n_embd][nb], block f32 [n_embd][nb], post f32 [n_hc][nb],
+ * comb f32 [n_hc * n_hc][nb]; each result rounded to bf16 (nearest even) once. */
+int affx_hc_post_batch(uint16_t* out_hc, float* block, const uint16_t* hc, const float* post, const float* comb,
+                       uint32_t n_embd, uint32_t n_hc, uint32_t nb, int zero_block, void* stream);
+
+/* Lane 0 of the bf16 batch state += block over n = n_embd * nb elements, rounded to bf16
+ * (batch_hc_add_bf16_kernel, src/gpu/batch_kernels.hip:2011-2018). */
+int affx_hc_add_batch(uint16_t* hc, float* block, uint64_t n, int zero_block, void* stream);
+
 /* ---- engine hook ---------------------------------------------------------------------------- */
 
 /* State behind affx_expert_ffn_batch: the per-layer expert tables and the engine's device

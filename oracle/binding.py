@@ -89,6 +89,13 @@ class Oracle:
         L.orc_sqrtsoftplus.restype = C.c_float
         L.orc_route_topk.argtypes = [_f32p, _f32p, C.c_uint32, C.c_uint32, C.c_int, C.c_float, _u32p, _f32p]
         L.orc_route_topk.restype = C.c_uint32
+        L.orc_e8m0_to_float.argtypes = [C.c_uint8]
+        L.orc_e8m0_to_float.restype = C.c_float
+        L.orc_matvec_fp8.argtypes = [_u8p, _u8p, C.c_uint64, C.c_uint64, _f32p, _f32p]
+        L.orc_shared_expert.argtypes = [_u8p, _u8p, _u8p, _u8p, _u8p, _u8p, C.c_uint64, C.c_uint64, C.c_float,
+                                        _f32p, _f32p]
+        L.orc_hc_expand.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, C.c_uint32, C.c_uint32]
+        L.orc_hc_add.argtypes = [_f32p, _f32p, C.c_uint32]
 
     # -- threads ---------------------------------------------------------------------------
     def set_threads(self, n: int) -> None:
@@ -220,6 +227,43 @@ class Oracle:
         self.lib.orc_route_softmax_topk(_p(lg, _f32p), lg.size, k, _p(sel, _u32p), _p(w, _f32p))
         return sel, w
 
+    # -- shared expert and hyper-connection post -----------------------------------------------
+    def e8m0_to_float(self, b: int) -> float:
+        return float(self.lib.orc_e8m0_to_float(b))
+
+    def matvec_fp8(self, w: np.ndarray, s: np.ndarray, x: np.ndarray) -> np.ndarray:
+        """w [rows x cols] E4M3 bytes, s [ceil(rows/128) x ceil(cols/128)] UE8M0 bytes."""
+        rows, cols = w.shape
+        out = np.zeros(rows, np.float32)
+        self.lib.orc_matvec_fp8(_p(w, _u8p), _p(s, _u8p), rows, cols,
+                                _p(np.ascontiguousarray(x, np.float32), _f32p), _p(out, _f32p))
+        return out
+
+    def shared_expert(self, wg, sg, wu, su, wd, sd, x: np.ndarray, limit: float = 10.0,
+                      block: np.ndarray | None = None) -> np.ndarray:
+        """block += W_d . swiglu(W_g x, W_u x) for one token (FP8 dense weights)."""
+        inter, hidden = wg.shape
+        block = np.zeros(hidden, np.float32) if block is None else block
+        self.lib.orc_shared_expert(_p(wg, _u8p), _p(sg, _u8p), _p(wu, _u8p), _p(su, _u8p), _p(wd, _u8p),
+                                   _p(sd, _u8p), hidden, inter, limit,
+                                   _p(np.ascontiguousarray(x, np.float32), _f32p), _p(block, _f32p))
+        return block
+
+    def hc_expand(self, block: np.ndarray, hc: np.ndarray, post: np.ndarray, comb: np.ndarray) -> np.ndarray:
+        """hc [n_hc x n_embd], post [n_hc], comb [n_hc * n_hc] -> next state [n_hc x n_embd]."""
+        n_hc, n = hc.shape
+        out = np.zeros((n_hc, n), np.float32)
+        self.lib.orc_hc_expand(_p(out, _f32p), _p(np.ascontiguousarray(block, np.float32), _f32p),
+                               _p(np.ascontiguousarray(hc, np.float32), _f32p),
+                               _p(np.ascontiguousarray(post, np.float32), _f32p),
+                               _p(np.ascontiguousarray(comb, np.float32), _f32p), n, n_hc)
+        return out
+
+    def hc_add(self, hc: np.ndarray, block: np.ndarray) -> np.ndarray:
+        out = np.ascontiguousarray(hc, np.float32).copy()
+        self.lib.orc_hc_add(_p(out, _f32p), _p(np.ascontiguousarray(block, np.float32), _f32p), block.size)
+        return out
+
 
 class RefLib:
     """The reference's own CPU path (oracle/_ref/libaffref.so)."""
@@ -258,6 +302,10 @@ class RefLib:
         L.affref_write_container.restype = C.c_int
         L.affref_expert_offset.argtypes = [C.c_char_p, C.c_uint32, C.c_uint32]
         L.affref_expert_offset.restype = C.c_int64
+        L.affref_matvec_fp8.argtypes = [_u8p, _u8p, C.c_uint64, C.c_uint64, _f32p, _f32p]
+        L.affref_e8m0_to_float.argtypes = [C.c_uint8]
+        L.affref_e8m0_to_float.restype = C.c_float
+        L.affref_hc_expand.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, C.c_uint32, C.c_uint32]
 
     def collect_samples(self, w: np.ndarray, budget: int) -> np.ndarray:
         rows, cols = w.shape
@@ -352,6 +400,25 @@ class RefLib:
 
     def e4m3_to_float(self, b: int) -> float:
         return float(self.lib.affref_e4m3_to_float(b))
+
+    def e8m0_to_float(self, b: int) -> float:
+        return float(self.lib.affref_e8m0_to_float(b))
+
+    def matvec_fp8(self, w: np.ndarray, s: np.ndarray, x: np.ndarray) -> np.ndarray:
+        rows, cols = w.shape
+        out = np.zeros(rows, np.float32)
+        self.lib.affref_matvec_fp8(_p(w, _u8p), _p(s, _u8p), rows, cols,
+                                   _p(np.ascontiguousarray(x, np.float32), _f32p), _p(out, _f32p))
+        return out
+
+    def hc_expand(self, block, hc, post, comb) -> np.ndarray:
+        n_hc, n = hc.shape
+        out = np.zeros((n_hc, n), np.float32)
+        self.lib.affref_hc_expand(_p(out, _f32p), _p(np.ascontiguousarray(block, np.float32), _f32p),
+                                  _p(np.ascontiguousarray(hc, np.float32), _f32p),
+                                  _p(np.ascontiguousarray(post, np.float32), _f32p),
+                                  _p(np.ascontiguousarray(comb, np.float32), _f32p), n, n_hc)
+        return out
 
     def float_to_bf16(self, f: float) -> int:
         return int(self.lib.affref_float_to_bf16(f))

@@ -678,3 +678,77 @@ uint32_t orc_route_topk(const float* logits, const float* bias, uint32_t n_exper
   free(taken);
   return kk;
 }
+
+/* ------------------------------------------------------------------------------------------ */
+/* the step after the routed experts                                                           */
+/* ------------------------------------------------------------------------------------------ */
+
+/* UE8M0: 2^(e - 127), 0xFF is NaN (src/quant/source_dtypes.cpp:41-50). */
+float orc_e8m0_to_float(uint8_t e) { return e == 0xFF ? NAN : ldexpf(1.0f, (int)e - 127); }
+
+/* FP8 dense matvec, the scalar form of src/engine/matvec_fp8.inc:42-82 (matvec_dense, ops.cpp:284-289):
+ * W row-major [rows x cols] E4M3, one UE8M0 scale per 128x128 tile in S row-major
+ * [ceil(rows/128)][ceil(cols/128)]. Per row, each 128-column run is summed on its own (a float
+ * chain over the run) and multiplied by its tile's scale into the row sum. */
+void orc_matvec_fp8(const uint8_t* w, const uint8_t* s, uint64_t rows, uint64_t cols, const float* x,
+                    float* out) {
+  const uint64_t sc_cols = (cols + 127) / 128;
+  float lut[256];
+  for (int i = 0; i < 256; ++i) lut[i] = orc_e4m3_to_float((uint8_t)i);
+#pragma omp parallel for schedule(static)
+  for (uint64_t r = 0; r < rows; ++r) {
+    const uint8_t* wr = w + r * cols;
+    const uint8_t* sr = s + (r >> 7) * sc_cols;
+    float acc = 0.0f;
+    for (uint64_t t = 0; t < sc_cols; ++t) {
+      const uint64_t c0 = t * 128, c1 = c0 + 128 < cols ? c0 + 128 : cols;
+      float sub = 0.0f;
+      for (uint64_t c = c0; c < c1; ++c) sub += lut[wr[c]] * x[c];
+      acc += sub * orc_e8m0_to_float(sr[t]);
+    }
+    out[r] = acc;
+  }
+}
+
+/* The shared expert on one token, the CPU composition of src/engine/model.cpp:1214-1222: gate and
+ * up [inter x hidden] and down [hidden x inter] FP8 dense, sh = W_d . swiglu(W_g x, W_u x), then
+ * block[d] += sh[d]. */
+void orc_shared_expert(const uint8_t* wg, const uint8_t* sg, const uint8_t* wu, const uint8_t* su,
+                       const uint8_t* wd, const uint8_t* sd, uint64_t hidden, uint64_t inter, float limit,
+                       const float* x, float* block) {
+  float* g = (float*)calloc(inter, sizeof(float));
+  float* u = (float*)calloc(inter, sizeof(float));
+  float* a = (float*)calloc(inter, sizeof(float));
+  float* sh = (float*)calloc(hidden, sizeof(float));
+  orc_matvec_fp8(wg, sg, inter, hidden, x, g);
+  orc_matvec_fp8(wu, su, inter, hidden, x, u);
+  orc_swiglu(g, u, inter, limit, a);
+  orc_matvec_fp8(wd, sd, hidden, inter, a, sh);
+  for (uint64_t d = 0; d < hidden; ++d) block[d] += sh[d];
+  free(g);
+  free(u);
+  free(a);
+  free(sh);
+}
+
+/* Hyper-connection expand (src/engine/ops.cpp:470-482): lane dst of the next state is
+ * block * post[dst] plus comb[dst + src * n_hc] * residual lane src, summed over src in order;
+ * each lane [n_embd] at out_hc + dst * n_embd. */
+void orc_hc_expand(float* out_hc, const float* block, const float* residual_hc, const float* post,
+                   const float* comb, uint32_t n_embd, uint32_t n_hc) {
+  for (uint32_t dst = 0; dst < n_hc; ++dst) {
+    float* o = out_hc + (uint64_t)dst * n_embd;
+    for (uint32_t d = 0; d < n_embd; ++d) o[d] = block[d] * post[dst];
+    for (uint32_t src = 0; src < n_hc; ++src) {
+      const float c = comb[dst + src * n_hc];
+      const float* r = residual_hc + (uint64_t)src * n_embd;
+      for (uint32_t d = 0; d < n_embd; ++d) o[d] += c * r[d];
+    }
+  }
+}
+
+/* A layer without a hyper-connection control adds the block into lane 0 only
+ * (src/engine/model.cpp:1237-1238; the device form src/gpu/dense_gpu.hip:1717-1724). */
+void orc_hc_add(float* hc, const float* block, uint32_t n_embd) {
+  for (uint32_t d = 0; d < n_embd; ++d) hc[d] += block[d];
+}

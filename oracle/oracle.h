@@ -84,6 +84,17 @@ float orc_sqrtsoftplus(float x);
 uint32_t orc_route_topk(const float* logits, const float* bias, uint32_t n_expert, uint32_t k,
                         int norm_topk_prob, float routed_scaling, uint32_t* sel, float* w);
 
+/* ---- the step after the routed experts: shared expert and hyper-connection post ---- */
+float orc_e8m0_to_float(uint8_t e);
+void orc_matvec_fp8(const uint8_t* w, const uint8_t* s, uint64_t rows, uint64_t cols, const float* x,
+                    float* out);
+void orc_shared_expert(const uint8_t* wg, const uint8_t* sg, const uint8_t* wu, const uint8_t* su,
+                       const uint8_t* wd, const uint8_t* sd, uint64_t hidden, uint64_t inter, float limit,
+                       const float* x, float* block);
+void orc_hc_expand(float* out_hc, const float* block, const float* residual_hc, const float* post,
+                   const float* comb, uint32_t n_embd, uint32_t n_hc);
+void orc_hc_add(float* hc, const float* block, uint32_t n_embd);
+
 #ifdef __cplusplus
 }
 #endif

@@ -230,4 +230,24 @@ int64_t affref_expert_offset(const char* path, uint32_t layer, uint32_t expert) 
   return (int64_t)(r.expert_ptr(layer, expert) - base);
 }
 
+// src/engine/ops.cpp:284-289 -> src/engine/matvec_fp8.inc:42-82: the FP8 dense matvec (E4M3
+// weights, one UE8M0 scale per 128x128 tile), single-threaded.
+void affref_matvec_fp8(const uint8_t* w, const uint8_t* s, uint64_t rows, uint64_t cols, const float* x,
+                       float* out) {
+  DenseW d;
+  d.data = w;
+  d.scales = s;
+  d.quant = AFF_FP8_E4M3;
+  matvec_dense(d, x, rows, cols, out);
+}
+
+// src/quant/source_dtypes.cpp:41-53
+float affref_e8m0_to_float(uint8_t e) { return e8m0_to_float(e); }
+
+// src/engine/ops.cpp:470-482
+void affref_hc_expand(float* out_hc, const float* block, const float* residual_hc, const float* post,
+                      const float* comb, uint32_t n_embd, uint32_t n_hc) {
+  hc_expand(out_hc, block, residual_hc, post, comb, n_embd, n_hc);
+}
+
 }  // extern "C"

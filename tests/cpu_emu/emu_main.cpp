@@ -11,6 +11,9 @@
 //   emu_main ffnptr  hidden inter n_experts seed          -> affx_expert_ffn (pointer table) vs
 //                    the staged decode (bit for bit) and the oracle
 //   emu_main route   n_tok n_experts top_k seed           -> the device router vs the oracle's
+//   emu_main shared  hidden inter M T seed                -> the shared expert (decode on M
+//                    tokens, batch on T with and without a low part) vs the oracle, and the
+//                    hyper-connection post (single and batch forms) bit for bit
 //   emu_main timeout hidden inter n_experts M K seed      -> a decode whose waiters give up (spin
 //                    limit 0 from the host) fails the engine hook and affx_decode_status; after
 //                    the reset, the next calls are correct
@@ -31,6 +34,7 @@ thread_local EmuBlock* emu_blk;
 #include "../../affinity_amd/csrc/affx_api.hip"
 #include "../../affinity_amd/csrc/affx_noalloc.hip"
 #include "../../affinity_amd/csrc/affx_route.hip"
+#include "../../affinity_amd/csrc/affx_shared.hip"
 
 extern "C" {
 #include "../../oracle/oracle.h"
@@ -368,6 +372,153 @@ int run_route(int argc, char** argv) {
   return ok && worst <= 2 ? 0 : 1;
 }
 
+// E4M3 weights that are never NaN (0x7F / 0xFF), UE8M0 tile scales around 2^-7
+void fp8_matrix(std::mt19937_64& rng, uint64_t rows, uint64_t cols, std::vector<uint8_t>& w, std::vector<uint8_t>& s) {
+  w.resize(rows * cols);
+  for (auto& b : w) {
+    b = rng() & 0xff;
+    if ((b & 0x7f) == 0x7f) b ^= 1;
+  }
+  s.resize(((rows + 127) / 128) * ((cols + 127) / 128));
+  for (auto& e : s) e = (uint8_t)(116 + rng() % 8);
+}
+
+int run_shared(int argc, char** argv) {
+  const uint32_t H = atoi(argv[2]), I = atoi(argv[3]), M = atoi(argv[4]), T = atoi(argv[5]);
+  std::mt19937_64 rng(atoi(argv[6]));
+  std::normal_distribution<float> nd;
+  std::vector<uint8_t> w[3], sc[3];
+  fp8_matrix(rng, I, H, w[0], sc[0]);
+  fp8_matrix(rng, I, H, w[1], sc[1]);
+  fp8_matrix(rng, H, I, w[2], sc[2]);
+  affx_shared_expert S{};
+  S.gate = {w[0].data(), sc[0].data(), I, H};
+  S.up = {w[1].data(), sc[1].data(), I, H};
+  S.down = {w[2].data(), sc[2].data(), H, I};
+  S.hidden = H;
+  S.inter = I;
+  S.swiglu_limit = 10.0f;
+  bool ok = true;
+  // decode: M tokens, accumulated into a y that already holds something (the routed sum)
+  {
+    std::vector<float> x((size_t)M * H), y0((size_t)M * H), y, yref;
+    for (auto& v : x) v = nd(rng);
+    for (auto& v : y0) v = 0.01f * nd(rng);
+    y = y0;
+    yref = y0;
+    std::vector<uint8_t> ws(affx_shared_decode_workspace_size(M, H, I));
+    const int rc = affx_shared_expert_decode(&S, x.data(), H, 1, M, y.data(), H, 1, 1, ws.data(), ws.size(), nullptr);
+    for (uint32_t t = 0; t < M; ++t)
+      orc_shared_expert(w[0].data(), sc[0].data(), w[1].data(), sc[1].data(), w[2].data(), sc[2].data(), H, I, 10.0f,
+                        x.data() + (size_t)t * H, yref.data() + (size_t)t * H);
+    // the shared expert's own contribution, compared on its own
+    std::vector<float> d(y.size()), dref(y.size());
+    for (size_t i = 0; i < y.size(); ++i) { d[i] = y[i] - y0[i]; dref[i] = yref[i] - y0[i]; }
+    const double e = rel_l2(d, dref);
+    printf("shared decode M=%u: rc=%d rel_l2=%.3e\n", M, rc, e);
+    ok = ok && rc == 0 && e <= 1e-3;
+  }
+  // batch: T bf16 tokens, with and without a low part, stored (accumulate 0)
+  for (int lo = 0; lo < 2; ++lo) {
+    std::vector<float> xf((size_t)T * H), xr((size_t)T * H);
+    std::vector<uint16_t> xh((size_t)T * H), xl((size_t)T * H);
+    for (size_t i = 0; i < xf.size(); ++i) {
+      xf[i] = nd(rng) * (i % 97 == 0 ? 8.0f : 1.0f);
+      xh[i] = bf16(xf[i]);
+      float hi;
+      uint32_t u = (uint32_t)xh[i] << 16;
+      memcpy(&hi, &u, 4);
+      xl[i] = bf16(xf[i] - hi);
+      float lw;
+      u = (uint32_t)xl[i] << 16;
+      memcpy(&lw, &u, 4);
+      xr[i] = lo ? hi + lw : hi;
+    }
+    std::vector<float> y((size_t)T * H, 123.0f), yref((size_t)T * H, 0.f);
+    std::vector<uint8_t> ws(affx_shared_batch_workspace_size(T, H, I));
+    const int rc = affx_shared_expert_batch(&S, xh.data(), lo ? xl.data() : nullptr, T, y.data(), 0, ws.data(),
+                                            ws.size(), nullptr);
+    for (uint32_t t = 0; t < T; ++t)
+      orc_shared_expert(w[0].data(), sc[0].data(), w[1].data(), sc[1].data(), w[2].data(), sc[2].data(), H, I, 10.0f,
+                        xr.data() + (size_t)t * H, yref.data() + (size_t)t * H);
+    const double e = rel_l2(y, yref);
+    printf("shared batch T=%u lo=%d: rc=%d rel_l2=%.3e\n", T, lo, rc, e);
+    ok = ok && rc == 0 && e <= 1e-3;
+  }
+  // hyper-connection post: single token (every n_hc), batch, and the no-control adds; bit for bit
+  for (uint32_t nh : {1u, 2u, 4u, 8u}) {
+    std::vector<float> hc((size_t)nh * H), blk(H), post(nh), comb(nh * nh), out((size_t)nh * H), ref((size_t)nh * H);
+    for (auto& v : hc) v = nd(rng);
+    for (auto& v : blk) v = nd(rng);
+    for (auto& v : post) v = nd(rng);
+    for (auto& v : comb) v = nd(rng);
+    orc_hc_expand(ref.data(), blk.data(), hc.data(), post.data(), comb.data(), H, nh);
+    const int rc = affx_hc_post(out.data(), blk.data(), hc.data(), post.data(), comb.data(), H, nh, 1, nullptr);
+    bool same = memcmp(out.data(), ref.data(), out.size() * 4) == 0, zero = true;
+    for (float v : blk) zero = zero && v == 0.f;
+    printf("hc_post n_hc=%u: rc=%d bit-exact=%d block zeroed=%d\n", nh, rc, (int)same, (int)zero);
+    ok = ok && rc == 0 && same && zero;
+  }
+  {
+    const uint32_t nh = 4, nb = 5;
+    std::vector<uint16_t> hc((size_t)nh * H * nb), out((size_t)nh * H * nb);
+    std::vector<float> blk((size_t)H * nb), post(nh * nb), comb(nh * nh * nb);
+    for (auto& v : hc) v = bf16(nd(rng));
+    for (auto& v : blk) v = nd(rng);
+    for (auto& v : post) v = nd(rng);
+    for (auto& v : comb) v = nd(rng);
+    const std::vector<float> blk0 = blk;
+    const int rc = affx_hc_post_batch(out.data(), blk.data(), hc.data(), post.data(), comb.data(), H, nh, nb, 0, nullptr);
+    bool same = true;
+    for (uint32_t b = 0; b < nb; ++b) {
+      std::vector<float> h((size_t)nh * H), bl(H), p(nh), cm(nh * nh), r((size_t)nh * H);
+      for (uint32_t s = 0; s < nh; ++s)
+        for (uint32_t d = 0; d < H; ++d) {
+          const uint32_t u = (uint32_t)hc[((size_t)s * H + d) * nb + b] << 16;
+          memcpy(&h[(size_t)s * H + d], &u, 4);
+        }
+      for (uint32_t d = 0; d < H; ++d) bl[d] = blk0[(size_t)d * nb + b];
+      for (uint32_t s = 0; s < nh; ++s) p[s] = post[(size_t)s * nb + b];
+      for (uint32_t s = 0; s < nh * nh; ++s) cm[s] = comb[(size_t)s * nb + b];
+      orc_hc_expand(r.data(), bl.data(), h.data(), p.data(), cm.data(), H, nh);
+      for (uint32_t s = 0; s < nh; ++s)
+        for (uint32_t d = 0; d < H; ++d) same = same && out[((size_t)s * H + d) * nb + b] == orc_f32_to_bf16(r[(size_t)s * H + d]);
+    }
+    const bool kept = blk == blk0;
+    printf("hc_post_batch nb=%u: rc=%d bit-exact=%d block kept=%d\n", nb, rc, (int)same, (int)kept);
+    ok = ok && rc == 0 && same && kept;
+    // the no-control adds
+    std::vector<float> h1(H), r1;
+    for (auto& v : h1) v = nd(rng);
+    r1 = h1;
+    orc_hc_add(r1.data(), blk.data(), H);
+    std::vector<float> bcopy(blk.begin(), blk.begin() + H);
+    int rc2 = affx_hc_add(h1.data(), bcopy.data(), H, 1, nullptr);
+    bool add_ok = rc2 == 0 && memcmp(h1.data(), r1.data(), H * 4) == 0;
+    std::vector<uint16_t> hb(hc.begin(), hc.begin() + (size_t)H * nb);
+    std::vector<float> bb = blk;
+    rc2 = affx_hc_add_batch(hb.data(), bb.data(), (uint64_t)H * nb, 1, nullptr);
+    for (size_t i = 0; i < hb.size() && add_ok; ++i) {
+      float v;
+      const uint32_t u = (uint32_t)hc[i] << 16;
+      memcpy(&v, &u, 4);
+      add_ok = hb[i] == orc_f32_to_bf16(v + blk[i]) && bb[i] == 0.f;
+    }
+    printf("hc_add and hc_add_batch: ok=%d\n", (int)(add_ok && rc2 == 0));
+    ok = ok && add_ok && rc2 == 0;
+    // declined shapes
+    const int d1 = affx_hc_post(h1.data(), bcopy.data(), h1.data(), post.data(), comb.data(), H, 3, 0, nullptr);
+    affx_shared_expert bad = S;
+    bad.swiglu_limit = 0.f;
+    std::vector<float> yy(H);
+    const int d2 = affx_shared_expert_decode(&bad, h1.data(), H, 1, 1, yy.data(), H, 1, 0, nullptr, 0, nullptr);
+    printf("declined: n_hc=3 -> %d, limit 0 -> %d\n", d1, d2);
+    ok = ok && d1 == AFFX_DECLINED && d2 != AFFX_OK;
+  }
+  printf("shared ok=%d\n", (int)ok);
+  return ok ? 0 : 1;
+}
+
 int run_quant(int argc, char** argv) {
   const uint32_t rows = atoi(argv[2]), cols = atoi(argv[3]);
   std::mt19937_64 rng(atoi(argv[4]));
@@ -485,6 +636,7 @@ int main(int argc, char** argv) {
   if (cmd == "slots" && argc >= 8) return run_slots(argc, argv);
   if (cmd == "ffnptr" && argc >= 6) return run_ffnptr(argc, argv);
   if (cmd == "route" && argc >= 6) return run_route(argc, argv);
+  if (cmd == "shared" && argc >= 7) return run_shared(argc, argv);
   fprintf(stderr, "usage: see header\n");
   return 2;
 }

@@ -223,19 +223,27 @@ inline emu_v2f __builtin_amdgcn_cvt_pk_f32_fp8(int w, bool hi) {
   return r;
 }
 
-inline emu_v4f __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(emu_v8i a, emu_v8i b, emu_v4f c, int, int, int, int, int, int) {
+// Scales: lane l's E8M0 byte (selected by opsel) multiplies its own 32 K values, row l % 16 of A or
+// column l % 16 of B in K group l / 16 (the layout checked on gfx950).
+inline emu_v4f __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(emu_v8i a, emu_v8i b, emu_v4f c, int, int, int opa,
+                                                                int sa, int opb, int sb) {
   uint32_t w = emu_wave(), l = emu_lane();
   for (int i = 0; i < 8; ++i) emu_blk->xfer[w][l][i] = (uint32_t)a[i] | ((uint64_t)(uint32_t)b[i] << 32);
+  emu_blk->xfer[w][l][8] = (((uint32_t)sa >> (8 * opa)) & 0xff) | ((uint64_t)(((uint32_t)sb >> (8 * opb)) & 0xff) << 32);
   emu_wave_sync();
   emu_v4f d = c;
   for (int v = 0; v < 4; ++v) {
     const uint32_t row = 4 * (l / 16) + v, col = l % 16;
     double acc = 0;
-    for (int g = 0; g < 4; ++g)
+    for (int g = 0; g < 4; ++g) {
+      double part = 0;
       for (int i = 0; i < 8; ++i) {
         uint32_t A = (uint32_t)emu_blk->xfer[w][row + 16 * g][i], B = (uint32_t)(emu_blk->xfer[w][col + 16 * g][i] >> 32);
-        for (int p = 0; p < 4; ++p) acc += (double)emu_e4m3((A >> (8 * p)) & 0xff) * emu_e4m3((B >> (8 * p)) & 0xff);
+        for (int p = 0; p < 4; ++p) part += (double)emu_e4m3((A >> (8 * p)) & 0xff) * emu_e4m3((B >> (8 * p)) & 0xff);
       }
+      const int ea = (int)(emu_blk->xfer[w][row + 16 * g][8] & 0xff), eb = (int)(emu_blk->xfer[w][col + 16 * g][8] >> 32);
+      acc += ldexp(part, ea + eb - 254);
+    }
     d[v] = c[v] + (float)acc;
   }
   emu_wave_sync();

@@ -21,6 +21,9 @@ Fixtures (data only: inputs and the reference's outputs):
   scalars.npz       E4M3 table, bf16 rounding cases, swiglu cases
   route.npz         the engine router (route_topk): logits and bias cases with the chosen
                     experts and weights
+  step.npz          the step after the routed experts: FP8 dense matvecs (matvec_dense over E4M3
+                    weights with UE8M0 128x128 tile scales, ragged shapes included), the E8M0
+                    table, and hc_expand cases for n_hc 1, 2, 4, 8
 """
 from __future__ import annotations
 
@@ -200,9 +203,34 @@ def make_route(R):
                         w=np.stack([c[7] for c in cases]).astype(np.float32))
 
 
+def make_step(R):
+    """matvec_fp8 (src/engine/matvec_fp8.inc:42-82) on three shapes, one ragged in both directions,
+    with every E4M3 code but the NaNs and scales 2^-16 .. 2^8; e8m0_to_float for every byte;
+    hc_expand (src/engine/ops.cpp:470-482) for each n_hc."""
+    rng = np.random.default_rng(23)
+    out = {"e8m0": np.array([R.e8m0_to_float(i) for i in range(256)], np.float32)}
+    for i, (rows, cols) in enumerate(((128, 256), (200, 300), (129, 512))):
+        w = rng.integers(0, 256, (rows, cols), dtype=np.uint8)
+        w[(w & 0x7F) == 0x7F] ^= 1
+        s = rng.integers(111, 136, ((rows + 127) // 128, (cols + 127) // 128), dtype=np.uint8)
+        x = rng.standard_normal(cols).astype(np.float32)
+        out[f"mv{i}_w"], out[f"mv{i}_s"], out[f"mv{i}_x"] = w, s, x
+        out[f"mv{i}_y"] = R.matvec_fp8(w, s, x)
+    for nh in (1, 2, 4, 8):
+        n = 300
+        hc = rng.standard_normal((nh, n)).astype(np.float32)
+        blk = rng.standard_normal(n).astype(np.float32)
+        post = rng.standard_normal(nh).astype(np.float32)
+        comb = rng.standard_normal(nh * nh).astype(np.float32)
+        out[f"hc{nh}_hc"], out[f"hc{nh}_block"], out[f"hc{nh}_post"], out[f"hc{nh}_comb"] = hc, blk, post, comb
+        out[f"hc{nh}_out"] = R.hc_expand(blk, hc, post, comb)
+    np.savez_compressed(os.path.join(OUT, "step.npz"), **out)
+
+
 def main():
     O, R = load_oracle(), load_ref()
     make_route(R)
+    make_step(R)
     make_scalars(O, R)
     cb = make_c1(O, R)
     make_small(O, R, cb)
@@ -212,5 +240,7 @@ def main():
 if __name__ == "__main__":
     if len(sys.argv) > 1 and sys.argv[1] == "route":     # only the router fixture
         make_route(load_ref())
+    elif len(sys.argv) > 1 and sys.argv[1] == "step":    # only the step-after fixture
+        make_step(load_ref())
     else:
         main()

@@ -21,9 +21,9 @@ def emu(tmp_path_factory):
     san = ["-fsanitize=address", "-fno-omit-frame-pointer", "-g", "-O1"]
     subprocess.run([CLANG, *san, "-ffp-contract=off", "-fopenmp=libgomp", "-c",
                     os.path.join(ROOT, "oracle", "oracle.c"), "-o", str(d / "oracle.o")], check=True)
-    # -ffp-contract=fast with FMA available mirrors the device compiler's default, so a kernel
-    # that needs exact float order has to say so itself
-    subprocess.run([CLANGXX, "-std=c++20", *san, "-march=x86-64-v3", "-ffp-contract=fast", "-w",
+    # -ffp-contract=fast-honor-pragmas with FMA available mirrors the device compiler's default
+    # for HIP, so a kernel that needs exact float order has to say so itself (a contract pragma)
+    subprocess.run([CLANGXX, "-std=c++20", *san, "-march=x86-64-v3", "-ffp-contract=fast-honor-pragmas", "-w",
                     "-I", os.path.join(ROOT, "tests", "cpu_emu"), "-I", os.path.join(ROOT, "affinity_amd", "csrc"),
                     os.path.join(ROOT, "tests", "cpu_emu", "emu_main.cpp"), str(d / "oracle.o"),
                     "-o", str(d / "emu_main"), "-lpthread", "-fopenmp=libgomp"], check=True)
@@ -112,3 +112,10 @@ def test_expert_ffn_pointer_table_emulated(emu):
 def test_route_emulated(emu):
     out = run(emu, "route", 21, 100, 6, 4)
     assert "route ids equal=1" in out, out
+
+
+def test_shared_expert_and_hc_post_emulated(emu):
+    """The shared expert's decode (6 tokens, two column groups) and batch kernels (40 tokens, with
+    and without a low part) against the oracle, the hyper-connection post bit for bit."""
+    out = run(emu, "shared", 1024, 1024, 6, 40, 5, timeout=900)
+    assert "shared ok=1" in out, out

@@ -1,0 +1,199 @@
+"""GPU parity of the step after the routed experts: the FP8 shared expert (decode and batch forms)
+against the oracle's restatement of the host composition (src/engine/model.cpp:1214-1222, its
+matvec pinned to the reference's own matvec_dense in tests/test_oracle.py), and the
+hyper-connection post bit for bit against the oracle's hc_expand (itself bit-identical to the
+reference's, tests/test_oracle.py). Shapes are V4-Flash's: hidden 4096, inter 2048."""
+import numpy as np
+import pytest
+
+from gpu_util import rel_l2
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+H, I = 4096, 2048
+
+
+@pytest.fixture(scope="module")
+def ax():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import affinity_amd.experts as ax
+    ax.init()
+    return ax
+
+
+def fp8_matrix(rng, rows, cols):
+    """E4M3 bytes over every non-NaN code, UE8M0 tile scales around 2^-7 (the reference decodes
+    0x7F / 0xFF as NaN, which no trained weight holds)."""
+    w = rng.integers(0, 256, (rows, cols), dtype=np.uint8)
+    w[(w & 0x7F) == 0x7F] ^= 1
+    s = rng.integers(116, 124, ((rows + 127) // 128, (cols + 127) // 128), dtype=np.uint8)
+    return w, s
+
+
+@pytest.fixture(scope="module")
+def shexp(ax):
+    rng = np.random.default_rng(41)
+    mats = [fp8_matrix(rng, I, H), fp8_matrix(rng, I, H), fp8_matrix(rng, H, I)]
+    dev = [torch.from_numpy(a).cuda() for m in mats for a in m]
+    return ax.SharedExpert(*dev), mats
+
+
+def oracle_rows(orc, mats, x):
+    (wg, sg), (wu, su), (wd, sd) = mats
+    return np.stack([orc.shared_expert(wg, sg, wu, su, wd, sd, np.ascontiguousarray(x[t]), 10.0)
+                     for t in range(x.shape[0])])
+
+
+@pytest.mark.parametrize("M", [1, 3, 5, 6, 8])
+def test_shared_decode_matches_oracle(ax, orc, shexp, M):
+    """M tokens, added into a block that already holds the routed sum: the addition is exact
+    f32 (the block afterwards minus before is the shared expert's output)."""
+    S, mats = shexp
+    rng = np.random.default_rng(100 + M)
+    x = rng.standard_normal((M, H)).astype(np.float32)
+    y0 = (rng.standard_normal((M, H)) * 0.01).astype(np.float32)
+    gx, gy = torch.from_numpy(x).cuda(), torch.from_numpy(y0).cuda()
+    S.decode(gx, gy, accumulate=True)
+    got = gy.cpu().numpy()
+    ref = oracle_rows(orc, mats, x)
+    err = rel_l2(got - y0, ref)
+    print(f"shared decode M={M}: rel_l2={err:.3e}")
+    assert err <= 1e-3
+    # stored form equals the accumulated contribution's recomputation
+    gy2 = torch.full((M, H), 7.0, device="cuda")
+    S.decode(gx, gy2, accumulate=False)
+    assert rel_l2(gy2.cpu().numpy(), ref) <= 1e-3
+
+
+def test_shared_decode_dim_major_arena(ax, orc, shexp):
+    """The engine's dim-major arenas: x and the block [hidden][nb] with nb = 8 slots, 6 live."""
+    S, mats = shexp
+    rng = np.random.default_rng(7)
+    nb, M = 8, 6
+    x = rng.standard_normal((H, nb)).astype(np.float32)
+    gx = torch.from_numpy(x).cuda()
+    gy = torch.zeros((H, nb), device="cuda")
+    S.decode(gx.t()[:M], gy.t()[:M], accumulate=True)   # (token stride 1, dim stride nb)
+    got = gy.cpu().numpy().T[:M]
+    ref = oracle_rows(orc, mats, np.ascontiguousarray(x.T[:M]))
+    assert rel_l2(got, ref) <= 1e-3
+    assert not gy.cpu().numpy()[:, M:].any()    # slots past M untouched
+
+
+@pytest.mark.parametrize("T,lo", [(200, False), (200, True), (61, True), (1, False)])
+def test_shared_batch_matches_oracle(ax, orc, shexp, T, lo):
+    S, mats = shexp
+    rng = np.random.default_rng(300 + T + lo)
+    xf = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).cuda()
+    xh = xf.to(torch.bfloat16)
+    xl = (xf - xh.float()).to(torch.bfloat16) if lo else None
+    xr = (xh.float() + (xl.float() if lo else 0)).cpu().numpy()
+    y0 = torch.from_numpy((rng.standard_normal((T, H)) * 0.01).astype(np.float32)).cuda()
+    y = y0.clone()
+    S.batch(xh, y, x_lo=xl, accumulate=True)
+    ref = oracle_rows(orc, mats, xr)
+    err = rel_l2((y - y0).cpu().numpy(), ref)
+    print(f"shared batch T={T} lo={lo}: rel_l2={err:.3e}")
+    assert err <= 1e-3
+
+
+def test_shared_batch_prefill_shape_sampled(ax, orc, shexp):
+    """The C4 prefill chunk (4096 tokens): 24 sampled tokens against the oracle, including the
+    first and last token tiles of both GEMMs (96 and 60 tokens a tile)."""
+    S, mats = shexp
+    T = 4096
+    g = torch.Generator(device="cuda").manual_seed(9)
+    xh = torch.randn((T, H), generator=g, device="cuda").to(torch.bfloat16)
+    y = torch.zeros((T, H), device="cuda")
+    S.batch(xh, y, accumulate=False)
+    pick = np.array([0, 1, 95, 96, 97, 1000, 2047, 2048, 3000, 4000, 4031, 4032, 4033, 4090, 4094, 4095,
+                     17, 333, 777, 1234, 2500, 3333, 3700, 3999])
+    ref = oracle_rows(orc, mats, xh.float().cpu().numpy()[pick])
+    err = rel_l2(y.cpu().numpy()[pick], ref)
+    print(f"shared batch T=4096 (24 sampled): rel_l2={err:.3e}")
+    assert err <= 1e-3
+
+
+def test_shared_declines(ax, shexp):
+    from affinity_amd._lib import AffxDeclined, AffxError
+    S, _ = shexp
+    x = torch.zeros((9, H), device="cuda")
+    with pytest.raises(AffxDeclined):
+        S.decode(x, torch.zeros_like(x))             # 9 tokens: the batch form's job
+    import ctypes
+    from affinity_amd._lib import AFFX_DECLINED, check, lib
+    y = torch.zeros((1, H), device="cuda")
+    ws = torch.empty(lib().affx_shared_decode_workspace_size(1, H, I), dtype=torch.uint8, device="cuda")
+    bad = type(S.abi).from_buffer_copy(S.abi)
+    bad.swiglu_limit = 0.0                           # the reference's "no clamp"
+    rc = lib().affx_shared_expert_decode(ctypes.byref(bad), x.data_ptr(), H, 1, 1, y.data_ptr(), H, 1, 0,
+                                         ws.data_ptr(), ws.numel(), 0)
+    assert rc == AFFX_DECLINED
+    bad = type(S.abi).from_buffer_copy(S.abi)
+    bad.down.rows = H - 1                            # shapes that do not chain
+    with pytest.raises(AffxError):
+        check(lib().affx_shared_expert_decode(ctypes.byref(bad), x.data_ptr(), H, 1, 1, y.data_ptr(), H, 1, 0,
+                                              ws.data_ptr(), ws.numel(), 0), "decode")
+    with pytest.raises(AffxError):                   # workspace too small
+        check(lib().affx_shared_expert_decode(ctypes.byref(S.abi), x.data_ptr(), H, 1, 1, y.data_ptr(), H, 1, 0,
+                                              ws.data_ptr(), 16, 0), "decode")
+
+
+@pytest.mark.parametrize("n_hc", [1, 2, 4, 8])
+def test_hc_post_bit_exact(ax, orc, n_hc):
+    rng = np.random.default_rng(n_hc)
+    hc = rng.standard_normal((n_hc, H)).astype(np.float32)
+    blk = rng.standard_normal(H).astype(np.float32)
+    post = rng.standard_normal(n_hc).astype(np.float32)
+    comb = rng.standard_normal(n_hc * n_hc).astype(np.float32)
+    gb = torch.from_numpy(blk).cuda()
+    out = ax.hc_post(gb, torch.from_numpy(hc).cuda(), torch.from_numpy(post).cuda(), torch.from_numpy(comb).cuda())
+    ref = orc.hc_expand(blk, hc, post, comb)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+    assert not gb.cpu().numpy().any()          # the block is left zero
+
+
+def test_hc_add_and_declines(ax, orc):
+    from affinity_amd._lib import AffxDeclined
+    rng = np.random.default_rng(5)
+    hc = rng.standard_normal((1, H)).astype(np.float32)
+    blk = rng.standard_normal(H).astype(np.float32)
+    ghc, gb = torch.from_numpy(hc).cuda(), torch.from_numpy(blk).cuda()
+    ax.hc_post(gb, ghc, None, None, zero_block=False)
+    assert np.array_equal(ghc.cpu().numpy()[0], orc.hc_add(hc[0], blk))
+    assert np.array_equal(gb.cpu().numpy(), blk)   # zero_block = 0 keeps it
+    with pytest.raises(AffxDeclined):
+        z = torch.zeros((3, H), device="cuda")
+        ax.hc_post(gb, z, torch.zeros(3, device="cuda"), torch.zeros(9, device="cuda"))
+
+
+@pytest.mark.parametrize("n_hc", [1, 4, 8])
+def test_hc_post_batch_bit_exact(ax, orc, n_hc):
+    """Dim-major bf16 arenas of nb = 37 tokens: every token against the oracle's hc_expand on the
+    same bf16 inputs, rounded to bf16 once."""
+    rng = np.random.default_rng(20 + n_hc)
+    nb = 37
+    hcf = torch.from_numpy(rng.standard_normal((n_hc, H, nb)).astype(np.float32))
+    hcb = hcf.to(torch.bfloat16)
+    blk = rng.standard_normal((H, nb)).astype(np.float32)
+    post = rng.standard_normal((n_hc, nb)).astype(np.float32)
+    comb = rng.standard_normal((n_hc * n_hc, nb)).astype(np.float32)
+    gb = torch.from_numpy(blk).cuda()
+    out = ax.hc_post_batch(gb, hcb.cuda(), torch.from_numpy(post).cuda(), torch.from_numpy(comb).cuda())
+    got = out.cpu().view(torch.int16).numpy().astype(np.uint16)
+    hin = hcb.float().numpy()
+    for b in range(nb):
+        ref = orc.hc_expand(blk[:, b].copy(), np.ascontiguousarray(hin[:, :, b]), post[:, b].copy(),
+                            comb[:, b].copy())
+        rb = np.array([orc.f32_to_bf16(float(v)) for v in ref.reshape(-1)], np.uint16).reshape(n_hc, H)
+        assert np.array_equal(got[:, :, b], rb), f"token {b}"
+    assert not gb.cpu().numpy().any()
+    # no control: lane 0 += block, rounded to bf16
+    hc0 = hcb[0].cuda().contiguous()
+    gb = torch.from_numpy(blk).cuda()
+    ax.hc_post_batch(gb, hc0.view(1, H, nb), None, None)
+    want = (hcb[0].float() + torch.from_numpy(blk)).to(torch.bfloat16)
+    assert torch.equal(hc0.cpu(), want)
+    assert not gb.cpu().numpy().any()

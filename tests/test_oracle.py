@@ -419,3 +419,116 @@ def test_route_topk_matches_live_reference(orc, ref):
         b = ref.route_topk(lg, bias, 6, True, 1.5)
         np.testing.assert_array_equal(a[0], b[0])
         np.testing.assert_array_equal(a[1].view(np.uint32), b[1].view(np.uint32))
+
+
+# ---------------------------------------------------------------------------------------------
+# the step after the routed experts: FP8 dense matvec, shared expert, hyper-connection post
+# ---------------------------------------------------------------------------------------------
+
+@pytest.fixture(scope="module")
+def step():
+    return np.load(os.path.join(GOLDEN, "step.npz"))
+
+
+def test_e8m0_matches_reference_and_closed_form(orc, step):
+    got = np.array([orc.e8m0_to_float(i) for i in range(256)], np.float32)
+    np.testing.assert_array_equal(got[:255].view(np.uint32), step["e8m0"][:255].view(np.uint32))
+    assert np.isnan(got[255]) and np.isnan(step["e8m0"][255])
+    np.testing.assert_array_equal(got[:255], np.ldexp(np.float32(1), np.arange(255) - 127).astype(np.float32))
+
+
+def test_matvec_fp8_matches_reference_fixture(orc, step):
+    """Bit for bit on the reference's outputs, ragged shapes included."""
+    for i in range(3):
+        y = orc.matvec_fp8(step[f"mv{i}_w"], step[f"mv{i}_s"], step[f"mv{i}_x"])
+        np.testing.assert_array_equal(y.view(np.uint32), step[f"mv{i}_y"].view(np.uint32))
+
+
+def test_matvec_fp8_matches_live_reference(orc, ref):
+    rng = np.random.default_rng(8)
+    for rows, cols in ((256, 4096), (2048, 1000), (1, 128)):
+        w = rng.integers(0, 256, (rows, cols), dtype=np.uint8)
+        w[(w & 0x7F) == 0x7F] ^= 1
+        s = rng.integers(100, 140, ((rows + 127) // 128, (cols + 127) // 128), dtype=np.uint8)
+        x = rng.standard_normal(cols).astype(np.float32)
+        np.testing.assert_array_equal(orc.matvec_fp8(w, s, x).view(np.uint32), ref.matvec_fp8(w, s, x).view(np.uint32))
+
+
+def test_matvec_fp8_closed_forms(orc, scalars):
+    """Against a float64 dense product of the decoded matrix (E4M3 table from the reference
+    fixture, each 128x128 tile times 2^(s - 127)): a wrong tile index (row and column of the scale
+    swapped, or the scale row not advancing every 128 rows) fails it. And an exact case: weights
+    1.0 (0x38) times scale 2^3 against x = 1 gives 8 * cols."""
+    rng = np.random.default_rng(9)
+    rows, cols = 300, 640
+    w = rng.integers(0, 256, (rows, cols), dtype=np.uint8)
+    w[(w & 0x7F) == 0x7F] ^= 1
+    s = rng.integers(110, 130, (3, 5), dtype=np.uint8)
+    x = rng.standard_normal(cols).astype(np.float32)
+    table = scalars["e4m3"].astype(np.float64)
+    dense = table[w] * np.ldexp(1.0, np.repeat(np.repeat(s.astype(np.int64) - 127, 128, 0), 128, 1)[:rows, :cols])
+    want = dense @ x.astype(np.float64)
+    got = orc.matvec_fp8(w, s, x)
+    assert np.max(np.abs(got - want) / (np.abs(dense) @ np.abs(x))) < 1e-5
+    ones = np.full((rows, cols), 0x38, np.uint8)
+    got = orc.matvec_fp8(ones, np.full((3, 5), 130, np.uint8), np.ones(cols, np.float32))
+    np.testing.assert_array_equal(got, np.full(rows, 8.0 * cols, np.float32))
+
+
+def test_shared_expert_composition(orc, scalars):
+    """block += W_d . swiglu(W_g x, W_u x) against a float64 restatement from the decoded
+    matrices; gate and up swapped, or the clamp dropped, fail it (the weights are scaled so that
+    gate values pass the clamp limit)."""
+    rng = np.random.default_rng(10)
+    hidden, inter = 256, 384
+    table = scalars["e4m3"].astype(np.float64)
+
+    def mat(rows, cols, lo, hi):
+        w = rng.integers(0, 256, (rows, cols), dtype=np.uint8)
+        w[(w & 0x7F) == 0x7F] ^= 1
+        s = rng.integers(lo, hi, ((rows + 127) // 128, (cols + 127) // 128), dtype=np.uint8)
+        d = table[w] * np.ldexp(1.0, np.repeat(np.repeat(s.astype(np.int64) - 127, 128, 0), 128, 1)[:rows, :cols])
+        return w, s, d
+
+    (wg, sg, dg), (wu, su, du), (wd, sd, dd) = mat(inter, hidden, 118, 121), mat(inter, hidden, 118, 121), \
+        mat(hidden, inter, 112, 116)
+    x = rng.standard_normal(hidden).astype(np.float32)
+    block0 = rng.standard_normal(hidden).astype(np.float32)
+    got = orc.shared_expert(wg, sg, wu, su, wd, sd, x, 10.0, block0.copy())
+    g, u = dg @ x, du @ x
+    assert (g > 10).any() and (np.abs(u) > 10).any()        # the clamp is exercised
+
+    def swiglu(g, u, L):
+        g = np.minimum(g, L)
+        u = np.clip(u, -L, L)
+        return g / (1 + np.exp(-g)) * u
+
+    want = block0 + dd @ swiglu(g, u, 10.0)
+    scale = np.abs(dd) @ np.abs(swiglu(g, u, 10.0)) + np.abs(block0)
+    assert np.max(np.abs(got - want) / scale) < 1e-5
+    for bad in (block0 + dd @ swiglu(u, g, 10.0), block0 + dd @ swiglu(g, u, 1e30)):
+        assert np.max(np.abs(got - bad) / scale) > 1e-3
+
+
+def test_hc_expand_matches_reference(orc, step):
+    for nh in (1, 2, 4, 8):
+        out = orc.hc_expand(step[f"hc{nh}_block"], step[f"hc{nh}_hc"], step[f"hc{nh}_post"], step[f"hc{nh}_comb"])
+        np.testing.assert_array_equal(out.view(np.uint32), step[f"hc{nh}_out"].view(np.uint32))
+
+
+def test_hc_expand_closed_form_and_add(orc):
+    """Identity mixing (comb = I, post = 1) gives block + lane; a transposed comb index (dst * n_hc
+    + src) fails the asymmetric case. hc_add is lane 0 + block."""
+    rng = np.random.default_rng(11)
+    nh, n = 4, 100
+    hc = rng.standard_normal((nh, n)).astype(np.float32)
+    blk = rng.standard_normal(n).astype(np.float32)
+    out = orc.hc_expand(blk, hc, np.ones(nh, np.float32), np.eye(nh, dtype=np.float32).reshape(-1))
+    np.testing.assert_array_equal(out, hc + blk)
+    comb = np.arange(nh * nh, dtype=np.float32)
+    out = orc.hc_expand(blk, hc, np.zeros(nh, np.float32), comb)
+    want = np.stack([sum(comb[d + s * nh] * hc[s].astype(np.float64) for s in range(nh)) for d in range(nh)])
+    np.testing.assert_allclose(out, want, rtol=1e-5, atol=1e-5)
+    wrong = np.stack([sum(comb[d * nh + s] * hc[s].astype(np.float64) for s in range(nh)) for d in range(nh)])
+    assert np.max(np.abs(out - wrong)) > 1.0
+    np.testing.assert_array_equal(orc.hc_add(hc[0], blk), hc[0] + blk)
