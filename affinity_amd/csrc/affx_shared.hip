@@ -11,10 +11,10 @@
 // is one per wave (decode, and the batch down), else applied in the epilogue.
 //
 // Decode, 1..8 tokens (DenseOps::shexp, src/engine/model.h:314-319; the reference's device form
-// mv_gate_up_swiglu_hip + launch_mv, src/gpu/dense_gpu.hip:2030-2116):
-//   shexp_prep       x -> three E4M3 terms per (token, 1024-column segment) and its exponent
+// mv_gate_up_swiglu_hip + launch_mv, src/gpu/dense_gpu.hip:2030-2116), two launches:
 //   shexp_gateup     one workgroup per 16 rows of inter; 8 waves = {gate, up} x 4 K quarters, every
-//                    weight and activation load issued at the start; fixed-order sum of the
+//                    weight load issued at the start; meanwhile the workgroup turns x into three
+//                    E4M3 terms per element in LDS (one exponent per token); fixed-order sum of the
 //                    quarters, SwiGLU with the clamp, three E4M3 terms out
 //   shexp_down       one workgroup per 16 rows of hidden; 8 waves = 8 K eighths; fixed-order sum,
 //                    y (+)= result
@@ -33,10 +33,7 @@ struct SharedArgs {
   const uint8_t* w[3];  // gate, up [inter x hidden], down [hidden x inter]: E4M3 row-major
   const uint8_t* s[3];  // their UE8M0 tile scales, [rows / 128][cols / 128]
   uint32_t hidden, inter, m_tokens;
-  const uint8_t* xq;       // [M][3][hidden], natural column order
-  const int32_t* x_sigma;  // [M][4]: exponent of each (token, 1024-column segment)
   uint8_t* aq;             // [M][3][inter]: SwiGLU output terms, exponent sigma_a
-  const uint8_t* zeros;    // 256 zero bytes: the B source of unused columns
   float limit;
   int32_t sigma_a;
   float* y;
@@ -70,87 +67,142 @@ __device__ __forceinline__ float swiglu_clamped(float g, float u, float L) {
 // ------------------------------------------------------------------------------------------------
 // decode
 // ------------------------------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) shexp_prep_kernel(const float* __restrict__ x, uint64_t xts, uint64_t xds,
-                                                         uint32_t hidden, int32_t* __restrict__ x_sigma,
-                                                         uint8_t* __restrict__ xq, uint32_t* __restrict__ zeros) {
-  const uint32_t nst = hidden / kTileCols, t = blockIdx.x / nst, S = blockIdx.x % nst;
-  if (blockIdx.x == 0 && threadIdx.x < 64) zeros[threadIdx.x] = 0u;
-  __shared__ float red[4];
-  const int sigma = segment_terms(x, xts, xds, t, S, hidden, xq, red);
-  if (threadIdx.x == 0) x_sigma[t * kMaxSeg + S] = sigma;
-}
+// K order inside a 128-column MFMA step: lane group kg holds columns 16 kg .. 16 kg + 15 and
+// 64 + 16 kg .. 64 + 16 kg + 15 (any order works as long as A and B agree), so each of a step's two
+// 16-byte weight loads reads 64 contiguous bytes of each of the tile's 16 rows.
 
-// One wave's share of a 16-row tile: rows row0 .. row0 + 15 of W ([.. x K]), K columns k0 ..
-// k0 + 128 STEPS - 1, against CG groups of 16 B columns (column c of group cg: token 5 cg + c / 3,
-// term c % 3; column 15 unused). The B
-// rows are loaded first (small, in the cache), then the weights; each MFMA waits only for its own
-// step's weights. bscale(t, k) is the B exponent of token t at column k.
-template <int CG, int STEPS, typename BScale>
-__device__ __forceinline__ void shexp_tile(const uint8_t* __restrict__ W, const uint8_t* __restrict__ S, uint32_t K,
-                                           uint32_t row0, uint32_t k0, const uint8_t* __restrict__ bsrc,
-                                           uint32_t brow, uint32_t M, const uint8_t* zeros, BScale bscale,
-                                           v4f (&acc)[CG]) {
+// The weights of one wave's share of a 16-row tile, all requested at once: rows row0 .. row0 + 15
+// of W [.. x K], columns k0 .. k0 + 128 STEPS - 1; sa[m] = the tile scale of step m (the rows lie
+// in one 128-row band: uniform).
+template <int STEPS>
+__device__ __forceinline__ void load_a_tile(const uint8_t* __restrict__ W, const uint8_t* __restrict__ S, uint32_t K,
+                                            uint32_t row0, uint32_t k0, v8i (&a)[STEPS], int (&sa)[STEPS]) {
   const uint32_t lane = threadIdx.x & 63, c = lane & 15, kg = lane >> 4;
-  v8i b[STEPS][CG];
-  int sb[STEPS][CG];
-#pragma unroll
-  for (int cg = 0; cg < CG; ++cg) {
-    const uint32_t t = 5u * cg + c / 3u, tau = c % 3u;  // five tokens per 16-column group
-    const bool valid = c < 15u && t < M;
-    // an unused column reads the 32 zero bytes of every step
-    const u32x4* p = reinterpret_cast<const u32x4*>(valid ? bsrc + (uint64_t)(t * kTerms + tau) * brow + k0 + 32u * kg
-                                                          : zeros);
-    const uint32_t st = valid ? 8u : 0u;
-#pragma unroll
-    for (int m = 0; m < STEPS; ++m) {
-      b[m][cg] = join8(p[st * m], p[st * m + 1]);
-      sb[m][cg] = valid ? bscale(t, k0 + 128u * m) : 127;
-    }
-  }
-  __builtin_amdgcn_sched_barrier(0);
   const __amdgpu_buffer_rsrc_t wr =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(W), (short)0, 0x7FFFFFFF, 0x00020000);
-  const uint32_t vo = (row0 + c) * K + k0 + 32u * kg;
-  v8i a[STEPS];
+  const uint32_t vo = (row0 + c) * K + k0 + 16u * kg;
 #pragma unroll
   for (int m = 0; m < STEPS; ++m)
     a[m] = join8(__builtin_amdgcn_raw_buffer_load_b128(wr, vo + 128u * m, 0, 2),
-                 __builtin_amdgcn_raw_buffer_load_b128(wr, vo + 128u * m + 16u, 0, 2));
-  // the tile scales of the wave's rows (one 128-row band) over its K range: uniform per step
+                 __builtin_amdgcn_raw_buffer_load_b128(wr, vo + 128u * m + 64u, 0, 2));
   const uint8_t* srow = S + (uint64_t)(row0 >> 7) * (K >> 7) + (k0 >> 7);
-  int sa[STEPS];
 #pragma unroll
   for (int m = 0; m < STEPS; ++m) sa[m] = __builtin_amdgcn_readfirstlane((int)srow[m]);
-#pragma unroll
-  for (int cg = 0; cg < CG; ++cg) acc[cg] = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int m = 0; m < STEPS; ++m)
-#pragma unroll
-    for (int cg = 0; cg < CG; ++cg) acc[cg] = mfma_scaled(a[m], b[m][cg], acc[cg], sa[m], sb[m][cg]);
 }
+
+// Column c of B column group cg: token 5 cg + c / 3, term c % 3 (column 15 unused).
+__device__ __forceinline__ uint32_t bcol_token(int cg, uint32_t c) { return 5u * cg + c / 3u; }
 
 // The three E4M3 terms of token t held in columns c, c + 1, c + 2 of a 16-column group.
 __device__ __forceinline__ float part_terms(const float (&p)[16], uint32_t col) {
   return p[col] + p[col + 1] * 0.0625f + p[col + 2] * 0.00390625f;
 }
 
+// gate/up + SwiGLU: one workgroup per 16 rows of inter, wave w = {gate, up}[w & 1] x K quarter
+// w >> 1 (STEPS = hidden / 512 steps each). The activation's terms are made here, into LDS: each
+// thread holds 8 columns of every token, the token's largest magnitude fixes its exponent (the B
+// scale), three E4M3 terms per element.
 template <int CG, int STEPS>
-__global__ void __launch_bounds__(kSxWaves * 64) shexp_gateup_kernel(SharedArgs A) {
-  const uint32_t rt = blockIdx.x, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const uint32_t mat = wv & 1u, q = wv >> 1, M = A.m_tokens;
-  const uint32_t k0 = q * (A.hidden / 4u);  // = 128 STEPS q
+__global__ void __launch_bounds__(kSxWaves * 64) shexp_gateup_kernel(SharedArgs A, const float* __restrict__ x,
+                                                                     uint64_t xts, uint64_t xds, int vec) {
+  const uint32_t rt = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const uint32_t c = lane & 15, kg = lane >> 4;
+  const uint32_t mat = wv & 1u, q = wv >> 1, M = A.m_tokens, H = A.hidden;
+  const uint32_t k0 = q * (H / 4u);
+  __shared__ __align__(16) uint8_t xq_l[kMaxTok * kTerms * 4096];
   __shared__ float part[kSxWaves][CG][16][16];
+  __shared__ float red[kSxWaves][kMaxTok];
+  // 1. the activation (small, in the cache) first: loads complete in issue order, so the wait for
+  // it does not wait for the weights issued after it
+  const uint32_t h0 = 8u * tid;
+  const bool mine = h0 < H;
+  float xv[kMaxTok][8];
+#pragma unroll
+  for (int t = 0; t < kMaxTok; ++t)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xv[t][i] = 0.f;
+  if (vec) {  // token-major rows, 16-byte aligned
+#pragma unroll
+    for (int t = 0; t < kMaxTok; ++t)
+      if ((uint32_t)t < M && mine) {
+        const float4 v0 = *reinterpret_cast<const float4*>(x + t * xts + h0);
+        const float4 v1 = *reinterpret_cast<const float4*>(x + t * xts + h0 + 4);
+        xv[t][0] = v0.x; xv[t][1] = v0.y; xv[t][2] = v0.z; xv[t][3] = v0.w;
+        xv[t][4] = v1.x; xv[t][5] = v1.y; xv[t][6] = v1.z; xv[t][7] = v1.w;
+      }
+  } else {
+#pragma unroll
+    for (int t = 0; t < kMaxTok; ++t)
+      if ((uint32_t)t < M && mine)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xv[t][i] = x[t * xts + (h0 + i) * xds];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // 2. the weights
+  v8i a[STEPS];
+  int sa[STEPS];
+  load_a_tile<STEPS>(A.w[mat], A.s[mat], H, rt * 16u, k0, a, sa);
+  __builtin_amdgcn_sched_barrier(0);
+  // 3. exponent per token: its largest magnitude times 2^sigma in [128, 256)
+#pragma unroll
+  for (int t = 0; t < kMaxTok; ++t) {
+    float mx = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(xv[t][i]));
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if (lane == 0) red[wv][t] = mx;
+  }
+  __syncthreads();
+  int sig[kMaxTok];
+#pragma unroll
+  for (int t = 0; t < kMaxTok; ++t) {
+    float mx = 0.f;
+#pragma unroll
+    for (int w = 0; w < kSxWaves; ++w) mx = fmaxf(mx, red[w][t]);
+    sig[t] = mx > 0.f ? 7 - ilogbf(mx) : 0;
+  }
+  // 4. three E4M3 terms of every element into LDS, [token][term][column]
+#pragma unroll
+  for (int t = 0; t < kMaxTok; ++t)
+    if ((uint32_t)t < M && mine) {
+      uint32_t p0, p1, p2, q0, q1, q2;
+      split3x4(ldexpf(xv[t][0], sig[t]), ldexpf(xv[t][1], sig[t]), ldexpf(xv[t][2], sig[t]), ldexpf(xv[t][3], sig[t]),
+               p0, p1, p2);
+      split3x4(ldexpf(xv[t][4], sig[t]), ldexpf(xv[t][5], sig[t]), ldexpf(xv[t][6], sig[t]), ldexpf(xv[t][7], sig[t]),
+               q0, q1, q2);
+      uint8_t* dst = xq_l + (uint32_t)t * kTerms * H + h0;
+      *reinterpret_cast<uint2*>(dst) = uint2{p0, q0};
+      *reinterpret_cast<uint2*>(dst + H) = uint2{p1, q1};
+      *reinterpret_cast<uint2*>(dst + 2 * H) = uint2{p2, q2};
+    }
+  __syncthreads();
+  // 5. one MFMA per step and column group, B from LDS
   v4f acc[CG];
-  const int32_t* xs = A.x_sigma;
-  shexp_tile<CG, STEPS>(A.w[mat], A.s[mat], A.hidden, rt * 16u, k0, A.xq, A.hidden, M, A.zeros,
-                        [&](uint32_t t, uint32_t k) { return 127 - xs[t * kMaxSeg + (k >> 10)]; }, acc);
+  int sb[CG];
+  const uint8_t* bp[CG];
+  bool bv[CG];
+#pragma unroll
+  for (int cg = 0; cg < CG; ++cg) {
+    const uint32_t t = bcol_token(cg, c);
+    bv[cg] = c < 15u && t < M;
+    bp[cg] = xq_l + (bv[cg] ? (t * kTerms + c % 3u) * H : 0u) + k0 + 16u * kg;
+    sb[cg] = 127 - (bv[cg] ? sig[t < (uint32_t)kMaxTok ? t : 0] : 0);
+    acc[cg] = v4f{0.f, 0.f, 0.f, 0.f};
+  }
+#pragma unroll
+  for (int m = 0; m < STEPS; ++m)
+#pragma unroll
+    for (int cg = 0; cg < CG; ++cg) {
+      v8i b = join8(*reinterpret_cast<const u32x4*>(bp[cg] + 128 * m), *reinterpret_cast<const u32x4*>(bp[cg] + 128 * m + 64));
+      if (!bv[cg]) b = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+      acc[cg] = mfma_scaled(a[m], b, acc[cg], sa[m], sb[cg]);
+    }
   // accumulator lane l, element v = D[row 4 (l / 16) + v][column l % 16]
 #pragma unroll
   for (int cg = 0; cg < CG; ++cg)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) part[wv][cg][4 * (lane >> 4) + v][lane & 15] = acc[cg][v];
+    for (int v = 0; v < 4; ++v) part[wv][cg][4 * kg + v][c] = acc[cg][v];
   __syncthreads();
-  const uint32_t tid = threadIdx.x;
   if (tid < 16u * M) {
     const uint32_t r = tid & 15u, t = tid >> 4, cg = t / 5u, col = (t % 5u) * 3u;
     float g = 0.f, u = 0.f;
@@ -168,21 +220,44 @@ __global__ void __launch_bounds__(kSxWaves * 64) shexp_gateup_kernel(SharedArgs 
   }
 }
 
+// down: one workgroup per 16 rows of hidden, wave w = K eighth w (STEPS = inter / 1024 steps); B
+// (the SwiGLU terms, small, in the cache) requested before the weights; fixed-order sum of the
+// eighths; y (+)= result.
 template <int CG, int STEPS>
 __global__ void __launch_bounds__(kSxWaves * 64) shexp_down_kernel(SharedArgs A) {
-  const uint32_t rt = blockIdx.x, lane = threadIdx.x & 63, wv = threadIdx.x >> 6, M = A.m_tokens;
-  const uint32_t k0 = wv * (A.inter / 8u);  // = 128 STEPS wv
+  const uint32_t rt = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, M = A.m_tokens;
+  const uint32_t c = lane & 15, kg = lane >> 4;
+  const uint32_t k0 = wv * (A.inter / 8u);
   __shared__ float part[kSxWaves][CG][16][16];
-  v4f acc[CG];
+  v8i b[STEPS][CG];
+#pragma unroll
+  for (int cg = 0; cg < CG; ++cg) {
+    const uint32_t t = bcol_token(cg, c);
+    const bool ok = c < 15u && t < M;
+    const uint8_t* p = A.aq + (ok ? (uint64_t)(t * kTerms + c % 3u) * A.inter : 0u) + k0 + 16u * kg;
+#pragma unroll
+    for (int m = 0; m < STEPS; ++m) {
+      b[m][cg] = join8(*reinterpret_cast<const u32x4*>(p + 128 * m), *reinterpret_cast<const u32x4*>(p + 128 * m + 64));
+      if (!ok) b[m][cg] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  v8i a[STEPS];
+  int sa[STEPS];
+  load_a_tile<STEPS>(A.w[2], A.s[2], A.inter, rt * 16u, k0, a, sa);
   const int sb = 127 - A.sigma_a;
-  shexp_tile<CG, STEPS>(A.w[2], A.s[2], A.inter, rt * 16u, k0, A.aq, A.inter, M, A.zeros,
-                        [&](uint32_t, uint32_t) { return sb; }, acc);
+  v4f acc[CG];
+#pragma unroll
+  for (int cg = 0; cg < CG; ++cg) acc[cg] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int m = 0; m < STEPS; ++m)
+#pragma unroll
+    for (int cg = 0; cg < CG; ++cg) acc[cg] = mfma_scaled(a[m], b[m][cg], acc[cg], sa[m], sb);
 #pragma unroll
   for (int cg = 0; cg < CG; ++cg)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) part[wv][cg][4 * (lane >> 4) + v][lane & 15] = acc[cg][v];
+    for (int v = 0; v < 4; ++v) part[wv][cg][4 * kg + v][c] = acc[cg][v];
   __syncthreads();
-  const uint32_t tid = threadIdx.x;
   if (tid < 16u * M) {
     const uint32_t r = tid & 15u, t = tid >> 4, cg = t / 5u, col = (t % 5u) * 3u;
     float sum = 0.f;
@@ -538,14 +613,12 @@ struct SharedWs {
   uint64_t sigma, zeros, xq, aq, total;
 };
 
-// decode: [x_sigma M x 4][zeros][xq M x 3 x hidden][aq M x 3 x inter]
+// decode: [aq M x 3 x inter]
 SharedWs shared_decode_ws(uint32_t M, uint32_t hidden, uint32_t inter) {
+  (void)hidden;
   SharedWs w;
-  w.sigma = 0;
-  w.zeros = a256(4ull * kMaxSeg * M);
-  w.xq = w.zeros + 256;
-  w.aq = w.xq + a256((uint64_t)M * kTerms * hidden);
-  w.total = w.aq + a256((uint64_t)M * kTerms * inter);
+  w.sigma = w.zeros = w.xq = w.aq = 0;
+  w.total = a256((uint64_t)M * kTerms * inter);
   return w;
 }
 
@@ -581,12 +654,14 @@ int shared_check(const affx_shared_expert* S, const char* what, uint32_t max_hid
 }
 
 template <int CG>
-void launch_gateup(uint32_t steps, dim3 g, hipStream_t s, const SharedArgs& A) {
+void launch_gateup(uint32_t steps, dim3 g, hipStream_t s, const SharedArgs& A, const float* x, uint64_t xts,
+                   uint64_t xds, int vec) {
+  const dim3 b(kSxWaves * 64);
   switch (steps) {
-    case 2: hipLaunchKernelGGL((shexp_gateup_kernel<CG, 2>), g, dim3(kSxWaves * 64), 0, s, A); break;
-    case 4: hipLaunchKernelGGL((shexp_gateup_kernel<CG, 4>), g, dim3(kSxWaves * 64), 0, s, A); break;
-    case 6: hipLaunchKernelGGL((shexp_gateup_kernel<CG, 6>), g, dim3(kSxWaves * 64), 0, s, A); break;
-    default: hipLaunchKernelGGL((shexp_gateup_kernel<CG, 8>), g, dim3(kSxWaves * 64), 0, s, A); break;
+    case 2: hipLaunchKernelGGL((shexp_gateup_kernel<CG, 2>), g, b, 0, s, A, x, xts, xds, vec); break;
+    case 4: hipLaunchKernelGGL((shexp_gateup_kernel<CG, 4>), g, b, 0, s, A, x, xts, xds, vec); break;
+    case 6: hipLaunchKernelGGL((shexp_gateup_kernel<CG, 6>), g, b, 0, s, A, x, xts, xds, vec); break;
+    default: hipLaunchKernelGGL((shexp_gateup_kernel<CG, 8>), g, b, 0, s, A, x, xts, xds, vec); break;
   }
 }
 
@@ -642,27 +717,22 @@ int affx_shared_expert_decode(const affx_shared_expert* S, const float* x, uint6
   A.hidden = S->hidden;
   A.inter = S->inter;
   A.m_tokens = m_tokens;
-  A.xq = b + lay.xq;
-  A.x_sigma = (const int32_t*)(b + lay.sigma);
   A.aq = b + lay.aq;
-  A.zeros = b + lay.zeros;
   A.limit = S->swiglu_limit;
   A.sigma_a = 7 - ilogbf(S->swiglu_limit * S->swiglu_limit);
   A.y = y;
   A.y_ts = y_ts;
   A.y_ds = y_ds;
   A.accumulate = accumulate;
-  const uint32_t nst = S->hidden / kTileCols;
-  hipLaunchKernelGGL(shexp_prep_kernel, dim3(m_tokens * nst), dim3(256), 0, s, x, x_ts, x_ds, S->hidden,
-                     (int32_t*)(b + lay.sigma), b + lay.xq, (uint32_t*)(b + lay.zeros));
-  if ((rc = check_launch("shexp_prep_kernel"))) return rc;
   const uint32_t gsteps = S->hidden / 512u, dsteps = S->inter / 1024u;
+  // token-major rows with 16-byte alignment take 16-byte loads, any other strides element loads
+  const int vec = x_ds == 1 && (x_ts % 4) == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
   if (m_tokens <= 5) {
-    launch_gateup<1>(gsteps, dim3(S->inter / 16u), s, A);
+    launch_gateup<1>(gsteps, dim3(S->inter / 16u), s, A, x, x_ts, x_ds, vec);
     if ((rc = check_launch("shexp_gateup_kernel"))) return rc;
     launch_down<1>(dsteps, dim3(S->hidden / 16u), s, A);
   } else {
-    launch_gateup<2>(gsteps, dim3(S->inter / 16u), s, A);
+    launch_gateup<2>(gsteps, dim3(S->inter / 16u), s, A, x, x_ts, x_ds, vec);
     if ((rc = check_launch("shexp_gateup_kernel"))) return rc;
     launch_down<2>(dsteps, dim3(S->hidden / 16u), s, A);
   }
