@@ -11,6 +11,9 @@
 //                    input: exact for every element of at least 2^-13 of the token's largest
 //                    magnitude, where both terms are normal E4M3 numbers, and within 2^-20 of that
 //                    maximum below it; 3 when a low bf16 term is given)
+//   (each GEMM runs twice: the wide tiles, then the narrow ones, an expert's partial last tile of
+//   at most kGNarrow column tiles of tokens, in an instantiation whose MFMAs, fragment reads and
+//   direct loads cover just those columns)
 //   grouped_gemm<0>  gate/up: (row block of 128 inter rows, token tile): 8 waves x 16 rows of
 //                    gate and the same 16 of up, K = hidden in 128-column MFMA steps, 12 column
 //                    tiles per A fragment; epilogue combines terms, applies row scales, SwiGLU,
@@ -33,35 +36,42 @@ struct Tile {
   uint32_t expert, slot0, n;
 };
 
+// Tiles of each GEMM: the wide ones (up to kGCT column tiles of tokens) first, then the narrow ones
+// (an expert's last, partial tile when it needs at most kGNarrow column tiles), which a narrower
+// instantiation of the GEMM runs.
 struct GroupedHdr {
   uint32_t n_slots;
-  uint32_t n_tiles1, n_tiles2;
+  uint32_t n_tiles1, n_tiles2;     // wide tiles
   uint32_t tx;                     // activation terms of the gate/up input (2 or 3)
   uint32_t bad;                    // a caller's slot list needed more tiles than it can hold
+  uint32_t n_narrow1, n_narrow2;   // narrow tiles, after the wide ones
 };
 
 // ------------------------------------------------------------------------------------------------
 // plan
 // ------------------------------------------------------------------------------------------------
-// Exclusive scan over the workgroup (kPlanThreads threads, thread i holds v[i]) of three counts
-// at once; returns thread i's prefixes and writes the totals to tot.
-__device__ __forceinline__ void plan_scan3(uint32_t (&v)[3], uint32_t* wsum, uint32_t (&tot)[3]) {
+// Exclusive scan over the workgroup (kPlanThreads threads, thread i holds v[i]) of N counts at
+// once; returns thread i's prefixes and writes the totals to tot.
+template <int N>
+__device__ __forceinline__ void plan_scan(uint32_t (&v)[N], uint32_t* wsum, uint32_t (&tot)[N]) {
   const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   constexpr uint32_t kW = kPlanThreads / 64;
-  uint32_t inc[3] = {v[0], v[1], v[2]};
+  uint32_t inc[N];
+#pragma unroll
+  for (int q = 0; q < N; ++q) inc[q] = v[q];
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1)
 #pragma unroll
-    for (int q = 0; q < 3; ++q) {
+    for (int q = 0; q < N; ++q) {
       const uint32_t n = __shfl_up(inc[q], o);
       if (lane >= (uint32_t)o) inc[q] += n;
     }
   if (lane == 63)
 #pragma unroll
-    for (int q = 0; q < 3; ++q) wsum[q * kW + wv] = inc[q];
+    for (int q = 0; q < N; ++q) wsum[q * kW + wv] = inc[q];
   __syncthreads();
 #pragma unroll
-  for (int q = 0; q < 3; ++q) {
+  for (int q = 0; q < N; ++q) {
     uint32_t before = 0, all = 0;
     for (uint32_t w = 0; w < kW; ++w) {
       const uint32_t x = wsum[q * kW + w];
@@ -73,73 +83,83 @@ __device__ __forceinline__ void plan_scan3(uint32_t (&v)[3], uint32_t* wsum, uin
   }
 }
 
+// An expert's c slots in tiles of tt tokens: its wide tiles (the full ones, and a partial one of
+// more than nar tokens) and narrow tiles (a partial one of at most nar tokens: 0 or 1).
+__device__ __forceinline__ uint32_t n_wide(uint32_t c, uint32_t tt, uint32_t nar) {
+  return c / tt + (c % tt > nar ? 1u : 0u);
+}
+__device__ __forceinline__ uint32_t n_narrow(uint32_t c, uint32_t tt, uint32_t nar) {
+  return (c % tt != 0u && c % tt <= nar) ? 1u : 0u;
+}
+// Writes the tiles of one expert (slots b0 .. b0 + c - 1): wide ones from tiles[w0], the narrow
+// one at tiles[n0].
+__device__ __forceinline__ void put_tiles(Tile* tiles, uint32_t e, uint32_t b0, uint32_t c, uint32_t tt, uint32_t nar,
+                                          uint32_t w0, uint32_t n0) {
+  const uint32_t full = c / tt, r = c % tt;
+  for (uint32_t k = 0; k < full; ++k) tiles[w0 + k] = Tile{e, b0 + k * tt, tt};
+  if (r > nar) tiles[w0 + full] = Tile{e, b0 + full * tt, r};
+  else if (r > 0) tiles[n0] = Tile{e, b0 + full * tt, r};
+}
+
 // start_in: a caller's slot list, expert e owning slots [start_in[e], start_in[e+1]) of n_slots_in
 // (each bound clamped to n_slots_in; a range that runs backwards is empty); null: count the routes.
 __global__ void __launch_bounds__(kPlanThreads) grouped_plan_kernel(
     const uint32_t* __restrict__ sel, uint32_t n_pairs, uint32_t n_experts, uint32_t tt1,
-    uint32_t tt2, uint32_t tx, const uint32_t* __restrict__ start_in, uint32_t n_slots_in,
-    uint32_t max_tiles1, uint32_t max_tiles2, GroupedHdr* __restrict__ hdr, uint32_t* __restrict__ offsets,
-    Tile* __restrict__ tiles1, Tile* __restrict__ tiles2) {
+    uint32_t tt2, uint32_t nar1, uint32_t nar2, uint32_t tx, const uint32_t* __restrict__ start_in,
+    uint32_t n_slots_in, uint32_t max_tiles1, uint32_t max_tiles2, GroupedHdr* __restrict__ hdr,
+    uint32_t* __restrict__ offsets, Tile* __restrict__ tiles1, Tile* __restrict__ tiles2) {
   static_assert(AFFX_MAX_EXPERTS <= kPlanThreads, "one thread per expert in the scan");
   __shared__ uint32_t cnt[AFFX_MAX_EXPERTS];
-  __shared__ uint32_t wsum[3 * (kPlanThreads / 64)];
+  __shared__ uint32_t wsum[5 * (kPlanThreads / 64)];
   const uint32_t tid = threadIdx.x;
+  uint32_t c = 0, b0 = 0;
   if (start_in) {
-    uint32_t c = 0, b0 = 0;
     if (tid < n_experts) {
       const uint32_t a = min(start_in[tid], n_slots_in), b = min(start_in[tid + 1], n_slots_in);
       c = b > a ? b - a : 0u;
       b0 = a;
     }
-    uint32_t v[3] = {c, (c + tt1 - 1) / tt1, (c + tt2 - 1) / tt2}, tot[3];
-    plan_scan3(v, wsum, tot);
-    // overlapping ranges could ask for more tiles than the workspace holds: then no tile at all
-    const bool fits = tot[1] <= max_tiles1 && tot[2] <= max_tiles2;
-    if (fits && tid < n_experts) {
-      for (uint32_t k = 0; k * tt1 < c; ++k) tiles1[v[1] + k] = Tile{tid, b0 + k * tt1, min(tt1, c - k * tt1)};
-      for (uint32_t k = 0; k * tt2 < c; ++k) tiles2[v[2] + k] = Tile{tid, b0 + k * tt2, min(tt2, c - k * tt2)};
-    }
-    if (tid == 0) {
-      hdr->n_slots = n_slots_in;
-      hdr->n_tiles1 = fits ? tot[1] : 0u;
-      hdr->n_tiles2 = fits ? tot[2] : 0u;
-      hdr->tx = tx;
-      hdr->bad = fits ? 0u : 1u;
-    }
-    return;
-  }
-  for (uint32_t e = tid; e < AFFX_MAX_EXPERTS; e += kPlanThreads) cnt[e] = 0;
-  __syncthreads();
-  // counts per expert: eight routes per thread in flight at a time
-  constexpr uint32_t kU = 8;
-  for (uint32_t i0 = 0; i0 < n_pairs; i0 += kU * kPlanThreads) {
-    uint32_t ev[kU];
+  } else {
+    for (uint32_t e = tid; e < AFFX_MAX_EXPERTS; e += kPlanThreads) cnt[e] = 0;
+    __syncthreads();
+    // counts per expert: eight routes per thread in flight at a time
+    constexpr uint32_t kU = 8;
+    for (uint32_t i0 = 0; i0 < n_pairs; i0 += kU * kPlanThreads) {
+      uint32_t ev[kU];
 #pragma unroll
-    for (uint32_t u = 0; u < kU; ++u) {
-      const uint32_t i = i0 + u * kPlanThreads + tid;
-      ev[u] = i < n_pairs ? sel[i] : ~0u;
-    }
+      for (uint32_t u = 0; u < kU; ++u) {
+        const uint32_t i = i0 + u * kPlanThreads + tid;
+        ev[u] = i < n_pairs ? sel[i] : ~0u;
+      }
 #pragma unroll
-    for (uint32_t u = 0; u < kU; ++u)
-      if (ev[u] < n_experts) atomicAdd(&cnt[ev[u]], 1u);
+      for (uint32_t u = 0; u < kU; ++u)
+        if (ev[u] < n_experts) atomicAdd(&cnt[ev[u]], 1u);
+    }
+    __syncthreads();
+    c = tid < n_experts ? cnt[tid] : 0u;
   }
-  __syncthreads();
-  // slot offsets and tile offsets: one exclusive scan (expert order) of count and tiles
-  const uint32_t c = tid < n_experts ? cnt[tid] : 0u;
-  uint32_t v[3] = {c, (c + tt1 - 1) / tt1, (c + tt2 - 1) / tt2}, tot[3];
-  plan_scan3(v, wsum, tot);
-  if (tid < n_experts) {
-    offsets[tid] = v[0];
-    for (uint32_t k = 0; k * tt1 < c; ++k) tiles1[v[1] + k] = Tile{tid, v[0] + k * tt1, min(tt1, c - k * tt1)};
-    for (uint32_t k = 0; k * tt2 < c; ++k) tiles2[v[2] + k] = Tile{tid, v[0] + k * tt2, min(tt2, c - k * tt2)};
+  // slot offsets and tile offsets: one exclusive scan (expert order) of the count and the wide and
+  // narrow tiles of both GEMMs
+  uint32_t v[5] = {c, n_wide(c, tt1, nar1), n_narrow(c, tt1, nar1), n_wide(c, tt2, nar2), n_narrow(c, tt2, nar2)};
+  uint32_t tot[5];
+  plan_scan<5>(v, wsum, tot);
+  if (!start_in) b0 = v[0];
+  // a caller's overlapping ranges could ask for more tiles than the workspace holds: then no tile
+  const bool fits = tot[1] + tot[2] <= max_tiles1 && tot[3] + tot[4] <= max_tiles2;
+  if (fits && tid < n_experts) {
+    if (!start_in) offsets[tid] = v[0];
+    put_tiles(tiles1, tid, b0, c, tt1, nar1, v[1], tot[1] + v[2]);
+    put_tiles(tiles2, tid, b0, c, tt2, nar2, v[3], tot[3] + v[4]);
   }
   if (tid == 0) {
-    offsets[n_experts] = tot[0];
-    hdr->n_slots = tot[0];
-    hdr->n_tiles1 = tot[1];
-    hdr->n_tiles2 = tot[2];
+    if (!start_in) offsets[n_experts] = tot[0];
+    hdr->n_slots = start_in ? n_slots_in : tot[0];
+    hdr->n_tiles1 = fits ? tot[1] : 0u;
+    hdr->n_narrow1 = fits ? tot[2] : 0u;
+    hdr->n_tiles2 = fits ? tot[3] : 0u;
+    hdr->n_narrow2 = fits ? tot[4] : 0u;
     hdr->tx = tx;
-    hdr->bad = 0;
+    hdr->bad = fits ? 0u : 1u;
   }
 }
 
@@ -148,13 +168,13 @@ __global__ void __launch_bounds__(kPlanThreads) grouped_plan_kernel(
 __global__ void __launch_bounds__(kPlanThreads) grouped_run_kernel(const uint32_t* __restrict__ sel,
                                                                   uint32_t n_tok, uint32_t top_k,
                                                                   uint32_t n_experts, uint32_t* __restrict__ run) {
-  __shared__ uint32_t wsum[3 * (kPlanThreads / 64)];
+  __shared__ uint32_t wsum[kPlanThreads / 64];
   const uint32_t tid = threadIdx.x, per = (n_tok + kPlanThreads - 1) / kPlanThreads;
   const uint32_t t0 = tid * per, t1 = min(n_tok, t0 + per);
   uint32_t c = 0;
   for (uint32_t i = t0 * top_k; i < t1 * top_k; ++i) c += sel[i] < n_experts ? 1u : 0u;
-  uint32_t v[3] = {c, 0u, 0u}, tot[3];
-  plan_scan3(v, wsum, tot);
+  uint32_t v[1] = {c}, tot[1];
+  plan_scan<1>(v, wsum, tot);
   uint32_t r = v[0];
   for (uint32_t t = t0; t < t1; ++t) {
     run[t] = r;
@@ -273,10 +293,16 @@ constexpr int kGW = 8;                      // waves per workgroup (two per SIMD
 constexpr int kGRT = 16 / kGW;              // 16-row tiles per wave (a workgroup covers 256 rows)
 constexpr int kGT = kGW * 64;
 constexpr int kGKC = 2;                     // codebook copies (pre-rotated tables)
-constexpr int kGCT = 12;                    // 16-column tiles of B per wave
-constexpr int kGCols = kGCT * 16;           // B columns per workgroup
-constexpr uint32_t kGBuf = kGCols * 128;    // bytes of one B buffer (one MFMA step)
-constexpr int kGDma = kGCols / 8 / kGW;     // direct-load instructions per wave per step (8 columns each)
+constexpr int kGCT = 12;                    // 16-column tiles of B per wave (a wide tile)
+constexpr int kGNarrow = 4;                 // the same for a narrow tile
+// A tile of CT column tiles (kGCT wide, kGNarrow narrow): its B columns, the bytes of one B buffer
+// (one MFMA step) and the direct-load instructions per wave per step (8 columns each).
+template <int CT>
+struct GTile {
+  static constexpr int kCols = CT * 16;
+  static constexpr uint32_t kBuf = kCols * 128;
+  static constexpr int kDma = kCols / 8 / kGW;
+};
 
 struct GemmArgs {
   const uint8_t* base;
@@ -345,7 +371,7 @@ __device__ __forceinline__ void ring_load(Unit& u, __amdgpu_buffer_rsrc_t cr, __
   if constexpr (M == 7) { chunk(4); field(2); }
 }
 
-template <int PH, int TX>
+template <int PH, int TX, int CT>
 __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
   constexpr int TPG = 16 / TX;  // tokens per 16-column tile
   constexpr int kHalf = kGRT / 2;  // gate/up: units [0, kHalf) gate, [kHalf, kGRT) the same rows of up
@@ -377,10 +403,16 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
   uint32_t cbv[kPer];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) cbv[i] = A.codebook[tid + (uint32_t)kGT * i];
-  const uint32_t n_tiles = PH == 0 ? A.hdr->n_tiles1 : A.hdr->n_tiles2;
+  // this instantiation's tiles: the wide ones, or the narrow ones stored after them
+  const uint32_t n_wide_t = PH == 0 ? A.hdr->n_tiles1 : A.hdr->n_tiles2;
+  const uint32_t n_tiles = CT == kGCT ? n_wide_t : (PH == 0 ? A.hdr->n_narrow1 : A.hdr->n_narrow2);
+  // (entries below max_t are allocated: read before it is known whether a tile is in use)
+  const uint32_t room = CT == kGCT ? A.max_tiles : A.max_tiles - min(n_wide_t, A.max_tiles);
+  const Tile* tiles = room ? A.tiles + (CT == kGCT ? 0u : n_wide_t) : A.tiles;
+  const uint32_t max_t = room ? room : 1u;
   uint32_t w = blockIdx.x, rb, tile_id;
   item_of(w, rb, tile_id);
-  Tile tl = A.tiles[tile_id < A.max_tiles ? tile_id : 0u];
+  Tile tl = tiles[tile_id < max_t ? tile_id : 0u];
   if (tile_id >= n_tiles || tl.n == 0) return;  // (a tile in use has n >= 1: the test only makes
                                                 // both loads precede the branch, in one round trip)
 
@@ -389,10 +421,10 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
   const uint8_t* btbl = reinterpret_cast<const uint8_t*>(blk_s);
   // B of step t in buffer t % 4, written two steps at a time, two steps ahead (four separate
   // arrays: the compiler can then tell the buffers being read from the ones being written)
-  __shared__ __align__(16) uint8_t buf0[kGBuf];
-  __shared__ __align__(16) uint8_t buf1[kGBuf];
-  __shared__ __align__(16) uint8_t buf2[kGBuf];
-  __shared__ __align__(16) uint8_t buf3[kGBuf];
+  __shared__ __align__(16) uint8_t buf0[GTile<CT>::kBuf];
+  __shared__ __align__(16) uint8_t buf1[GTile<CT>::kBuf];
+  __shared__ __align__(16) uint8_t buf2[GTile<CT>::kBuf];
+  __shared__ __align__(16) uint8_t buf3[GTile<CT>::kBuf];
   uint32_t* rowoff = reinterpret_cast<uint32_t*>(buf3);  // set-up only, before buffer 3 is written
   const uint8_t* lut = reinterpret_cast<const uint8_t*>(lut_s);
   auto bufsel = [&](int i) -> uint8_t* { return i == 0 ? buf0 : i == 1 ? buf1 : i == 2 ? buf2 : buf3; };
@@ -421,28 +453,30 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
     for (int r = 0; r < kGRT; ++r)
       load_unit_buf(u[r], PH == 0 && r >= kHalf ? c1 : c0, PH == 0 && r >= kHalf ? f1 : f0, rt_of(r) * nst, lane);
   };
-  // B row of column tid (threads below kGCols): a column past the tile's tokens reads the tile's
+  // B row of column tid (threads below GTile<CT>::kCols): a column past the tile's tokens reads the tile's
   // first slot (unconditional load) and gets the zero row
   const uint32_t bcol_j = (tid >> 4) * TPG + (tid & 15u) / TX;
   auto brow_load = [&](const Tile& t) -> uint32_t {
-    const uint32_t bslot = t.slot0 + ((tid < kGCols && (tid & 15u) < TX * TPG && bcol_j < t.n) ? bcol_j : 0u);
+    const uint32_t bslot = t.slot0 + ((tid < GTile<CT>::kCols && (tid & 15u) < TX * TPG && bcol_j < t.n) ? bcol_j : 0u);
     return PH == 0 ? min(A.slot_tok[bslot], A.n_tok - 1u) : bslot;
   };
   auto rowoff_store = [&](const Tile& t, uint32_t brow) {
-    const bool used = tid < kGCols && (tid & 15u) < TX * TPG && bcol_j < t.n;
-    if (tid < kGCols)
+    const bool used = tid < GTile<CT>::kCols && (tid & 15u) < TX * TPG && bcol_j < t.n;
+    if (tid < GTile<CT>::kCols)
       rowoff[tid] = used ? (uint32_t)(A.b_off + ((uint64_t)brow * TX + (tid & 15u) % TX) * K) : (uint32_t)A.zero_off;
   };
-  // DMA lane map: instruction i of wave w writes columns 8b..8b+7 (b = kGDma w + i), lane l to
+  // DMA lane map: instruction i of wave w writes columns 8b..8b+7 (b = GTile<CT>::kDma w + i), lane l to
   // LDS slot l & 7 of column 8b + (l >> 3); slot p of column col holds global chunk p ^ f(col),
   // f(col) = (c ^ (c >> 3)) & 7 with c = col & 15 (the column within its 16-column tile), that
   // is (col & 7) ^ ((col >> 3) & 1). A fragment read (lane = column c + 16 k-group) then puts lanes
   // 0-7, 8-15 (and so on) on 8 distinct 16-byte bank groups, and lanes 0-15 on 16.
-  uint32_t roff[kGDma];
+  // (sized for the wide tile, a narrow one uses the first entries: with a size that depends on CT,
+  // captured by the lambdas below, ROCm 7.2's hipcc emits no host stub for the kernel)
+  uint32_t roff[GTile<kGCT>::kDma];
   auto roff_load = [&]() {
 #pragma unroll
-    for (int i = 0; i < kGDma; ++i) {
-      const uint32_t col = 8u * (kGDma * wv + i) + (lane >> 3);
+    for (int i = 0; i < GTile<CT>::kDma; ++i) {
+      const uint32_t col = 8u * (GTile<CT>::kDma * wv + i) + (lane >> 3);
       const uint32_t q = (lane & 7u) ^ ((col & 7u) ^ ((col >> 3) & 1u));
       roff[i] = rowoff[col] + (q << 4);
     }
@@ -450,8 +484,8 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
   const __amdgpu_buffer_rsrc_t wsr = buffer_rsrc(A.ws, 0xFFFFFFFFu);
   auto dma = [&](uint8_t* buf, uint32_t step) {
 #pragma unroll
-    for (int i = 0; i < kGDma; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(wsr, AFFX_LDS_PTR(buf + (kGDma * wv + i) * 1024u), 16, roff[i],
+    for (int i = 0; i < GTile<CT>::kDma; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(wsr, AFFX_LDS_PTR(buf + (GTile<CT>::kDma * wv + i) * 1024u), 16, roff[i],
                                                step * 128u, 0, 0);
   };
 
@@ -507,11 +541,11 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
       lut_lookup_step<kGKC, true>(u[r], lut, btbl, copy4, 0, raw, sx);
       a_cur[r] = lut_finish(raw, sx);
     }
-    v4f acc[kGRT][kGCT];
+    v4f acc[kGRT][CT];
 #pragma unroll
     for (int r = 0; r < kGRT; ++r)
 #pragma unroll
-      for (int ct = 0; ct < kGCT; ++ct) acc[r][ct] = v4f{0.f, 0.f, 0.f, 0.f};
+      for (int ct = 0; ct < CT; ++ct) acc[r][ct] = v4f{0.f, 0.f, 0.f, 0.f};
 
     // ---- main loop: 1024 columns of K per iteration, eight MFMA steps ---------------------------
     // (each step is instantiated with its index as a constant: the ring loads, the code positions
@@ -548,7 +582,7 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
       // only: with two waves per SIMD a wave has 256 registers, accumulators included. (Step 0 of
       // the next 1024 columns after step 7: the ring has reloaded every register those reads use.)
       constexpr int mn = (m + 1) & 7;
-      constexpr int kLook = 4, kFin = 8;
+      constexpr int kLook = CT >= 12 ? 4 : 0, kFin = CT >= 12 ? 8 : 2;
       uint32_t rawn[kGRT][8], sxn[kGRT][4];
       v8i a_next[kGRT];
       auto bread = [&](int ct) -> v8i {
@@ -560,10 +594,10 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
         return b;
       };
       v8i bq0 = bread(0), bq1 = bread(1);
-      static_for<0, kGCT>([&](auto cc) {
+      static_for<0, CT>([&](auto cc) {
         constexpr int ct = decltype(cc)::value;
         v8i bq2;
-        if constexpr (ct + 2 < kGCT) bq2 = bread(ct + 2);
+        if constexpr (ct + 2 < CT) bq2 = bread(ct + 2);
 #pragma unroll
         for (int r = 0; r < kGRT; ++r) acc[r][ct] = mfma(a_cur[r], bq0, acc[r][ct]);
         if constexpr (ct >= kLook && ct < kLook + kGRT) {
@@ -583,7 +617,7 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
         __builtin_amdgcn_sched_group_barrier(0x100, 10, 0);
         __builtin_amdgcn_sched_barrier(0);
         bq0 = bq1;
-        if constexpr (ct + 2 < kGCT) bq1 = bq2;
+        if constexpr (ct + 2 < CT) bq1 = bq2;
       });
       // the accumulators are materialised here (else the compiler sinks every MFMA below all
       // eight steps' table reads and holds those in registers). They stay in VGPRs: a kernel that
@@ -592,7 +626,7 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
 #pragma unroll
       for (int r = 0; r < kGRT; ++r)
 #pragma unroll
-        for (int ct = 0; ct < kGCT; ++ct) AFFX_PIN(acc[r][ct]);
+        for (int ct = 0; ct < CT; ++ct) AFFX_PIN(acc[r][ct]);
 #pragma unroll
       for (int r = 0; r < kGRT; ++r) a_cur[r] = a_next[r];
       // After an odd step t: the B of steps t + 1 and t + 2 (issued at the top of step t - 1) is in
@@ -627,17 +661,17 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
     // first weights -------------------------------------------------------------------------------
     uint32_t rb2, tile2;
     item_of(w + gridDim.x, rb2, tile2);
-    const Tile tl2 = A.tiles[tile2 < A.max_tiles ? tile2 : 0u];
+    const Tile tl2 = tiles[tile2 < max_t ? tile2 : 0u];
     const bool next = tile2 < n_tiles && tl2.n != 0;
 
     // ---- epilogue inputs: every one requested before the first is used ----------------------
     // (gate/up: the activation exponent of the lane's token in each column tile, columns past the
     // tile's tokens read its last token and store nothing; the row scales. Down: row scales.)
-    int sig[PH == 0 ? kGCT : 1];
+    int sig[PH == 0 ? CT : 1];
     uint2 rgw[kHalf], ruw[kHalf], rdw[kGRT];
     if constexpr (PH == 0) {
 #pragma unroll
-      for (int ct = 0; ct < kGCT; ++ct) {
+      for (int ct = 0; ct < CT; ++ct) {
         const uint32_t j = ct * TPG + c / TX;
         sig[ct] = A.slot_sigma[tl.slot0 + (j < tl.n ? j : tl.n - 1u)];
       }
@@ -670,7 +704,7 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
         bf16x4(rgw[p], rg);
         bf16x4(ruw[p], ru);
         const uint32_t prow = kperm(row0);
-        static_for<0, kGCT>([&](auto cc) {
+        static_for<0, CT>([&](auto cc) {
           constexpr int ct = decltype(cc)::value;
           if (ct * TPG >= tl_cur.n) return;  // no token in this column tile (the same for the whole wave)
           float sg[4], su[4];
@@ -743,7 +777,7 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
         const uint32_t row0 = rt_cur(r) * 16u + 4u * kg;
         float rd[4];
         bf16x4(rdw[r], rd);
-        static_for<0, kGCT>([&](auto cc) {
+        static_for<0, CT>([&](auto cc) {
           constexpr int ct = decltype(cc)::value;
           if (ct * TPG >= tl_cur.n) return;  // no token in this column tile (the same for the whole wave)
           float sd[4];
@@ -902,8 +936,10 @@ int grouped_body(const affx_layer* L, const void* x, const void* x_lo, uint32_t 
 
   const uint32_t tt1 = tile_tokens(tx), tt2 = tile_tokens(3);
   const uint32_t Pp = sel ? T * K : 0u;
-  hipLaunchKernelGGL(grouped_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, sel, Pp, L->n_experts, tt1, tt2, tx,
-                     sel ? nullptr : start, sel ? 0u : n_slots, lay.max_tiles1, lay.max_tiles2,
+  // an expert's last tile is narrow when its tokens fill at most kGNarrow column tiles
+  const uint32_t nar1 = kGNarrow * (16 / tx), nar2 = kGNarrow * (16 / 3);
+  hipLaunchKernelGGL(grouped_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, sel, Pp, L->n_experts, tt1, tt2, nar1,
+                     nar2, tx, sel ? nullptr : start, sel ? 0u : n_slots, lay.max_tiles1, lay.max_tiles2,
                      (GroupedHdr*)(b + lay.hdr), (uint32_t*)(b + lay.offsets), (Tile*)(b + lay.tiles1),
                      (Tile*)(b + lay.tiles2));
   int rc = check_launch("grouped_plan_kernel");
@@ -931,21 +967,30 @@ int grouped_body(const affx_layer* L, const void* x, const void* x_lo, uint32_t 
   if ((rc = check_hip(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "hipDeviceGetAttribute")))
     return rc;
   const uint32_t gmax = cus >= 8 ? (uint32_t)cus / 8u * 8u : 8u;
-  const uint32_t i1 = (L->inter / 128) * ((lay.max_tiles1 + 7) / 8 * 8);
-  const uint32_t i2 = (L->hidden / 256) * ((lay.max_tiles2 + 7) / 8 * 8);
-  const uint32_t g1 = i1 < gmax ? i1 : gmax, g2 = i2 < gmax ? i2 : gmax;
+  // (the narrow tiles: at most one per expert)
+  auto grid = [&](uint32_t row_blocks, uint32_t tiles) {
+    const uint32_t items = row_blocks * ((tiles + 7) / 8 * 8);
+    return items < gmax ? items : gmax;
+  };
+  const uint32_t E8 = L->n_experts < lay.max_tiles1 ? L->n_experts : lay.max_tiles1;
   A.tiles = (const Tile*)(b + lay.tiles1);
   A.max_tiles = lay.max_tiles1;
   A.b_off = lay.xq;
-  if (tx == 2)
-    hipLaunchKernelGGL((grouped_gemm_kernel<0, 2>), dim3(g1), dim3(kGT), 0, s, A);
-  else
-    hipLaunchKernelGGL((grouped_gemm_kernel<0, 3>), dim3(g1), dim3(kGT), 0, s, A);
+  const uint32_t g1 = grid(L->inter / 128, lay.max_tiles1), gn1 = grid(L->inter / 128, E8);
+  if (tx == 2) {
+    hipLaunchKernelGGL((grouped_gemm_kernel<0, 2, kGCT>), dim3(g1), dim3(kGT), 0, s, A);
+    hipLaunchKernelGGL((grouped_gemm_kernel<0, 2, kGNarrow>), dim3(gn1), dim3(kGT), 0, s, A);
+  } else {
+    hipLaunchKernelGGL((grouped_gemm_kernel<0, 3, kGCT>), dim3(g1), dim3(kGT), 0, s, A);
+    hipLaunchKernelGGL((grouped_gemm_kernel<0, 3, kGNarrow>), dim3(gn1), dim3(kGT), 0, s, A);
+  }
   if ((rc = check_launch("grouped_gemm_kernel (gate/up)"))) return rc;
   A.tiles = (const Tile*)(b + lay.tiles2);
   A.max_tiles = lay.max_tiles2;
   A.b_off = lay.aq;
-  hipLaunchKernelGGL((grouped_gemm_kernel<1, 3>), dim3(g2), dim3(kGT), 0, s, A);
+  const uint32_t g2 = grid(L->hidden / 256, lay.max_tiles2), gn2 = grid(L->hidden / 256, E8);
+  hipLaunchKernelGGL((grouped_gemm_kernel<1, 3, kGCT>), dim3(g2), dim3(kGT), 0, s, A);
+  hipLaunchKernelGGL((grouped_gemm_kernel<1, 3, kGNarrow>), dim3(gn2), dim3(kGT), 0, s, A);
   if ((rc = check_launch("grouped_gemm_kernel (down)"))) return rc;
   hipLaunchKernelGGL(grouped_combine_kernel, dim3((L->hidden / 4 + 255) / 256, T), dim3(256), 0, s,
                      (const float*)(b + lay.z), ord_d, run_d, slot_w, n_sl, L->hidden, y, accumulate);
