@@ -254,20 +254,22 @@ def main() -> int:
         tf = flops / (msp * 1e-3) / 1e12
         log(f"C4 prefill: {msp:.3f} ms/layer -> {tf:.1f} TFLOP/s ({100 * tf * 1e12 / BF16_PEAK:.1f}% of bf16 peak)")
         # the form the engine hook runs: an f32 activation as a bf16 pair (three terms for gate/up)
+        # (its own output buffer: yp keeps the bf16 run's result for the parity check below)
         xf = ax.gen_normal(S_X + 1, T * H, 1.0, bf16_round=False).view(T, H)
         xh = xf.to(torch.bfloat16)
         xl = (xf - xh.float()).to(torch.bfloat16)
         del xf
-        ax.expert_ffn_grouped(pools[0], xh, sel_t, w_t, y=yp, x_lo=xl, workspace=gws)
+        y3 = torch.zeros_like(yp)
+        ax.expert_ffn_grouped(pools[0], xh, sel_t, w_t, y=y3, x_lo=xl, workspace=gws)
         torch.cuda.synchronize()
         st.record()
         for _ in range(args.prefill_steps):
-            ax.expert_ffn_grouped(pools[0], xh, sel_t, w_t, y=yp, x_lo=xl, workspace=gws)
+            ax.expert_ffn_grouped(pools[0], xh, sel_t, w_t, y=y3, x_lo=xl, workspace=gws)
         en.record()
         torch.cuda.synchronize()
         msp3 = st.elapsed_time(en) / args.prefill_steps
         tf3 = flops / (msp3 * 1e-3) / 1e12
-        del xh, xl
+        del xh, xl, y3
         log(f"C4 prefill, hi/lo input (the engine hook's form): {msp3:.3f} ms/layer -> {tf3:.1f} TFLOP/s")
         result["prefill"] = {"tflop_per_s": round(tf, 1), "ms_per_layer": round(msp, 4),
                              "frac_of_bf16_peak": round(tf * 1e12 / BF16_PEAK, 4),
@@ -290,8 +292,16 @@ def main() -> int:
             toks, _, _ = synthetic.prefill_sample(sel_np, E)
             gpu["c4"] = (sel_np, w_np, xb.float().cpu().numpy()[toks], yp.cpu().numpy()[toks], toks)
         result["cpu_baseline"], result["parity"] = cpu_baseline(ax, cont, gpu, L)
+        # every GPU result checked against the CPU path must be within the path's 1e-3 (the dequant
+        # bit-exact): a number measured on a wrong result is not a measurement
+        def failed(v) -> bool:
+            return (not v) if isinstance(v, bool) else (isinstance(v, float) and not v <= 1e-3)
+        bad = [k for k, v in result["parity"].items() if failed(v)]
+        result["parity_ok"] = not bad
+        if bad:
+            log(f"PARITY FAILED: {bad}")
     print(json.dumps(result), flush=True)
-    return 0
+    return 0 if result.get("parity_ok", True) else 1
 
 
 def cpu_model() -> str:
