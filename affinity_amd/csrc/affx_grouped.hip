@@ -3,7 +3,8 @@
 //
 //   grouped_plan     one workgroup: per-expert counts (from the routes, or from a slot list the
 //                    caller built), exclusive scan, tile lists
-//   grouped_run      one workgroup: per-token prefix of valid routes (the slot list's `run`)
+//   grouped_run      per route: `run` (token t's routes are entries t k .. t k + k - 1 of `ord`)
+//                    and a no-slot mark in `ord` for a route naming no expert of the layer
 //   grouped_place    one workgroup per expert: its (token, route) pairs in token order (stable),
 //                    so every slot and every output sum has a fixed order; writes the slot list
 //                    (token and weight per slot, `ord`: each token's slots in route order)
@@ -163,34 +164,25 @@ __global__ void __launch_bounds__(kPlanThreads) grouped_plan_kernel(
   }
 }
 
-// run[t] = number of routes of tokens before t that name an expert of the layer (run[n_tok] = all
-// of them): one workgroup, each thread a contiguous run of tokens.
-__global__ void __launch_bounds__(kPlanThreads) grouped_run_kernel(const uint32_t* __restrict__ sel,
-                                                                  uint32_t n_tok, uint32_t top_k,
-                                                                  uint32_t n_experts, uint32_t* __restrict__ run) {
-  __shared__ uint32_t wsum[kPlanThreads / 64];
-  const uint32_t tid = threadIdx.x, per = (n_tok + kPlanThreads - 1) / kPlanThreads;
-  const uint32_t t0 = tid * per, t1 = min(n_tok, t0 + per);
-  uint32_t c = 0;
-  for (uint32_t i = t0 * top_k; i < t1 * top_k; ++i) c += sel[i] < n_experts ? 1u : 0u;
-  uint32_t v[1] = {c}, tot[1];
-  plan_scan<1>(v, wsum, tot);
-  uint32_t r = v[0];
-  for (uint32_t t = t0; t < t1; ++t) {
-    run[t] = r;
-    for (uint32_t j = 0; j < top_k; ++j) r += sel[t * top_k + j] < n_experts ? 1u : 0u;
-  }
-  if (tid == 0) run[n_tok] = tot[0];
+// The routes form's ord/run: token t owns entries t k .. t k + k - 1 of ord, in route order
+// (run[t] = t k); a route that names no expert of the layer keeps ~0u there (the consumers skip
+// slot numbers past the slot count), grouped_place writes the slot of every other.
+__global__ void __launch_bounds__(256) grouped_run_kernel(const uint32_t* __restrict__ sel, uint32_t n_tok,
+                                                          uint32_t top_k, uint32_t n_experts,
+                                                          uint32_t* __restrict__ run, uint32_t* __restrict__ ord) {
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+  if (i < n_tok * top_k && !(sel[i] < n_experts)) ord[i] = ~0u;
+  if (i <= n_tok) run[i] = i * top_k;
 }
 
-// One workgroup per expert (plus the padding pass in workgroup n_experts): walks all pairs in
-// order and gives this expert's pairs consecutive slots. Thread tid takes 8 consecutive pairs of
-// each 2048-pair block (so thread order is pair order), an exclusive scan of the match counts
-// places them; the next block's routes are loaded before this block is placed.
+// One workgroup per expert: walks all pairs in order and gives this expert's pairs consecutive
+// slots (pair i's slot goes to ord[i]). Thread tid takes 8 consecutive pairs of each 2048-pair
+// block (so thread order is pair order), an exclusive scan of the match counts places them; the
+// next block's routes are loaded before this block is placed.
 __global__ void __launch_bounds__(256) grouped_place_kernel(
     const uint32_t* __restrict__ sel, const float* __restrict__ w, uint32_t n_pairs, uint32_t top_k,
-    uint32_t n_experts, const uint32_t* __restrict__ offsets, const uint32_t* __restrict__ run,
-    uint32_t* __restrict__ slot_tok, float* __restrict__ slot_w, uint32_t* __restrict__ ord) {
+    const uint32_t* __restrict__ offsets, uint32_t* __restrict__ slot_tok, float* __restrict__ slot_w,
+    uint32_t* __restrict__ ord) {
   const uint32_t e = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   uint32_t base = offsets[e];
   const uint32_t end = offsets[e + 1];
@@ -227,13 +219,10 @@ __global__ void __launch_bounds__(256) grouped_place_kernel(
 #pragma unroll
     for (uint32_t k = 0; k < kPer; ++k)
       if ((m >> k) & 1u) {
-        const uint32_t i = i0 + tid * kPer + k, t = i / top_k;
-        // the route's rank among its token's routes to the layer: its place in ord
-        uint32_t rank = 0;
-        for (uint32_t j = t * top_k; j < i; ++j) rank += sel[j] < n_experts ? 1u : 0u;
-        slot_tok[pos] = t;
+        const uint32_t i = i0 + tid * kPer + k;
+        slot_tok[pos] = i / top_k;
         slot_w[pos] = w[i];
-        ord[run[t] + rank] = pos;
+        ord[i] = pos;
         ++pos;
       }
     base += total;
@@ -945,12 +934,13 @@ int grouped_body(const affx_layer* L, const void* x, const void* x_lo, uint32_t 
   int rc = check_launch("grouped_plan_kernel");
   if (rc) return rc;
   if (sel) {
-    hipLaunchKernelGGL(grouped_run_kernel, dim3(1), dim3(kPlanThreads), 0, s, sel, T, K, L->n_experts,
-                       (uint32_t*)(b + lay.run));
+    const uint32_t nr = Pp > T ? Pp : T + 1;
+    hipLaunchKernelGGL(grouped_run_kernel, dim3((nr + 255) / 256), dim3(256), 0, s, sel, T, K, L->n_experts,
+                       (uint32_t*)(b + lay.run), (uint32_t*)(b + lay.ord));
     if ((rc = check_launch("grouped_run_kernel"))) return rc;
-    hipLaunchKernelGGL(grouped_place_kernel, dim3(L->n_experts), dim3(256), 0, s, sel, w, Pp, K, L->n_experts,
-                       (const uint32_t*)(b + lay.offsets), (const uint32_t*)(b + lay.run),
-                       (uint32_t*)(b + lay.slot_tok), (float*)(b + lay.slot_w), (uint32_t*)(b + lay.ord));
+    hipLaunchKernelGGL(grouped_place_kernel, dim3(L->n_experts), dim3(256), 0, s, sel, w, Pp, K,
+                       (const uint32_t*)(b + lay.offsets), (uint32_t*)(b + lay.slot_tok), (float*)(b + lay.slot_w),
+                       (uint32_t*)(b + lay.ord));
     if ((rc = check_launch("grouped_place_kernel"))) return rc;
   }
   const uint32_t n_sl = (uint32_t)P;  // slot indices are below this (the routes form's taken slots too)
