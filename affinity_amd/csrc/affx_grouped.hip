@@ -12,9 +12,9 @@
 //                    input: exact for every element of at least 2^-13 of the token's largest
 //                    magnitude, where both terms are normal E4M3 numbers, and within 2^-20 of that
 //                    maximum below it; 3 when a low bf16 term is given)
-//   (each GEMM runs twice: the wide tiles, then the narrow ones, an expert's partial last tile of
-//   at most kGNarrow column tiles of tokens, in an instantiation whose MFMAs, fragment reads and
-//   direct loads cover just those columns)
+//   (each GEMM runs three times: the wide tiles, then the mid and the narrow ones, an expert's
+//   partial last tile of at most kGMid or kGNarrow column tiles of tokens, in instantiations
+//   whose MFMAs, fragment reads and direct loads cover just those columns)
 //   grouped_gemm<0>  gate/up: (row block of 128 inter rows, token tile): 8 waves x 16 rows of
 //                    gate and the same 16 of up, K = hidden in 128-column MFMA steps, 12 column
 //                    tiles per A fragment; epilogue combines terms, applies row scales, SwiGLU,
@@ -37,15 +37,16 @@ struct Tile {
   uint32_t expert, slot0, n;
 };
 
-// Tiles of each GEMM: the wide ones (up to kGCT column tiles of tokens) first, then the narrow ones
-// (an expert's last, partial tile when it needs at most kGNarrow column tiles), which a narrower
-// instantiation of the GEMM runs.
+// Tiles of each GEMM by width class: wide (kGCT column tiles of tokens: every full tile, and a
+// partial one that needs more than kGMid), mid (an expert's partial last tile of at most kGMid) and
+// narrow (at most kGNarrow), stored in that order; each class runs in its own instantiation of the
+// GEMM.
+constexpr int kNCls = 3;
 struct GroupedHdr {
   uint32_t n_slots;
-  uint32_t n_tiles1, n_tiles2;     // wide tiles
   uint32_t tx;                     // activation terms of the gate/up input (2 or 3)
   uint32_t bad;                    // a caller's slot list needed more tiles than it can hold
-  uint32_t n_narrow1, n_narrow2;   // narrow tiles, after the wide ones
+  uint32_t n_cls[2][kNCls];        // [GEMM][class] tile counts
 };
 
 // ------------------------------------------------------------------------------------------------
@@ -84,34 +85,39 @@ __device__ __forceinline__ void plan_scan(uint32_t (&v)[N], uint32_t* wsum, uint
   }
 }
 
-// An expert's c slots in tiles of tt tokens: its wide tiles (the full ones, and a partial one of
-// more than nar tokens) and narrow tiles (a partial one of at most nar tokens: 0 or 1).
-__device__ __forceinline__ uint32_t n_wide(uint32_t c, uint32_t tt, uint32_t nar) {
-  return c / tt + (c % tt > nar ? 1u : 0u);
+// Width class of an expert's partial last tile of r tokens (r > 0): 2 narrow, 1 mid, 0 wide; nar
+// and mid are the token capacities of the narrow and mid widths.
+__device__ __forceinline__ uint32_t tile_cls(uint32_t r, uint32_t nar, uint32_t mid) {
+  return r <= nar ? 2u : r <= mid ? 1u : 0u;
 }
-__device__ __forceinline__ uint32_t n_narrow(uint32_t c, uint32_t tt, uint32_t nar) {
-  return (c % tt != 0u && c % tt <= nar) ? 1u : 0u;
+// An expert's c slots in tiles of tt tokens: how many tiles of class k it has.
+__device__ __forceinline__ uint32_t n_cls_of(uint32_t c, uint32_t tt, uint32_t nar, uint32_t mid, uint32_t k) {
+  const uint32_t r = c % tt;
+  return (k == 0 ? c / tt : 0u) + (r != 0u && tile_cls(r, nar, mid) == k ? 1u : 0u);
 }
-// Writes the tiles of one expert (slots b0 .. b0 + c - 1): wide ones from tiles[w0], the narrow
-// one at tiles[n0].
+// Writes the tiles of one expert (slots b0 .. b0 + c - 1): the full ones from tiles[at[0]], the
+// partial one at tiles[at[its class]] (at[0] past the full ones for a wide partial tile).
 __device__ __forceinline__ void put_tiles(Tile* tiles, uint32_t e, uint32_t b0, uint32_t c, uint32_t tt, uint32_t nar,
-                                          uint32_t w0, uint32_t n0) {
+                                          uint32_t mid, const uint32_t (&at)[kNCls]) {
   const uint32_t full = c / tt, r = c % tt;
-  for (uint32_t k = 0; k < full; ++k) tiles[w0 + k] = Tile{e, b0 + k * tt, tt};
-  if (r > nar) tiles[w0 + full] = Tile{e, b0 + full * tt, r};
-  else if (r > 0) tiles[n0] = Tile{e, b0 + full * tt, r};
+  for (uint32_t k = 0; k < full; ++k) tiles[at[0] + k] = Tile{e, b0 + k * tt, tt};
+  if (r > 0) {
+    const uint32_t k = tile_cls(r, nar, mid);
+    tiles[k == 0 ? at[0] + full : at[k]] = Tile{e, b0 + full * tt, r};
+  }
 }
 
 // start_in: a caller's slot list, expert e owning slots [start_in[e], start_in[e+1]) of n_slots_in
 // (each bound clamped to n_slots_in; a range that runs backwards is empty); null: count the routes.
 __global__ void __launch_bounds__(kPlanThreads) grouped_plan_kernel(
     const uint32_t* __restrict__ sel, uint32_t n_pairs, uint32_t n_experts, uint32_t tt1,
-    uint32_t tt2, uint32_t nar1, uint32_t nar2, uint32_t tx, const uint32_t* __restrict__ start_in,
+    uint32_t tt2, uint32_t nar1, uint32_t nar2, uint32_t mid1, uint32_t mid2, uint32_t tx,
+    const uint32_t* __restrict__ start_in,
     uint32_t n_slots_in, uint32_t max_tiles1, uint32_t max_tiles2, GroupedHdr* __restrict__ hdr,
     uint32_t* __restrict__ offsets, Tile* __restrict__ tiles1, Tile* __restrict__ tiles2) {
   static_assert(AFFX_MAX_EXPERTS <= kPlanThreads, "one thread per expert in the scan");
   __shared__ uint32_t cnt[AFFX_MAX_EXPERTS];
-  __shared__ uint32_t wsum[5 * (kPlanThreads / 64)];
+  __shared__ uint32_t wsum[(1 + 2 * kNCls) * (kPlanThreads / 64)];
   const uint32_t tid = threadIdx.x;
   uint32_t c = 0, b0 = 0;
   if (start_in) {
@@ -139,26 +145,44 @@ __global__ void __launch_bounds__(kPlanThreads) grouped_plan_kernel(
     __syncthreads();
     c = tid < n_experts ? cnt[tid] : 0u;
   }
-  // slot offsets and tile offsets: one exclusive scan (expert order) of the count and the wide and
-  // narrow tiles of both GEMMs
-  uint32_t v[5] = {c, n_wide(c, tt1, nar1), n_narrow(c, tt1, nar1), n_wide(c, tt2, nar2), n_narrow(c, tt2, nar2)};
-  uint32_t tot[5];
-  plan_scan<5>(v, wsum, tot);
+  // slot offsets and tile offsets: one exclusive scan (expert order) of the count and the tiles of
+  // each width class of both GEMMs
+  constexpr int NV = 1 + 2 * kNCls;
+  uint32_t v[NV], tot[NV];
+  v[0] = c;
+#pragma unroll
+  for (int k = 0; k < kNCls; ++k) {
+    v[1 + k] = n_cls_of(c, tt1, nar1, mid1, k);
+    v[1 + kNCls + k] = n_cls_of(c, tt2, nar2, mid2, k);
+  }
+  plan_scan<NV>(v, wsum, tot);
   if (!start_in) b0 = v[0];
+  uint32_t need1 = 0, need2 = 0;
+#pragma unroll
+  for (int k = 0; k < kNCls; ++k) { need1 += tot[1 + k]; need2 += tot[1 + kNCls + k]; }
   // a caller's overlapping ranges could ask for more tiles than the workspace holds: then no tile
-  const bool fits = tot[1] + tot[2] <= max_tiles1 && tot[3] + tot[4] <= max_tiles2;
+  const bool fits = need1 <= max_tiles1 && need2 <= max_tiles2;
   if (fits && tid < n_experts) {
     if (!start_in) offsets[tid] = v[0];
-    put_tiles(tiles1, tid, b0, c, tt1, nar1, v[1], tot[1] + v[2]);
-    put_tiles(tiles2, tid, b0, c, tt2, nar2, v[3], tot[3] + v[4]);
+    uint32_t at1[kNCls], at2[kNCls], base1 = 0, base2 = 0;
+#pragma unroll
+    for (int k = 0; k < kNCls; ++k) {
+      at1[k] = base1 + v[1 + k];
+      at2[k] = base2 + v[1 + kNCls + k];
+      base1 += tot[1 + k];
+      base2 += tot[1 + kNCls + k];
+    }
+    put_tiles(tiles1, tid, b0, c, tt1, nar1, mid1, at1);
+    put_tiles(tiles2, tid, b0, c, tt2, nar2, mid2, at2);
   }
   if (tid == 0) {
     if (!start_in) offsets[n_experts] = tot[0];
     hdr->n_slots = start_in ? n_slots_in : tot[0];
-    hdr->n_tiles1 = fits ? tot[1] : 0u;
-    hdr->n_narrow1 = fits ? tot[2] : 0u;
-    hdr->n_tiles2 = fits ? tot[3] : 0u;
-    hdr->n_narrow2 = fits ? tot[4] : 0u;
+#pragma unroll
+    for (int k = 0; k < kNCls; ++k) {
+      hdr->n_cls[0][k] = fits ? tot[1 + k] : 0u;
+      hdr->n_cls[1][k] = fits ? tot[1 + kNCls + k] : 0u;
+    }
     hdr->tx = tx;
     hdr->bad = fits ? 0u : 1u;
   }
@@ -283,8 +307,9 @@ constexpr int kGRT = 16 / kGW;              // 16-row tiles per wave (a workgrou
 constexpr int kGT = kGW * 64;
 constexpr int kGKC = 2;                     // codebook copies (pre-rotated tables)
 constexpr int kGCT = 12;                    // 16-column tiles of B per wave (a wide tile)
+constexpr int kGMid = 8;                    // the same for a mid tile
 constexpr int kGNarrow = 4;                 // the same for a narrow tile
-// A tile of CT column tiles (kGCT wide, kGNarrow narrow): its B columns, the bytes of one B buffer
+// A tile of CT column tiles (kGCT, kGMid or kGNarrow): its B columns, the bytes of one B buffer
 // (one MFMA step) and the direct-load instructions per wave per step (8 columns each).
 template <int CT>
 struct GTile {
@@ -392,12 +417,14 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
   uint32_t cbv[kPer];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) cbv[i] = A.codebook[tid + (uint32_t)kGT * i];
-  // this instantiation's tiles: the wide ones, or the narrow ones stored after them
-  const uint32_t n_wide_t = PH == 0 ? A.hdr->n_tiles1 : A.hdr->n_tiles2;
-  const uint32_t n_tiles = CT == kGCT ? n_wide_t : (PH == 0 ? A.hdr->n_narrow1 : A.hdr->n_narrow2);
+  // this instantiation's tiles: those of its width class, stored after the wider classes' tiles
+  constexpr int cls = CT == kGCT ? 0 : CT == kGMid ? 1 : 2;
+  const uint32_t* ncls = A.hdr->n_cls[PH];
+  const uint32_t n_tiles = ncls[cls];
+  const uint32_t first = (cls > 0 ? ncls[0] : 0u) + (cls > 1 ? ncls[1] : 0u);
   // (entries below max_t are allocated: read before it is known whether a tile is in use)
-  const uint32_t room = CT == kGCT ? A.max_tiles : A.max_tiles - min(n_wide_t, A.max_tiles);
-  const Tile* tiles = room ? A.tiles + (CT == kGCT ? 0u : n_wide_t) : A.tiles;
+  const uint32_t room = A.max_tiles - min(first, A.max_tiles);
+  const Tile* tiles = room ? A.tiles + first : A.tiles;
   const uint32_t max_t = room ? room : 1u;
   uint32_t w = blockIdx.x, rb, tile_id;
   item_of(w, rb, tile_id);
@@ -571,7 +598,7 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
       // only: with two waves per SIMD a wave has 256 registers, accumulators included. (Step 0 of
       // the next 1024 columns after step 7: the ring has reloaded every register those reads use.)
       constexpr int mn = (m + 1) & 7;
-      constexpr int kLook = CT >= 12 ? 4 : 0, kFin = CT >= 12 ? 8 : 2;
+      constexpr int kLook = CT >= 12 ? 4 : CT >= 8 ? 2 : 0, kFin = CT >= 12 ? 8 : CT >= 8 ? 5 : 2;
       uint32_t rawn[kGRT][8], sxn[kGRT][4];
       v8i a_next[kGRT];
       auto bread = [&](int ct) -> v8i {
@@ -925,10 +952,12 @@ int grouped_body(const affx_layer* L, const void* x, const void* x_lo, uint32_t 
 
   const uint32_t tt1 = tile_tokens(tx), tt2 = tile_tokens(3);
   const uint32_t Pp = sel ? T * K : 0u;
-  // an expert's last tile is narrow when its tokens fill at most kGNarrow column tiles
+  // an expert's partial last tile is narrow (mid) when its tokens fill at most kGNarrow (kGMid)
+  // column tiles
   const uint32_t nar1 = kGNarrow * (16 / tx), nar2 = kGNarrow * (16 / 3);
+  const uint32_t mid1 = kGMid * (16 / tx), mid2 = kGMid * (16 / 3);
   hipLaunchKernelGGL(grouped_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, sel, Pp, L->n_experts, tt1, tt2, nar1,
-                     nar2, tx, sel ? nullptr : start, sel ? 0u : n_slots, lay.max_tiles1, lay.max_tiles2,
+                     nar2, mid1, mid2, tx, sel ? nullptr : start, sel ? 0u : n_slots, lay.max_tiles1, lay.max_tiles2,
                      (GroupedHdr*)(b + lay.hdr), (uint32_t*)(b + lay.offsets), (Tile*)(b + lay.tiles1),
                      (Tile*)(b + lay.tiles2));
   int rc = check_launch("grouped_plan_kernel");
@@ -957,7 +986,7 @@ int grouped_body(const affx_layer* L, const void* x, const void* x_lo, uint32_t 
   if ((rc = check_hip(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "hipDeviceGetAttribute")))
     return rc;
   const uint32_t gmax = cus >= 8 ? (uint32_t)cus / 8u * 8u : 8u;
-  // (the narrow tiles: at most one per expert)
+  // (the mid and narrow tiles: at most one per expert)
   auto grid = [&](uint32_t row_blocks, uint32_t tiles) {
     const uint32_t items = row_blocks * ((tiles + 7) / 8 * 8);
     return items < gmax ? items : gmax;
@@ -969,9 +998,11 @@ int grouped_body(const affx_layer* L, const void* x, const void* x_lo, uint32_t 
   const uint32_t g1 = grid(L->inter / 128, lay.max_tiles1), gn1 = grid(L->inter / 128, E8);
   if (tx == 2) {
     hipLaunchKernelGGL((grouped_gemm_kernel<0, 2, kGCT>), dim3(g1), dim3(kGT), 0, s, A);
+    hipLaunchKernelGGL((grouped_gemm_kernel<0, 2, kGMid>), dim3(gn1), dim3(kGT), 0, s, A);
     hipLaunchKernelGGL((grouped_gemm_kernel<0, 2, kGNarrow>), dim3(gn1), dim3(kGT), 0, s, A);
   } else {
     hipLaunchKernelGGL((grouped_gemm_kernel<0, 3, kGCT>), dim3(g1), dim3(kGT), 0, s, A);
+    hipLaunchKernelGGL((grouped_gemm_kernel<0, 3, kGMid>), dim3(gn1), dim3(kGT), 0, s, A);
     hipLaunchKernelGGL((grouped_gemm_kernel<0, 3, kGNarrow>), dim3(gn1), dim3(kGT), 0, s, A);
   }
   if ((rc = check_launch("grouped_gemm_kernel (gate/up)"))) return rc;
@@ -980,6 +1011,7 @@ int grouped_body(const affx_layer* L, const void* x, const void* x_lo, uint32_t 
   A.b_off = lay.aq;
   const uint32_t g2 = grid(L->hidden / 256, lay.max_tiles2), gn2 = grid(L->hidden / 256, E8);
   hipLaunchKernelGGL((grouped_gemm_kernel<1, 3, kGCT>), dim3(g2), dim3(kGT), 0, s, A);
+  hipLaunchKernelGGL((grouped_gemm_kernel<1, 3, kGMid>), dim3(gn2), dim3(kGT), 0, s, A);
   hipLaunchKernelGGL((grouped_gemm_kernel<1, 3, kGNarrow>), dim3(gn2), dim3(kGT), 0, s, A);
   if ((rc = check_launch("grouped_gemm_kernel (down)"))) return rc;
   hipLaunchKernelGGL(grouped_combine_kernel, dim3((L->hidden / 4 + 255) / 256, T), dim3(256), 0, s,
