@@ -95,6 +95,7 @@ _SIGS = {
                                        C.c_int, _vp, C.c_size_t, _vp], C.c_int),
     "affx_route_topk": ([_vp, _u64, _u64, _vp, _u32, _u32, _u32, C.c_int, C.c_int, C.c_float, _vp, _vp, _vp],
                         C.c_int),
+    "affx_dense_fp8_to_device_layout": ([_vp, _vp, _u64, _u64, _vp], C.c_int),
     "affx_shared_decode_workspace_size": ([_u32, _u32, _u32], C.c_size_t),
     "affx_shared_batch_workspace_size": ([_u32, _u32, _u32], C.c_size_t),
     "affx_shared_expert_decode": ([C.POINTER(AffxSharedExpert), _vp, _u64, _u64, _u32, _vp, _u64, _u64, C.c_int,

@@ -2,11 +2,12 @@
 // every token runs, added into the block the routed experts wrote) and the hyper-connection post
 // (the block folded into the residual lanes, leaving the block zero for the next sublayer).
 //
-// The shared expert's weights are the checkpoint's FP8 exactly as the container holds them
-// (src/engine/matvec_fp8.inc:1-16): E4M3 bytes row-major and one UE8M0 scale per 128x128 tile.
-// They go to the fp8 MFMA as they are: a lane's A operand is 32 weight bytes of one row straight
-// from memory, and the tile scale is the MFMA's own A scale (a lane's scale covers its 32 K values
-// of one row, which never straddle a 128-column tile). The activations are E4M3 terms as on the
+// The shared expert's weights are the checkpoint's FP8 values (src/engine/matvec_fp8.inc:1-16):
+// E4M3 bytes and one UE8M0 scale per 128x128 tile, the bytes permuted once at upload into a tile
+// layout (below) so that each load instruction of a wave reads 1 KiB contiguous. They go to the
+// fp8 MFMA as they are: a lane's A operand is 32 weight bytes of one row straight from memory, and
+// the tile scale is the MFMA's own A scale (a lane's scale covers its 32 K values of one row,
+// which never straddle a 128-column tile). The activations are E4M3 terms as on the
 // routed path (t0 + t1/16 + t2/256 in adjacent B columns); their exponent is the B scale where it
 // is one per wave (decode, and the batch down), else applied in the epilogue.
 //
@@ -65,6 +66,29 @@ __device__ __forceinline__ float swiglu_clamped(float g, float u, float L) {
 }
 
 // ------------------------------------------------------------------------------------------------
+// device layout of a dense FP8 matrix
+// ------------------------------------------------------------------------------------------------
+// [rows x cols] (rows % 16 == 0, cols % 128 == 0) in 2 KiB chunks, one per 16-row tile rt
+// (row-tile major) and 128-column step m: [half h][lane][16 B], lane = c + 16 kg holding row
+// 16 rt + c, columns 128 m + 64 h + 16 kg .. + 15. One 16-byte load per lane then reads 1 KiB
+// contiguous, already in the K order of the scaled fp8 MFMA used here (lane group kg holds the
+// step's columns 16 kg + [0, 16) and 64 + 16 kg + [0, 16)).
+__host__ __device__ inline uint32_t dense_tile_offset(uint32_t rt, uint32_t m, uint32_t cols) {
+  return (rt * (cols >> 7) + m) * 2048u;
+}
+
+__global__ void __launch_bounds__(256) dense_fp8_permute_kernel(const uint8_t* __restrict__ src,
+                                                                uint8_t* __restrict__ dst, uint32_t rows,
+                                                                uint32_t cols) {
+  const uint64_t q = (uint64_t)blockIdx.x * 256u + threadIdx.x;  // 16-byte chunk of dst
+  if (q >= (uint64_t)rows * cols / 16u) return;
+  const uint32_t lane = (uint32_t)(q & 63u), h = (uint32_t)((q >> 6) & 1u);
+  const uint32_t tm = (uint32_t)(q >> 7), steps = cols >> 7, rt = tm / steps, m = tm % steps;
+  const uint32_t r = 16u * rt + (lane & 15u), k = 128u * m + 64u * h + 16u * (lane >> 4);
+  *reinterpret_cast<uint4*>(dst + 16u * q) = *reinterpret_cast<const uint4*>(src + (uint64_t)r * cols + k);
+}
+
+// ------------------------------------------------------------------------------------------------
 // decode
 // ------------------------------------------------------------------------------------------------
 // K order inside a 128-column MFMA step: lane group kg holds columns 16 kg .. 16 kg + 15 and
@@ -80,11 +104,11 @@ __device__ __forceinline__ void load_a_tile(const uint8_t* __restrict__ W, const
   const uint32_t lane = threadIdx.x & 63, c = lane & 15, kg = lane >> 4;
   const __amdgpu_buffer_rsrc_t wr =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(W), (short)0, 0x7FFFFFFF, 0x00020000);
-  const uint32_t vo = (row0 + c) * K + k0 + 16u * kg;
+  const uint32_t vo = dense_tile_offset(row0 >> 4, k0 >> 7, K) + 16u * lane;
 #pragma unroll
   for (int m = 0; m < STEPS; ++m)
-    a[m] = join8(__builtin_amdgcn_raw_buffer_load_b128(wr, vo + 128u * m, 0, 2),
-                 __builtin_amdgcn_raw_buffer_load_b128(wr, vo + 128u * m + 64u, 0, 2));
+    a[m] = join8(__builtin_amdgcn_raw_buffer_load_b128(wr, vo + 2048u * m, 0, 2),
+                 __builtin_amdgcn_raw_buffer_load_b128(wr, vo + 2048u * m + 1024u, 0, 2));
   const uint8_t* srow = S + (uint64_t)(row0 >> 7) * (K >> 7) + (k0 >> 7);
 #pragma unroll
   for (int m = 0; m < STEPS; ++m) sa[m] = __builtin_amdgcn_readfirstlane((int)srow[m]);
@@ -332,14 +356,14 @@ __global__ void __launch_bounds__(kBT, 1) shexp_gemm_kernel(SharedGemmArgs A) {
       const_cast<uint8_t*>(PH == 0 ? A.w1 : A.w0), (short)0, 0x7FFFFFFF, 0x00020000);
   uint32_t vo[kBRT];
 #pragma unroll
-  for (int r = 0; r < kBRT; ++r) vo[r] = (row_of(r) + c) * K + 32u * kg;
+  for (int r = 0; r < kBRT; ++r) vo[r] = dense_tile_offset(row_of(r) >> 4, 0, K) + 16u * lane;
   v8i ring[4][kBRT];
   auto a_load = [&](int slot, uint32_t t) {
 #pragma unroll
     for (int r = 0; r < kBRT; ++r) {
       const __amdgpu_buffer_rsrc_t wr = r == 0 ? wr0 : wr1;
-      ring[slot][r] = join8(__builtin_amdgcn_raw_buffer_load_b128(wr, vo[r] + 128u * t, 0, 2),
-                            __builtin_amdgcn_raw_buffer_load_b128(wr, vo[r] + 128u * t + 16u, 0, 2));
+      ring[slot][r] = join8(__builtin_amdgcn_raw_buffer_load_b128(wr, vo[r] + 2048u * t, 0, 2),
+                            __builtin_amdgcn_raw_buffer_load_b128(wr, vo[r] + 2048u * t + 1024u, 0, 2));
     }
   };
   // scale rows of the two tiles (a 128-row band each), one dword = four steps
@@ -379,8 +403,10 @@ __global__ void __launch_bounds__(kBT, 1) shexp_gemm_kernel(SharedGemmArgs A) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(wsr, AFFX_LDS_PTR(b + (kBDma * wv + d) * 1024u), 16, roff[d],
                                                t * 128u, 0, 0);
   };
-  const uint32_t bo0 = c * 128u + (((2u * kg) ^ ((c ^ (c >> 3)) & 7u)) << 4);
-  const uint32_t bo1 = c * 128u + (((2u * kg + 1u) ^ ((c ^ (c >> 3)) & 7u)) << 4);
+  // the lane's two 16-byte chunks of a step in the MFMA K order (kg and 4 + kg; the swizzle keeps
+  // the 16 lanes of each K group on 16 distinct bank groups)
+  const uint32_t bo0 = c * 128u + (((kg) ^ ((c ^ (c >> 3)) & 7u)) << 4);
+  const uint32_t bo1 = c * 128u + (((4u + kg) ^ ((c ^ (c >> 3)) & 7u)) << 4);
   auto bread = [&](const uint8_t* b, int ct) -> v8i {
     return join8(*reinterpret_cast<const u32x4*>(b + ct * 2048 + bo0),
                  *reinterpret_cast<const u32x4*>(b + ct * 2048 + bo1));
@@ -795,6 +821,19 @@ int affx_shared_expert_batch(const affx_shared_expert* S, const void* x, const v
   g = dim3(8u * ((A.n_rb + 7u) / 8u) * A.n_tiles);
   hipLaunchKernelGGL((shexp_gemm_kernel<1, 3>), g, dim3(kBT), 0, s, A);
   return check_launch("shexp_gemm_kernel (down)");
+}
+
+int affx_dense_fp8_to_device_layout(const void* src, void* dst, uint64_t rows, uint64_t cols, void* stream) {
+  if (!src || !dst) return set_error(AFFX_ERR_ARG, "dense_fp8_to_device_layout: null pointer");
+  if (rows == 0 || cols == 0 || rows % 16 || cols % 128 || rows * cols > 0xFFFFFFFFull ||
+      ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15u))
+    return set_error(AFFX_ERR_ARG, "dense_fp8_to_device_layout: rows must be a multiple of 16, cols of 128, "
+                     "rows*cols < 4 GiB, both buffers 16-byte aligned");
+  if (src == dst) return set_error(AFFX_ERR_ARG, "dense_fp8_to_device_layout: src and dst must differ");
+  const uint64_t chunks = rows * cols / 16u;
+  hipLaunchKernelGGL(dense_fp8_permute_kernel, dim3((uint32_t)((chunks + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint8_t*)src, (uint8_t*)dst, (uint32_t)rows, (uint32_t)cols);
+  return check_launch("dense_fp8_permute_kernel");
 }
 
 int affx_hc_post(float* out_hc, float* block, const float* hc, const float* post, const float* comb,

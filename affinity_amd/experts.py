@@ -240,13 +240,24 @@ def fill_synthetic_experts(container: torch.Tensor, first: int, count: int, code
 
 # ---- the step after: shared expert and hyper-connection post ------------------------------------
 
+def dense_fp8_to_device_layout(w: torch.Tensor, stream=None) -> torch.Tensor:
+    """The container's row-major E4M3 bytes [rows x cols] (uint8, on the device) in the device
+    layout the shared-expert kernels read (a new tensor of the same shape)."""
+    out = torch.empty_like(w)
+    check(lib().affx_dense_fp8_to_device_layout(w.contiguous().data_ptr(), out.data_ptr(), w.shape[0], w.shape[1],
+                                                _stream(stream)), "dense_fp8_to_device_layout")
+    return out
+
+
 class SharedExpert:
     """A layer's FP8 shared expert on the device (the reference's shexp_gate/up/down DenseW,
-    src/engine/model.h:125-127): E4M3 weights [rows x cols] (uint8 tensors) and UE8M0 tile scales
+    src/engine/model.h:125-127): E4M3 weights [rows x cols] (uint8 tensors, row-major as the
+    container holds them; permuted here into the device layout) and UE8M0 tile scales
     [rows / 128][cols / 128]."""
 
     def __init__(self, gate, gate_s, up, up_s, down, down_s, swiglu_limit: float = SWIGLU_LIMIT):
         inter, hidden = gate.shape
+        gate, up, down = (dense_fp8_to_device_layout(m) for m in (gate, up, down))
         self.tensors = (gate, gate_s, up, up_s, down, down_s)   # keeps the memory alive
         mk = lambda w, s: _lib.AffxDenseFp8(w.data_ptr(), s.data_ptr(), w.shape[0], w.shape[1])
         self.abi = _lib.AffxSharedExpert(mk(gate, gate_s), mk(up, up_s), mk(down, down_s), hidden, inter,

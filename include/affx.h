@@ -319,11 +319,12 @@ int affx_route_topk(const float* logits, uint64_t tok_stride, uint64_t expert_st
 
 /* ---- the step after: shared expert and hyper-connection post -------------------------------- */
 
-/* One FP8 dense matrix as the container holds it: the reference's DenseW with quant
- * AFF_FP8_E4M3 (src/engine/ops.h:142-151; format src/engine/matvec_fp8.inc:8-10). data: device
- * E4M3 bytes, row-major [rows x cols], 16-byte aligned; scales: device UE8M0 bytes, one per
- * 128 x 128 tile, row-major [rows / 128][cols / 128], 4-byte aligned. E4M3 0x7F / 0xFF are NaN
- * (as in the reference's scalar decode, src/quant/source_dtypes.cpp:24-25). */
+/* One FP8 dense matrix: the reference's DenseW with quant AFF_FP8_E4M3 (src/engine/ops.h:142-151;
+ * format src/engine/matvec_fp8.inc:8-10). data: device E4M3 bytes of the [rows x cols] matrix in
+ * the device layout affx_dense_fp8_to_device_layout writes (the container's row-major bytes,
+ * permuted once at upload), 16-byte aligned; scales: device UE8M0 bytes, one per 128 x 128 tile,
+ * row-major [rows / 128][cols / 128] as the container holds them, 4-byte aligned. E4M3 0x7F / 0xFF
+ * are NaN (as in the reference's scalar decode, src/quant/source_dtypes.cpp:24-25). */
 typedef struct affx_dense_fp8 {
   const void* data;
   const uint8_t* scales;
@@ -339,6 +340,15 @@ typedef struct affx_shared_expert {
   uint32_t hidden, inter;
   float swiglu_limit;
 } affx_shared_expert;
+
+/* The container's row-major E4M3 bytes (device, src) into the device layout (device, dst, a
+ * different buffer) the shared-expert kernels read: 2 KiB per (16-row tile, 128-column step),
+ * [half][lane][16 B], lane c + 16 kg holding row 16 tile + c, columns 128 step + 64 half + 16 kg
+ * .. + 15: the scaled fp8 MFMA's fragment order. rows % 16 == 0, cols % 128 == 0. The
+ * counterpart of the reference's preshuffle of these same tensors into its WMMA fragment order
+ * at registration (preshuffle_fp8_hip, src/gpu/dense_gpu.hip:940-965; the allowlist ps_for,
+ * 791-813, names shexp_gate/up/down). Stream-ordered. */
+int affx_dense_fp8_to_device_layout(const void* src, void* dst, uint64_t rows, uint64_t cols, void* stream);
 
 size_t affx_shared_decode_workspace_size(uint32_t m_tokens, uint32_t hidden, uint32_t inter);
 size_t affx_shared_batch_workspace_size(uint32_t n_tok, uint32_t hidden, uint32_t inter);

@@ -391,10 +391,17 @@ int run_shared(int argc, char** argv) {
   fp8_matrix(rng, I, H, w[0], sc[0]);
   fp8_matrix(rng, I, H, w[1], sc[1]);
   fp8_matrix(rng, H, I, w[2], sc[2]);
+  // the kernels read the device layout; the oracle the row-major bytes
+  std::vector<uint8_t> wd[3];
+  for (int i = 0; i < 3; ++i) {
+    wd[i].resize(w[i].size());
+    const uint64_t rows = i < 2 ? I : H, cols = i < 2 ? H : I;
+    if (affx_dense_fp8_to_device_layout(w[i].data(), wd[i].data(), rows, cols, nullptr) != 0) return 1;
+  }
   affx_shared_expert S{};
-  S.gate = {w[0].data(), sc[0].data(), I, H};
-  S.up = {w[1].data(), sc[1].data(), I, H};
-  S.down = {w[2].data(), sc[2].data(), H, I};
+  S.gate = {wd[0].data(), sc[0].data(), I, H};
+  S.up = {wd[1].data(), sc[1].data(), I, H};
+  S.down = {wd[2].data(), sc[2].data(), H, I};
   S.hidden = H;
   S.inter = I;
   S.swiglu_limit = 10.0f;

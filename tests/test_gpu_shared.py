@@ -40,6 +40,29 @@ def shexp(ax):
     return ax.SharedExpert(*dev), mats
 
 
+def device_layout_np(w: np.ndarray) -> np.ndarray:
+    """The dense FP8 device layout restated: 2 KiB per (16-row tile, 128-column step), [half][lane]
+    [16 B], lane c + 16 kg holding row 16 tile + c, columns 128 step + 64 half + 16 kg .. + 15."""
+    rows, cols = w.shape
+    t = w.reshape(rows // 16, 16, cols // 128, 2, 4, 16)        # tile, c, step, half, kg, byte
+    return np.ascontiguousarray(t.transpose(0, 2, 3, 4, 1, 5)).reshape(rows, cols)
+
+
+def test_dense_device_layout(ax):
+    """The GPU permutation equals the restatement byte for byte, and is a bijection (a matrix of
+    distinct 32-bit indices comes back as a permutation of itself)."""
+    rng = np.random.default_rng(2)
+    for rows, cols in ((16, 128), (2048, 4096), (4096, 2048), (48, 384)):
+        w = rng.integers(0, 256, (rows, cols), dtype=np.uint8)
+        got = ax.dense_fp8_to_device_layout(torch.from_numpy(w).cuda()).cpu().numpy()
+        np.testing.assert_array_equal(got, device_layout_np(w))
+    idx = np.arange(64 * 512, dtype=np.uint32).view(np.uint8).reshape(64, 2048)
+    got = ax.dense_fp8_to_device_layout(torch.from_numpy(idx).cuda()).cpu().numpy()
+    # (the layout moves 16-byte chunks, so 4-byte indices stay whole: every index appears once)
+    assert np.array_equal(np.sort(np.ascontiguousarray(got).view(np.uint32).reshape(-1)),
+                          np.arange(64 * 512, dtype=np.uint32))
+
+
 def oracle_rows(orc, mats, x):
     (wg, sg), (wu, su), (wd, sd) = mats
     return np.stack([orc.shared_expert(wg, sg, wu, su, wd, sd, np.ascontiguousarray(x[t]), 10.0)
