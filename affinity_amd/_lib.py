@@ -112,6 +112,15 @@ _SIGS = {
     "affx_gen_normal": ([_u64, _u64, C.c_double, _vp, C.c_int, _vp], C.c_int),
     "affx_quantize_matrix": ([_vp, _u32, _u32, _vp, _vp, _vp, _vp, _vp, _vp], C.c_int),
     "affx_fill_expert": ([_vp, _u64, _u64, _vp, _u32, _vp, _vp], C.c_int),
+    "affx_collect_samples_bound": ([_u64, _u64, _u64], _u64),
+    "affx_collect_samples_workspace_size": ([_u64, _u64, _u64], C.c_size_t),
+    "affx_collect_samples": ([_vp, _u64, _u64, _u64, _vp, _u64, _vp, _vp, C.c_size_t, _vp], C.c_int),
+    "affx_fit_codebook_workspace_size": ([_u64], C.c_size_t),
+    "affx_fit_codebook": ([_vp, _u64, _vp, _u32, _u64, _u32, _vp, _vp, C.c_size_t, _vp], C.c_int),
+    "affx_fit_codebook_stats": ([_vp, _u64p, _u64p, _vp], C.c_int),
+    "affx_project_codebook": ([_vp, _u64, _vp], C.c_int),
+    "affx_pack_codebook": ([_vp, _vp, _vp], C.c_int),
+    "affx_unpack_codebook": ([_vp, _vp, _vp], C.c_int),
 }
 
 # every symbol include/affx.h declares (tests check the library exports them all)

@@ -17,6 +17,9 @@ synthetic.py):
              per launch (6 x 9,060,352 B) over its average duration, timed with HIP events on the
              launch stream (the C5 graph holds only these launches); traffic = HBM bytes per
              launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary.
+  producer   the config-1 codebook recipe (3 x 2^19 samples of the config-1 matrices, the joint
+             fit, projection, packing) on the GPU, timed, and compared with the reference's packed
+             codebook bit for bit.
   cpu_baseline  the reference's own CPU path (oracle/_ref/libaffref.so, else the oracle that
              restates it) on bounded samples of every config, on this host's cores; its outputs are
              also the checker of the GPU results reported under "parity".
@@ -280,6 +283,37 @@ def main() -> int:
                                                "max": int(counts.max())}}
         prefill = (sel_np, w_np, xb, yp)
 
+    # ---- the codebook producer: the config-1 recipe fitted on the GPU ----------------------------
+    producer_exact = None
+    if args.only == "all":
+        import affinity_amd.codebook as cbk
+        mats = [ax.gen_normal(1000, I * H, 0.02).view(I, H), ax.gen_normal(1001, I * H, 0.02).view(I, H),
+                ax.gen_normal(1002, H * I, 0.02).view(H, I)]
+        torch.cuda.synchronize()
+        st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        st.record()
+        samples = torch.cat([cbk.collect_normalized_samples(m, 1 << 19) for m in mats])
+        en.record()
+        torch.cuda.synchronize()
+        ms_collect = st.elapsed_time(en)
+        fitter = cbk.CodebookFit(samples.numel())
+        st.record()
+        cbf = fitter.fit(samples, 50, 1)
+        packed = cbk.pack_codebook_e4m3_quads(cbk.project_codebook_e4m3(cbf))
+        en.record()
+        torch.cuda.synchronize()
+        ms_fit = st.elapsed_time(en)
+        seq_draws, passes = fitter.stats()
+        producer_exact = bool(np.array_equal(packed.cpu().numpy().view(np.uint32), cb_packed))
+        log(f"config-1 codebook on the GPU: collect {ms_collect:.1f} ms, fit + project + pack {ms_fit:.1f} ms, "
+            f"{passes} Lloyd passes, {seq_draws} sequential draws, equal to the reference's: {producer_exact}")
+        result["producer"] = {"workload": "config-1 codebook: 3 x 2^19 samples, fit_codebook(50, seed 1), "
+                                          "projection and packing",
+                              "collect_ms": round(ms_collect, 2), "fit_project_pack_ms": round(ms_fit, 2),
+                              "lloyd_passes": passes, "sequential_draws": seq_draws,
+                              "bit_exact_vs_reference": producer_exact}
+        del mats, samples, fitter, cbf, packed
+
     # ---- CPU baseline (and the checker of the GPU results) ----------------------------------------
     if not args.no_cpu_baseline:
         gpu = {"c1_dequant": [ax.dequant_matrix(pools[0], 0, m).cpu().numpy() for m in range(3)],
@@ -296,6 +330,8 @@ def main() -> int:
         # bit-exact): a number measured on a wrong result is not a measurement
         def failed(v) -> bool:
             return (not v) if isinstance(v, bool) else (isinstance(v, float) and not v <= 1e-3)
+        if producer_exact is not None:
+            result["parity"]["c1_codebook_fit_bit_exact"] = producer_exact
         bad = [k for k, v in result["parity"].items() if failed(v)]
         result["parity_ok"] = not bad
         if bad:

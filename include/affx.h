@@ -121,6 +121,48 @@ int affx_matrix_to_device_layout(const void* src_codes, const void* src_fields, 
 int affx_permute_experts(const void* src_container, void* dst_device, uint64_t n_experts,
                          uint64_t hidden, uint64_t inter, void* stream);
 
+/* ---- the codebook producer (what aff-quantize runs before it quantises) ----------------------
+ * The quad format only (4-wide codes, 1024 entries, 2 variants, power-of-two block scales). All
+ * pointers are device buffers; calls are stream-ordered. Every result equals the reference CPU
+ * path's bit for bit. */
+
+/* collect_normalized_samples (src/quant/blockquant.cpp:386-423, declared blockquant.h:149-154)
+ * without importance: every stride-th row of the row-major f32 matrix w (stride = max(1,
+ * rows*cols / max(1, max_samples))), rows whose max |w| is 0 skipped, then each 16-block whose
+ * max |w| is nonzero as blk[i] / bmax, in row and column order. Writes at most `cap` floats of
+ * out and the full count to *n_out (device uint64). The count is at most
+ * affx_collect_samples_bound(); ws holds affx_collect_samples_workspace_size() bytes. The call
+ * site is aff-quantize's sampling loop (tools/aff_quantize.cpp:420-425). */
+uint64_t affx_collect_samples_bound(uint64_t rows, uint64_t cols, uint64_t max_samples);
+size_t affx_collect_samples_workspace_size(uint64_t rows, uint64_t cols, uint64_t max_samples);
+int affx_collect_samples(const float* w, uint64_t rows, uint64_t cols, uint64_t max_samples,
+                         float* out, uint64_t cap, uint64_t* n_out, void* ws, size_t ws_bytes,
+                         void* stream);
+
+/* fit_codebook (src/quant/blockquant.cpp:252-384, declared blockquant.h:141-144) for the quad
+ * format: samples [n_samples] (16-byte aligned) -> cb [2][1024][4] floats (16-byte aligned), the
+ * raw fit before projection. weights must be NULL (aff-quantize passes none,
+ * tools/aff_quantize.cpp:430; AFFX_DECLINED otherwise). flags: 0, or
+ * AFFX_FIT_SEQUENTIAL_PICKS to take every k-means++ draw by the sequential sums (the same result,
+ * slower; for tests). ws: affx_fit_codebook_workspace_size(n_samples) bytes, 256-byte aligned;
+ * its first bytes hold the fit's counters afterwards (affx_fit_codebook_stats). */
+#define AFFX_FIT_SEQUENTIAL_PICKS 1u
+size_t affx_fit_codebook_workspace_size(uint64_t n_samples);
+int affx_fit_codebook(const float* samples, uint64_t n_samples, const float* weights,
+                      uint32_t iters, uint64_t seed, uint32_t flags, float* cb, void* ws,
+                      size_t ws_bytes, void* stream);
+/* The last fit's k-means++ draws that took the sequential sums and its Lloyd passes (host
+ * values; synchronises the stream). No counterpart in the reference. */
+int affx_fit_codebook_stats(const void* ws, uint64_t* seq_picks, uint64_t* passes, void* stream);
+
+/* project_codebook_e4m3 (blockquant.cpp:463-466) with pow2 scales, in place on n floats;
+ * pack_codebook_e4m3_quads (468-480): cb [2048][4] -> packed [2048] dwords;
+ * unpack_codebook_e4m3_quads (482-492): packed -> cb. The call sites: aff_quantize.cpp:434, 519
+ * and 391. */
+int affx_project_codebook(float* cb, uint64_t n, void* stream);
+int affx_pack_codebook(const float* cb, uint32_t* packed, void* stream);
+int affx_unpack_codebook(const uint32_t* packed, float* cb, void* stream);
+
 /* ---- the .aff container ------------------------------------------------------------------- */
 
 /* An open .aff file: one read-only mapping of it, checked. Opaque. */

@@ -14,6 +14,9 @@
 //   emu_main shared  hidden inter M T seed                -> the shared expert (decode on M
 //                    tokens, batch on T with and without a low part) vs the oracle, and the
 //                    hyper-connection post (single and batch forms) bit for bit
+//   emu_main fit     rows cols budget iters seed [seq]    -> sample collection, the codebook fit
+//                    (with `seq` every k-means++ draw by the sequential sums), projection, packing
+//                    and unpacking, each bit for bit vs the oracle
 //   emu_main timeout hidden inter n_experts M K seed      -> a decode whose waiters give up (spin
 //                    limit 0 from the host) fails the engine hook and affx_decode_status; after
 //                    the reset, the next calls are correct
@@ -35,6 +38,7 @@ thread_local EmuBlock* emu_blk;
 #include "../../affinity_amd/csrc/affx_noalloc.hip"
 #include "../../affinity_amd/csrc/affx_route.hip"
 #include "../../affinity_amd/csrc/affx_shared.hip"
+#include "../../affinity_amd/csrc/affx_fit.hip"
 
 extern "C" {
 #include "../../oracle/oracle.h"
@@ -629,6 +633,69 @@ int run_timeout(int argc, char** argv) {
   return ok ? 0 : 1;
 }
 
+int run_fit(int argc, char** argv) {
+  const uint64_t rows = atoi(argv[2]), cols = atoi(argv[3]), budget = atoi(argv[4]);
+  const uint32_t iters = atoi(argv[5]);
+  const uint64_t seed = atoi(argv[6]);
+  const bool seq = argc > 7 && std::string(argv[7]) == "seq";
+  std::mt19937_64 rng(seed);
+  std::normal_distribution<float> nd;
+  std::vector<float> w(rows * cols);
+  for (auto& v : w) v = 0.02f * nd(rng);
+  for (uint64_t c = 0; c < cols; ++c) w[3 * cols + c] = 0.0f;             // an all-zero row
+  for (uint64_t c = 0; c < 16 && c < cols; ++c) w[c] = 0.0f;               // an all-zero block
+  bool ok = true;
+  // collection
+  const uint64_t bound = affx_collect_samples_bound(rows, cols, budget);
+  std::vector<float> got(bound + 16, -1.0f);
+  std::vector<uint8_t> cws(affx_collect_samples_workspace_size(rows, cols, budget));
+  uint64_t n_got = 0;
+  if (affx_collect_samples(w.data(), rows, cols, budget, got.data(), bound, &n_got, cws.data(), cws.size(),
+                           nullptr) != 0) return 1;
+  const uint64_t n_ref = orc_collect_samples(w.data(), rows, cols, budget, nullptr, 0);
+  std::vector<float> ref(n_ref + 1);
+  orc_collect_samples(w.data(), rows, cols, budget, ref.data(), n_ref);
+  ok = ok && n_got == n_ref && memcmp(got.data(), ref.data(), n_ref * 4) == 0;
+  printf("collect: %llu samples, exact=%d\n", (unsigned long long)n_got, (int)ok);
+  // the fit
+  const size_t wsb = affx_fit_codebook_workspace_size(n_ref);
+  std::vector<uint8_t> fws(wsb + 256);
+  void* fw = (void*)(((uintptr_t)fws.data() + 255) & ~(uintptr_t)255);
+  std::vector<float> cb(kCbFloats + 4, 7.0f), cref(kCbFloats);
+  float* cb16 = (float*)(((uintptr_t)cb.data() + 15) & ~(uintptr_t)15);
+  std::vector<float> sm(n_ref + 4);
+  float* s16 = (float*)(((uintptr_t)sm.data() + 15) & ~(uintptr_t)15);
+  memcpy(s16, ref.data(), n_ref * 4);
+  if (affx_fit_codebook(s16, n_ref, nullptr, iters, seed, seq ? AFFX_FIT_SEQUENTIAL_PICKS : 0, cb16, fw, wsb,
+                        nullptr) != 0) {
+    printf("fit failed: %s\n", affx_last_error());
+    return 1;
+  }
+  orc_fit_codebook(ref.data(), n_ref, iters, seed, cref.data());
+  uint64_t seq_picks = 0, passes = 0;
+  affx_fit_codebook_stats(fw, &seq_picks, &passes, nullptr);
+  uint32_t diff = 0;
+  for (uint32_t i = 0; i < kCbFloats; ++i) diff += memcmp(&cb16[i], &cref[i], 4) != 0;
+  printf("fit: %u of %u floats differ, %llu sequential draws, %llu Lloyd passes\n", diff, kCbFloats,
+         (unsigned long long)seq_picks, (unsigned long long)passes);
+  ok = ok && diff == 0;
+  // projection, packing, unpacking
+  if (affx_project_codebook(cb16, kCbFloats, nullptr) != 0) return 1;
+  orc_project_codebook(cref.data(), kCbFloats);
+  std::vector<uint32_t> pk(kVariants * kLut), pref(kVariants * kLut);
+  if (affx_pack_codebook(cb16, pk.data(), nullptr) != 0) return 1;
+  orc_pack_codebook(cref.data(), pref.data());
+  std::vector<float> un(kCbFloats), uref(kCbFloats);
+  if (affx_unpack_codebook(pk.data(), un.data(), nullptr) != 0) return 1;
+  orc_unpack_codebook(pref.data(), uref.data());
+  const bool pj = memcmp(cb16, cref.data(), kCbFloats * 4) == 0, pkok = pk == pref,
+             unok = memcmp(un.data(), uref.data(), kCbFloats * 4) == 0;
+  printf("project exact=%d pack exact=%d unpack exact=%d\n", (int)pj, (int)pkok, (int)unok);
+  ok = ok && pj && pkok && unok;
+  printf("fit ok=%d\n", (int)ok);
+  return ok ? 0 : 1;
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -644,6 +711,7 @@ int main(int argc, char** argv) {
   if (cmd == "ffnptr" && argc >= 6) return run_ffnptr(argc, argv);
   if (cmd == "route" && argc >= 6) return run_route(argc, argv);
   if (cmd == "shared" && argc >= 7) return run_shared(argc, argv);
+  if (cmd == "fit" && argc >= 7) return run_fit(argc, argv);
   fprintf(stderr, "usage: see header\n");
   return 2;
 }

@@ -1,0 +1,120 @@
+"""GPU codebook producer parity: sample collection, the joint codebook fit, E4M3 projection,
+packing and unpacking (src/quant/blockquant.cpp:252-492) against the reference's own fixtures
+(small.npz, written by the compiled reference; c1_codebook.bin, the packed codebook of the config-1
+recipe) and the oracle, bit for bit."""
+import os
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+H, I = 4096, 2048
+
+
+@pytest.fixture(scope="module")
+def cbk():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import affinity_amd.codebook as cbk
+    import affinity_amd.experts as ax
+    ax.init()
+    return cbk
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def same(a, b, msg=""):
+    """Bit for bit, except that any NaN matches any NaN (payloads are the platform's)."""
+    a, b = np.ascontiguousarray(a, np.float32), np.ascontiguousarray(b, np.float32)
+    assert a.shape == b.shape, msg
+    na, nb = np.isnan(a), np.isnan(b)
+    np.testing.assert_array_equal(na, nb, err_msg=msg)
+    np.testing.assert_array_equal(bits(a[~na]), bits(b[~nb]), err_msg=msg)
+
+
+def gpu_fit(cbk, samples, iters=50, seed=1, flags=0):
+    f = cbk.CodebookFit(samples.size)
+    cb = f.fit(torch.from_numpy(np.ascontiguousarray(samples, np.float32)).cuda(), iters, seed, flags)
+    return cb.cpu().numpy().reshape(-1), f.stats()
+
+
+def test_collect_samples_matches_oracle(cbk, orc):
+    rng = np.random.default_rng(3)
+    for rows, cols, budget in ((64, 512, 4096), (100, 256, 1 << 22), (33, 200, 1000), (7, 64, 1), (128, 4096, 1 << 14)):
+        w = (0.02 * rng.standard_normal((rows, cols))).astype(np.float32)
+        w[1] = 0.0                       # a zero row
+        w[2, 16:32] = 0.0                # a zero block
+        w[4, :cols - cols % 16] = 0.0    # only the columns past the last block nonzero
+        w[5, 3] = np.nan                 # NaN: ignored by the maxima, divided like any value
+        got = cbk.collect_normalized_samples(torch.from_numpy(w).cuda(), budget).cpu().numpy()
+        ref = orc.collect_samples(w, budget)
+        same(got, ref, f"{rows}x{cols} budget {budget}")
+
+
+def test_fit_matches_reference_fixture(cbk, small):
+    s = small["fit_samples"]
+    raw, (seq, passes) = gpu_fit(cbk, s, 50, 1)
+    np.testing.assert_array_equal(bits(raw), bits(small["fit_cb_raw"]))
+    proj = cbk.project_codebook_e4m3(torch.from_numpy(raw.copy()).cuda()).cpu().numpy()
+    np.testing.assert_array_equal(bits(proj), bits(small["fit_cb_proj"]))
+    assert passes > 0
+    print(f"small fixture: {seq} sequential draws, {passes} Lloyd passes")
+
+
+@pytest.mark.parametrize("n,iters,seed", [(16, 50, 1), (20, 5, 2), (64, 50, 3), (1000, 7, 4), (4101, 3, 5),
+                                          (20000, 10, 9)])
+def test_fit_matches_oracle(cbk, orc, n, iters, seed):
+    # sizes below one block, below the 1024 entries (duplicate draws, an all-zero d2), ragged
+    # tails (items outside a whole block), a single-block EM (an empty variant is reseeded)
+    rng = np.random.default_rng(seed)
+    s = np.clip(rng.standard_normal(n) * 0.4, -1, 1).astype(np.float32)
+    raw, _ = gpu_fit(cbk, s, iters, seed)
+    np.testing.assert_array_equal(bits(raw), bits(orc.fit_codebook(s, iters, seed)))
+
+
+def test_fit_sequential_draws_give_the_same_codebook(cbk, small):
+    s = small["fit_samples"][:24000]
+    a, (seq_a, _) = gpu_fit(cbk, s, 8, 11)
+    b, (seq_b, _) = gpu_fit(cbk, s, 8, 11, cbk.SEQUENTIAL_PICKS)
+    assert seq_b == 1023
+    np.testing.assert_array_equal(bits(a), bits(b))
+
+
+def test_config1_codebook_on_gpu(cbk):
+    """The config-1 recipe end to end on the GPU (weights from the GPU generator, 3 x 2^19 samples,
+    fit_codebook(50, seed 1), projection, packing) reproduces the reference's packed codebook."""
+    import affinity_amd.experts as ax
+    mats = [ax.gen_normal(1000, I * H, 0.02).view(I, H), ax.gen_normal(1001, I * H, 0.02).view(I, H),
+            ax.gen_normal(1002, H * I, 0.02).view(H, I)]
+    s = torch.cat([cbk.collect_normalized_samples(m, 1 << 19) for m in mats])
+    assert s.numel() == 3 * (1 << 19)
+    f = cbk.CodebookFit(s.numel())
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    cb = f.fit(s, 50, 1)
+    e1.record()
+    torch.cuda.synchronize()
+    seq, passes = f.stats()
+    print(f"config-1 fit: {e0.elapsed_time(e1):.1f} ms, {seq} sequential draws, {passes} Lloyd passes")
+    packed = cbk.pack_codebook_e4m3_quads(cbk.project_codebook_e4m3(cb)).cpu().numpy().view(np.uint32)
+    ref = np.fromfile(os.path.join(GOLDEN, "c1_codebook.bin"), dtype="<u4")
+    np.testing.assert_array_equal(packed, ref)
+
+
+def test_project_pack_unpack_match_oracle(cbk, orc, c1_codebook):
+    rng = np.random.default_rng(1)
+    cb = np.concatenate([rng.uniform(-2, 2, 6000), rng.standard_normal(1000) * 0.01,
+                         [0.0, -0.0, 1.875, -1.875, 2.0, 100.0, -100.0, 1e-9, np.nan],
+                         rng.uniform(-1, 1, 8192 - 7009)]).astype(np.float32)
+    proj = cbk.project_codebook_e4m3(torch.from_numpy(cb.copy()).cuda()).cpu().numpy()
+    same(proj, orc.project_codebook(cb))
+    packed = cbk.pack_codebook_e4m3_quads(torch.from_numpy(cb).cuda()).cpu().numpy().view(np.uint32)
+    np.testing.assert_array_equal(packed, orc.pack_codebook(cb))
+    un = cbk.unpack_codebook_e4m3_quads(torch.from_numpy(c1_codebook.view(np.int32)).cuda()).cpu().numpy().reshape(-1)
+    np.testing.assert_array_equal(bits(un), bits(orc.unpack_codebook(c1_codebook)))
