@@ -5,6 +5,7 @@ runs each work-item as an OS thread."""
 import os
 import shutil
 import subprocess
+from concurrent.futures import ThreadPoolExecutor
 
 import pytest
 
@@ -30,7 +31,7 @@ def emu(tmp_path_factory):
     return str(d / "emu_main")
 
 
-def run(emu, *args, timeout=600, cus=4):
+def run(emu, *args, timeout=900, cus=4):
     # cus: compute units of the emulated device; the fused decode sizes its grid (all workgroups
     # resident, run concurrently here) to it
     env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=0", AFFX_EMU_CUS=str(cus))
@@ -42,80 +43,116 @@ def run(emu, *args, timeout=600, cus=4):
     return out
 
 
-def test_dequant_emulated(emu):
-    assert "exact=1" in run(emu, "dequant", 1024, 1024, 1)
+# Every case's arguments (and emulated CU count). The runs are started together, three at a time,
+# when the first test asks for one: each is a long single-threaded-per-lane emulation, and
+# running them side by side keeps the module's wall time near the longest few.
+CASES = {
+    "dequant": (("dequant", 1024, 1024, 1), 4),
+    # decode: the fused launch is checked bit-identical to the staged launches, its counters zero
+    # after two launches on one workspace, and both against the oracle at 1e-3 relative L2
+    "decode_m1": (("decode", 1024, 1024, 7, 1, 6, 1), 4),   # 4 workgroups: gate/up in rounds
+    "decode_allpad": (("decode", 1024, 1024, 5, 2, 3, 4, "allpad"), 3),
+    "decode_m1_single": (("decode", 1024, 1024, 5, 1, 1, 9), 6),
+    "decode_m6_two_cg": (("decode", 2048, 1024, 5, 6, 2, 2), 4),
+    "decode_m6_dm16": (("decode", 2048, 1024, 5, 6, 2, 2, "dm16"), 4),
+    "decode_m8_wide": (("decode", 1024, 1024, 7, 8, 3, 6), 3),
+    "quant": (("quant", 4, 256, 3), 4),
+    "grouped": (("grouped", 1024, 1024, 5, 12, 3, 4, 1), 4),
+    "timeout": (("timeout", 1024, 1024, 6, 2, 3, 8), 4),
+    "slots": (("slots", 1024, 1024, 4, 6, 2, 9), 4),
+    "ffnptr": (("ffnptr", 1024, 1024, 3, 12), 4),
+    "route": (("route", 21, 100, 6, 4), 4),
+    "shared": (("shared", 1024, 1024, 6, 40, 5), 4),
+}
+# longest first, so the three lanes finish together
+ORDER = ["decode_m8_wide", "decode_m6_dm16", "decode_m6_two_cg", "slots", "shared", "decode_m1_single", "grouped",
+         "decode_m1", "ffnptr", "quant", "timeout", "route", "decode_allpad", "dequant"]
 
 
-# decode: the fused launch is checked bit-identical to the staged launches, its counters zero
-# after two launches on one workspace, and both against the oracle at 1e-3 relative L2
+@pytest.fixture(scope="module")
+def runs(emu):
+    pool = ThreadPoolExecutor(max_workers=3)
+    futs = {name: pool.submit(run, emu, *CASES[name][0], cus=CASES[name][1]) for name in ORDER}
+    yield futs
+    for f in futs.values():
+        f.cancel()
+    pool.shutdown(wait=True)
 
 
-def test_decode_emulated_m1(emu):
+def result(runs, name):
+    return runs[name].result()
+
+
+def test_dequant_emulated(runs):
+    assert "exact=1" in result(runs, "dequant")
+
+
+def test_decode_emulated_m1(runs):
     # 4 workgroups: gate/up in rounds, several output tiles per workgroup
-    assert "identical to staged=1" in run(emu, "decode", 1024, 1024, 7, 1, 6, 1)
+    assert "identical to staged=1" in result(runs, "decode_m1")
 
 
-def test_decode_emulated_all_padding(emu):
+def test_decode_emulated_all_padding(runs):
     # no route names an expert of the layer: nothing to wait for, y written as zeros
-    out = run(emu, "decode", 1024, 1024, 5, 2, 3, 4, "allpad", cus=3)
+    out = result(runs, "decode_allpad")
     assert "identical to staged=1" in out and "rel_l2=0.000e+00" in out
 
 
-def test_decode_emulated_m1_single_pass(emu):
+def test_decode_emulated_m1_single_pass(runs):
     # 6 workgroups hold all 64 gate/up items: the straight-line batch-1 variant
-    assert "identical to staged=1" in run(emu, "decode", 1024, 1024, 5, 1, 1, 9, cus=6)
+    assert "identical to staged=1" in result(runs, "decode_m1_single")
 
 
-def test_decode_emulated_m6_two_column_groups(emu):
-    assert "identical to staged=1" in run(emu, "decode", 2048, 1024, 5, 6, 2, 2)
+def test_decode_emulated_m6_two_column_groups(runs):
+    assert "identical to staged=1" in result(runs, "decode_m6_two_cg")
 
 
-def test_decode_emulated_m6_dim_major_arena(emu):
+def test_decode_emulated_m6_dim_major_arena(runs):
     # the engine's dim-major batch arena at its 16-token stride: whole-row reads of four tokens
     # per wave (two token quads x two column segments), the second quad half padding slots
-    assert "identical to staged=1" in run(emu, "decode", 2048, 1024, 5, 6, 2, 2, "dm16")
+    assert "identical to staged=1" in result(runs, "decode_m6_dm16")
 
 
-def test_decode_emulated_m8_wide_epilogue(emu):
+def test_decode_emulated_m8_wide_epilogue(runs):
     # 12 gate/up groups x 16 rows x 8 tokens: the epilogue takes two passes of the workgroup
     # (hidden 1024: one column segment, so 12 wave groups; inter 1024 keeps the emulation short)
-    assert "identical to staged=1" in run(emu, "decode", 1024, 1024, 7, 8, 3, 6, cus=3)
+    assert "identical to staged=1" in result(runs, "decode_m8_wide")
 
 
-def test_quantizer_emulated(emu):
-    assert "exact=1" in run(emu, "quant", 4, 256, 3)
+def test_quantizer_emulated(runs):
+    assert "exact=1" in result(runs, "quant")
 
 
-def test_grouped_emulated(emu):
-    assert "rel_l2" in run(emu, "grouped", 1024, 1024, 5, 12, 3, 4, 1, timeout=900)
+def test_grouped_emulated(runs):
+    assert "rel_l2" in result(runs, "grouped")
 
 
-def test_decode_wait_give_up_fails_loudly(emu):
+def test_decode_wait_give_up_fails_loudly(runs):
     # the host forces the bounded wait to give up (no polls); the hook returns 0 with an error,
     # affx_decode_status reports it, and after the reset the next call is right
-    out = run(emu, "timeout", 1024, 1024, 6, 2, 3, 8, cus=4)
+    out = result(runs, "timeout")
     assert "timeout path ok=1" in out, out
 
 
-def test_grouped_slot_list_emulated(emu):
+def test_grouped_slot_list_emulated(runs):
     # the slot-list entry: bit-identical to the routes entry on the list the routes build, and
     # within tolerance on a reordered list
-    out = run(emu, "slots", 1024, 1024, 4, 6, 2, 9, timeout=900)
+    out = result(runs, "slots")
     assert "routes==slots=1" in out, out
 
 
-def test_expert_ffn_pointer_table_emulated(emu):
-    out = run(emu, "ffnptr", 1024, 1024, 3, 12)
+def test_expert_ffn_pointer_table_emulated(runs):
+    out = result(runs, "ffnptr")
     assert "identical to staged=1" in out, out
 
 
-def test_route_emulated(emu):
-    out = run(emu, "route", 21, 100, 6, 4)
+def test_route_emulated(runs):
+    out = result(runs, "route")
     assert "route ids equal=1" in out, out
 
 
-def test_shared_expert_and_hc_post_emulated(emu):
+def test_shared_expert_and_hc_post_emulated(runs):
     """The shared expert's decode (6 tokens, two column groups) and batch kernels (40 tokens, with
     and without a low part) against the oracle, the hyper-connection post bit for bit."""
-    out = run(emu, "shared", 1024, 1024, 6, 40, 5, timeout=900)
+    out = result(runs, "shared")
     assert "shared ok=1" in out, out
