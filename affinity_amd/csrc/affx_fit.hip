@@ -37,7 +37,8 @@ constexpr uint32_t kEmIters = 6;                       // Lloyd passes per varia
 constexpr uint32_t kKppThreads = 256, kKppPer = 16;
 constexpr uint32_t kKppChunk = kKppThreads * kKppPer;  // items per d2-update workgroup
 constexpr uint32_t kPickThreads = kKppChunk / 4;       // the pick scans one chunk, 4 items a thread
-constexpr uint32_t kSortChunk = 4096;                  // keys per counting-sort wave
+constexpr uint32_t kSortSteps = 32;                    // 64-key steps per counting-sort wave
+constexpr uint32_t kSortChunk = 64 * kSortSteps;      // keys per counting-sort wave
 constexpr uint32_t kAssignThreads = 256;
 constexpr uint32_t kSeqBuf = 512;                      // doubles staged per step of a sequential sum
 
@@ -369,7 +370,8 @@ __global__ void __launch_bounds__(kAssignThreads) lloyd_assign_kernel(const floa
   key[t] = (uint16_t)nearest_entry(cent, x[blk * 4 + (t & 3)], d);
 }
 
-// Per-chunk key counts (one wave a chunk of kSortChunk keys): counts[chunk][key].
+// Per-chunk key counts (one wave a chunk of kSortChunk keys): counts[chunk][key]. The wave requests
+// all of its keys first (one per lane and step), then counts them step by step.
 template <uint32_t NK, int BITS>
 __global__ void __launch_bounds__(64) sort_count_kernel(const uint16_t* __restrict__ key, uint64_t n_blocks,
                                                         int mode, uint32_t v, const FitState* __restrict__ st,
@@ -379,14 +381,19 @@ __global__ void __launch_bounds__(64) sort_count_kernel(const uint16_t* __restri
   if (e0 >= n) return;
   __shared__ uint32_t cnt[NK];
   const uint32_t lane = threadIdx.x;
+  uint32_t kk[kSortSteps];
+#pragma unroll
+  for (uint32_t q = 0; q < kSortSteps; ++q) {
+    const uint64_t el = e0 + 64u * q + lane;
+    kk[q] = el < n ? key[el] : 0u;
+  }
   for (uint32_t k = lane; k < NK; k += 64) cnt[k] = 0;
   __syncthreads();
-  const uint64_t e1 = e0 + kSortChunk < n ? e0 + kSortChunk : n;
-  for (uint64_t e = e0; e < e1; e += 64) {
-    const bool valid = e + lane < e1;
-    const uint32_t k = valid ? key[e + lane] : 0u;
-    const uint64_t m = same_key_lanes<BITS>(k, valid);
-    if (valid && (uint32_t)__builtin_ctzll(m) == lane) cnt[k] += (uint32_t)__popcll(m);
+#pragma unroll
+  for (uint32_t q = 0; q < kSortSteps; ++q) {
+    const bool valid = e0 + 64u * q + lane < n;
+    const uint64_t m = same_key_lanes<BITS>(kk[q], valid);
+    if (valid && (uint32_t)__builtin_ctzll(m) == lane) cnt[kk[q]] += (uint32_t)__popcll(m);
     __syncthreads();
   }
   for (uint32_t k = lane; k < NK; k += 64) counts[(uint64_t)blockIdx.x * NK + k] = cnt[k];
@@ -420,7 +427,7 @@ __global__ void __launch_bounds__(1024) sort_scan_kernel(uint64_t n_blocks, int 
 
 // Stable scatter: each chunk's wave walks its keys in order; an element's place is its key's
 // run start + the chunk's offset + the earlier equal keys of the chunk. The Lloyd passes move
-// the item quads (xs), the partition the block ids (part).
+// the item quads (xs, requested four steps ahead), the partition the block ids (part).
 template <uint32_t NK, int BITS>
 __global__ void __launch_bounds__(64) sort_scatter_kernel(const uint16_t* __restrict__ key, uint64_t n_blocks,
                                                           int mode, uint32_t v, const FitState* __restrict__ st,
@@ -433,72 +440,93 @@ __global__ void __launch_bounds__(64) sort_scatter_kernel(const uint16_t* __rest
   if (e0 >= n) return;
   __shared__ uint32_t runp[NK];
   const uint32_t lane = threadIdx.x;
+  const uint32_t* list = mode == kMember ? part + (v ? st->nm[0] : 0) : nullptr;
+  uint32_t kk[kSortSteps];
+#pragma unroll
+  for (uint32_t q = 0; q < kSortSteps; ++q) {
+    const uint64_t el = e0 + 64u * q + lane;
+    kk[q] = el < n ? key[el] : 0u;
+  }
+  auto quad = [&](uint32_t q) -> float4 {
+    const uint64_t el = e0 + 64u * q + lane;
+    if (mode == kPartition || el >= n) return make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const uint64_t blk = mode == kAll ? (el >> 2) : list[el >> 2];
+    return x[blk * 4 + (el & 3)];
+  };
+  constexpr uint32_t kAhead = 4;
+  float4 ring[kAhead];
+#pragma unroll
+  for (uint32_t q = 0; q < kAhead; ++q) ring[q] = quad(q);
   for (uint32_t k = lane; k < NK; k += 64) runp[k] = segbase[k] + counts[(uint64_t)blockIdx.x * NK + k];
   __syncthreads();
-  const uint32_t* list = mode == kMember ? part + (v ? st->nm[0] : 0) : nullptr;
-  const uint64_t e1 = e0 + kSortChunk < n ? e0 + kSortChunk : n;
   const uint64_t below = (1ull << lane) - 1ull;
-  for (uint64_t e = e0; e < e1; e += 64) {
-    const uint64_t el = e + lane;
-    const bool valid = el < e1;
-    const uint32_t k = valid ? key[el] : 0u;
+#pragma unroll
+  for (uint32_t q = 0; q < kSortSteps; ++q) {
+    const uint64_t el = e0 + 64u * q + lane;
+    const bool valid = el < n;
+    const uint32_t k = kk[q];
+    const float4 xq = ring[q % kAhead];
+    if (q + kAhead < kSortSteps) ring[q % kAhead] = quad(q + kAhead);
     const uint64_t m = same_key_lanes<BITS>(k, valid);
     const uint32_t pos = valid ? runp[k] + (uint32_t)__popcll(m & below) : 0u;
     __syncthreads();
     if (valid) {
       if ((uint32_t)__builtin_ctzll(m) == lane) runp[k] += (uint32_t)__popcll(m);
-      if (mode == kPartition) {
+      if (mode == kPartition)
         part[pos] = (uint32_t)el;
-      } else {
-        const uint64_t blk = mode == kAll ? (el >> 2) : list[el >> 2];
-        xs[pos] = x[blk * 4 + (el & 3)];
-      }
+      else
+        xs[pos] = xq;
     }
     __syncthreads();
   }
 }
 
-// New centroids of variant v: per entry, the double sums of its items in item order / count,
-// rounded to float (blockquant.cpp:235-241); the shift summed by one thread in entry order.
-__global__ void __launch_bounds__(1024) lloyd_update_kernel(const float4* __restrict__ xs, uint64_t n_blocks,
-                                                            int mode, uint32_t v,
-                                                            const uint32_t* __restrict__ segbase,
-                                                            float* __restrict__ cb, FitState* __restrict__ st) {
-  const uint64_t n = pass_len(st, mode, v, n_blocks);
-  if (n == 0) return;
-  __shared__ float diff[kFitK * 4];
-  const uint32_t c = threadIdx.x;
-  const uint32_t j0 = segbase[c], j1 = segbase[c + 1];
-  double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
-  uint32_t j = j0;
-  for (; j + 4 <= j1; j += 4) {
-    const float4 p0 = xs[j], p1 = xs[j + 1], p2 = xs[j + 2], p3 = xs[j + 3];
-    a0 = a0 + (double)p0.x; a1 = a1 + (double)p0.y; a2 = a2 + (double)p0.z; a3 = a3 + (double)p0.w;
-    a0 = a0 + (double)p1.x; a1 = a1 + (double)p1.y; a2 = a2 + (double)p1.z; a3 = a3 + (double)p1.w;
-    a0 = a0 + (double)p2.x; a1 = a1 + (double)p2.y; a2 = a2 + (double)p2.z; a3 = a3 + (double)p2.w;
-    a0 = a0 + (double)p3.x; a1 = a1 + (double)p3.y; a2 = a2 + (double)p3.z; a3 = a3 + (double)p3.w;
+// New centroids of variant v (blockquant.cpp:235-241): one thread per (entry, dimension) adds the
+// entry's run of that dimension in item order (the run's values requested 16 ahead of the adds),
+// divides by the count and rounds to float; |new - old| goes to diff[4 entry + dimension].
+constexpr uint32_t kSumAhead = 16;
+__global__ void __launch_bounds__(256) lloyd_sum_kernel(const float4* __restrict__ xs, uint64_t n_blocks, int mode,
+                                                        uint32_t v, const uint32_t* __restrict__ segbase,
+                                                        float* __restrict__ cb, float* __restrict__ diff,
+                                                        const FitState* __restrict__ st) {
+  if (pass_len(st, mode, v, n_blocks) == 0) return;
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;  // entry i / 4, dimension i % 4
+  const uint32_t c = i >> 2, p = i & 3u;
+  const uint32_t j0 = segbase[c], j1 = segbase[c + 1], cnt = j1 - j0;
+  const float* src = reinterpret_cast<const float*>(xs + j0) + p;
+  double acc = 0.0;
+  float cur[kSumAhead], nxt[kSumAhead];
+#pragma unroll
+  for (uint32_t q = 0; q < kSumAhead; ++q) cur[q] = q < cnt ? src[4u * q] : 0.0f;
+  for (uint32_t b = 0; b < cnt; b += kSumAhead) {
+#pragma unroll
+    for (uint32_t q = 0; q < kSumAhead; ++q) nxt[q] = b + kSumAhead + q < cnt ? src[4u * (b + kSumAhead + q)] : 0.0f;
+#pragma unroll
+    for (uint32_t q = 0; q < kSumAhead; ++q)
+      if (b + q < cnt) acc = acc + (double)cur[q];
+#pragma unroll
+    for (uint32_t q = 0; q < kSumAhead; ++q) cur[q] = nxt[q];
   }
-  for (; j < j1; ++j) {
-    const float4 p = xs[j];
-    a0 = a0 + (double)p.x; a1 = a1 + (double)p.y; a2 = a2 + (double)p.z; a3 = a3 + (double)p.w;
-  }
-  float4* cent = reinterpret_cast<float4*>(cb) + (uint64_t)v * kFitK + c;
-  float4 d = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  if (j1 > j0) {
-    const double cnt = (double)(j1 - j0);
-    const float4 old = *cent;
-    const float4 nv = make_float4((float)(a0 / cnt), (float)(a1 / cnt), (float)(a2 / cnt), (float)(a3 / cnt));
-    d = make_float4(fabsf(nv.x - old.x), fabsf(nv.y - old.y), fabsf(nv.z - old.z), fabsf(nv.w - old.w));
+  float* cent = cb + ((uint64_t)v * kFitK + c) * 4 + p;
+  float d = 0.0f;  // an empty entry adds +0 to the shift, which leaves it as it is
+  if (cnt > 0) {
+    const float nv = (float)(acc / (double)cnt);
+    d = fabsf(nv - *cent);
     *cent = nv;
   }
-  diff[4 * c + 0] = d.x;
-  diff[4 * c + 1] = d.y;
-  diff[4 * c + 2] = d.z;
-  diff[4 * c + 3] = d.w;
+  diff[i] = d;
+}
+
+// The shift of the pass, summed by one lane in entry order; below 1e-7 the refit has converged.
+__global__ void __launch_bounds__(64) lloyd_shift_kernel(const float* __restrict__ diff, uint64_t n_blocks, int mode,
+                                                         uint32_t v, FitState* __restrict__ st) {
+  if (pass_len(st, mode, v, n_blocks) == 0) return;
+  __shared__ float buf[kFitK * 4];
+  for (uint32_t i = threadIdx.x; i < kFitK * 4; i += 64) buf[i] = diff[i];
   __syncthreads();
-  if (c == 0) {
-    double shift = 0.0;  // an empty entry adds +0, which leaves the sum as it is
-    for (uint32_t i = 0; i < kFitK * 4; ++i) shift = shift + (double)diff[i];
+  if (threadIdx.x == 0) {
+    double shift = 0.0;
+    for (uint32_t i = 0; i < kFitK * 4; ++i) shift = shift + (double)buf[i];
     if (shift < 1e-7) st->lloyd_done = 1u;
     st->n_passes += 1;
   }
@@ -743,7 +771,7 @@ uint64_t splitmix_next(uint64_t& z) {
 }
 
 struct FitWs {
-  uint64_t st, d2, wgsum, key, ckey, counts, segbase, xs, part, total;
+  uint64_t st, d2, wgsum, key, ckey, counts, segbase, xs, part, diff, total;
 };
 
 FitWs fit_ws(uint64_t n_samples) {
@@ -761,6 +789,7 @@ FitWs fit_ws(uint64_t n_samples) {
   w.segbase = o; o += a256((kFitK + 1) * 4);
   w.xs = o; o += a256(4 * n_blocks * 16 + 16);
   w.part = o; o += a256(n_blocks * 4 + 4);
+  w.diff = o; o += a256(kFitK * 4 * 4);
   w.total = o;
   return w;
 }
@@ -783,7 +812,10 @@ int fit_pass(int mode, uint32_t v, const float4* x, uint64_t n_blocks, float* cb
   hipLaunchKernelGGL((sort_scan_kernel<kFitK>), dim3(1), dim3(1024), 0, s, n_blocks, mode, v, st, counts, segbase);
   hipLaunchKernelGGL((sort_scatter_kernel<kFitK, 10>), dim3(g_sort), dim3(64), 0, s, key, n_blocks, mode, v, st,
                      counts, segbase, x, xs, part);
-  hipLaunchKernelGGL(lloyd_update_kernel, dim3(1), dim3(1024), 0, s, xs, n_blocks, mode, v, segbase, cb, st);
+  float* diff = reinterpret_cast<float*>(ws + L.diff);
+  hipLaunchKernelGGL(lloyd_sum_kernel, dim3(kFitK * 4 / 256), dim3(256), 0, s, xs, n_blocks, mode, v, segbase, cb,
+                     diff, st);
+  hipLaunchKernelGGL(lloyd_shift_kernel, dim3(1), dim3(64), 0, s, diff, n_blocks, mode, v, st);
   return check_launch("fit: Lloyd pass");
 }
 
