@@ -139,6 +139,33 @@ __device__ __forceinline__ T block_scan_incl(T v, T* sc) {
   return v;
 }
 
+// The same scan by wave: shuffle scans within each wave, then the waves' totals (one thread). The
+// order of the additions differs from the LDS form; the callers bound the error either way.
+template <int NT>
+__device__ __forceinline__ double block_scan_incl_waves(double v, double* sc) {
+  const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const double o = __shfl_up(v, d);
+    if ((int)lane >= d) v = v + o;
+  }
+  __shared__ double wtot[NT / 64];
+  if (lane == 63) wtot[wv] = v;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double run = 0.0;
+    for (int w = 0; w < NT / 64; ++w) {
+      run = run + wtot[w];
+      wtot[w] = run;
+    }
+  }
+  __syncthreads();
+  if (wv > 0) v = v + wtot[wv - 1];
+  sc[threadIdx.x] = v;
+  __syncthreads();
+  return v;
+}
+
 // ---- fit set-up --------------------------------------------------------------------------------
 
 // cb = 0 but entry 0 of variant 0 = the first sample quad (blockquant.cpp:274); state cleared.
@@ -203,7 +230,7 @@ __global__ void __launch_bounds__(kPickThreads) kpp_pick_kernel(const float4* __
     const uint32_t w = t * per + j;
     if (w < n_wg) run = run + wgsum[w];
   }
-  block_scan_incl<kPickThreads>(run, sc);
+  block_scan_incl_waves<kPickThreads>(run, sc);
   const double T = sc[kPickThreads - 1];
   const double aT = a * T;
   const double excl = t ? sc[t - 1] : 0.0;
@@ -246,7 +273,7 @@ __global__ void __launch_bounds__(kPickThreads) kpp_pick_kernel(const float4* __
       loc[q] = tsum;
     }
   }
-  block_scan_incl<kPickThreads>(tsum, sc);
+  block_scan_incl_waves<kPickThreads>(tsum, sc);
   const double pre = t ? sc[t - 1] : 0.0;  // the sum of the chunk's items before this thread's
   if (w != ~0u) {
 #pragma unroll
@@ -412,11 +439,16 @@ __global__ void __launch_bounds__(1024) sort_scan_kernel(uint64_t n_blocks, int 
   const uint32_t k = threadIdx.x;
   uint32_t tot = 0;
   if (k < NK) {
-    for (uint32_t w = 0; w < n_w; ++w) {
-      uint32_t* p = counts + (uint64_t)w * NK + k;
-      const uint32_t cv = *p;
-      *p = tot;
-      tot += cv;
+    for (uint32_t w0 = 0; w0 < n_w; w0 += 16) {
+      uint32_t cv[16];
+#pragma unroll
+      for (uint32_t q = 0; q < 16; ++q) cv[q] = w0 + q < n_w ? counts[(uint64_t)(w0 + q) * NK + k] : 0u;
+#pragma unroll
+      for (uint32_t q = 0; q < 16; ++q)
+        if (w0 + q < n_w) {
+          counts[(uint64_t)(w0 + q) * NK + k] = tot;
+          tot += cv[q];
+        }
     }
   }
   const uint32_t incl = block_scan_incl<1024>(tot, sc);
@@ -517,17 +549,36 @@ __global__ void __launch_bounds__(256) lloyd_sum_kernel(const float4* __restrict
   diff[i] = d;
 }
 
-// The shift of the pass, summed by one lane in entry order; below 1e-7 the refit has converged.
-__global__ void __launch_bounds__(64) lloyd_shift_kernel(const float* __restrict__ diff, uint64_t n_blocks, int mode,
-                                                         uint32_t v, FitState* __restrict__ st) {
+// The shift of the pass against 1e-7 (blockquant.cpp:242): the 4096 |new - old| are summed in
+// parallel; any order of n non-negative additions lands within n * 2^-53 of the exact sum, the
+// reference's entry-order sum included, so the comparison is decided from the parallel sum unless
+// it lies within twice that bound of 1e-7 (or is NaN): then one lane repeats the sum in entry order.
+__global__ void __launch_bounds__(256) lloyd_shift_kernel(const float* __restrict__ diff, uint64_t n_blocks, int mode,
+                                                          uint32_t v, FitState* __restrict__ st) {
   if (pass_len(st, mode, v, n_blocks) == 0) return;
   __shared__ float buf[kFitK * 4];
-  for (uint32_t i = threadIdx.x; i < kFitK * 4; i += 64) buf[i] = diff[i];
+  __shared__ double red[4];
+  double part = 0.0;
+  for (uint32_t i = threadIdx.x; i < kFitK * 4; i += 256) {
+    const float d = diff[i];
+    buf[i] = d;
+    part = part + (double)d;
+  }
+  const double S = block_sum<256>(part, red);  // (thread 0)
   __syncthreads();
   if (threadIdx.x == 0) {
-    double shift = 0.0;
-    for (uint32_t i = 0; i < kFitK * 4; ++i) shift = shift + (double)buf[i];
-    if (shift < 1e-7) st->lloyd_done = 1u;
+    const double G = (double)(kFitK * 4 + 64) * 0x1p-53 * 2.0;
+    int done;
+    if (S * (1.0 + G) < 1e-7) {
+      done = 1;
+    } else if (S * (1.0 - G) >= 1e-7) {
+      done = 0;
+    } else {  // (and NaN)
+      double shift = 0.0;
+      for (uint32_t i = 0; i < kFitK * 4; ++i) shift = shift + (double)buf[i];
+      done = shift < 1e-7;
+    }
+    if (done) st->lloyd_done = 1u;
     st->n_passes += 1;
   }
 }
@@ -815,7 +866,7 @@ int fit_pass(int mode, uint32_t v, const float4* x, uint64_t n_blocks, float* cb
   float* diff = reinterpret_cast<float*>(ws + L.diff);
   hipLaunchKernelGGL(lloyd_sum_kernel, dim3(kFitK * 4 / 256), dim3(256), 0, s, xs, n_blocks, mode, v, segbase, cb,
                      diff, st);
-  hipLaunchKernelGGL(lloyd_shift_kernel, dim3(1), dim3(64), 0, s, diff, n_blocks, mode, v, st);
+  hipLaunchKernelGGL(lloyd_shift_kernel, dim3(1), dim3(256), 0, s, diff, n_blocks, mode, v, st);
   return check_launch("fit: Lloyd pass");
 }
 
