@@ -28,17 +28,8 @@ thread_local emu_dim3 threadIdx, blockIdx;
 emu_dim3 blockDim, gridDim;
 thread_local EmuBlock* emu_blk;
 
-#define AFFX_PIN(x) ((void)0)
-#include "../../affinity_amd/csrc/affx_layout.hip"
-#include "../../affinity_amd/csrc/affx_decode.hip"
-#include "../../affinity_amd/csrc/affx_fused.hip"
-#include "../../affinity_amd/csrc/affx_quant.hip"
-#include "../../affinity_amd/csrc/affx_grouped.hip"
-#include "../../affinity_amd/csrc/affx_api.hip"
-#include "../../affinity_amd/csrc/affx_noalloc.hip"
-#include "../../affinity_amd/csrc/affx_route.hip"
-#include "../../affinity_amd/csrc/affx_shared.hip"
-#include "../../affinity_amd/csrc/affx_fit.hip"
+#include "../../affinity_amd/csrc/affx_common.h"
+using namespace affx;
 
 extern "C" {
 #include "../../oracle/oracle.h"
@@ -48,6 +39,8 @@ extern "C" {
 #include <string>
 
 namespace {
+
+constexpr uint32_t kCbFloats = kVariants * kLut * 4;  // a codebook as floats [2][1024][4]
 
 uint16_t bf16(float f) {
   uint32_t u;

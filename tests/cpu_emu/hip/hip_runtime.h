@@ -27,6 +27,7 @@
 #define __device__
 #define __host__
 #define __forceinline__ inline
+#define AFFX_PIN(x) ((void)0)  // (the library's register pin is device assembly)
 #define __launch_bounds__(...)
 #define __restrict__
 #define __shared__ static

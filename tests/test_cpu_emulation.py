@@ -14,20 +14,33 @@ CLANG = "/opt/rocm/llvm/bin/clang"
 CLANGXX = "/opt/rocm/llvm/bin/clang++"
 
 
+# the library sources the emulator links, each its own translation unit as in the device build
+SOURCES = ["affx_layout.hip", "affx_decode.hip", "affx_fused.hip", "affx_quant.hip", "affx_grouped.hip",
+           "affx_api.hip", "affx_noalloc.hip", "affx_route.hip", "affx_shared.hip", "affx_fit.hip"]
+
+
 @pytest.fixture(scope="module")
 def emu(tmp_path_factory):
     if not (os.path.exists(CLANGXX) and os.path.exists(CLANG)):
         pytest.skip("clang++ not available")
     d = tmp_path_factory.mktemp("emu")
     san = ["-fsanitize=address", "-fno-omit-frame-pointer", "-g", "-O1"]
-    subprocess.run([CLANG, *san, "-ffp-contract=off", "-fopenmp=libgomp", "-c",
-                    os.path.join(ROOT, "oracle", "oracle.c"), "-o", str(d / "oracle.o")], check=True)
     # -ffp-contract=fast-honor-pragmas with FMA available mirrors the device compiler's default
     # for HIP, so a kernel that needs exact float order has to say so itself (a contract pragma)
-    subprocess.run([CLANGXX, "-std=c++20", *san, "-march=x86-64-v3", "-ffp-contract=fast-honor-pragmas", "-w",
-                    "-I", os.path.join(ROOT, "tests", "cpu_emu"), "-I", os.path.join(ROOT, "affinity_amd", "csrc"),
-                    os.path.join(ROOT, "tests", "cpu_emu", "emu_main.cpp"), str(d / "oracle.o"),
-                    "-o", str(d / "emu_main"), "-lpthread", "-fopenmp=libgomp"], check=True)
+    cxx = [CLANGXX, "-std=c++20", *san, "-march=x86-64-v3", "-ffp-contract=fast-honor-pragmas", "-w",
+           "-I", os.path.join(ROOT, "tests", "cpu_emu"), "-I", os.path.join(ROOT, "affinity_amd", "csrc")]
+    jobs = [[CLANG, *san, "-ffp-contract=off", "-fopenmp=libgomp", "-c",
+             os.path.join(ROOT, "oracle", "oracle.c"), "-o", str(d / "oracle.o")],
+            [*cxx, "-c", os.path.join(ROOT, "tests", "cpu_emu", "emu_main.cpp"), "-o", str(d / "emu_main.o")]]
+    objs = [str(d / "oracle.o"), str(d / "emu_main.o")]
+    for src in SOURCES:
+        o = str(d / (src + ".o"))
+        jobs.append([*cxx, "-x", "c++", "-c", os.path.join(ROOT, "affinity_amd", "csrc", src), "-o", o])
+        objs.append(o)
+    with ThreadPoolExecutor(max_workers=8) as pool:
+        for r in pool.map(lambda cmd: subprocess.run(cmd, capture_output=True, text=True), jobs):
+            assert r.returncode == 0, r.stderr[-4000:]
+    subprocess.run([CLANGXX, *san, *objs, "-o", str(d / "emu_main"), "-lpthread", "-fopenmp=libgomp"], check=True)
     return str(d / "emu_main")
 
 
