@@ -70,7 +70,7 @@ struct FusedArgs {
 // plan. The codebook copies are the kernel's one static LDS array (at address 0, so a table
 // address needs no base add).
 struct FusedLds {
-  uint32_t xq, zero, part, plan, total;
+  uint32_t xq, zero, part, plan, count, total;
 };
 
 __host__ __device__ inline FusedLds fused_lds(uint32_t M) {
@@ -81,7 +81,8 @@ __host__ __device__ inline FusedLds fused_lds(uint32_t M) {
   const uint32_t part_bytes = (uint32_t)kFW * 2u * 16u * M * 4u;  // gate/up [wave][mat][row][tok]
   L.plan = L.part + part_bytes;
   // slot_expert[128] slot_mask[128] rs[12][32] sigma[32] slot_w[128][M]
-  L.total = L.plan + (2u * kPlanRoutes + kFW * 32u + 32u) * 4u + kPlanRoutes * M * 4u;
+  L.count = L.plan + (2u * kPlanRoutes + kFW * 32u + 32u) * 4u + kPlanRoutes * M * 4u;
+  L.total = L.count + 16u;
   return L;
 }
 
@@ -176,6 +177,13 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
 
   AFFX_TRACE_INIT;
   AFFX_TRACE(0);
+  // batch 1: the count of waves whose share of the LDS set-up (plan, activation terms, codebook
+  // copies) is written; it replaces the workgroup barrier before gate/up (step 3)
+  uint32_t* parts_in = reinterpret_cast<uint32_t*>(lds + L.count);
+  if constexpr (SINGLE) {
+    if (tid == 0) *parts_in = 0u;
+    __syncthreads();
+  }
   // ---- 1. the small loads first (routes, then codebook and activation: loads complete in issue
   // order, so waiting for them never waits for the weight stream issued after them); every wave
   // dedupes the routes itself (registers only) so that it can issue its weight loads as soon as
@@ -324,7 +332,8 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   const bool has_down = g < dtiles && wv < NU;
   // the waves that write the SwiGLU output drain their memory counter before the release
   const uint32_t epi_waves = (groups * 16 * M + 63) / 64;
-  load_gu(rounds > 0 ? gu_item(0) : ~0u);
+  // (batch 1 issues them after its share of the LDS set-up, step 3)
+  if constexpr (!SINGLE) load_gu(rounds > 0 ? gu_item(0) : ~0u);
   AFFX_TRACE(13);
   AFFX_TRACE(2);
 
@@ -405,7 +414,27 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   build_lut<KC, kFT, 3, ROT>(lut_s, cbv, tid);
   if (tid < 64) reinterpret_cast<uint32_t*>(zero_l)[tid] = 0u;
   AFFX_TRACEW(1);
-  __syncthreads();  // plan, activation terms and codebook copies visible
+  if constexpr (SINGLE) {
+    // Batch 1: a wave counts its share in, then issues its gate/up weight loads, then waits for
+    // every wave's share. With the loads issued first and a workgroup barrier here, the barrier
+    // waited for the waves still issuing loads (the third wave of each SIMD issues its loads about
+    // 3 us after the first, held by the memory pipeline), and no wave could start on weights that
+    // had arrived. Every wave counts in exactly once, before it waits, so the wait always ends
+    // (the waves of a workgroup are resident together). The release add orders the wave's LDS
+    // writes before its count; the acquire load and fence order the reads of the other waves'
+    // writes after it. (Larger batches issue their loads first and keep the barrier: measured
+    // faster there, where each wave's share of the activation split is three times larger.)
+    __builtin_amdgcn_wave_barrier();
+    if (lane == 0) __hip_atomic_fetch_add(parts_in, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    load_gu(rounds > 0 ? gu_item(0) : ~0u);
+    if (lane == 0)
+      while (__hip_atomic_load(parts_in, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < (uint32_t)kFW)
+        __builtin_amdgcn_s_sleep(1);
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  } else {
+    __syncthreads();  // plan, activation terms and codebook copies visible
+  }
   AFFX_TRACE(1);
 
   // B source of this lane for gate/up: its (token, term) row at this wave's segment
