@@ -97,18 +97,24 @@ __global__ void __launch_bounds__(256) dense_fp8_permute_kernel(const uint8_t* _
 
 // The weights of one wave's share of a 16-row tile, all requested at once: rows row0 .. row0 + 15
 // of W [.. x K], columns k0 .. k0 + 128 STEPS - 1; sa[m] = the tile scale of step m (the rows lie
-// in one 128-row band: uniform).
+// in one 128-row band: uniform). half >= 0: only rows row0 + 8 half .. + 7 are read, the others'
+// A rows are zero.
 template <int STEPS>
 __device__ __forceinline__ void load_a_tile(const uint8_t* __restrict__ W, const uint8_t* __restrict__ S, uint32_t K,
-                                            uint32_t row0, uint32_t k0, v8i (&a)[STEPS], int (&sa)[STEPS]) {
+                                            uint32_t row0, uint32_t k0, v8i (&a)[STEPS], int (&sa)[STEPS],
+                                            int half = -1) {
   const uint32_t lane = threadIdx.x & 63, c = lane & 15, kg = lane >> 4;
   const __amdgpu_buffer_rsrc_t wr =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(W), (short)0, 0x7FFFFFFF, 0x00020000);
   const uint32_t vo = dense_tile_offset(row0 >> 4, k0 >> 7, K) + 16u * lane;
+  const bool mine = half < 0 || (int)(c >> 3) == half;
 #pragma unroll
-  for (int m = 0; m < STEPS; ++m)
-    a[m] = join8(__builtin_amdgcn_raw_buffer_load_b128(wr, vo + 2048u * m, 0, 2),
-                 __builtin_amdgcn_raw_buffer_load_b128(wr, vo + 2048u * m + 1024u, 0, 2));
+  for (int m = 0; m < STEPS; ++m) {
+    a[m] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+    if (mine)
+      a[m] = join8(__builtin_amdgcn_raw_buffer_load_b128(wr, vo + 2048u * m, 0, 2),
+                   __builtin_amdgcn_raw_buffer_load_b128(wr, vo + 2048u * m + 1024u, 0, 2));
+  }
   const uint8_t* srow = S + (uint64_t)(row0 >> 7) * (K >> 7) + (k0 >> 7);
 #pragma unroll
   for (int m = 0; m < STEPS; ++m) sa[m] = __builtin_amdgcn_readfirstlane((int)srow[m]);
@@ -122,14 +128,15 @@ __device__ __forceinline__ float part_terms(const float (&p)[16], uint32_t col) 
   return p[col] + p[col + 1] * 0.0625f + p[col + 2] * 0.00390625f;
 }
 
-// gate/up + SwiGLU: one workgroup per 16 rows of inter, wave w = {gate, up}[w & 1] x K quarter
-// w >> 1 (STEPS = hidden / 512 steps each). The activation's terms are made here, into LDS: each
-// thread holds 8 columns of every token, the token's largest magnitude fixes its exponent (the B
-// scale), three E4M3 terms per element.
+// gate/up + SwiGLU: one workgroup per 8 rows of inter (half of a 16-row tile: twice the
+// workgroups of one per tile, so every CU streams weights; the MFMA rows of the other half are
+// zero), wave w = {gate, up}[w & 1] x K quarter w >> 1 (STEPS = hidden / 512 steps each). The
+// activation's terms are made here, into LDS: each thread holds 8 columns of every token, the
+// token's largest magnitude fixes its exponent (the B scale), three E4M3 terms per element.
 template <int CG, int STEPS>
 __global__ void __launch_bounds__(kSxWaves * 64) shexp_gateup_kernel(SharedArgs A, const float* __restrict__ x,
                                                                      uint64_t xts, uint64_t xds, int vec) {
-  const uint32_t rt = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const uint32_t rt = blockIdx.x >> 1, half = blockIdx.x & 1u, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const uint32_t c = lane & 15, kg = lane >> 4;
   const uint32_t mat = wv & 1u, q = wv >> 1, M = A.m_tokens, H = A.hidden;
   const uint32_t k0 = q * (H / 4u);
@@ -165,7 +172,7 @@ __global__ void __launch_bounds__(kSxWaves * 64) shexp_gateup_kernel(SharedArgs 
   // 2. the weights
   v8i a[STEPS];
   int sa[STEPS];
-  load_a_tile<STEPS>(A.w[mat], A.s[mat], H, rt * 16u, k0, a, sa);
+  load_a_tile<STEPS>(A.w[mat], A.s[mat], H, rt * 16u, k0, a, sa, (int)half);
   __builtin_amdgcn_sched_barrier(0);
   // 3. exponent per token: its largest magnitude times 2^sigma in [128, 256)
 #pragma unroll
@@ -227,7 +234,7 @@ __global__ void __launch_bounds__(kSxWaves * 64) shexp_gateup_kernel(SharedArgs 
 #pragma unroll
     for (int v = 0; v < 4; ++v) part[wv][cg][4 * kg + v][c] = acc[cg][v];
   __syncthreads();
-  if (tid < 16u * M) {
+  if (tid < 16u * M && ((tid & 15u) >> 3) == half) {
     const uint32_t r = tid & 15u, t = tid >> 4, cg = t / 5u, col = (t % 5u) * 3u;
     float g = 0.f, u = 0.f;
     for (uint32_t qq = 0; qq < 4; ++qq) {  // K quarters in order
@@ -754,11 +761,11 @@ int affx_shared_expert_decode(const affx_shared_expert* S, const float* x, uint6
   // token-major rows with 16-byte alignment take 16-byte loads, any other strides element loads
   const int vec = x_ds == 1 && (x_ts % 4) == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
   if (m_tokens <= 5) {
-    launch_gateup<1>(gsteps, dim3(S->inter / 16u), s, A, x, x_ts, x_ds, vec);
+    launch_gateup<1>(gsteps, dim3(S->inter / 8u), s, A, x, x_ts, x_ds, vec);
     if ((rc = check_launch("shexp_gateup_kernel"))) return rc;
     launch_down<1>(dsteps, dim3(S->hidden / 16u), s, A);
   } else {
-    launch_gateup<2>(gsteps, dim3(S->inter / 16u), s, A, x, x_ts, x_ds, vec);
+    launch_gateup<2>(gsteps, dim3(S->inter / 8u), s, A, x, x_ts, x_ds, vec);
     if ((rc = check_launch("shexp_gateup_kernel"))) return rc;
     launch_down<2>(dsteps, dim3(S->hidden / 16u), s, A);
   }
