@@ -118,3 +118,35 @@ def test_project_pack_unpack_match_oracle(cbk, orc, c1_codebook):
     np.testing.assert_array_equal(packed, orc.pack_codebook(cb))
     un = cbk.unpack_codebook_e4m3_quads(torch.from_numpy(c1_codebook.view(np.int32)).cuda()).cpu().numpy().reshape(-1)
     np.testing.assert_array_equal(bits(un), bits(orc.unpack_codebook(c1_codebook)))
+
+
+def test_producer_declines_and_limits(cbk):
+    """The C-ABI's refusals and the collection's cap: weights are declined, a misaligned sample
+    pointer and a short workspace are argument errors, and a collection into a buffer smaller
+    than its count writes only `cap` floats while reporting the full count."""
+    import ctypes as C
+    from affinity_amd._lib import AFFX_DECLINED, AFFX_ERR_ARG, lib
+    L = lib()
+    s = torch.rand(4096, device="cuda")
+    cb = torch.empty(8192, device="cuda")
+    ws = torch.empty(int(L.affx_fit_codebook_workspace_size(4096)) + 256, dtype=torch.uint8, device="cuda")
+    wsp = ws.data_ptr() + (-ws.data_ptr()) % 256
+    n = int(L.affx_fit_codebook_workspace_size(4096))
+    stream = torch.cuda.current_stream().cuda_stream
+    assert L.affx_fit_codebook(s.data_ptr(), 4096, s.data_ptr(), 5, 1, 0, cb.data_ptr(), wsp, n, stream) == AFFX_DECLINED
+    assert L.affx_fit_codebook(s.data_ptr() + 4, 4092, None, 5, 1, 0, cb.data_ptr(), wsp, n, stream) == AFFX_ERR_ARG
+    assert L.affx_fit_codebook(s.data_ptr(), 4096, None, 5, 1, 0, cb.data_ptr(), wsp, n - 256, stream) == AFFX_ERR_ARG
+    w = torch.randn(64, 256, device="cuda") * 0.02
+    bound = int(L.affx_collect_samples_bound(64, 256, 1 << 20))
+    assert bound == 64 * 256
+    out = torch.full((bound,), -7.0, device="cuda")
+    n_out = torch.zeros(1, dtype=torch.int64, device="cuda")
+    cws = torch.empty(int(L.affx_collect_samples_workspace_size(64, 256, 1 << 20)), dtype=torch.uint8, device="cuda")
+    cap = 1000   # not a multiple of 16: the block that would cross it is not written
+    assert L.affx_collect_samples(w.data_ptr(), 64, 256, 1 << 20, out.data_ptr(), cap, n_out.data_ptr(),
+                                  cws.data_ptr(), cws.numel(), stream) == 0
+    full = cbk.collect_normalized_samples(w, 1 << 20)
+    assert int(n_out.item()) == full.numel() == 64 * 256
+    got = out.cpu().numpy()
+    np.testing.assert_array_equal(bits(got[:992]), bits(full.cpu().numpy()[:992]))
+    assert (got[992:] == -7.0).all()
