@@ -285,6 +285,7 @@ def main() -> int:
 
     # ---- the codebook producer: the config-1 recipe fitted on the GPU ----------------------------
     producer_exact = None
+    producer_sample = None
     if args.only == "all":
         import affinity_amd.codebook as cbk
         mats = [ax.gen_normal(1000, I * H, 0.02).view(I, H), ax.gen_normal(1001, I * H, 0.02).view(I, H),
@@ -305,6 +306,16 @@ def main() -> int:
         ms_fit = st.elapsed_time(en)
         seq_draws, passes = fitter.stats()
         producer_exact = bool(np.array_equal(packed.cpu().numpy().view(np.uint32), cb_packed))
+        # a bounded sample of the same samples for the CPU comparison (the CPU baseline leg)
+        sub = samples[: 1 << 16].contiguous()
+        fit_sub = cbk.CodebookFit(sub.numel())
+        fit_sub.fit(sub, 50, 1)
+        torch.cuda.synchronize()
+        st.record()
+        cb_sub = fit_sub.fit(sub, 50, 1)
+        en.record()
+        torch.cuda.synchronize()
+        producer_sample = (sub.cpu().numpy(), cb_sub.cpu().numpy().reshape(-1), st.elapsed_time(en))
         log(f"config-1 codebook on the GPU: collect {ms_collect:.1f} ms, fit + project + pack {ms_fit:.1f} ms, "
             f"{passes} Lloyd passes, {seq_draws} sequential draws, equal to the reference's: {producer_exact}")
         result["producer"] = {"workload": "config-1 codebook: 3 x 2^19 samples, fit_codebook(50, seed 1), "
@@ -312,7 +323,7 @@ def main() -> int:
                               "collect_ms": round(ms_collect, 2), "fit_project_pack_ms": round(ms_fit, 2),
                               "lloyd_passes": passes, "sequential_draws": seq_draws,
                               "bit_exact_vs_reference": producer_exact}
-        del mats, samples, fitter, cbf, packed
+        del mats, samples, fitter, cbf, packed, sub, fit_sub, cb_sub
 
     # ---- CPU baseline (and the checker of the GPU results) ----------------------------------------
     if not args.no_cpu_baseline:
@@ -325,6 +336,8 @@ def main() -> int:
             sel_np, w_np, xb, yp = prefill
             toks, _, _ = synthetic.prefill_sample(sel_np, E)
             gpu["c4"] = (sel_np, w_np, xb.float().cpu().numpy()[toks], yp.cpu().numpy()[toks], toks)
+        if producer_sample is not None:
+            gpu["fit"] = producer_sample
         result["cpu_baseline"], result["parity"] = cpu_baseline(ax, cont, gpu, L)
         # every GPU result checked against the CPU path must be within the path's 1e-3 (the dequant
         # bit-exact): a number measured on a wrong result is not a measurement
@@ -459,6 +472,17 @@ def cpu_baseline(ax, cont, gpu, L):
         parity["c4_sample_rel_l2"] = rel_l2(yg, yc)
         parity["c4_sample_worst_token_rel_l2"] = max(rel_l2(yg[i], yc[i]) for i in range(len(toks)))
         msg += f"; C4 {len(toks)} tokens {t_c4:.1f} s"
+    if "fit" in gpu:
+        # the codebook fit on 2^16 of the config-1 samples (50 iterations, seed 1), one run
+        fs, cb_gpu, ms_gpu = gpu["fit"]
+        t0 = time.perf_counter()
+        cb_cpu = lib.fit_codebook(fs, 50, 1, project=False) if kind == "reference" else lib.fit_codebook(fs, 50, 1)
+        t_fit = time.perf_counter() - t0
+        out["producer"] = {"sample": f"fit_codebook on {fs.size} of the config-1 samples, 50 iterations, seed 1",
+                           "cpu_s": round(t_fit, 2), "gpu_ms": round(ms_gpu, 2),
+                           "cpu_threads": 1 if kind == "reference" else n_all}
+        parity["fit_sample_bit_exact"] = bool(np.array_equal(cb_cpu.view(np.uint32), cb_gpu.view(np.uint32)))
+        msg += f"; fit of {fs.size} samples {t_fit:.1f} s (GPU {ms_gpu:.1f} ms)"
     parity = {k: (round(v, 9) if isinstance(v, float) else v) for k, v in parity.items()}
     log(msg)
     log(f"parity vs the CPU path: {parity}")
