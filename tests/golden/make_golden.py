@@ -21,6 +21,9 @@ Fixtures (data only: inputs and the reference's outputs):
   scalars.npz       E4M3 table, bf16 rounding cases, swiglu cases
   route.npz         the engine router (route_topk): logits and bias cases with the chosen
                     experts and weights
+  fit_large.npz     a codebook fit at aff-quantize's scale: 8 matrices (seeds 3000-3007, 2048x4096
+                    and 4096x2048 alternating, bf16 0.02 N(0,1)), 2^19 samples each, the raw
+                    fit_codebook(50, seed 1) (written by `make_golden.py fit_large`)
   step.npz          the step after the routed experts: FP8 dense matvecs (matvec_dense over E4M3
                     weights with UE8M0 128x128 tile scales, ragged shapes included), the E8M0
                     table, and hc_expand cases for n_hc 1, 2, 4, 8
@@ -158,6 +161,21 @@ def make_small(O, R, cb):
     np.savez_compressed(os.path.join(OUT, "small.npz"), **cases)
 
 
+def make_fit_large(O, R):
+    t0 = time.time()
+    parts = []
+    for i in range(8):
+        rows, cols = (I, H) if i % 2 == 0 else (H, I)
+        w = O.normal_bf16(3000 + i, rows * cols, 0.02).reshape(rows, cols)
+        parts.append(R.collect_samples(w, 1 << 19))
+    s = np.concatenate(parts)
+    print(f"fit_large: {s.size} samples", flush=True)
+    cb = R.fit_codebook(s, 50, 1, project=False)
+    np.savez_compressed(os.path.join(OUT, "fit_large.npz"), cb_raw=cb, n_samples=np.array(s.size),
+                        samples_sha256=np.array(sha(s)))
+    print(f"fit_large done in {time.time() - t0:.0f} s", flush=True)
+
+
 def make_scalars(O, R):
     e4 = np.array([R.e4m3_to_float(b) for b in range(256)], np.float32)
     rng = np.random.default_rng(7)
@@ -238,7 +256,9 @@ def main():
 
 
 if __name__ == "__main__":
-    if len(sys.argv) > 1 and sys.argv[1] == "route":     # only the router fixture
+    if len(sys.argv) > 1 and sys.argv[1] == "fit_large":  # only the large-fit fixture
+        make_fit_large(load_oracle(), load_ref())
+    elif len(sys.argv) > 1 and sys.argv[1] == "route":     # only the router fixture
         make_route(load_ref())
     elif len(sys.argv) > 1 and sys.argv[1] == "step":    # only the step-after fixture
         make_step(load_ref())

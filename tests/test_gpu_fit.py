@@ -150,3 +150,26 @@ def test_producer_declines_and_limits(cbk):
     got = out.cpu().numpy()
     np.testing.assert_array_equal(bits(got[:992]), bits(full.cpu().numpy()[:992]))
     assert (got[992:] == -7.0).all()
+
+
+def test_fit_at_quantizer_scale_matches_reference_fixture(cbk):
+    """aff-quantize's scale (tools/aff_quantize.cpp:402-430 samples 24 matrices): 8 matrices of
+    2^19 samples each, 4.2 M samples, fitted with fit_codebook(50, seed 1), against the raw
+    codebook the compiled reference wrote for the same samples (tests/golden/fit_large.npz)."""
+    import hashlib
+    import affinity_amd.experts as ax
+    f = np.load(os.path.join(GOLDEN, "fit_large.npz"))
+    parts = []
+    for i in range(8):
+        rows, cols = (I, H) if i % 2 == 0 else (H, I)
+        w = ax.gen_normal(3000 + i, rows * cols, 0.02).view(rows, cols)
+        parts.append(cbk.collect_normalized_samples(w, 1 << 19))
+        del w
+    s = torch.cat(parts)
+    assert s.numel() == int(f["n_samples"])
+    assert hashlib.sha256(s.cpu().numpy().tobytes()).hexdigest() == str(f["samples_sha256"])
+    fit = cbk.CodebookFit(s.numel())
+    cb = fit.fit(s, 50, 1)
+    seq, passes = fit.stats()
+    print(f"quantizer-scale fit: {seq} sequential draws, {passes} Lloyd passes")
+    np.testing.assert_array_equal(bits(cb.cpu().numpy().reshape(-1)), bits(f["cb_raw"]))
