@@ -17,6 +17,9 @@ synthetic.py):
              per launch (6 x 9,060,352 B) over its average duration, timed with HIP events on the
              launch stream (the C5 graph holds only these launches); traffic = HBM bytes per
              launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary.
+  shared_expert  the FP8 shared expert that follows the routed experts (hidden 4096, inter 2048,
+             one per layer, random E4M3 weights): batch-1 decode over the layers in a graph (GB/s
+             of its 25 MB of weights) and one 4096-token bf16 chunk (TFLOP/s).
   producer   the config-1 codebook recipe (3 x 2^19 samples of the config-1 matrices, the joint
              fit, projection, packing) on the GPU, timed, and compared with the reference's packed
              codebook bit for bit.
@@ -48,6 +51,7 @@ STRIDE = 9_060_352
 HBM_PEAK = 8.0e12               # B/s, MI355X
 BF16_PEAK = 2.5e15              # FLOP/s dense, MI355X
 FLOP_PER_SLOT = 2 * (2 * I * H + H * I)
+S_SHEXP = 17                    # seed of the synthetic shared-expert weights
 
 
 def log(msg: str) -> None:
@@ -283,6 +287,73 @@ def main() -> int:
                                                "max": int(counts.max())}}
         prefill = (sel_np, w_np, xb, yp)
 
+    # ---- the step after: the FP8 shared expert (V4-Flash: hidden 4096, inter 2048) ---------------
+    # one expert per layer, L layers resident (1.1 GB: none is served from the 256 MB last-level
+    # cache when the next token comes), batch-1 decode in a graph like C5, then one 4096-token chunk
+    shared = None
+    if args.only == "all":
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(S_SHEXP)
+
+        def fp8(rows, cols):
+            w = torch.randint(0, 256, (rows, cols), dtype=torch.uint8, device="cuda", generator=gen)
+            w[(w & 0x7F) == 0x7F] ^= 1          # no NaN codes (the reference decodes them as NaN)
+            s = torch.randint(116, 124, (rows // 128, cols // 128), dtype=torch.uint8, device="cuda",
+                              generator=gen)
+            return w, s
+
+        sh_mats0 = None
+        shexps = []
+        for l in range(L):
+            mats = [fp8(I, H), fp8(I, H), fp8(H, I)]
+            if l == 0:
+                sh_mats0 = [(w.cpu().numpy(), s.cpu().numpy()) for w, s in mats]
+            shexps.append(ax.SharedExpert(*[a for m in mats for a in m]))
+            del mats
+        sh_bytes = 3 * I * H + 3 * (I // 128) * (H // 128)
+        ys = torch.zeros((L, H), device="cuda")
+        sws = torch.empty(int(lib().affx_shared_decode_workspace_size(1, H, I)), dtype=torch.uint8, device="cuda")
+
+        def shared_step():
+            s = torch.cuda.current_stream().cuda_stream
+            for l in range(L):
+                check(lib().affx_shared_expert_decode(C.byref(shexps[l].abi), x1.data_ptr(), H, 1, 1,
+                                                      ys[l].data_ptr(), H, 1, 0, sws.data_ptr(), sws.numel(), s),
+                      "shared_expert_decode")
+            return ys
+
+        ms_sh, _, _ = time_graph(torch, shared_step, args.steps, args.warmup)
+        gbs_sh = L * sh_bytes / (ms_sh * 1e-3) / 1e9
+        T = 4096
+        xs_b = ax.gen_normal(S_X, T * H, 1.0).view(T, H).to(torch.bfloat16)
+        yb = torch.zeros((T, H), device="cuda")
+        shexps[0].batch(xs_b, yb, accumulate=False)
+        torch.cuda.synchronize()
+        st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        st.record()
+        for l in range(args.prefill_steps):
+            shexps[l % L].batch(xs_b, yb, accumulate=False)
+        en.record()
+        torch.cuda.synchronize()
+        ms_shb = st.elapsed_time(en) / args.prefill_steps
+        shexps[0].batch(xs_b, yb, accumulate=False)   # layer 0's result for the parity check
+        torch.cuda.synchronize()
+        tf_shb = T * 2 * 3 * I * H / (ms_shb * 1e-3) / 1e12
+        log(f"shared expert: decode {ms_sh * 1e3 / L:.2f} us/layer -> {gbs_sh:.0f} GB/s "
+            f"({100 * gbs_sh * 1e9 / HBM_PEAK:.1f}% of HBM peak); {T}-token chunk {ms_shb:.3f} ms -> "
+            f"{tf_shb:.1f} TFLOP/s")
+        result["shared_expert"] = {
+            "workload": f"FP8 shared expert (hidden {H}, inter {I}, UE8M0 128x128 tile scales), one per layer "
+                        f"x {L} layers; batch-1 decode in a graph, and one {T}-token bf16 chunk",
+            "decode_us_per_layer": round(ms_sh * 1e3 / L, 3), "decode_gb_per_s": round(gbs_sh, 1),
+            "decode_hbm_fraction": round(gbs_sh * 1e9 / HBM_PEAK, 4), "bytes_per_layer": sh_bytes,
+            "batch_ms": round(ms_shb, 4), "batch_tflop_per_s": round(tf_shb, 1),
+            "batch_frac_of_bf16_peak": round(tf_shb * 1e12 / BF16_PEAK, 4)}
+        toks = np.array([0, 1, 1000, 2047, 4095])
+        shared = (sh_mats0, x1.cpu().numpy()[0], ys[0].cpu().numpy(), xs_b.float().cpu().numpy()[toks],
+                  yb.cpu().numpy()[toks])
+        del shexps, xs_b, yb, ys, sws
+
     # ---- the codebook producer: the config-1 recipe fitted on the GPU ----------------------------
     producer_exact = None
     producer_sample = None
@@ -338,6 +409,8 @@ def main() -> int:
             gpu["c4"] = (sel_np, w_np, xb.float().cpu().numpy()[toks], yp.cpu().numpy()[toks], toks)
         if producer_sample is not None:
             gpu["fit"] = producer_sample
+        if shared is not None:
+            gpu["shared"] = shared
         result["cpu_baseline"], result["parity"] = cpu_baseline(ax, cont, gpu, L)
         # every GPU result checked against the CPU path must be within the path's 1e-3 (the dequant
         # bit-exact): a number measured on a wrong result is not a measurement
@@ -483,6 +556,22 @@ def cpu_baseline(ax, cont, gpu, L):
                            "cpu_threads": 1 if kind == "reference" else n_all}
         parity["fit_sample_bit_exact"] = bool(np.array_equal(cb_cpu.view(np.uint32), cb_gpu.view(np.uint32)))
         msg += f"; fit of {fs.size} samples {t_fit:.1f} s (GPU {ms_gpu:.1f} ms)"
+    if "shared" in gpu:
+        # the shared expert of layer 0: the host composition (src/engine/model.cpp:1214-1222) over
+        # the reference's FP8 matvec, for the decode token and five tokens of the 4096-token chunk
+        ((wg, sg), (wu, su), (wd, sd)), xd, yd, xb, yb = gpu["shared"]
+
+        def shexp(x):
+            g, u = lib.matvec_fp8(wg, sg, x), lib.matvec_fp8(wu, su, x)
+            return lib.matvec_fp8(wd, sd, lib.swiglu(g, u, 10.0))
+
+        t_sh, y_sh = timed(lambda: shexp(xd), 3)
+        out["shared_expert"] = {"sample": "layer 0's shared expert on the decode token (three FP8 matvecs)",
+                                "ms_per_token_layer": round(t_sh * 1e3, 2),
+                                "gb_per_s": round(3 * I * H / t_sh / 1e9, 3)}
+        parity["shared_expert_decode_rel_l2"] = rel_l2(yd, y_sh)
+        parity["shared_expert_batch_sample_rel_l2"] = rel_l2(yb, np.stack([shexp(x) for x in xb]))
+        msg += f"; shared expert {t_sh * 1e3:.1f} ms per token-layer"
     parity = {k: (round(v, 9) if isinstance(v, float) else v) for k, v in parity.items()}
     log(msg)
     log(f"parity vs the CPU path: {parity}")
