@@ -13,7 +13,7 @@
 //
 // Decode, 1..8 tokens (DenseOps::shexp, src/engine/model.h:314-319; the reference's device form
 // mv_gate_up_swiglu_hip + launch_mv, src/gpu/dense_gpu.hip:2030-2116), two launches:
-//   shexp_gateup     one workgroup per 16 rows of inter; 8 waves = {gate, up} x 4 K quarters, every
+//   shexp_gateup     one workgroup per 8 rows of inter; 8 waves = {gate, up} x 4 K quarters, every
 //                    weight load issued at the start; meanwhile the workgroup turns x into three
 //                    E4M3 terms per element in LDS (one exponent per token); fixed-order sum of the
 //                    quarters, SwiGLU with the clamp, three E4M3 terms out
@@ -98,7 +98,9 @@ __global__ void __launch_bounds__(256) dense_fp8_permute_kernel(const uint8_t* _
 // The weights of one wave's share of a 16-row tile, all requested at once: rows row0 .. row0 + 15
 // of W [.. x K], columns k0 .. k0 + 128 STEPS - 1; sa[m] = the tile scale of step m (the rows lie
 // in one 128-row band: uniform). half >= 0: only rows row0 + 8 half .. + 7 are read, the others'
-// A rows are zero.
+// A rows are zero. The scales are requested before the weights: loads complete in issue order, so
+// their readfirstlane waits for them alone, not for the weights behind them (issued after the
+// weights, it made the whole wave wait for every weight before its activation work).
 template <int STEPS>
 __device__ __forceinline__ void load_a_tile(const uint8_t* __restrict__ W, const uint8_t* __restrict__ S, uint32_t K,
                                             uint32_t row0, uint32_t k0, v8i (&a)[STEPS], int (&sa)[STEPS],
@@ -106,18 +108,27 @@ __device__ __forceinline__ void load_a_tile(const uint8_t* __restrict__ W, const
   const uint32_t lane = threadIdx.x & 63, c = lane & 15, kg = lane >> 4;
   const __amdgpu_buffer_rsrc_t wr =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(W), (short)0, 0x7FFFFFFF, 0x00020000);
-  const uint32_t vo = dense_tile_offset(row0 >> 4, k0 >> 7, K) + 16u * lane;
+  // lanes outside the half take an offset past the buffer's range: the load returns zero and
+  // touches no memory, with no branch around it (a branch made the compiler wait for every load
+  // at its join)
   const bool mine = half < 0 || (int)(c >> 3) == half;
+  const uint32_t vo = mine ? dense_tile_offset(row0 >> 4, k0 >> 7, K) + 16u * lane : 0x80000000u;
+  // (one byte load each: byte reads of an ordinary pointer are merged into one wide load whose
+  // byte extraction then waits for it before the weights are requested)
+  const __amdgpu_buffer_rsrc_t sr =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(S), (short)0, 0x7FFFFFFF, 0x00020000);
+  const uint32_t so = (row0 >> 7) * (K >> 7) + (k0 >> 7);
+  int sv[STEPS];
 #pragma unroll
-  for (int m = 0; m < STEPS; ++m) {
-    a[m] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
-    if (mine)
-      a[m] = join8(__builtin_amdgcn_raw_buffer_load_b128(wr, vo + 2048u * m, 0, 2),
-                   __builtin_amdgcn_raw_buffer_load_b128(wr, vo + 2048u * m + 1024u, 0, 2));
-  }
-  const uint8_t* srow = S + (uint64_t)(row0 >> 7) * (K >> 7) + (k0 >> 7);
+  for (int m = 0; m < STEPS; ++m) sv[m] = (int)__builtin_amdgcn_raw_buffer_load_b8(sr, so + (uint32_t)m, 0, 0);
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int m = 0; m < STEPS; ++m) sa[m] = __builtin_amdgcn_readfirstlane((int)srow[m]);
+  for (int m = 0; m < STEPS; ++m)
+    a[m] = join8(__builtin_amdgcn_raw_buffer_load_b128(wr, vo + 2048u * m, 0, 2),
+                 __builtin_amdgcn_raw_buffer_load_b128(wr, vo + 2048u * m + 1024u, 0, 2));
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int m = 0; m < STEPS; ++m) sa[m] = __builtin_amdgcn_readfirstlane(sv[m]);
 }
 
 // Column c of B column group cg: token 5 cg + c / 3, term c % 3 (column 15 unused).
@@ -133,40 +144,46 @@ __device__ __forceinline__ float part_terms(const float (&p)[16], uint32_t col) 
 // zero), wave w = {gate, up}[w & 1] x K quarter w >> 1 (STEPS = hidden / 512 steps each). The
 // activation's terms are made here, into LDS: each thread holds 8 columns of every token, the
 // token's largest magnitude fixes its exponent (the B scale), three E4M3 terms per element.
-template <int CG, int STEPS>
+template <int CG, int STEPS, bool VEC, int TOK>
 __global__ void __launch_bounds__(kSxWaves * 64) shexp_gateup_kernel(SharedArgs A, const float* __restrict__ x,
-                                                                     uint64_t xts, uint64_t xds, int vec) {
-  const uint32_t rt = blockIdx.x >> 1, half = blockIdx.x & 1u, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+                                                                     uint64_t xts, uint64_t xds) {
+  const uint32_t rt = blockIdx.x >> 1, half = blockIdx.x & 1u, tid = threadIdx.x, lane = tid & 63;
+  // the wave index in a scalar register: the weight and scale pointers it selects stay scalar (a
+  // vector index made the compiler fetch them with vector loads and wrap every weight load in a
+  // loop over the distinct buffer descriptors)
+  const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t c = lane & 15, kg = lane >> 4;
   const uint32_t mat = wv & 1u, q = wv >> 1, M = A.m_tokens, H = A.hidden;
   const uint32_t k0 = q * (H / 4u);
-  __shared__ __align__(16) uint8_t xq_l[kMaxTok * kTerms * 4096];
+  __shared__ __align__(16) uint8_t xq_l[TOK * kTerms * 4096];
   __shared__ float part[kSxWaves][CG][16][16];
   __shared__ float red[kSxWaves][kMaxTok];
   // 1. the activation (small, in the cache) first: loads complete in issue order, so the wait for
-  // it does not wait for the weights issued after it
+  // it does not wait for the weights issued after it. The loads are unconditional (tokens past M
+  // and columns past H read token 0 and column 0, and are zeroed at their use): a load under a
+  // branch made the compiler wait for it at the join, before the weights were requested. TOK is
+  // the most tokens the launch holds (1 for batch 1: every workgroup reads the whole activation,
+  // so padding tokens would multiply that traffic).
+  static_assert(TOK <= 5 * CG && TOK <= kMaxTok, "");
   const uint32_t h0 = 8u * tid;
   const bool mine = h0 < H;
+  const uint32_t hl = mine ? h0 : 0u;
   float xv[kMaxTok][8];
 #pragma unroll
-  for (int t = 0; t < kMaxTok; ++t)
+  for (int t = 0; t < kMaxTok; ++t) {
+    const uint64_t tt = (uint32_t)t < M ? (uint32_t)t : 0u;
+    if (t >= TOK) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) xv[t][i] = 0.f;
-  if (vec) {  // token-major rows, 16-byte aligned
+      for (int i = 0; i < 8; ++i) xv[t][i] = 0.f;
+    } else if constexpr (VEC) {  // token-major rows, 16-byte aligned
+      const float4 v0 = *reinterpret_cast<const float4*>(x + tt * xts + hl);
+      const float4 v1 = *reinterpret_cast<const float4*>(x + tt * xts + hl + 4);
+      xv[t][0] = v0.x; xv[t][1] = v0.y; xv[t][2] = v0.z; xv[t][3] = v0.w;
+      xv[t][4] = v1.x; xv[t][5] = v1.y; xv[t][6] = v1.z; xv[t][7] = v1.w;
+    } else {
 #pragma unroll
-    for (int t = 0; t < kMaxTok; ++t)
-      if ((uint32_t)t < M && mine) {
-        const float4 v0 = *reinterpret_cast<const float4*>(x + t * xts + h0);
-        const float4 v1 = *reinterpret_cast<const float4*>(x + t * xts + h0 + 4);
-        xv[t][0] = v0.x; xv[t][1] = v0.y; xv[t][2] = v0.z; xv[t][3] = v0.w;
-        xv[t][4] = v1.x; xv[t][5] = v1.y; xv[t][6] = v1.z; xv[t][7] = v1.w;
-      }
-  } else {
-#pragma unroll
-    for (int t = 0; t < kMaxTok; ++t)
-      if ((uint32_t)t < M && mine)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) xv[t][i] = x[t * xts + (h0 + i) * xds];
+      for (int i = 0; i < 8; ++i) xv[t][i] = x[tt * xts + (hl + i) * xds];
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
   // 2. the weights
@@ -176,7 +193,12 @@ __global__ void __launch_bounds__(kSxWaves * 64) shexp_gateup_kernel(SharedArgs 
   __builtin_amdgcn_sched_barrier(0);
   // 3. exponent per token: its largest magnitude times 2^sigma in [128, 256)
 #pragma unroll
-  for (int t = 0; t < kMaxTok; ++t) {
+  for (int t = 0; t < TOK; ++t)
+    if (!((uint32_t)t < M && mine))
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xv[t][i] = 0.f;
+#pragma unroll
+  for (int t = 0; t < TOK; ++t) {
     float mx = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(xv[t][i]));
@@ -188,8 +210,9 @@ __global__ void __launch_bounds__(kSxWaves * 64) shexp_gateup_kernel(SharedArgs 
 #pragma unroll
   for (int t = 0; t < kMaxTok; ++t) {
     float mx = 0.f;
+    if (t < TOK)
 #pragma unroll
-    for (int w = 0; w < kSxWaves; ++w) mx = fmaxf(mx, red[w][t]);
+      for (int w = 0; w < kSxWaves; ++w) mx = fmaxf(mx, red[w][t]);
     sig[t] = mx > 0.f ? 7 - ilogbf(mx) : 0;
   }
   // 4. three E4M3 terms of every element into LDS, [token][term][column]
@@ -261,16 +284,18 @@ __global__ void __launch_bounds__(kSxWaves * 64) shexp_down_kernel(SharedArgs A)
   const uint32_t k0 = wv * (A.inter / 8u);
   __shared__ float part[kSxWaves][CG][16][16];
   v8i b[STEPS][CG];
+  // columns without a token read past the buffer's range (zero, no memory touched): a select on
+  // the loaded values would make the wave wait for them before it requests the weights
+  const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(A.aq, (short)0, 0x7FFFFFFF, 0x00020000);
 #pragma unroll
   for (int cg = 0; cg < CG; ++cg) {
     const uint32_t t = bcol_token(cg, c);
     const bool ok = c < 15u && t < M;
-    const uint8_t* p = A.aq + (ok ? (uint64_t)(t * kTerms + c % 3u) * A.inter : 0u) + k0 + 16u * kg;
+    const uint32_t bo = ok ? (t * kTerms + c % 3u) * A.inter + k0 + 16u * kg : 0x80000000u;
 #pragma unroll
-    for (int m = 0; m < STEPS; ++m) {
-      b[m][cg] = join8(*reinterpret_cast<const u32x4*>(p + 128 * m), *reinterpret_cast<const u32x4*>(p + 128 * m + 64));
-      if (!ok) b[m][cg] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
-    }
+    for (int m = 0; m < STEPS; ++m)
+      b[m][cg] = join8(__builtin_amdgcn_raw_buffer_load_b128(br, bo + 128u * m, 0, 0),
+                       __builtin_amdgcn_raw_buffer_load_b128(br, bo + 128u * m + 64u, 0, 0));
   }
   __builtin_amdgcn_sched_barrier(0);
   v8i a[STEPS];
@@ -686,16 +711,26 @@ int shared_check(const affx_shared_expert* S, const char* what, uint32_t max_hid
   return AFFX_OK;
 }
 
-template <int CG>
-void launch_gateup(uint32_t steps, dim3 g, hipStream_t s, const SharedArgs& A, const float* x, uint64_t xts,
-                   uint64_t xds, int vec) {
+template <int CG, bool VEC, int TOK>
+void launch_gateup_form(uint32_t steps, dim3 g, hipStream_t s, const SharedArgs& A, const float* x, uint64_t xts,
+                        uint64_t xds) {
   const dim3 b(kSxWaves * 64);
   switch (steps) {
-    case 2: hipLaunchKernelGGL((shexp_gateup_kernel<CG, 2>), g, b, 0, s, A, x, xts, xds, vec); break;
-    case 4: hipLaunchKernelGGL((shexp_gateup_kernel<CG, 4>), g, b, 0, s, A, x, xts, xds, vec); break;
-    case 6: hipLaunchKernelGGL((shexp_gateup_kernel<CG, 6>), g, b, 0, s, A, x, xts, xds, vec); break;
-    default: hipLaunchKernelGGL((shexp_gateup_kernel<CG, 8>), g, b, 0, s, A, x, xts, xds, vec); break;
+    case 2: hipLaunchKernelGGL((shexp_gateup_kernel<CG, 2, VEC, TOK>), g, b, 0, s, A, x, xts, xds); break;
+    case 4: hipLaunchKernelGGL((shexp_gateup_kernel<CG, 4, VEC, TOK>), g, b, 0, s, A, x, xts, xds); break;
+    case 6: hipLaunchKernelGGL((shexp_gateup_kernel<CG, 6, VEC, TOK>), g, b, 0, s, A, x, xts, xds); break;
+    default: hipLaunchKernelGGL((shexp_gateup_kernel<CG, 8, VEC, TOK>), g, b, 0, s, A, x, xts, xds); break;
   }
+}
+
+// (a kernel per activation form: the two load shapes under one runtime branch share a join)
+template <int CG, int TOK>
+void launch_gateup(uint32_t steps, dim3 g, hipStream_t s, const SharedArgs& A, const float* x, uint64_t xts,
+                   uint64_t xds, int vec) {
+  if (vec)
+    launch_gateup_form<CG, true, TOK>(steps, g, s, A, x, xts, xds);
+  else
+    launch_gateup_form<CG, false, TOK>(steps, g, s, A, x, xts, xds);
 }
 
 template <int CG>
@@ -761,11 +796,14 @@ int affx_shared_expert_decode(const affx_shared_expert* S, const float* x, uint6
   // token-major rows with 16-byte alignment take 16-byte loads, any other strides element loads
   const int vec = x_ds == 1 && (x_ts % 4) == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
   if (m_tokens <= 5) {
-    launch_gateup<1>(gsteps, dim3(S->inter / 8u), s, A, x, x_ts, x_ds, vec);
+    if (m_tokens == 1)
+      launch_gateup<1, 1>(gsteps, dim3(S->inter / 8u), s, A, x, x_ts, x_ds, vec);
+    else
+      launch_gateup<1, 5>(gsteps, dim3(S->inter / 8u), s, A, x, x_ts, x_ds, vec);
     if ((rc = check_launch("shexp_gateup_kernel"))) return rc;
     launch_down<1>(dsteps, dim3(S->hidden / 16u), s, A);
   } else {
-    launch_gateup<2>(gsteps, dim3(S->inter / 8u), s, A, x, x_ts, x_ds, vec);
+    launch_gateup<2, kMaxTok>(gsteps, dim3(S->inter / 8u), s, A, x, x_ts, x_ds, vec);
     if ((rc = check_launch("shexp_gateup_kernel"))) return rc;
     launch_down<2>(dsteps, dim3(S->hidden / 16u), s, A);
   }

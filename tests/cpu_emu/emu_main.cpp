@@ -403,23 +403,29 @@ int run_shared(int argc, char** argv) {
   S.inter = I;
   S.swiglu_limit = 10.0f;
   bool ok = true;
-  // decode: M tokens, accumulated into a y that already holds something (the routed sum)
-  {
-    std::vector<float> x((size_t)M * H), y0((size_t)M * H), y, yref;
+  // decode: M tokens, accumulated into a y that already holds something (the routed sum); also one
+  // token (its own instantiation) and three tokens read dim-major (the strided form)
+  for (const uint32_t Md : {1u, 3u, M}) {
+    const bool dim_major = Md == 3;
+    std::vector<float> x((size_t)Md * H), xt((size_t)Md * H), y0((size_t)Md * H), y, yref;
     for (auto& v : x) v = nd(rng);
     for (auto& v : y0) v = 0.01f * nd(rng);
+    for (uint32_t t = 0; t < Md; ++t)
+      for (uint32_t h = 0; h < H; ++h) xt[(size_t)h * Md + t] = x[(size_t)t * H + h];
     y = y0;
     yref = y0;
-    std::vector<uint8_t> ws(affx_shared_decode_workspace_size(M, H, I));
-    const int rc = affx_shared_expert_decode(&S, x.data(), H, 1, M, y.data(), H, 1, 1, ws.data(), ws.size(), nullptr);
-    for (uint32_t t = 0; t < M; ++t)
+    std::vector<uint8_t> ws(affx_shared_decode_workspace_size(Md, H, I));
+    const int rc = dim_major
+        ? affx_shared_expert_decode(&S, xt.data(), 1, Md, Md, y.data(), H, 1, 1, ws.data(), ws.size(), nullptr)
+        : affx_shared_expert_decode(&S, x.data(), H, 1, Md, y.data(), H, 1, 1, ws.data(), ws.size(), nullptr);
+    for (uint32_t t = 0; t < Md; ++t)
       orc_shared_expert(w[0].data(), sc[0].data(), w[1].data(), sc[1].data(), w[2].data(), sc[2].data(), H, I, 10.0f,
                         x.data() + (size_t)t * H, yref.data() + (size_t)t * H);
     // the shared expert's own contribution, compared on its own
     std::vector<float> d(y.size()), dref(y.size());
     for (size_t i = 0; i < y.size(); ++i) { d[i] = y[i] - y0[i]; dref[i] = yref[i] - y0[i]; }
     const double e = rel_l2(d, dref);
-    printf("shared decode M=%u: rc=%d rel_l2=%.3e\n", M, rc, e);
+    printf("shared decode M=%u%s: rc=%d rel_l2=%.3e\n", Md, dim_major ? " (dim-major)" : "", rc, e);
     ok = ok && rc == 0 && e <= 1e-3;
   }
   // batch: T bf16 tokens, with and without a low part, stored (accumulate 0)

@@ -188,6 +188,7 @@ template <typename T> inline T emu_buf_load(emu_rsrc r, uint32_t voff, uint32_t 
   return v;
 }
 typedef uint32_t emu_u32x4 __attribute__((ext_vector_type(4)));
+inline uint8_t __builtin_amdgcn_raw_buffer_load_b8(emu_rsrc r, uint32_t v, uint32_t s, int) { return emu_buf_load<uint8_t>(r, v, s); }
 inline uint32_t __builtin_amdgcn_raw_buffer_load_b32(emu_rsrc r, uint32_t v, uint32_t s, int) { return emu_buf_load<uint32_t>(r, v, s); }
 inline emu_u32x4 __builtin_amdgcn_raw_buffer_load_b128(emu_rsrc r, uint32_t v, uint32_t s, int) { return emu_buf_load<emu_u32x4>(r, v, s); }
 inline void __builtin_amdgcn_raw_ptr_buffer_load_lds(emu_rsrc r, void* lds, int size, uint32_t v, uint32_t s, int off, int) {

@@ -165,7 +165,8 @@ def test_route_emulated(runs):
 
 
 def test_shared_expert_and_hc_post_emulated(runs):
-    """The shared expert's decode (6 tokens, two column groups) and batch kernels (40 tokens, with
-    and without a low part) against the oracle, the hyper-connection post bit for bit."""
+    """The shared expert's decode (1 token; 3 tokens read dim-major; 6 tokens, two column groups)
+    and batch kernels (40 tokens, with and without a low part) against the oracle, the
+    hyper-connection post bit for bit."""
     out = result(runs, "shared")
     assert "shared ok=1" in out, out
