@@ -328,6 +328,7 @@ struct GemmArgs {
   const Tile* tiles;
   uint32_t max_tiles;       // entries of tiles (allocated; the header says how many are used)
   const uint32_t* slot_tok;
+  uint32_t n_sl;              // entries of slot_tok and slot_sigma
   uint32_t n_tok;             // tokens of the batch (a slot's token id is clamped below it)
   const int32_t* slot_sigma;  // activation exponent of the slot's token
   const uint8_t* ws;        // B rows and the zero row, addressed by 32-bit offsets from here
@@ -426,11 +427,14 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
   const uint32_t room = A.max_tiles - min(first, A.max_tiles);
   const Tile* tiles = room ? A.tiles + first : A.tiles;
   const uint32_t max_t = room ? room : 1u;
-  uint32_t w = blockIdx.x, rb, tile_id;
+  uint32_t w = blockIdx.x, rb, tile_id, rbn, tile_n;
   item_of(w, rb, tile_id);
+  item_of(w + gridDim.x, rbn, tile_n);
   Tile tl = tiles[tile_id < max_t ? tile_id : 0u];
+  Tile tln = tiles[tile_n < max_t ? tile_n : 0u];  // the next item's tile
   if (tile_id >= n_tiles || tl.n == 0) return;  // (a tile in use has n >= 1: the test only makes
-                                                // both loads precede the branch, in one round trip)
+                                                // the loads precede the branch, in one round trip)
+  bool has_next = tile_n < n_tiles && tln.n != 0;
 
   __shared__ __align__(16) uint32_t lut_s[Lut<kGKC, true>::kDwords];
   __shared__ __align__(16) uint2 blk_s[16];
@@ -442,6 +446,15 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
   __shared__ __align__(16) uint8_t buf2[GTile<CT>::kBuf];
   __shared__ __align__(16) uint8_t buf3[GTile<CT>::kBuf];
   uint32_t* rowoff = reinterpret_cast<uint32_t*>(buf3);  // set-up only, before buffer 3 is written
+  // Staged at the start of each item by direct-to-LDS loads, so that neither the epilogue nor the
+  // step to the next item waits for memory: the item's activation exponents (gate/up: one per
+  // slot of the tile, 128 entries) and row scales (256 bf16: the 128 gate and 128 up rows, or the
+  // 256 down rows), the next item's B rows (gate/up: its slots' tokens) and the tile of the item
+  // after it.
+  __shared__ __align__(16) uint32_t ep_sig[128];
+  __shared__ __align__(16) uint32_t ep_rs[128];
+  __shared__ __align__(16) uint32_t ep_tok[128];
+  __shared__ __align__(16) uint32_t ep_tile[64];
   const uint8_t* lut = reinterpret_cast<const uint8_t*>(lut_s);
   auto bufsel = [&](int i) -> uint8_t* { return i == 0 ? buf0 : i == 1 ? buf1 : i == 2 ? buf2 : buf3; };
 
@@ -471,15 +484,30 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
   };
   // B row of column tid (threads below GTile<CT>::kCols): a column past the tile's tokens reads the tile's
   // first slot (unconditional load) and gets the zero row
+  // (these and the per-item lane values below are derived from an opaque copy of the thread index
+  // where they are used: derived once, outside the item loop, they were held across it, spilled,
+  // and every reload from scratch memory waited for all the loads in flight)
+  auto tid_now = [&]() -> uint32_t {
+    uint32_t t = threadIdx.x;
+    AFFX_PIN(t);
+    return t;
+  };
   const uint32_t bcol_j = (tid >> 4) * TPG + (tid & 15u) / TX;
   auto brow_load = [&](const Tile& t) -> uint32_t {
     const uint32_t bslot = t.slot0 + ((tid < GTile<CT>::kCols && (tid & 15u) < TX * TPG && bcol_j < t.n) ? bcol_j : 0u);
     return PH == 0 ? min(A.slot_tok[bslot], A.n_tok - 1u) : bslot;
   };
+  // the same from the tokens staged in ep_tok (slot t.slot0 + j at entry j)
+  auto brow_staged = [&](const Tile& t) -> uint32_t {
+    const uint32_t tp = tid_now(), bj = (tp >> 4) * TPG + (tp & 15u) / TX;
+    const uint32_t j = (tp < GTile<CT>::kCols && (tp & 15u) < TX * TPG && bj < t.n) ? bj : 0u;
+    return PH == 0 ? min(ep_tok[j], A.n_tok - 1u) : t.slot0 + j;
+  };
   auto rowoff_store = [&](const Tile& t, uint32_t brow) {
-    const bool used = tid < GTile<CT>::kCols && (tid & 15u) < TX * TPG && bcol_j < t.n;
-    if (tid < GTile<CT>::kCols)
-      rowoff[tid] = used ? (uint32_t)(A.b_off + ((uint64_t)brow * TX + (tid & 15u) % TX) * K) : (uint32_t)A.zero_off;
+    const uint32_t tp = tid_now(), bj = (tp >> 4) * TPG + (tp & 15u) / TX;
+    const bool used = tp < GTile<CT>::kCols && (tp & 15u) < TX * TPG && bj < t.n;
+    if (tp < GTile<CT>::kCols)
+      rowoff[tp] = used ? (uint32_t)(A.b_off + ((uint64_t)brow * TX + (tp & 15u) % TX) * K) : (uint32_t)A.zero_off;
   };
   // DMA lane map: instruction i of wave w writes columns 8b..8b+7 (b = GTile<CT>::kDma w + i), lane l to
   // LDS slot l & 7 of column 8b + (l >> 3); slot p of column col holds global chunk p ^ f(col),
@@ -490,10 +518,11 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
   // captured by the lambdas below, ROCm 7.2's hipcc emits no host stub for the kernel)
   uint32_t roff[GTile<kGCT>::kDma];
   auto roff_load = [&]() {
+    const uint32_t lp = tid_now() & 63u;
 #pragma unroll
     for (int i = 0; i < GTile<CT>::kDma; ++i) {
-      const uint32_t col = 8u * (GTile<CT>::kDma * wv + i) + (lane >> 3);
-      const uint32_t q = (lane & 7u) ^ ((col & 7u) ^ ((col >> 3) & 1u));
+      const uint32_t col = 8u * (GTile<CT>::kDma * wv + i) + (lp >> 3);
+      const uint32_t q = (lp & 7u) ^ ((col & 7u) ^ ((col >> 3) & 1u));
       roff[i] = rowoff[col] + (q << 4);
     }
   };
@@ -525,10 +554,6 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  const uint32_t copy4 = (lane & (kGKC - 1)) * 4u;
-  const uint32_t c = lane & 15, kg = lane >> 4;
-  const uint32_t bo0 = c * 128u + (((2u * kg) ^ ((c ^ (c >> 3)) & 7u)) << 4);
-  const uint32_t bo1 = c * 128u + (((2u * kg + 1u) ^ ((c ^ (c >> 3)) & 7u)) << 4);
   // epilogue helpers: accumulator lane (c, kg), element v = D[4 kg + v][c]: row 4 kg + v of the
   // row tile, column c. (Every accumulator index is a compile-time constant: a runtime index
   // would put the whole accumulator array in scratch memory.)
@@ -549,7 +574,51 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
   };
   const float L = A.limit;
 
+  const __amdgpu_buffer_rsrc_t sig_r = buffer_rsrc(A.slot_sigma, 4u * A.n_sl);
+  const __amdgpu_buffer_rsrc_t tok_r = buffer_rsrc(A.slot_tok, 4u * A.n_sl);
+  const __amdgpu_buffer_rsrc_t tile_r = buffer_rsrc(tiles, (uint32_t)sizeof(Tile) * max_t);
+  auto lds4 = [&](__amdgpu_buffer_rsrc_t r, uint32_t* dst, uint32_t byte_off) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, AFFX_LDS_PTR(dst), 4, lane * 4u, byte_off, 0, 0);
+  };
   for (;;) {
+    // ---- staging (one wave each; issued before the steps' loads, so the steps' exact wait
+    // counts are unchanged: loads complete in issue order) ----------------------------------------
+    {
+      uint32_t rb2s, tile2s;
+      item_of(w + 2u * gridDim.x, rb2s, tile2s);
+      if (wv == 0) {
+        if constexpr (PH == 0) {
+          lds4(sig_r, ep_sig, 4u * tl.slot0);
+          lds4(sig_r, ep_sig + 64, 4u * tl.slot0 + 256u);
+        }
+      } else if (wv == 1) {
+        const __amdgpu_buffer_rsrc_t rs_r =
+            buffer_rsrc(ex + A.off[PH == 0 ? kGateRs : kDownRs], 2u * (PH == 0 ? A.inter : A.hidden));
+        if constexpr (PH == 0) {
+          lds4(rs_r, ep_rs, 256u * rb);
+          lds4(buffer_rsrc(ex + A.off[kUpRs], 2u * A.inter), ep_rs + 64, 256u * rb);
+        } else {
+          lds4(rs_r, ep_rs, 512u * rb);
+          lds4(rs_r, ep_rs + 64, 512u * rb + 256u);
+        }
+      } else if (wv == 2) {
+        if constexpr (PH == 0) {
+          if (has_next) {
+            lds4(tok_r, ep_tok, 4u * tln.slot0);
+            lds4(tok_r, ep_tok + 64, 4u * tln.slot0 + 256u);
+          }
+        }
+      } else if (wv == 3) {
+        lds4(tile_r, ep_tile, (uint32_t)sizeof(Tile) * (tile2s < max_t ? tile2s : 0u));
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // the lane's table copy, fragment offsets and epilogue position (derived per item: see tid_now)
+    const uint32_t lane_p = tid_now() & 63u;
+    const uint32_t copy4 = (lane_p & (kGKC - 1)) * 4u;
+    const uint32_t c = lane_p & 15, kg = lane_p >> 4;
+    const uint32_t bo0 = c * 128u + (((2u * kg) ^ ((c ^ (c >> 3)) & 7u)) << 4);
+    const uint32_t bo1 = c * 128u + (((2u * kg + 1u) ^ ((c ^ (c >> 3)) & 7u)) << 4);
     v8i a_cur[kGRT];
 #pragma unroll
     for (int r = 0; r < kGRT; ++r) {
@@ -673,41 +742,35 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
 
-    // ---- next item: tile (scalar loads), then, with this item's epilogue inputs, its B rows and
-    // first weights -------------------------------------------------------------------------------
-    uint32_t rb2, tile2;
-    item_of(w + gridDim.x, rb2, tile2);
-    const Tile tl2 = tiles[tile2 < max_t ? tile2 : 0u];
-    const bool next = tile2 < n_tiles && tl2.n != 0;
-
-    // ---- epilogue inputs: every one requested before the first is used ----------------------
+    // ---- epilogue inputs, from the staging in LDS -------------------------------------------
     // (gate/up: the activation exponent of the lane's token in each column tile, columns past the
     // tile's tokens read its last token and store nothing; the row scales. Down: row scales.)
+    const bool next = has_next;
     int sig[PH == 0 ? CT : 1];
     uint2 rgw[kHalf], ruw[kHalf], rdw[kGRT];
     if constexpr (PH == 0) {
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) {
         const uint32_t j = ct * TPG + c / TX;
-        sig[ct] = A.slot_sigma[tl.slot0 + (j < tl.n ? j : tl.n - 1u)];
+        sig[ct] = (int)ep_sig[j < tl.n ? j : tl.n - 1u];
       }
 #pragma unroll
       for (int p = 0; p < kHalf; ++p) {
-        const uint32_t row0 = rt_of(p) * 16u + 4u * kg;
-        rgw[p] = *reinterpret_cast<const uint2*>(ex + A.off[kGateRs] + (uint64_t)row0 * 2);
-        ruw[p] = *reinterpret_cast<const uint2*>(ex + A.off[kUpRs] + (uint64_t)row0 * 2);
+        const uint32_t loc = (rt_of(p) - rb * 8u) * 16u + 4u * kg;  // row within the gate/up row block
+        rgw[p] = *reinterpret_cast<const uint2*>(ep_rs + loc / 2);
+        ruw[p] = *reinterpret_cast<const uint2*>(ep_rs + 64 + loc / 2);
       }
     } else {
 #pragma unroll
       for (int r = 0; r < kGRT; ++r)
-        rdw[r] = *reinterpret_cast<const uint2*>(ex + A.off[kDownRs] + (uint64_t)(rt_of(r) * 16u + 4u * kg) * 2);
+        rdw[r] = *reinterpret_cast<const uint2*>(ep_rs + ((rt_of(r) - rb * 16u) * 16u + 4u * kg) / 2);
     }
     __builtin_amdgcn_sched_barrier(0);
     // this item's row tiles and planes, kept for its epilogue (the next item's replace them)
     const uint32_t rt0_cur = rt0;
     const Tile tl_cur = tl;
     uint32_t brow2 = 0;
-    if (next) brow2 = brow_load(tl2);
+    if (next) brow2 = brow_staged(tln);
     __builtin_amdgcn_sched_barrier(0);
     auto rt_cur = [&](int r) -> uint32_t { return PH == 0 ? rt0_cur + (r % kHalf) : rt0_cur + r; };
 
@@ -813,18 +876,25 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
     }
     if (!next) break;
 
-    // ---- next item's weights and first two steps of B (its B rows have arrived during the
-    // epilogue) ----------------------------------------------------------------------------------
-    set_item(tl2, rb2);
+    // ---- next item's weights and first two steps of B; the tile of the item after it (staged,
+    // read before the next item's staging overwrites it) -----------------------------------------
+    Tile tl3;
+    tl3.expert = __builtin_amdgcn_readfirstlane(ep_tile[0]);
+    tl3.slot0 = __builtin_amdgcn_readfirstlane(ep_tile[1]);
+    tl3.n = __builtin_amdgcn_readfirstlane(ep_tile[2]);
+    set_item(tln, rbn);
     load_units();
-    rowoff_store(tl2, brow2);
+    rowoff_store(tln, brow2);
     __syncthreads();
     roff_load();
     dma(buf0, 0);
     dma(buf1, 1);
     w += gridDim.x;
-    rb = rb2;
-    tl = tl2;
+    rb = rbn;
+    tl = tln;
+    item_of(w + gridDim.x, rbn, tile_n);
+    tln = tl3;
+    has_next = tile_n < n_tiles && tln.n != 0;
     __builtin_amdgcn_s_waitcnt(AFFX_VMCNT(0));
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
@@ -941,6 +1011,7 @@ int grouped_body(const affx_layer* L, const void* x, const void* x_lo, uint32_t 
   A.codebook = (const uint32_t*)L->codebook;
   A.hdr = (const GroupedHdr*)(b + lay.hdr);
   A.slot_tok = slot_tok;
+  A.n_sl = (uint32_t)P;
   A.n_tok = T;
   A.slot_sigma = (const int32_t*)(b + lay.sigma);
   A.ws = b;
