@@ -775,6 +775,15 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
     auto rt_cur = [&](int r) -> uint32_t { return PH == 0 ? rt0_cur + (r % kHalf) : rt0_cur + r; };
 
     // ---- epilogue arithmetic and stores ------------------------------------------------------
+    // Gate/up: the SwiGLU terms go to LDS first, term t of the tile's token j at row x of the row
+    // block (x < 128) at stg(t) + j * 128 + x (terms 0-1 in buffer 2, term 2 in buffer 3 past the
+    // B-row offsets the next item writes there; both buffers are free once the steps are done),
+    // and then out in 16-byte pieces: each (token, term) is 128 bytes of the output row, four runs
+    // of 32 at a 128-byte stride in the down GEMM's step order. (Written from the accumulator
+    // lanes, two or four bytes per lane and term: 36 narrow stores per wave, whose
+    // acknowledgements the next item then waited for.)
+    constexpr uint32_t kTT = CT * TPG;  // tokens of a tile of this class
+    auto stg = [&](uint32_t t) -> uint8_t* { return t < 2 ? buf2 + t * kTT * 128u : buf3 + 1024u; };
     if constexpr (PH == 0) {
       static_for<0, kHalf>([&](auto pc) {
         constexpr int p = decltype(pc)::value;
@@ -782,7 +791,7 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
         float rg[4], ru[4];
         bf16x4(rgw[p], rg);
         bf16x4(ruw[p], ru);
-        const uint32_t prow = kperm(row0);
+        const uint32_t xloc = row0 - rb * 128u;  // the row within the row block
         static_for<0, CT>([&](auto cc) {
           constexpr int ct = decltype(cc)::value;
           if (ct * TPG >= tl_cur.n) return;  // no token in this column tile (the same for the whole wave)
@@ -806,7 +815,6 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
               u2[v] = odd ? uu : su[v];
             }
             if (j < tl_cur.n) {
-              const uint32_t slot = tl_cur.slot0 + j;
               float a2[2];
 #pragma unroll
               for (int v = 0; v < 2; ++v) {
@@ -820,13 +828,12 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
               }
               uint32_t o0, o1, o2;
               split3x2(a2[0], a2[1], o0, o1, o2);
-              uint8_t* dst = A.aq + (uint64_t)slot * 3 * A.inter + prow + (odd ? 2u : 0u);
-              *reinterpret_cast<uint16_t*>(dst) = (uint16_t)o0;
-              *reinterpret_cast<uint16_t*>(dst + A.inter) = (uint16_t)o1;
-              *reinterpret_cast<uint16_t*>(dst + 2 * (uint64_t)A.inter) = (uint16_t)o2;
+              const uint32_t at = j * 128u + xloc + (odd ? 2u : 0u);
+              *reinterpret_cast<uint16_t*>(stg(0) + at) = (uint16_t)o0;
+              *reinterpret_cast<uint16_t*>(stg(1) + at) = (uint16_t)o1;
+              *reinterpret_cast<uint16_t*>(stg(2) + at) = (uint16_t)o2;
             }
           } else if (c % TX == 0 && c < TX * TPG && j < tl_cur.n) {
-            const uint32_t slot = tl_cur.slot0 + j;
             float a[4];
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
@@ -843,13 +850,23 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
             }
             uint32_t o0, o1, o2;
             split3x4(a[0], a[1], a[2], a[3], o0, o1, o2);
-            uint8_t* dst = A.aq + (uint64_t)slot * 3 * A.inter + prow;
-            *reinterpret_cast<uint32_t*>(dst) = o0;
-            *reinterpret_cast<uint32_t*>(dst + A.inter) = o1;
-            *reinterpret_cast<uint32_t*>(dst + 2 * (uint64_t)A.inter) = o2;
+            const uint32_t at = j * 128u + xloc;
+            *reinterpret_cast<uint32_t*>(stg(0) + at) = o0;
+            *reinterpret_cast<uint32_t*>(stg(1) + at) = o1;
+            *reinterpret_cast<uint32_t*>(stg(2) + at) = o2;
           }
         });
       });
+      __syncthreads();
+      // out: piece q (16 bytes) of (token j, term t), k = (t n + j) 8 + q
+      const uint32_t n = tl_cur.n, d0 = kperm(rb * 128u);
+      const uint32_t tp = tid_now();
+      for (uint32_t k = tp; k < n * 24u; k += kGT) {
+        const uint32_t q = k & 7u, jt = k >> 3, t = jt / n, j = jt - t * n;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(stg(t) + j * 128u + q * 16u);
+        *reinterpret_cast<u32x4*>(A.aq + ((uint64_t)(tl_cur.slot0 + j) * 3 + t) * A.inter + d0 + (q >> 1) * 128u +
+                                  (q & 1u) * 16u) = v;
+      }
     } else {
       static_for<0, kGRT>([&](auto rc) {
         constexpr int r = decltype(rc)::value;
