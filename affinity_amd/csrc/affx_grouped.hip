@@ -446,6 +446,7 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
   __shared__ __align__(16) uint8_t buf2[GTile<CT>::kBuf];
   __shared__ __align__(16) uint8_t buf3[GTile<CT>::kBuf];
   uint32_t* rowoff = reinterpret_cast<uint32_t*>(buf3);  // set-up only, before buffer 3 is written
+  __shared__ __align__(16) uint32_t rowoff_n[GTile<CT>::kCols];  // the next tile's, during the last 1024 columns
   // Staged at the start of each item by direct-to-LDS loads, so that neither the epilogue nor the
   // step to the next item waits for memory: the item's activation exponents (gate/up: one per
   // slot of the tile, 128 entries) and row scales (256 bf16: the 128 gate and 128 up rows, or the
@@ -488,9 +489,9 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
   // where they are used: derived once, outside the item loop, they were held across it, spilled,
   // and every reload from scratch memory waited for all the loads in flight)
   auto tid_now = [&]() -> uint32_t {
-    uint32_t t = threadIdx.x;
-    AFFX_PIN(t);
-    return t;
+    uint32_t z = 0u;
+    AFFX_PIN(z);  // (the lane count below is made where it is used, from nothing held across)
+    return wv * 64u + __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, z));
   };
   const uint32_t bcol_j = (tid >> 4) * TPG + (tid & 15u) / TX;
   auto brow_load = [&](const Tile& t) -> uint32_t {
@@ -503,11 +504,19 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
     const uint32_t j = (tp < GTile<CT>::kCols && (tp & 15u) < TX * TPG && bj < t.n) ? bj : 0u;
     return PH == 0 ? min(ep_tok[j], A.n_tok - 1u) : t.slot0 + j;
   };
+  // (B rows are addressed by 32-bit offsets into the workspace, which the host checks fit, so the
+  // offsets are computed in 32 bits)
   auto rowoff_store = [&](const Tile& t, uint32_t brow) {
     const uint32_t tp = tid_now(), bj = (tp >> 4) * TPG + (tp & 15u) / TX;
     const bool used = tp < GTile<CT>::kCols && (tp & 15u) < TX * TPG && bj < t.n;
     if (tp < GTile<CT>::kCols)
-      rowoff[tp] = used ? (uint32_t)(A.b_off + ((uint64_t)brow * TX + (tp & 15u) % TX) * K) : (uint32_t)A.zero_off;
+      rowoff[tp] = used ? (uint32_t)A.b_off + (brow * TX + (tp & 15u) % TX) * K : (uint32_t)A.zero_off;
+  };
+  auto rowoff_store_next = [&](const Tile& t, uint32_t brow) {
+    const uint32_t tp = tid_now(), bj = (tp >> 4) * TPG + (tp & 15u) / TX;
+    const bool used = tp < GTile<CT>::kCols && (tp & 15u) < TX * TPG && bj < t.n;
+    if (tp < GTile<CT>::kCols)
+      rowoff_n[tp] = used ? (uint32_t)A.b_off + (brow * TX + (tp & 15u) % TX) * K : (uint32_t)A.zero_off;
   };
   // DMA lane map: instruction i of wave w writes columns 8b..8b+7 (b = GTile<CT>::kDma w + i), lane l to
   // LDS slot l & 7 of column 8b + (l >> 3); slot p of column col holds global chunk p ^ f(col),
@@ -524,6 +533,15 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
       const uint32_t col = 8u * (GTile<CT>::kDma * wv + i) + (lp >> 3);
       const uint32_t q = (lp & 7u) ^ ((col & 7u) ^ ((col >> 3) & 1u));
       roff[i] = rowoff[col] + (q << 4);
+    }
+  };
+  auto roff_load_next = [&]() {
+    const uint32_t lp = tid_now() & 63u;
+#pragma unroll
+    for (int i = 0; i < GTile<CT>::kDma; ++i) {
+      const uint32_t col = 8u * (GTile<CT>::kDma * wv + i) + (lp >> 3);
+      const uint32_t q = (lp & 7u) ^ ((col & 7u) ^ ((col >> 3) & 1u));
+      roff[i] = rowoff_n[col] + (q << 4);
     }
   };
   const __amdgpu_buffer_rsrc_t wsr = buffer_rsrc(A.ws, 0xFFFFFFFFu);
@@ -613,6 +631,15 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
       }
     }
     __builtin_amdgcn_sched_barrier(0);
+    // this item's row tiles (set_item moves rt0 to the next item's during the last 1024 columns)
+    const uint32_t rt0_cur = rt0;
+    auto rt_cur = [&](int r) -> uint32_t { return PH == 0 ? rt0_cur + (r % kHalf) : rt0_cur + r; };
+    // The next item's first weights stream into the register ring during this item's last 1024
+    // columns, in place of the ring's idle reloads, and its first two steps of B go out at step 6
+    // of those columns, so the step to the next item waits for no load (a burst of the next item's
+    // loads there or before the epilogue was held by the memory pipeline). Needs the next item's B
+    // rows staged (visible after the first barrier, so at least two sets of 1024 columns).
+    const bool cont = has_next && nst >= 2u;
     // the lane's table copy, fragment offsets and epilogue position (derived per item: see tid_now)
     const uint32_t lane_p = tid_now() & 63u;
     const uint32_t copy4 = (lane_p & (kGKC - 1)) * 4u;
@@ -644,8 +671,14 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
       // buffers nobody reads again, so the count of loads in flight is the same on every path.
       if constexpr ((m & 1) == 0) {
         const uint32_t t2 = s * 8u + m + 2u, t3 = t2 + 1u;
-        dma(bufsel((m + 2) & 3), t2 < nsteps ? t2 : nsteps - 1u);
-        dma(bufsel((m + 3) & 3), t3 < nsteps ? t3 : nsteps - 1u);
+        // (at step 6 of the last 1024 columns: the next item's steps 0 and 1, which go to buffers
+        // 0 and 1 as those of steps t + 2 and t + 3 would)
+        const bool nx = m == 6 && !more && cont;
+        if constexpr (m == 6) {
+          if (nx) roff_load_next();
+        }
+        dma(bufsel((m + 2) & 3), nx ? 0u : t2 < nsteps ? t2 : nsteps - 1u);
+        dma(bufsel((m + 3) & 3), nx ? 1u : t3 < nsteps ? t3 : nsteps - 1u);
       }
       __builtin_amdgcn_sched_barrier(0);
       // ring loads for the next 1024 columns; after the last ones, the same loads of tile 0 (hot
@@ -655,7 +688,7 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
 #pragma unroll
         for (int r = 0; r < kGRT; ++r)
           ring_load<m>(u[r], PH == 0 && r >= kHalf ? c1 : c0, PH == 0 && r >= kHalf ? f1 : f0,
-                       more ? rt_of(r) * nst + s + 1 : 0u, lane);
+                       more ? rt_of(r) * nst + s + 1 : cont ? rt_of(r) * nst : 0u, lane);
       }
       __builtin_amdgcn_sched_barrier(0);
       // The step is 12 groups, one per B column tile: the tile's two fragment reads go out two
@@ -728,6 +761,11 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
     };
     for (uint32_t s = 0; s < nst; ++s) {
       const bool more = s + 1 < nst;
+      if (!more && cont) {
+        // the next item's planes and B-row offsets (published by the barrier of step 1)
+        rowoff_store_next(tln, brow_staged(tln));
+        set_item(tln, rbn);
+      }
       step(IConst<0>{}, s, more);
       step(IConst<1>{}, s, more);
       step(IConst<2>{}, s, more);
@@ -737,8 +775,8 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
       step(IConst<6>{}, s, more);
       step(IConst<7>{}, s, more);
     }
-    // no direct-to-LDS load outlives the steps, and every wave is past its last B read
-    __builtin_amdgcn_s_waitcnt(AFFX_VMCNT(0));
+    // every wave is past its last B read; step 7 waited for every direct-to-LDS load (the next
+    // item's first B steps included), and the ring's last loads may stay in flight
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
 
@@ -756,23 +794,21 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
       }
 #pragma unroll
       for (int p = 0; p < kHalf; ++p) {
-        const uint32_t loc = (rt_of(p) - rb * 8u) * 16u + 4u * kg;  // row within the gate/up row block
+        const uint32_t loc = (rt_cur(p) - rb * 8u) * 16u + 4u * kg;  // row within the gate/up row block
         rgw[p] = *reinterpret_cast<const uint2*>(ep_rs + loc / 2);
         ruw[p] = *reinterpret_cast<const uint2*>(ep_rs + 64 + loc / 2);
       }
     } else {
 #pragma unroll
       for (int r = 0; r < kGRT; ++r)
-        rdw[r] = *reinterpret_cast<const uint2*>(ep_rs + ((rt_of(r) - rb * 16u) * 16u + 4u * kg) / 2);
+        rdw[r] = *reinterpret_cast<const uint2*>(ep_rs + ((rt_cur(r) - rb * 16u) * 16u + 4u * kg) / 2);
     }
     __builtin_amdgcn_sched_barrier(0);
-    // this item's row tiles and planes, kept for its epilogue (the next item's replace them)
-    const uint32_t rt0_cur = rt0;
+    // this item's tile, kept for its epilogue
     const Tile tl_cur = tl;
     uint32_t brow2 = 0;
-    if (next) brow2 = brow_staged(tln);
+    if (next && !cont) brow2 = brow_staged(tln);
     __builtin_amdgcn_sched_barrier(0);
-    auto rt_cur = [&](int r) -> uint32_t { return PH == 0 ? rt0_cur + (r % kHalf) : rt0_cur + r; };
 
     // ---- epilogue arithmetic and stores ------------------------------------------------------
     // Gate/up: the SwiGLU terms go to LDS first, term t of the tile's token j at row x of the row
@@ -899,13 +935,15 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
     tl3.expert = __builtin_amdgcn_readfirstlane(ep_tile[0]);
     tl3.slot0 = __builtin_amdgcn_readfirstlane(ep_tile[1]);
     tl3.n = __builtin_amdgcn_readfirstlane(ep_tile[2]);
-    set_item(tln, rbn);
-    load_units();
-    rowoff_store(tln, brow2);
-    __syncthreads();
-    roff_load();
-    dma(buf0, 0);
-    dma(buf1, 1);
+    if (!cont) {
+      set_item(tln, rbn);
+      load_units();
+      rowoff_store(tln, brow2);
+      __syncthreads();
+      roff_load();
+      dma(buf0, 0);
+      dma(buf1, 1);
+    }
     w += gridDim.x;
     rb = rbn;
     tl = tln;

@@ -122,6 +122,15 @@ inline void __syncthreads() { emu_blk->block_bar->arrive_and_wait(); }
 inline void __builtin_amdgcn_s_barrier() { __syncthreads(); }
 inline uint32_t emu_lane() { return threadIdx.x & 63; }
 inline uint32_t emu_wave() { return threadIdx.x >> 6; }
+// v_mbcnt_lo/hi: add the count of set mask bits below this lane (lanes 0-31 / 32-63)
+inline uint32_t __builtin_amdgcn_mbcnt_lo(uint32_t mask, uint32_t add) {
+  const uint32_t l = emu_lane() < 32 ? emu_lane() : 32;
+  return add + (uint32_t)__builtin_popcount(l >= 32 ? mask : mask & ((1u << l) - 1u));
+}
+inline uint32_t __builtin_amdgcn_mbcnt_hi(uint32_t mask, uint32_t add) {
+  const uint32_t l = emu_lane() > 32 ? emu_lane() - 32 : 0;
+  return add + (uint32_t)__builtin_popcount(mask & ((1u << l) - 1u));
+}
 inline void emu_wave_sync() { emu_blk->wave_bar[emu_wave()]->arrive_and_wait(); }
 #define __builtin_amdgcn_wave_barrier() emu_wave_sync()
 #define AFFX_DYN_LDS(name) uint8_t* name = emu_blk->lds
