@@ -410,10 +410,9 @@ __global__ void __launch_bounds__(kGT, 1) grouped_gemm_kernel(GemmArgs A) {
   // Set-up of the first item in three memory round trips: (1) the codebook, the tile count and
   // the tiles of the first two items (read before it is known to be in use: any index below
   // max_tiles is allocated); (2) the B row of every column, then the first weights; (3) the
-  // first two steps of B. Later items find their tile and B rows staged in LDS (see ep_sig); their
-  // weights and first two steps of B follow the previous item's epilogue. (Issued before that
-  // epilogue they only move the wait into it: the epilogue's store acknowledgements, which
-  // complete in order with the loads, are what the next item then waits for.)
+  // first two steps of B. Later items find their tile and B rows staged in LDS (see ep_sig), and
+  // their first weights and B steps are loaded during the previous item's last 1024 columns (see
+  // cont).
   constexpr int kPer = 2048 / kGT;
   uint32_t cbv[kPer];
 #pragma unroll
