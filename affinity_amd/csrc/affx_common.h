@@ -85,15 +85,26 @@ struct DecodePlan {
 #endif
 
 // Decode workspace: [sync][plan][zeros][xq][aq] (affx_decode.hip). The sync run holds the fused
-// decode's cross-workgroup state: a 256-byte header (dword 0: gate/up items published, dword 2:
-// error bits, dwords 8-9 reserved) and one release flag per waiting workgroup, 128 bytes apart so
-// that no two workgroups poll the same line. Zero before first use, left zero by every launch
-// (the error bits excepted).
+// decode's cross-workgroup state:
+//  * a 256-byte header: dword 0 gate/up items published (rounds kernels), dword 2 error bits,
+//    dword 8 the launch epoch of the one-pass (batch-1) kernel;
+//  * one release flag per waiting workgroup, 128 bytes apart so that no two workgroups poll the
+//    same line (rounds kernels);
+//  * the one-pass kernel's publish flags: kPubReplicas copies of one dword per workgroup, each
+//    copy a kPubStride run, holding the epoch in which that workgroup's SwiGLU output was last
+//    complete.
+// Zero before first use. Every launch leaves the counter and the release flags zero; the epoch
+// and the publish flags only ever advance (zero is their state after a reset as well).
 constexpr uint32_t kSyncHeader = 256;
 constexpr uint32_t kSyncFlagStride = 128;
 constexpr uint32_t kSyncFlags = 256;  // down-phase workgroups: output row tiles, hidden / 16 <= 256
-constexpr uint32_t kSyncBytes = kSyncHeader + kSyncFlags * kSyncFlagStride;
+constexpr uint32_t kSyncRunBytes = kSyncHeader + kSyncFlags * kSyncFlagStride;
+constexpr uint32_t kPubReplicas = 8;  // one per XCD: a waiter polls copy g % 8
+constexpr uint32_t kPubStride = 1024; // bytes per copy: 256 workgroups
+constexpr uint32_t kPubOff = kSyncRunBytes;
+constexpr uint32_t kSyncBytes = kPubOff + kPubReplicas * kPubStride;
 constexpr uint32_t kSyncErrWord = 2;  // dword of the error bits (bit 0: a waiter gave up)
+constexpr uint32_t kEpochWord = 8;    // dword of the one-pass kernel's launch epoch
 // Zeroes the sync run of a decode workspace (stream-ordered; after a wait gave up, the late
 // publisher may have raised flags that a later launch would take for its own).
 int decode_sync_reset(void* ws, hipStream_t s);

@@ -188,6 +188,10 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   // order, so waiting for them never waits for the weight stream issued after them); every wave
   // dedupes the routes itself (registers only) so that it can issue its weight loads as soon as
   // the routes arrive, with no barrier in between.
+  // Batch 1: the launch epoch, requested before anything else (needed only at the publish; loads
+  // complete in issue order, so no earlier wait covers it).
+  uint32_t ep_raw = 0;
+  if constexpr (SINGLE) ep_raw = __hip_atomic_load(&A.sync[kEpochWord], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   // Routes r = lane + 64 h. Slots are the distinct experts in order of first occurrence.
   uint32_t e[2];
   float wr[2];
@@ -613,7 +617,20 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   }
   AFFX_TRACE(10);
   __syncthreads();
-  if (wv == 0 && n_rounds > 0) {
+  // Batch 1 (one pass): no counter. Every workgroup, items or not, publishes epoch + 1 in its own
+  // dword of each replica of the publish flags once its stores have completed (the barrier above
+  // orders the storing waves' waits before these stores). A waiter polls one replica and is
+  // released when every workgroup of the launch has published: one round trip less than the
+  // counter add and the flag fan-out that follows it.
+  uint32_t ep = 0;
+  if constexpr (SINGLE) {
+    uint32_t er = ep_raw;
+    AFFX_PIN(er);  // the epoch's wait stays here
+    ep = __builtin_amdgcn_readfirstlane(er) + 1u;
+    if (wv == 0 && lane < kPubReplicas)
+      __hip_atomic_store(A.sync + (kPubOff + lane * kPubStride) / 4 + g, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (!SINGLE && wv == 0 && n_rounds > 0) {
     // the add that completes the count clears it for the next launch and raises the flag of each
     // waiting workgroup (one line each: the waiters poll without contending for one address)
     uint32_t old = 0;
@@ -651,7 +668,29 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   AFFX_TRACE(14);
   // ---- 5. wait for every gate/up item (this workgroup's flag), then the down tiles -------------
   if (g < dtiles) {
-    if (tid == 0 && NI > 0) {
+    if (SINGLE && wv == 0 && NI > 0) {
+      // every workgroup's publish flag in this workgroup's replica, four per lane
+      const __amdgpu_buffer_rsrc_t fr =
+          buffer_rsrc(reinterpret_cast<const uint8_t*>(A.sync) + kPubOff + (g % kPubReplicas) * kPubStride, kPubStride);
+      for (uint32_t n = 0;; ++n) {
+        if (n >= A.spin_limit) {
+          if (lane == 0)
+            __hip_atomic_fetch_or(&A.sync[kSyncErrWord], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+        const u32x4 f = __builtin_amdgcn_raw_buffer_load_b128(fr, 16u * lane, 0, kDevCoherent);
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ok = ok && (4u * lane + i >= A.n_wg || f[i] == ep);
+        if (__ballot(!ok) == 0ull) break;
+        __builtin_amdgcn_s_sleep(2);
+        asm volatile("" ::: "memory");  // the next poll reloads
+      }
+      // every workgroup has read the epoch (each published epoch + 1): the next launch's epoch
+      if (g == 0 && lane == 0) __hip_atomic_store(&A.sync[kEpochWord], ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
+    if (!SINGLE && tid == 0 && NI > 0) {
       uint32_t* flag = A.sync + (kSyncHeader + g * kSyncFlagStride) / 4;
       // at most spin_limit polls (none at 0: the give-up path runs deterministically)
       for (uint32_t n = 0;; ++n) {
@@ -699,8 +738,14 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
         v8i bpre[BPRE ? 8 : 1];
         v8i bc[CG];
         if constexpr (BPRE) {
+          // only the lanes of used columns load (exec-masked); the others hold zeros, with no
+          // address-unit time spent on a zero run
 #pragma unroll
-          for (int m = 0; m < 8; ++m) bpre[m] = b_step(b.p[0], m);
+          for (int m = 0; m < 8; ++m) bpre[m] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+          if (b.used) {
+#pragma unroll
+            for (int m = 0; m < 8; ++m) bpre[m] = b_step(b.p[0], m);
+          }
           __builtin_amdgcn_sched_barrier(0);
         } else {
 #pragma unroll

@@ -340,10 +340,6 @@ struct GemmArgs {
 };
 
 
-// Buffer resource over `bytes` bytes at p (raw buffer, no swizzle; reads past the end return 0).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
-}
 constexpr int kNT = 2;  // cache policy of streamed weights: non-temporal
 
 // One unit in full (fields first, then the code chunks in order): tile t of the code and field

@@ -52,6 +52,14 @@ template <int N>
 __device__ __forceinline__ float row_shr(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x110 + N, 0xF, 0xF, false));
 }
+// Buffer resource over `bytes` bytes at p (raw buffer, no swizzle; reads past the end return 0).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+// Cache policy of a buffer access that must see, or be seen by, other workgroups on any XCD
+// without a fence: the device-scope coherence bit (sc1 on gfx950), as the compiler emits it for
+// an agent-scope atomic load or store.
+constexpr int kDevCoherent = 16;
 // LDS pointer operand of a direct global->LDS load.
 #ifndef AFFX_LDS_PTR
 #define AFFX_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
@@ -203,6 +211,7 @@ __device__ __forceinline__ int segment_terms(const float* __restrict__ x, uint64
 template <int CG>
 struct BSrc {
   const u32x4* p[CG];
+  bool used;  // (column group 0) this lane's column is a used (token, term) column
 };
 
 template <int CG>
@@ -218,6 +227,7 @@ __device__ __forceinline__ BSrc<CG> b_source(const uint8_t* src_base, uint64_t t
     s.p[cg] = valid ? reinterpret_cast<const u32x4*>(src_base + (uint64_t)(t * kTerms + tau) * term_stride +
                                                      col0 + g * kSegCols)
                     : reinterpret_cast<const u32x4*>(zeros);
+    if (cg == 0) s.used = valid;
   }
   return s;
 }

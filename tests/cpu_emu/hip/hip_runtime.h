@@ -50,6 +50,8 @@ inline int hipMemsetAsync(void* p, int v, size_t n, hipStream_t) { memset(p, v, 
 enum hipMemcpyKind { hipMemcpyHostToDevice = 1, hipMemcpyDeviceToHost = 2, hipMemcpyDeviceToDevice = 3 };
 inline int hipMemcpyAsync(void* d, const void* s, size_t n, hipMemcpyKind, hipStream_t) { memmove(d, s, n); return 0; }
 inline int hipStreamSynchronize(hipStream_t) { return 0; }  // launches run to completion
+enum hipStreamCaptureStatus { hipStreamCaptureStatusNone = 0, hipStreamCaptureStatusActive = 1 };
+inline int hipStreamIsCapturing(hipStream_t, hipStreamCaptureStatus* st) { *st = hipStreamCaptureStatusNone; return 0; }
 #define HIP_SYMBOL(x) (&(x))
 inline int hipGetSymbolAddress(void** p, const void* sym) { *p = const_cast<void*>(sym); return 0; }
 // device shape of the emulation: AFFX_EMU_CUS compute units (default 4), one resident workgroup each
@@ -200,6 +202,12 @@ typedef uint32_t emu_u32x4 __attribute__((ext_vector_type(4)));
 inline uint8_t __builtin_amdgcn_raw_buffer_load_b8(emu_rsrc r, uint32_t v, uint32_t s, int) { return emu_buf_load<uint8_t>(r, v, s); }
 inline uint32_t __builtin_amdgcn_raw_buffer_load_b32(emu_rsrc r, uint32_t v, uint32_t s, int) { return emu_buf_load<uint32_t>(r, v, s); }
 inline emu_u32x4 __builtin_amdgcn_raw_buffer_load_b128(emu_rsrc r, uint32_t v, uint32_t s, int) { return emu_buf_load<emu_u32x4>(r, v, s); }
+template <typename T> inline void emu_buf_store(T v, emu_rsrc r, uint32_t voff, uint32_t soff) {
+  const uint64_t o = (uint64_t)voff + soff;
+  if (o + sizeof(T) > r.n) return;  // past the range: dropped, as on the device
+  memcpy(const_cast<uint8_t*>(r.base) + o, &v, sizeof(T));
+}
+inline void __builtin_amdgcn_raw_buffer_store_b128(emu_u32x4 v, emu_rsrc r, uint32_t vo, uint32_t so, int) { emu_buf_store(v, r, vo, so); }
 inline void __builtin_amdgcn_raw_ptr_buffer_load_lds(emu_rsrc r, void* lds, int size, uint32_t v, uint32_t s, int off, int) {
   const uint64_t o = (uint64_t)v + s;
   uint8_t* dst = (uint8_t*)lds + off + (threadIdx.x & 63) * size;
@@ -327,16 +335,21 @@ void emu_launch_all(F kernel, dim3 grid, size_t shm, dim3 block, Args... args) {
     blks[b].lds = new uint8_t[shm];
     memset(blks[b].lds, 0xA5, shm);  // LDS starts undefined on the device
   }
-  std::vector<std::thread> ts;
-  for (uint32_t b = 0; b < nb; ++b)
-    for (uint32_t t = 0; t < nt; ++t)
-      ts.emplace_back([&, b, t]() {
-        emu_blk = &blks[b];
-        threadIdx = {t, 0, 0};
-        blockIdx = {b, 0, 0};
-        kernel(args...);
-      });
-  for (auto& th : ts) th.join();
+  // at most emu_cus() workgroups at a time, as many as the emulated device holds: every grid
+  // that needs its workgroups co-resident is sized to that, and larger grids run in waves
+  const uint32_t chunk = (uint32_t)std::max(1, emu_cus());
+  for (uint32_t b0 = 0; b0 < nb; b0 += chunk) {
+    std::vector<std::thread> ts;
+    for (uint32_t b = b0; b < nb && b < b0 + chunk; ++b)
+      for (uint32_t t = 0; t < nt; ++t)
+        ts.emplace_back([&, b, t]() {
+          emu_blk = &blks[b];
+          threadIdx = {t, 0, 0};
+          blockIdx = {b, 0, 0};
+          kernel(args...);
+        });
+    for (auto& th : ts) th.join();
+  }
   for (auto& bl : blks) delete[] bl.lds;
   for (auto* p : owned) delete p;
 }
