@@ -75,12 +75,15 @@ _SIGS = {
     "affx_container_codebook": ([_vp, _vp], C.c_int),
     "affx_container_upload_layer": ([_vp, _u32, _vp, _vp, _vp], C.c_int),
     "affx_dequant_matrix": ([C.POINTER(AffxMatrix), _vp, _vp, _vp], C.c_int),
+    "affx_expert_gemv_batch": ([C.POINTER(AffxMatrix), _vp, _u32, _vp, _vp, _vp, _vp], C.c_int),
+    "affx_expert_gemv": ([C.POINTER(AffxMatrix), _vp, _vp, C.c_float, _vp, _vp], C.c_int),
     "affx_decode_workspace_size": ([_u32, _u32, _u32, _u32], C.c_size_t),
     "affx_decode_status": ([_vp, C.c_int, _vp], C.c_int),
     "affx_expert_ffn_decode": ([C.POINTER(AffxLayer), _vp, _u64, _u64, _u32, _vp, _vp, _u32, _vp,
                                 _u64, _u64, C.c_int, _vp, C.c_size_t, _vp], C.c_int),
     "affx_expert_ffn_decode_noalloc": ([C.POINTER(AffxLayer), _vp, _u64, _u64, _u32, _vp, _vp, _u32, _vp,
                                         _u64, _u64, C.c_int, _vp], C.c_int),
+    "affx_decode_noalloc_status": ([C.c_int, _vp], C.c_int),
     "affx_decode_prepare": ([C.POINTER(AffxLayer), _vp, _u64, _u64, _u32, _vp, _vp, _u32, _vp, C.c_size_t,
                              _vp], C.c_int),
     "affx_decode_gateup": ([C.POINTER(AffxLayer), _u32, _u32, _vp, C.c_size_t, _vp], C.c_int),

@@ -144,8 +144,9 @@ int affx_container_open(const char* path, affx_container** out) {
   c->pool = c->map + h.expert_pool_off;
   for (uint64_t i = 0; i < h.layer_count; ++i) {
     const DiskLayer& L = c->layers[i];
+    // (the experts' extent by division: n_experts * stride can wrap for a corrupt stride)
     if (L.stride == 0 || L.n_experts > AFFX_MAX_EXPERTS || L.base_off > h.expert_pool_size ||
-        (uint64_t)L.n_experts * L.stride > h.expert_pool_size - L.base_off)
+        (L.n_experts > 0 && L.stride > (h.expert_pool_size - L.base_off) / L.n_experts))
       return fail("container_open: corrupt layer descriptor %llu", (unsigned long long)i);
     uint64_t H = 0, I = 0;
     if (!layer_matches(L, &H, &I))

@@ -38,16 +38,26 @@ constexpr int kNaMaxDev = 64;
 std::mutex g_na_mu;
 uint8_t* g_na_ptr[kNaMaxDev];  // device address of `scratch` on each device (null: not set up)
 
-// Per-device set-up: the array's address on the current device, and its contents zeroed once.
+// Per-device set-up: the array's address on the current device, and its contents zeroed once,
+// synchronously on `s` before the array is marked ready, so that a first call from any other
+// stream (or thread) finds it zero. A set-up cannot synchronise a stream under capture: a first
+// call made under graph capture is refused with a message (affx_init does the set-up beforehand).
 int noalloc_setup(int dev, hipStream_t s, uint8_t** out) {
   std::lock_guard<std::mutex> lk(g_na_mu);
   if (!g_na_ptr[dev]) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    int rc = check_hip(hipStreamIsCapturing(s, &cap), "hipStreamIsCapturing");
+    if (rc) return rc;
+    if (cap != hipStreamCaptureStatusNone)
+      return set_error(AFFX_ERR_ARG, "ffn_decode_noalloc: the scratch array of device %d is not set up; call "
+                       "affx_init on that device before capturing", dev);
     void* p = nullptr;
-    int rc = check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    rc = check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
     if (rc) return rc;
     if (!p) return set_error(AFFX_ERR_HIP, "ffn_decode_noalloc: no device address for the scratch array");
     hipLaunchKernelGGL(noalloc_zero_kernel, dim3(256), dim3(256), 0, s, (uint4*)p, kNaScratchBytes / 16);
     if ((rc = check_launch("noalloc_zero_kernel"))) return rc;
+    if ((rc = check_hip(hipStreamSynchronize(s), "noalloc set-up sync"))) return rc;
     g_na_ptr[dev] = (uint8_t*)p;
   }
   *out = g_na_ptr[dev];
@@ -63,9 +73,7 @@ namespace affx {
 int noalloc_init_device(int dev) {
   if (dev < 0 || dev >= kNaMaxDev) return AFFX_OK;  // such a device is refused by the entry itself
   uint8_t* p = nullptr;
-  int rc = noalloc_setup(dev, nullptr, &p);
-  if (rc) return rc;
-  return check_hip(hipStreamSynchronize(nullptr), "noalloc set-up sync");
+  return noalloc_setup(dev, nullptr, &p);
 }
 
 }  // namespace affx
@@ -95,6 +103,34 @@ int affx_expert_ffn_decode_noalloc(const affx_layer* L, const float* x, uint64_t
   if ((rc = noalloc_setup(dev, (hipStream_t)stream, &ws))) return rc;
   return affx_expert_ffn_decode(L, x, x_ts, x_ds, M, sel, w, K, y, y_ts, y_ds, accumulate, ws,
                                 (size_t)kNaScratchBytes, stream);
+}
+
+int affx_decode_noalloc_status(int reset, void* stream) {
+  int dev = 0;
+  int rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
+  if (rc) return rc;
+  if (dev < 0 || dev >= kNaMaxDev) return set_error(AFFX_ERR_ARG, "decode_noalloc_status: device id %d", dev);
+  uint8_t* ws = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(g_na_mu);
+    ws = g_na_ptr[dev];
+  }
+  if (!ws) return AFFX_OK;  // never set up: no call ran on this device
+  hipStream_t s = (hipStream_t)stream;
+  uint32_t err = 0;
+  rc = check_hip(hipMemcpyAsync(&err, ws + kSyncErrWord * 4, 4, hipMemcpyDeviceToHost, s), "noalloc status D2H");
+  if (!rc) rc = check_hip(hipStreamSynchronize(s), "noalloc status sync");
+  if (rc) return rc;
+  if (!err) return AFFX_OK;
+  if (reset) {
+    // the sync run again as after the set-up (a fill kernel: no memset node if the caller's stream
+    // is later captured)
+    hipLaunchKernelGGL(noalloc_zero_kernel, dim3(64), dim3(256), 0, s, (uint4*)ws, (uint64_t)(kSyncBytes / 16));
+    if ((rc = check_launch("noalloc_zero_kernel"))) return rc;
+    if ((rc = check_hip(hipStreamSynchronize(s), "noalloc status sync"))) return rc;
+  }
+  return set_error(AFFX_ERR_DEVICE, "decode_noalloc_status: an allocation-free decode launch gave up waiting for its "
+                   "workgroups (error bits 0x%x); its output was invalid%s", err, reset ? " (state reset)" : "");
 }
 
 }  // extern "C"

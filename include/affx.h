@@ -201,6 +201,30 @@ int affx_container_upload_layer(const affx_container* c, uint32_t layer, void* s
  * reference checks the same identity through its decode (src/gpu/expert_kernel.hip:594-619). */
 int affx_dequant_matrix(const affx_matrix* m, const void* codebook, float* out, void* stream);
 
+/* ---- single-matrix GEMV (the inner API aff-gpucheck binds) ---------------------------------- */
+
+/* y[r] += sum_i weights[i] * (W_i . x)[r] for n_mats matrices of one shape [rows x cols] given as
+ * a host array of affx_matrix (planes in device layout): expert_gemv_batch_hip with its arguments
+ * unchanged (src/gpu/expert_kernel_hip.h:152-153, expert_kernel.hip:2687-2722), the call of
+ * aff-gpucheck's GEMV bandwidth figure (tools/aff_gpucheck.cpp:544-548). weights: device
+ * f32[n_mats]; x: device f32[cols], 16-byte aligned; y: device f32[rows], accumulated; codebook:
+ * device uint32[2048] (the packed quads the reference passes through a float pointer). Launches
+ * of at most 32 matrices (the reference's kMaxBatch), each after the one before; every y element
+ * is summed in a fixed order. rows % 16 == 0, cols a multiple of 1024 up to 8192 (AFFX_DECLINED
+ * otherwise: the reference needs cols % 512 == 0). The activation enters the MFMA as three E4M3
+ * terms per element (relative error below 2^-12 per element); fp32 accumulation. Stream-ordered,
+ * no synchronisation. */
+int affx_expert_gemv_batch(const affx_matrix* mats, const float* weights, uint32_t n_mats,
+                           const void* codebook, const float* x, float* y, void* stream);
+
+/* y[r] += w * (W . x)[r] for one matrix, w a host scalar: expert_gemv_hip with its arguments
+ * unchanged (src/gpu/expert_kernel_hip.h:147-148, expert_kernel.hip:2810-2819), the per-matrix
+ * check of aff-gpucheck (tools/aff_gpucheck.cpp:278). As the reference's, it synchronises the
+ * stream before returning (y is ready); unlike it, it allocates nothing (w travels in the kernel
+ * arguments instead of a device singleton). */
+int affx_expert_gemv(const affx_matrix* m, const void* codebook, const float* x, float w, float* y,
+                     void* stream);
+
 /* ---- decode: M <= 8 tokens, fused gate/up -> SwiGLU -> down -> weighted combine ------------- */
 
 /* Workspace bytes affx_expert_ffn_decode needs for m tokens with top-k routing. The workspace
@@ -249,12 +273,22 @@ int affx_expert_ffn_decode(const affx_layer* layer, const float* x, uint64_t x_t
  * by the first call on a device) and shared by every call on that GPU, so calls that overlap on
  * one GPU (other streams, other threads) race. Serves m_tokens <= 8, m_tokens * top_k <= 64,
  * hidden <= 4096, inter <= 2048; larger sizes return AFFX_ERR_ARG with a message. Calls no
- * hipMalloc, hipFree or allocating routine. affx_decode_status does not see its array: a wait
- * that gave up is invisible here (the workspace entry reports it). */
+ * hipMalloc, hipFree or allocating routine. The set-up zeroes the array and synchronises once;
+ * a first call on a device made under graph capture (which cannot synchronise) is refused with a
+ * message: call affx_init on that device before capturing. A launch whose workgroups gave up
+ * waiting for each other is reported by affx_decode_noalloc_status, as the workspace entry's by
+ * affx_decode_status. */
 int affx_expert_ffn_decode_noalloc(const affx_layer* layer, const float* x, uint64_t x_tok_stride,
                                    uint64_t x_dim_stride, uint32_t m_tokens, const uint32_t* sel,
                                    const float* w, uint32_t top_k, float* y, uint64_t y_tok_stride,
                                    uint64_t y_dim_stride, int accumulate, void* stream);
+
+/* affx_decode_status for the current device's allocation-free decode array (no counterpart in the
+ * reference; for the callers affx_expert_ffn_decode_noalloc serves): AFFX_OK, or AFFX_ERR_DEVICE
+ * when a launch on the array gave up waiting for its workgroups (its output was invalid); reset = 1
+ * then zeroes the array's sync run (with a fill kernel on `stream`) so the next call is right.
+ * Copies 4 bytes to the host and synchronises `stream`. */
+int affx_decode_noalloc_status(int reset, void* stream);
 
 /* out[h] += sum_k weights[k] * FFN_k(x)[h] for one token through n_experts experts given as a
  * host array of per-matrix device pointers (planes in device layout): expert_ffn_hip with its

@@ -159,11 +159,12 @@ int run_decode(int argc, char** argv) {
                                        ws.data(), wsb, nullptr)
               : affx_expert_ffn_decode(&abi, x.data(), hidden, 1, M, sel.data(), w.data(), K, y.data(), hidden, 1, 0,
                                        ws.data(), wsb, nullptr);
-    // the sync run (counters, error bits, release flags: everything before the plan) is zero again
+    // the sync run's counter, error bits and release flags are zero again (the one-pass kernel's
+    // epoch and publish flags advance from launch to launch)
     uint32_t sync[3];
     memcpy(sync, ws.data(), sizeof(sync));
     uint32_t nonzero = 0;
-    for (size_t i = 0; i < 256 + 256 * 128; ++i) nonzero += ws[i] != 0;
+    for (size_t i = 0; i < kSyncRunBytes; ++i) nonzero += ws[i] != 0 && i / 4 != kEpochWord;
     same = memcmp(y.data(), y2.data(), y.size() * 4) == 0 && nonzero == 0;
     printf("fused: identical to staged=%d counters=%u,%u,%u nonzero_sync_bytes=%u\n", (int)same, sync[0], sync[1],
            sync[2], nonzero);
@@ -327,6 +328,38 @@ int run_ffnptr(int argc, char** argv) {
   const double e = rel_l2(y, yref);
   printf("ffnptr rc=%d identical to staged=%d rel_l2=%.3e %s\n", rc, (int)same, e, rc ? affx_last_error() : "");
   return rc == 0 && same && e <= 1e-3 ? 0 : 1;
+}
+
+// The single-matrix GEMV entries against the oracle's GEMV: every down matrix of n experts (rows
+// hidden, cols inter) through affx_expert_gemv_batch with per-matrix weights, and the first one
+// through affx_expert_gemv with a host weight, both accumulating into a nonzero y.
+int run_gemv(int argc, char** argv) {
+  const uint32_t hidden = atoi(argv[2]), inter = atoi(argv[3]), n = atoi(argv[4]);
+  std::mt19937_64 rng(atoi(argv[5]));
+  Layer L(hidden, inter, n, rng);
+  std::vector<affx_matrix> mats(n);
+  for (uint32_t k = 0; k < n; ++k) {
+    const uint8_t* d = L.dev.data() + (uint64_t)k * L.stride;
+    mats[k] = affx_matrix{d + L.off[6], d + L.off[7], d + L.off[8], hidden, inter};
+  }
+  std::normal_distribution<float> nd;
+  std::vector<float> x(inter), w(n), y(hidden), yref(hidden), y1(hidden), y1ref(hidden);
+  for (auto& v : x) v = nd(rng);
+  for (uint32_t k = 0; k < n; ++k) w[k] = 0.2f + 0.11f * k;
+  for (uint32_t h = 0; h < hidden; ++h) y[h] = yref[h] = y1[h] = y1ref[h] = 0.1f * nd(rng);
+  int rc = affx_expert_gemv_batch(mats.data(), w.data(), n, L.cb.data(), x.data(), y.data(), nullptr);
+  if (rc == 0) rc = affx_expert_gemv(&mats[0], L.cb.data(), x.data(), 0.75f, y1.data(), nullptr);
+  for (uint32_t k = 0; k < n; ++k) {
+    const uint8_t* ex = L.cont.data() + (uint64_t)k * L.stride;
+    orc_expert_gemv(ex + L.off[6], ex + L.off[7], (const uint16_t*)(ex + L.off[8]), hidden, inter, L.cbf.data(),
+                    x.data(), w[k], yref.data());
+    if (k == 0)
+      orc_expert_gemv(ex + L.off[6], ex + L.off[7], (const uint16_t*)(ex + L.off[8]), hidden, inter, L.cbf.data(),
+                      x.data(), 0.75f, y1ref.data());
+  }
+  const double e = rel_l2(y, yref), e1 = rel_l2(y1, y1ref);
+  printf("gemv rc=%d batch rel_l2=%.3e single rel_l2=%.3e %s\n", rc, e, e1, rc ? affx_last_error() : "");
+  return rc == 0 && e <= 1e-3 && e1 <= 1e-3 ? 0 : 1;
 }
 
 // The device router against the oracle's: token-major and dim-major logits, both rules, a
@@ -592,7 +625,15 @@ int run_timeout(int argc, char** argv) {
   std::vector<uint8_t> ws(wsb, 0);
   affx_engine_ctx ctx{&abi, 1, dx.data(), db.data(), nb, ws.data(), wsb, nullptr};
   std::vector<uint8_t> handled(M * K, 0);
+  // bytes of the sync run that every launch (and every reset) leaves zero: all but the one-pass
+  // kernel's epoch and publish flags
   auto sync_nonzero = [&]() {
+    uint32_t z = 0;
+    for (uint32_t i = 0; i < kSyncRunBytes; ++i) z += ws[i] != 0 && i / 4 != kEpochWord;
+    return z;
+  };
+  // all of it, epoch and publish flags included: zero right after a reset
+  auto run_nonzero = [&]() {
     uint32_t z = 0;
     for (uint32_t i = 0; i < kSyncBytes; ++i) z += ws[i] != 0;
     return z;
@@ -614,8 +655,9 @@ int run_timeout(int argc, char** argv) {
                                   ws.data(), wsb, nullptr);
   const int st1 = affx_decode_status(ws.data(), 1, nullptr);
   const int st2 = affx_decode_status(ws.data(), 0, nullptr);
-  printf("direct with spin limit 0: rc=%d status=%d then %d\n", rc, st1, st2);
-  ok = ok && rc == 0 && st1 == AFFX_ERR_DEVICE && st2 == AFFX_OK;
+  printf("direct with spin limit 0: rc=%d status=%d then %d, sync run nonzero after the reset %u\n", rc, st1, st2,
+         run_nonzero());
+  ok = ok && rc == 0 && st1 == AFFX_ERR_DEVICE && st2 == AFFX_OK && run_nonzero() == 0;
   // 3. normal waits again: the hook takes every pair and the result is right
   unsetenv("AFFX_DECODE_SPIN_LIMIT");
   std::fill(db.begin(), db.end(), 0.f);
@@ -628,6 +670,22 @@ int run_timeout(int argc, char** argv) {
   printf("hook after reset: returned %u of %u, rel_l2=%.3e, sync bytes nonzero %u, status %d\n", got, M * K, e,
          sync_nonzero(), affx_decode_status(ws.data(), 0, nullptr));
   ok = ok && got == M * K && e <= 1e-3 && sync_nonzero() == 0;
+  // 4. the allocation-free entry: a launch that gives up is reported by its own status entry,
+  // the reset clears the array's sync run, and the next call is right
+  setenv("AFFX_DECODE_SPIN_LIMIT", "0", 1);
+  std::vector<float> yn(M * hidden, 0.f);
+  rc = affx_expert_ffn_decode_noalloc(&abi, x.data(), hidden, 1, M, sel.data(), w.data(), K, yn.data(), hidden, 1, 0,
+                                      nullptr);
+  const int na1 = affx_decode_noalloc_status(1, nullptr);
+  const int na2 = affx_decode_noalloc_status(0, nullptr);
+  unsetenv("AFFX_DECODE_SPIN_LIMIT");
+  int rc2 = affx_expert_ffn_decode_noalloc(&abi, x.data(), hidden, 1, M, sel.data(), w.data(), K, yn.data(), hidden,
+                                           1, 0, nullptr);
+  const int na3 = affx_decode_noalloc_status(0, nullptr);
+  const double en = rel_l2(yn, yref);
+  printf("noalloc with spin limit 0: rc=%d status=%d then %d; next call rc=%d rel_l2=%.3e status %d\n", rc, na1, na2,
+         rc2, en, na3);
+  ok = ok && rc == 0 && na1 == AFFX_ERR_DEVICE && na2 == AFFX_OK && rc2 == 0 && en <= 1e-3 && na3 == AFFX_OK;
   printf("timeout path ok=%d\n", (int)ok);
   return ok ? 0 : 1;
 }
@@ -711,6 +769,7 @@ int main(int argc, char** argv) {
   if (cmd == "route" && argc >= 6) return run_route(argc, argv);
   if (cmd == "shared" && argc >= 7) return run_shared(argc, argv);
   if (cmd == "fit" && argc >= 7) return run_fit(argc, argv);
+  if (cmd == "gemv" && argc >= 6) return run_gemv(argc, argv);
   fprintf(stderr, "usage: see header\n");
   return 2;
 }

@@ -103,6 +103,13 @@ def test_reader_refuses_bad_files(L, container, tmp_path):
     bad = raw.copy()
     bad[layer_dir + 24 + 16] = 32                               # gate.quant = AFF_Q2P875
     refused(bad, "quad-format")
+    # a layer stride whose product with the expert count wraps past 2^64 to a small extent
+    n_exp = int(raw[layer_dir + 4:layer_dir + 8].view(np.uint32)[0])
+    assert n_exp >= 2
+    wrap = -(-(1 << 64) // n_exp)                               # n_exp * wrap = 2^64 + (< n_exp)
+    bad = raw.copy()
+    bad[layer_dir + 16:layer_dir + 24] = np.array([wrap], np.uint64).view(np.uint8)
+    refused(bad, "corrupt layer descriptor")
     rc, h = _open(L, str(tmp_path / "missing.aff"))
     assert rc != 0
 

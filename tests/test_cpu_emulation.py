@@ -16,7 +16,7 @@ CLANGXX = "/opt/rocm/llvm/bin/clang++"
 
 # the library sources the emulator links, each its own translation unit as in the device build
 SOURCES = ["affx_layout.hip", "affx_decode.hip", "affx_fused.hip", "affx_quant.hip", "affx_grouped.hip",
-           "affx_api.hip", "affx_noalloc.hip", "affx_route.hip", "affx_shared.hip", "affx_fit.hip"]
+           "affx_api.hip", "affx_noalloc.hip", "affx_route.hip", "affx_shared.hip", "affx_fit.hip", "affx_gemv.hip"]
 
 
 @pytest.fixture(scope="module")
@@ -47,7 +47,10 @@ def emu(tmp_path_factory):
 def run(emu, *args, timeout=900, cus=4):
     # cus: compute units of the emulated device; the fused decode sizes its grid (all workgroups
     # resident, run concurrently here) to it
-    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=0", AFFX_EMU_CUS=str(cus))
+    # (a generous bound on the decode's waits: an emulated waiter polls with a thread yield, and
+    # on a loaded host 2^22 yields can pass before the emulated workgroups it waits for are done)
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=0", AFFX_EMU_CUS=str(cus),
+               AFFX_DECODE_SPIN_LIMIT=str(1 << 30))
     r = subprocess.run([emu, *map(str, args)], cwd=ROOT, capture_output=True, text=True,
                        timeout=timeout, env=env)
     out = r.stdout + r.stderr
@@ -72,14 +75,18 @@ CASES = {
     "quant": (("quant", 4, 256, 3), 4),
     "grouped": (("grouped", 1024, 1024, 5, 12, 3, 4, 1), 4),
     "timeout": (("timeout", 1024, 1024, 6, 2, 3, 8), 4),
+    # batch 1 in one pass (6 workgroups hold the 64 gate/up items): per-workgroup publish flags
+    "timeout_m1": (("timeout", 1024, 1024, 6, 1, 1, 8), 6),
     "slots": (("slots", 1024, 1024, 4, 6, 2, 9), 4),
     "ffnptr": (("ffnptr", 1024, 1024, 3, 12), 4),
     "route": (("route", 21, 100, 6, 4), 4),
+    # the single-matrix GEMV entries: 3 down matrices (1024 x 2048) in one batch, one alone
+    "gemv": (("gemv", 1024, 2048, 3, 5), 4),
     "shared": (("shared", 1024, 1024, 6, 40, 5), 4),
 }
 # longest first, so the three lanes finish together
 ORDER = ["decode_m8_wide", "decode_m6_dm16", "decode_m6_two_cg", "slots", "shared", "decode_m1_single", "grouped",
-         "decode_m1", "ffnptr", "quant", "timeout", "route", "decode_allpad", "dequant"]
+         "decode_m1", "ffnptr", "quant", "timeout", "timeout_m1", "route", "gemv", "decode_allpad", "dequant"]
 
 
 @pytest.fixture(scope="module")
@@ -147,6 +154,13 @@ def test_decode_wait_give_up_fails_loudly(runs):
     assert "timeout path ok=1" in out, out
 
 
+def test_decode_wait_give_up_fails_loudly_batch1(runs):
+    # the same on the one-pass batch-1 kernel, whose waiters poll every workgroup's publish flag:
+    # the give-up is reported, the reset clears the epoch and the flags, the next call is right
+    out = result(runs, "timeout_m1")
+    assert "timeout path ok=1" in out, out
+
+
 def test_grouped_slot_list_emulated(runs):
     # the slot-list entry: bit-identical to the routes entry on the list the routes build, and
     # within tolerance on a reordered list
@@ -157,6 +171,11 @@ def test_grouped_slot_list_emulated(runs):
 def test_expert_ffn_pointer_table_emulated(runs):
     out = result(runs, "ffnptr")
     assert "identical to staged=1" in out, out
+
+
+def test_gemv_emulated(runs):
+    out = result(runs, "gemv")
+    assert "gemv rc=0" in out, out
 
 
 def test_route_emulated(runs):

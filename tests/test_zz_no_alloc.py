@@ -1,7 +1,8 @@
 """The allocation-free decode entry (affx_expert_ffn_decode_noalloc) against the workspace entry
-(affx_expert_ffn_decode), through the C-ABI: bit-identical outputs on two calls in a row, the
-second smaller than the first (the scratch array keeps the last call's contents), and a clear
-refusal of a size beyond the array."""
+(affx_expert_ffn_decode), through the C-ABI: bit-identical outputs on calls in a row, each smaller
+than the one before (the scratch array keeps the last call's contents); the call captured in a
+HIP graph and replayed with new inputs, every replay bit-identical to the workspace decode and no
+device memory taken; its status entry; and a clear refusal of a size beyond the array."""
 import ctypes as C
 
 import numpy as np
@@ -72,3 +73,59 @@ def test_noalloc_decode_refuses_oversize(ax, c1_codebook):
     y = torch.zeros((8, hidden), device="cuda")
     assert _call_noalloc(pool, x, sel, w, y) == AFFX_ERR_ARG
     assert "exceed the scratch array" in last_error()
+
+
+def test_noalloc_decode_graph_replays_allocate_nothing(ax, c1_codebook):
+    """The stated use: the call under graph capture. Static input buffers, three replays with new
+    inputs copied in between (batch 1, the one-pass kernel, and M = 5), each replay equal bit for
+    bit to the workspace decode of the same inputs; the device's free memory is the same before
+    the first call and after the last replay (the entry allocates nothing); the status entry
+    reports no give-up."""
+    from affinity_amd._lib import last_error, lib
+    hidden, inter, n, k = 4096, 2048, 256, 6
+    pool = _pool(ax, c1_codebook, n, hidden, inter, seed=91)
+    rng = np.random.default_rng(92)
+    for M in (1, 5):
+        x = torch.zeros((M, hidden), device="cuda")
+        sel = torch.zeros((M, k), dtype=torch.int32, device="cuda")
+        w = torch.zeros((M, k), device="cuda")
+        y = torch.zeros((M, hidden), device="cuda")
+        ws = ax.DecodeWorkspace(M, k, hidden, inter)
+        want = torch.zeros((M, hidden), device="cuda")
+        inputs = []
+        for rep in range(4):
+            inputs.append((torch.from_numpy((rng.standard_normal((M, hidden)) * 0.7).astype(np.float32)).cuda(),
+                           torch.from_numpy(np.stack([rng.choice(n, k, replace=False) for _ in range(M)])
+                                            .astype(np.int32)).cuda(),
+                           torch.from_numpy(rng.uniform(0.05, 1.0, (M, k)).astype(np.float32)).cuda()))
+        torch.cuda.synchronize()
+        free0 = torch.cuda.mem_get_info()[0]
+        # eager calls first (the entry's first call on a device may set up, outside capture)
+        x.copy_(inputs[0][0]); sel.copy_(inputs[0][1]); w.copy_(inputs[0][2])
+        for _ in range(3):
+            assert _call_noalloc(pool, x, sel, w, y) == 0, last_error()
+        torch.cuda.synchronize()
+        assert torch.cuda.mem_get_info()[0] == free0, "an eager call of the allocation-free entry took device memory"
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            rc = _call_noalloc(pool, x, sel, w, y)
+        assert rc == 0, last_error()
+        torch.cuda.synchronize()
+        free0 = torch.cuda.mem_get_info()[0]   # (the instantiated graph's own memory excluded)
+        for rep in range(1, 4):
+            xi, si, wi = inputs[rep]
+            x.copy_(xi); sel.copy_(si); w.copy_(wi)
+            y.fill_(float("nan"))
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            ax.expert_ffn_decode(pool, xi, si, wi, y=want, workspace=ws)
+            torch.cuda.synchronize()
+            assert torch.equal(y, want), (M, rep)
+        torch.cuda.synchronize()
+        assert torch.cuda.mem_get_info()[0] == free0, "a replay took device memory"
+        del g
+        assert lib().affx_decode_noalloc_status(0, None) == 0, last_error()
+        print(f"M={M}: three graph replays identical to the workspace decode, no device memory taken")
