@@ -96,6 +96,9 @@ _SIGS = {
                                  _vp, C.c_size_t, _vp], C.c_int),
     "affx_expert_ffn_grouped_slots": ([C.POINTER(AffxLayer), _vp, _vp, _u32, _vp, _vp, _vp, _vp, _vp, _u32, _vp,
                                        C.c_int, _vp, C.c_size_t, _vp], C.c_int),
+    "affx_expert_swiglu_quant": ([_vp, _vp, _vp, _vp, _vp, _u32, _u32, C.c_float, _vp], C.c_int),
+    "affx_expert_scatter_slots": ([_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp], C.c_int),
+    "affx_expert_gather_tokens": ([_vp, _vp, _vp, _u32, _u32, _u32, _vp], C.c_int),
     "affx_route_topk": ([_vp, _u64, _u64, _vp, _u32, _u32, _u32, C.c_int, C.c_int, C.c_float, _vp, _vp, _vp],
                         C.c_int),
     "affx_dense_fp8_to_device_layout": ([_vp, _vp, _u64, _u64, _vp], C.c_int),

@@ -370,6 +370,38 @@ int affx_expert_ffn_grouped_slots(const affx_layer* layer, const void* x, const 
                                   uint32_t n_slots, float* y, int accumulate, void* workspace,
                                   size_t workspace_bytes, void* stream);
 
+/* ---- the reference's separable batch-pipeline steps ------------------------------------------
+ * For a caller that drives the reference's own step sequence (run_batch_device's prefill arm:
+ * gather -> W8A8 GEMM -> SwiGLU + requantise -> W8A8 GEMM -> fixed-order scatter,
+ * src/gpu/static_placement.hip:1856-1914). affx_expert_ffn_grouped(_slots) fuses these into its
+ * grouped GEMM and combine; these keep the reference's formats. Device pointers, stream-ordered,
+ * no synchronisation. */
+
+/* SwiGLU times the router weight, then the E4M3 requantise: expert_swiglu_quant_hip with its
+ * arguments unchanged (src/gpu/expert_kernel_hip.h:238-240, expert_kernel.hip:862-931, 2822-2835).
+ * g, u: bf16 [dim][total] (dim-major, one column per slot); w: f32 [total] or NULL (weight 1);
+ * v = silu(min(g, L)) * clamp(u, -L, L) * w (no clamp when limit <= 0). Per (slot, 128-row band):
+ * scales[slot][band] = max |v| / 448 (1 when the band is zero), out[slot][k] (E4M3, slot-major
+ * [total][dim]) = E4M3(clamp(v / scale, +-448)), round to nearest even. dim % 128 == 0, out
+ * 16-byte aligned (AFFX_ERR_ARG otherwise). */
+int affx_expert_swiglu_quant(const uint16_t* g, const uint16_t* u, const float* w, uint8_t* out,
+                             float* scales, uint32_t dim, uint32_t total, float limit, void* stream);
+
+/* Fixed-order reduction of a [dim][total] bf16 slot arena into the chunk's f32 accumulator:
+ * expert_scatter_slots_hip with its arguments unchanged (src/gpu/expert_kernel_hip.h:249-251,
+ * expert_kernel.hip:935-947, 2837-2843). block[h * nb_stride + t] += sum over i in
+ * run[t] .. run[t+1]-1, in that order from zero, of y[h * total + ord[i]]; tokens whose run is
+ * empty are not written. Deterministic (no atomics). dim <= 65535. */
+int affx_expert_scatter_slots(const uint16_t* y, float* block, const uint32_t* ord, const uint32_t* run,
+                              uint32_t dim, uint32_t nb_tok, uint32_t nb_stride, uint32_t total,
+                              void* stream);
+
+/* nt token columns of a dim-major [dim][nb] arena into a compact [dim][nt] tile:
+ * dst[c * nt + t] = src[c * nb + tok[t]]. expert_gather_tokens_hip with its arguments unchanged
+ * (src/gpu/expert_kernel_hip.h:255-256, expert_kernel.hip:828-835, 1673-1680). */
+int affx_expert_gather_tokens(const float* src, float* dst, const uint32_t* tok, uint32_t dim,
+                              uint32_t nb, uint32_t nt, void* stream);
+
 /* ---- routing on the device ------------------------------------------------------------------ */
 
 #define AFFX_ROUTE_ENGINE 0  /* the engine router: sqrtsoftplus scores, bias for selection only */

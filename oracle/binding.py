@@ -96,6 +96,11 @@ class Oracle:
                                         _f32p, _f32p]
         L.orc_hc_expand.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, C.c_uint32, C.c_uint32]
         L.orc_hc_add.argtypes = [_f32p, _f32p, C.c_uint32]
+        L.orc_f32_to_e4m3.argtypes = [C.c_float]
+        L.orc_f32_to_e4m3.restype = C.c_uint8
+        L.orc_swiglu_quant.argtypes = [_u16p, _u16p, _f32p, _u8p, _f32p, C.c_uint32, C.c_uint32, C.c_float]
+        L.orc_scatter_slots.argtypes = [_u16p, _f32p, _u32p, _u32p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32]
+        L.orc_gather_tokens.argtypes = [_f32p, _f32p, _u32p, C.c_uint32, C.c_uint32, C.c_uint32]
 
     # -- threads ---------------------------------------------------------------------------
     def set_threads(self, n: int) -> None:
@@ -110,6 +115,36 @@ class Oracle:
 
     def f32_to_bf16(self, f: float) -> int:
         return int(self.lib.orc_f32_to_bf16(f))
+
+    def f32_to_e4m3(self, f: float) -> int:
+        return int(self.lib.orc_f32_to_e4m3(f))
+
+    # -- the reference's separable batch-pipeline steps ----------------------------------------
+    def swiglu_quant(self, g: np.ndarray, u: np.ndarray, w, limit: float):
+        """g, u: uint16 (bf16 bits) [dim][total]; w f32 [total] or None -> (out u8 [total][dim],
+        scales f32 [total][dim/128])."""
+        dim, total = g.shape
+        out = np.zeros((total, dim), np.uint8)
+        scales = np.zeros((total, dim // 128), np.float32)
+        wp = None if w is None else _p(np.ascontiguousarray(w, np.float32), _f32p)
+        self.lib.orc_swiglu_quant(_p(np.ascontiguousarray(g, np.uint16), _u16p), _p(np.ascontiguousarray(u, np.uint16), _u16p),
+                                  wp, _p(out, _u8p), _p(scales, _f32p), dim, total, float(limit))
+        return out, scales
+
+    def scatter_slots(self, y: np.ndarray, block: np.ndarray, ord_: np.ndarray, run: np.ndarray, nb_tok: int):
+        dim, total = y.shape
+        self.lib.orc_scatter_slots(_p(np.ascontiguousarray(y, np.uint16), _u16p), _p(block, _f32p),
+                                   _p(np.ascontiguousarray(ord_, np.uint32), _u32p),
+                                   _p(np.ascontiguousarray(run, np.uint32), _u32p), dim, nb_tok, block.shape[1], total)
+        return block
+
+    def gather_tokens(self, src: np.ndarray, tok: np.ndarray) -> np.ndarray:
+        dim, nb = src.shape
+        nt = tok.size
+        dst = np.zeros((dim, nt), np.float32)
+        self.lib.orc_gather_tokens(_p(np.ascontiguousarray(src, np.float32), _f32p), _p(dst, _f32p),
+                                   _p(np.ascontiguousarray(tok, np.uint32), _u32p), dim, nb, nt)
+        return dst
 
     def e4m3_nearest(self, f: float) -> int:
         return int(self.lib.orc_e4m3_nearest(f))

@@ -752,3 +752,78 @@ void orc_hc_expand(float* out_hc, const float* block, const float* residual_hc, 
 void orc_hc_add(float* hc, const float* block, uint32_t n_embd) {
   for (uint32_t d = 0; d < n_embd; ++d) hc[d] += block[d];
 }
+
+/* ------------------------------------------------------------------------------------------ */
+/* the reference's separable batch-pipeline steps                                              */
+/* ------------------------------------------------------------------------------------------ */
+
+/* f32 -> E4M3 (OCP fn) to nearest, ties to the even code, for |v| <= 448: the conversion the
+ * reference's requantise calls (v_cvt_pk_fp8_f32) on inputs it has clamped to +-448
+ * (src/gpu/expert_kernel.hip:913-924). Chooses the nearer of the two neighbouring codes by value,
+ * so it follows from the value table alone. */
+uint8_t orc_f32_to_e4m3(float v) {
+  const float* t = e4m3_table();
+  const uint8_t s = signbit(v) ? 0x80 : 0x00;
+  const float a = fabsf(v);
+  int lo = 0;
+  for (int c = 1; c <= 0x7E; ++c)
+    if (t[c] <= a) lo = c;
+  if (lo == 0x7E) return s | 0x7E;
+  const float dl = a - t[lo], dh = t[lo + 1] - a;
+  const int c = dl < dh ? lo : dh < dl ? lo + 1 : ((lo & 1) ? lo + 1 : lo);
+  return s | (uint8_t)c;
+}
+
+/* expert_swiglu_quant_kernel, src/gpu/expert_kernel.hip:862-931: g, u bf16 [dim][total]
+ * (dim-major), w f32 [total] or NULL; v = silu(min(g, L)) * clamp(u, -L, L) * w (no clamp when
+ * L <= 0, fminf/fmaxf forms), then per (slot, 128-row band) scale = max |v| / 448 (1 when zero),
+ * scales [total][dim / 128], out E4M3 [total][dim] = e4m3(clamp(v * (1 / scale), -448, 448)). */
+void orc_swiglu_quant(const uint16_t* g, const uint16_t* u, const float* w, uint8_t* out, float* scales,
+                      uint32_t dim, uint32_t total, float limit) {
+  const uint32_t nkb = dim >> 7;
+  float v[128];
+  for (uint32_t sl = 0; sl < total; ++sl) {
+    const float wv = w ? w[sl] : 1.0f;
+    for (uint32_t kb = 0; kb < nkb; ++kb) {
+      float m = 0.0f;
+      for (uint32_t k = 0; k < 128; ++k) {
+        const size_t o = (size_t)(kb * 128 + k) * total + sl;
+        float gv = orc_bf16_to_f32(g[o]), uv = orc_bf16_to_f32(u[o]);
+        if (limit > 0.0f) {
+          gv = fminf(gv, limit);
+          uv = fminf(limit, fmaxf(-limit, uv));
+        }
+        v[k] = (gv / (1.0f + expf(-gv))) * uv * wv;
+        m = fmaxf(m, fabsf(v[k]));
+      }
+      const float sc = m > 0.0f ? m * (1.0f / 448.0f) : 1.0f;
+      scales[(size_t)sl * nkb + kb] = sc;
+      const float inv = 1.0f / sc;
+      for (uint32_t k = 0; k < 128; ++k)
+        out[(size_t)sl * dim + kb * 128 + k] = orc_f32_to_e4m3(fminf(fmaxf(v[k] * inv, -448.0f), 448.0f));
+    }
+  }
+}
+
+/* expert_scatter_slots_kernel, src/gpu/expert_kernel.hip:935-947: block[h][t] += (the float sum
+ * from zero, in ord order, of bf16 y[h][ord[i]] for i in run[t] .. run[t+1]-1); tokens with an
+ * empty run are left as they are. */
+void orc_scatter_slots(const uint16_t* y, float* block, const uint32_t* ord, const uint32_t* run, uint32_t dim,
+                       uint32_t nb_tok, uint32_t nb_stride, uint32_t total) {
+  for (uint32_t h = 0; h < dim; ++h) {
+    const uint16_t* row = y + (size_t)h * total;
+    for (uint32_t t = 0; t < nb_tok; ++t) {
+      const uint32_t a = run[t], b = run[t + 1];
+      if (a == b) continue;
+      float acc = 0.0f;
+      for (uint32_t i = a; i < b; ++i) acc += orc_bf16_to_f32(row[ord[i]]);
+      block[(size_t)h * nb_stride + t] += acc;
+    }
+  }
+}
+
+/* expert_gather_tokens_kernel, src/gpu/expert_kernel.hip:828-835: dst[c][t] = src[c][tok[t]]. */
+void orc_gather_tokens(const float* src, float* dst, const uint32_t* tok, uint32_t dim, uint32_t nb, uint32_t nt) {
+  for (uint32_t c = 0; c < dim; ++c)
+    for (uint32_t t = 0; t < nt; ++t) dst[(size_t)c * nt + t] = src[(size_t)c * nb + tok[t]];
+}

@@ -95,6 +95,14 @@ void orc_hc_expand(float* out_hc, const float* block, const float* residual_hc, 
                    const float* comb, uint32_t n_embd, uint32_t n_hc);
 void orc_hc_add(float* hc, const float* block, uint32_t n_embd);
 
+/* ---- the reference's separable batch-pipeline steps ---- */
+uint8_t orc_f32_to_e4m3(float v);
+void orc_swiglu_quant(const uint16_t* g, const uint16_t* u, const float* w, uint8_t* out, float* scales,
+                      uint32_t dim, uint32_t total, float limit);
+void orc_scatter_slots(const uint16_t* y, float* block, const uint32_t* ord, const uint32_t* run, uint32_t dim,
+                       uint32_t nb_tok, uint32_t nb_stride, uint32_t total);
+void orc_gather_tokens(const float* src, float* dst, const uint32_t* tok, uint32_t dim, uint32_t nb, uint32_t nt);
+
 #ifdef __cplusplus
 }
 #endif

@@ -35,6 +35,7 @@ extern "C" {
 #include "../../oracle/oracle.h"
 }
 
+#include <algorithm>
 #include <random>
 #include <string>
 
@@ -360,6 +361,50 @@ int run_gemv(int argc, char** argv) {
   const double e = rel_l2(y, yref), e1 = rel_l2(y1, y1ref);
   printf("gemv rc=%d batch rel_l2=%.3e single rel_l2=%.3e %s\n", rc, e, e1, rc ? affx_last_error() : "");
   return rc == 0 && e <= 1e-3 && e1 <= 1e-3 ? 0 : 1;
+}
+
+// The separable batch-pipeline steps against the oracle: gather and scatter bit for bit, the
+// SwiGLU requantise with equal scales and bytes (the emulation's expf is the oracle's).
+int run_steps(int argc, char** argv) {
+  const uint32_t dim = atoi(argv[2]), nb_tok = atoi(argv[3]);
+  std::mt19937_64 rng(atoi(argv[4]));
+  std::normal_distribution<float> nd;
+  // gather
+  const uint32_t nb = nb_tok + 3, nt = nb_tok / 2 + 1;
+  std::vector<float> src((size_t)dim * nb), dst((size_t)dim * nt, -1.f), dref((size_t)dim * nt);
+  std::vector<uint32_t> tok(nt);
+  for (auto& v : src) v = nd(rng);
+  for (auto& t : tok) t = rng() % nb;
+  int rc = affx_expert_gather_tokens(src.data(), dst.data(), tok.data(), dim, nb, nt, nullptr);
+  orc_gather_tokens(src.data(), dref.data(), tok.data(), dim, nb, nt);
+  bool ok = rc == 0 && memcmp(dst.data(), dref.data(), dst.size() * 4) == 0;
+  // scatter
+  std::vector<uint32_t> run(nb_tok + 1, 0);
+  for (uint32_t t = 0; t < nb_tok; ++t) run[t + 1] = run[t] + (t == 1 ? 0 : (uint32_t)(rng() % 5));
+  const uint32_t total = run[nb_tok];
+  std::vector<uint32_t> ordv(total);
+  for (uint32_t i = 0; i < total; ++i) ordv[i] = i;
+  std::shuffle(ordv.begin(), ordv.end(), rng);
+  std::vector<uint16_t> y((size_t)dim * total);
+  for (auto& v : y) v = bf16(nd(rng));
+  std::vector<float> blk((size_t)dim * nb), bref;
+  for (auto& v : blk) v = nd(rng);
+  bref = blk;
+  if (rc == 0) rc = affx_expert_scatter_slots(y.data(), blk.data(), ordv.data(), run.data(), dim, nb_tok, nb, total, nullptr);
+  orc_scatter_slots(y.data(), bref.data(), ordv.data(), run.data(), dim, nb_tok, nb, total);
+  ok = ok && rc == 0 && memcmp(blk.data(), bref.data(), blk.size() * 4) == 0;
+  // swiglu + requantise over the slot arena
+  std::vector<uint16_t> g((size_t)dim * total), u((size_t)dim * total);
+  for (auto& v : g) v = bf16(2.5f * nd(rng));
+  for (auto& v : u) v = bf16(2.5f * nd(rng));
+  std::vector<float> w(total), sc((size_t)total * (dim / 128)), scr(sc.size());
+  for (auto& v : w) v = 0.05f + (float)(rng() % 1000) / 1000.f;
+  std::vector<uint8_t> out((size_t)total * dim), outr(out.size());
+  if (rc == 0) rc = affx_expert_swiglu_quant(g.data(), u.data(), w.data(), out.data(), sc.data(), dim, total, 10.f, nullptr);
+  orc_swiglu_quant(g.data(), u.data(), w.data(), outr.data(), scr.data(), dim, total, 10.f);
+  ok = ok && rc == 0 && memcmp(out.data(), outr.data(), out.size()) == 0 && memcmp(sc.data(), scr.data(), sc.size() * 4) == 0;
+  printf("steps rc=%d total=%u equal=%d %s\n", rc, total, (int)ok, rc ? affx_last_error() : "");
+  return ok ? 0 : 1;
 }
 
 // The device router against the oracle's: token-major and dim-major logits, both rules, a
@@ -770,6 +815,7 @@ int main(int argc, char** argv) {
   if (cmd == "shared" && argc >= 7) return run_shared(argc, argv);
   if (cmd == "fit" && argc >= 7) return run_fit(argc, argv);
   if (cmd == "gemv" && argc >= 6) return run_gemv(argc, argv);
+  if (cmd == "steps" && argc >= 5) return run_steps(argc, argv);
   fprintf(stderr, "usage: see header\n");
   return 2;
 }

@@ -225,11 +225,11 @@ inline float emu_e4m3(uint32_t b) {
   return s ? -f : f;
 }
 // hardware f32 -> E4M3 (OCP) conversion, round to nearest even, for the in-range values kernels
-// pass (|v| < 448)
+// pass (|v| <= 448, the largest finite E4M3)
 inline uint32_t emu_to_e4m3(float v) {
   const uint32_t s = (__float_as_uint(v) >> 24) & 0x80u;
   const float a = fabsf(v);
-  if (!(a < 448.f)) { fprintf(stderr, "cvt_pk_fp8_f32: out of range %g\n", v); abort(); }
+  if (!(a <= 448.f)) { fprintf(stderr, "cvt_pk_fp8_f32: out of range %g\n", v); abort(); }
   if (a < 0.015625f) return s | (uint32_t)rintf(a * 512.0f);
   const uint32_t au = __float_as_uint(a);
   int e = (int)(au >> 23) - 127;

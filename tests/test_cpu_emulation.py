@@ -16,7 +16,8 @@ CLANGXX = "/opt/rocm/llvm/bin/clang++"
 
 # the library sources the emulator links, each its own translation unit as in the device build
 SOURCES = ["affx_layout.hip", "affx_decode.hip", "affx_fused.hip", "affx_quant.hip", "affx_grouped.hip",
-           "affx_api.hip", "affx_noalloc.hip", "affx_route.hip", "affx_shared.hip", "affx_fit.hip", "affx_gemv.hip"]
+           "affx_api.hip", "affx_noalloc.hip", "affx_route.hip", "affx_shared.hip", "affx_fit.hip", "affx_gemv.hip",
+           "affx_steps.hip"]
 
 
 @pytest.fixture(scope="module")
@@ -82,11 +83,13 @@ CASES = {
     "route": (("route", 21, 100, 6, 4), 4),
     # the single-matrix GEMV entries: 3 down matrices (1024 x 2048) in one batch, one alone
     "gemv": (("gemv", 1024, 2048, 3, 5), 4),
+    # gather / scatter / SwiGLU requantise against the oracle (bounds checked)
+    "steps": (("steps", 256, 40, 3), 4),
     "shared": (("shared", 1024, 1024, 6, 40, 5), 4),
 }
 # longest first, so the three lanes finish together
 ORDER = ["decode_m8_wide", "decode_m6_dm16", "decode_m6_two_cg", "slots", "shared", "decode_m1_single", "grouped",
-         "decode_m1", "ffnptr", "quant", "timeout", "timeout_m1", "route", "gemv", "decode_allpad", "dequant"]
+         "decode_m1", "ffnptr", "quant", "timeout", "timeout_m1", "route", "gemv", "steps", "decode_allpad", "dequant"]
 
 
 @pytest.fixture(scope="module")
@@ -176,6 +179,11 @@ def test_expert_ffn_pointer_table_emulated(runs):
 def test_gemv_emulated(runs):
     out = result(runs, "gemv")
     assert "gemv rc=0" in out, out
+
+
+def test_separable_steps_emulated(runs):
+    out = result(runs, "steps")
+    assert "equal=1" in out, out
 
 
 def test_route_emulated(runs):

@@ -532,3 +532,90 @@ def test_hc_expand_closed_form_and_add(orc):
     wrong = np.stack([sum(comb[d * nh + s] * hc[s].astype(np.float64) for s in range(nh)) for d in range(nh)])
     assert np.max(np.abs(out - wrong)) > 1.0
     np.testing.assert_array_equal(orc.hc_add(hc[0], blk), hc[0] + blk)
+
+
+# ---- the reference's separable batch-pipeline steps ----------------------------------------------
+
+def test_f32_to_e4m3_pinned(orc):
+    """orc_f32_to_e4m3 against torch's float8_e4m3fn conversion (round to nearest even) on every
+    code's value, every midpoint between neighbouring codes, points just off the midpoints and
+    random values in +-448; a dropped tie rule or a wrong neighbour fails one of them."""
+    torch = pytest.importorskip("torch")
+    vals = np.array([orc.e4m3_to_float(c) for c in range(0x7F)], np.float32)
+    mids = (vals[:-1] + vals[1:]) / 2
+    off = np.concatenate([np.nextafter(mids, np.float32(0)), np.nextafter(mids, np.float32(1e9))])
+    rng = np.random.default_rng(6)
+    rnd = (rng.random(4000) * 2 - 1).astype(np.float32) * rng.choice([448, 8, 1 / 64], 4000).astype(np.float32)
+    x = np.concatenate([vals, mids, off, rnd]).astype(np.float32)
+    x = np.concatenate([x, -x])
+    got = np.array([orc.f32_to_e4m3(float(v)) for v in x], np.uint8)
+    want = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(got, want)
+    # ties really go to the even code (the midpoint above an odd code rounds up)
+    assert orc.f32_to_e4m3(1.0625) == 0x38 and orc.f32_to_e4m3(1.1875) == 0x3A
+
+
+def test_swiglu_quant_oracle_pinned(orc):
+    """orc_swiglu_quant against the pinned orc_swiglu (the reference's SwiGLU, bit-identical to
+    it) and orc_f32_to_e4m3: scale = max |v| / 448 per (slot, 128-row band), every byte the E4M3
+    of v / scale, the band maximum at +-448; with the router weight, without it (w NULL = 1), and
+    without the clamp (limit 0)."""
+    rng = np.random.default_rng(8)
+    dim, total = 256, 37
+    g = rng.normal(0, 3, (dim, total)).astype(np.float32)
+    u = rng.normal(0, 3, (dim, total)).astype(np.float32)
+    g[:128, 5] = 0.0                               # an all-zero band: scale 1, bytes 0
+    u[:128, 5] = 0.0
+    gb = (g.view(np.uint32) >> 16).astype(np.uint16)   # truncated to bf16 bits (any bf16 will do)
+    ub = (u.view(np.uint32) >> 16).astype(np.uint16)
+    gf = (gb.astype(np.uint32) << 16).view(np.float32)
+    uf = (ub.astype(np.uint32) << 16).view(np.float32)
+    w = (0.1 + rng.random(total)).astype(np.float32)
+    for wv, limit in ((w, 10.0), (None, 10.0), (w, 0.0)):
+        out, sc = orc.swiglu_quant(gb, ub, wv, limit)
+        a = np.zeros((dim, total), np.float32)
+        for t in range(total):
+            a[:, t] = orc.swiglu(np.ascontiguousarray(gf[:, t]), np.ascontiguousarray(uf[:, t]), limit)
+        v = a * (np.float32(1) if wv is None else wv[None, :])
+        for t in range(total):
+            for kb in range(dim // 128):
+                band = v[128 * kb:128 * kb + 128, t]
+                m = np.float32(np.abs(band).max())
+                want_sc = m * np.float32(1.0 / 448.0) if m > 0 else np.float32(1.0)
+                assert sc[t, kb] == want_sc, (t, kb)
+                inv = np.float32(1.0) / want_sc
+                q = np.clip(band * inv, -448, 448).astype(np.float32)
+                want = np.array([orc.f32_to_e4m3(float(e)) for e in q], np.uint8)
+                np.testing.assert_array_equal(out[t, 128 * kb:128 * kb + 128], want)
+                if m > 0:
+                    assert (out[t, 128 * kb:128 * kb + 128] & 0x7F).max() == 0x7E
+        assert (out[5, :128] == 0).all() and sc[5, 0] == 1.0
+
+
+def test_scatter_slots_and_gather_tokens_oracle_brute_force(orc):
+    """orc_scatter_slots and orc_gather_tokens against direct loops: the per-token sums in ord
+    order from zero (float32, sequential), empty runs untouched; the gather a plain index copy."""
+    rng = np.random.default_rng(9)
+    dim, nb_tok, nb_stride = 24, 19, 32
+    counts = rng.integers(0, 5, nb_tok)
+    counts[3] = 0
+    total = int(counts.sum())
+    run = np.concatenate([[0], np.cumsum(counts)]).astype(np.uint32)
+    ordv = rng.permutation(total).astype(np.uint32)
+    y = (rng.normal(0, 1, (dim, total)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    block0 = rng.normal(0, 1, (dim, nb_stride)).astype(np.float32)
+    got = orc.scatter_slots(y, block0.copy(), ordv, run, nb_tok)
+    want = block0.copy()
+    yf = (y.astype(np.uint32) << 16).view(np.float32)
+    for h in range(dim):
+        for t in range(nb_tok):
+            if run[t] == run[t + 1]:
+                continue
+            acc = np.float32(0)
+            for i in range(run[t], run[t + 1]):
+                acc = np.float32(acc + yf[h, ordv[i]])
+            want[h, t] = np.float32(want[h, t] + acc)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    src = rng.normal(0, 1, (dim, nb_stride)).astype(np.float32)
+    tok = rng.integers(0, nb_stride, 11).astype(np.uint32)
+    np.testing.assert_array_equal(orc.gather_tokens(src, tok), src[:, tok])
