@@ -341,11 +341,12 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   AFFX_TRACE(13);
   AFFX_TRACE(2);
 
-  // ---- the plan for the epilogue and the down phase (wave 0): expert of every slot, token
-  // masks, and per (slot, token) the summed weight of the token's routes to the slot, added in
-  // route order as the staged plan does (lane t walks token t's routes; no two lanes touch the
-  // same entry)
-  if (wv == 0) {
+  // ---- the plan for the epilogue and the down phase: expert of every slot, token masks, and
+  // per (slot, token) the summed weight of the token's routes to the slot, added in route order
+  // as the staged plan does (lane t walks token t's routes; no two lanes touch the same entry).
+  // Batch 1: the last wave writes it (the first waves split the activation; with both on wave 0
+  // that wave's share of the set-up was the last to finish); larger batches: wave 0.
+  if (wv == (SINGLE ? (uint32_t)kFW - 1u : 0u)) {
     if (lane < ns) slot_expert[lane] = se[0];
     if (lane + 64u < ns) slot_expert[lane + 64u] = se[1];
     for (uint32_t i = lane; i < ns * M; i += 64u) slot_w[i] = 0.f;
@@ -646,13 +647,11 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   }
   AFFX_TRACE(4);
   // ---- 4b. one pass (batch 1): the A fragments of this wave's first down unit (the one loaded
-  // before the publish) do not depend on the activations, so they are decoded now, while the
-  // layer publishes and this workgroup waits; after the release only the activation loads and
-  // eight MFMAs remain for it
-  // (the first kPreSteps of the eight steps: with the activation operand loaded whole after the
-  // wait, all eight would not fit the registers; the last steps are decoded after the wait)
+  // before the publish) do not depend on the activations, so all eight steps are decoded now,
+  // while the layer publishes and this workgroup waits; after the release only the staging of
+  // the activations and eight MFMAs remain for it
   static_assert(!SINGLE || (CG == 1 && BPRE), "the one-pass down phase holds one column group");
-  constexpr int kPreSteps = 6;
+  constexpr int kPreSteps = 8;
   v8i ad[SINGLE ? kPreSteps : 1];
   if constexpr (SINGLE) {
     if (has_down) {
@@ -835,8 +834,75 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
     };
     uint32_t td0 = g;
     if constexpr (SINGLE) {
-      down_tile(g, std::true_type{});
+      // Batch 1, the first output tile. The SwiGLU terms of all units (at most 12 units x 3
+      // terms x 1024 columns = 36 KiB, [slot][term][inter] as in memory) are copied into LDS over
+      // the codebook tables, which the barrier above frees (every wave's down fragments are
+      // decoded): one coalesced 16-byte load per thread and round instead of each wave's
+      // scattered 256-byte runs, after the release when every request is a miss. Each wave then
+      // reads its B operand from LDS (only the lanes of used columns) for its eight MFMAs.
+      {
+        const uint32_t n16 = ns * kTerms * A.inter / 16u;
+        u32x4* dst = reinterpret_cast<u32x4*>(lut_s);
+        const u32x4* src = reinterpret_cast<const u32x4*>(A.aq);
+        for (uint32_t i = tid; i < n16; i += kFT) dst[i] = src[i];
+      }
+      __syncthreads();
+      {
+        float yacc[4] = {0.f, 0.f, 0.f, 0.f};
+        if (has_down) {
+          const uint32_t slot = wv / nsi, S2 = wv % nsi;
+          const uint32_t mask = __builtin_amdgcn_readfirstlane(slot_mask[slot]);
+          const bool used = c < 3u && (mask & 1u) != 0u;
+          const uint8_t* bl = reinterpret_cast<const uint8_t*>(lut_s) + (slot * kTerms + (used ? c : 0u)) * A.inter +
+                              S2 * kTileCols + kg * kSegCols;
+          uint2 rsv = rs_d;
+          AFFX_PIN(rsv.x);
+          AFFX_PIN(rsv.y);
+          v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int m = 0; m < 8; ++m) {
+            v8i b = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+            if (used) b = b_step_lds(bl, m);
+            acc = mfma(ad[m], b, acc);
+          }
+          const float rs[4] = {__uint_as_float(rsv.x << 16), __uint_as_float(rsv.x & 0xFFFF0000u),
+                               __uint_as_float(rsv.y << 16), __uint_as_float(rsv.y & 0xFFFF0000u)};
+          const bool mine = c == 0u && (mask & 1u) != 0u;
+          const float wt = mine ? ldexpf(slot_w[slot * M], -A.sigma_a) : 0.f;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const float val = fused_terms(acc[v]);
+            if (mine) yacc[v] += val * rs[v] * wt;
+          }
+        }
+        AFFX_TRACE(6);
+        if (c == 0u) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) part[wv * 16 + 4 * rg4 + v] = yacc[v];
+        }
+        __syncthreads();
+        uint32_t et = tid;
+        AFFX_PIN(et);
+        if (et < 16u) {
+          float sum = 0.f;
+          for (int qw = 0; qw < kFW; ++qw) sum += part[qw * 16 + et];
+          float* dst = A.y + (uint64_t)(g * 16 + et) * A.yds;
+          *dst = A.accumulate ? *dst + sum : sum;
+        }
+      }
       td0 += A.n_wg;
+      if (td0 < dtiles) {
+        // further output tiles (a grid smaller than the tile count): the codebook tables again
+        __syncthreads();
+        uint32_t cb2[3];
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+          const uint32_t ce = tid + (uint32_t)i * kFT;
+          cb2[i] = A.codebook[ce < 2048u ? ce : 0u];
+        }
+        build_lut<KC, kFT, 3, ROT>(lut_s, cb2, tid);
+        __syncthreads();
+      }
     }
     for (uint32_t td = td0; td < dtiles; td += A.n_wg) down_tile(td, std::false_type{});
   }
