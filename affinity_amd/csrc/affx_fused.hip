@@ -19,8 +19,15 @@
 // Counter and flags are zero again when the launch ends, so the workspace is reusable by the next
 // launch on the stream without a memset (graph-capture safe).
 //
-// Reference counterparts: the decode branch of ExpertFfnBatch (src/engine/model.cpp:6045-6121)
-// over expert_ffn_hip (src/gpu/expert_kernel.hip:2737-2808) and moe_plan (src/gpu/moe_plan.hip).
+// Batch 1 (the one-pass kernel, SINGLE) replaces step 4's counter and flags: each workgroup stores
+// the launch's epoch into its own dword of eight publish-flag copies, and a down-phase workgroup
+// polls the copy of its XCD until every gate/up workgroup's dword shows the epoch; the last
+// workgroup then advances the epoch word. Nothing is cleared, so this form too needs no memset.
+//
+// Reference counterparts: the routed-expert batch hook ExpertFfnBatch (src/engine/model.h:658-666,
+// called at src/engine/model.cpp:1663-1664, bound to run_batch_device at tools/affinity.cpp:
+// 1218-1236) and the per-token expert_ffn_hip (src/gpu/expert_kernel.hip:2737-2808), with the
+// routing plan of moe_plan (src/gpu/moe_plan.hip).
 #include <mutex>
 
 #include "affx_lut.h"
@@ -28,6 +35,7 @@
 namespace affx {
 
 constexpr int kFW = 12;                      // waves per workgroup
+constexpr int kPollUnitsMax = kFW;           // down units of the one-pass kernel: one per wave
 constexpr int kFT = kFW * 64;                // threads per workgroup
 constexpr int kXqChunk = 272;                // LDS bytes of one 256-column chunk of an xq row
 constexpr int kXqRow = 16 * kXqChunk + 64;   // LDS bytes of one (token, term) row, hidden <= 4096
@@ -607,9 +615,15 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   //    count is performed after every other add, hence after every workgroup's stores completed;
   //    its wave reads the old value back before it raises the flags, so the add is performed
   //    before any flag store is issued;
-  //  * a waiter that sees its flag runs an agent-scope acquire fence (`buffer_inv sc1`) before
-  //    any workgroup thread reads the SwiGLU output, so no stale line of an earlier launch is
-  //    read from its CU's or its XCD's caches.
+  //  * rounds kernels: a waiter that sees its flag runs an agent-scope acquire fence
+  //    (`buffer_inv sc1`) before any workgroup thread reads the SwiGLU output, so no stale line of
+  //    an earlier launch is read from its CU's or its XCD's caches;
+  //  * the one-pass kernel instead reads the SwiGLU output with loads that carry the same
+  //    device-coherence bit (`buffer_load ... sc1`, what the compiler emits for an agent-scope
+  //    atomic load), issued only after the publish flags were seen (a compiler barrier after the
+  //    poll, the workgroup barrier for the other waves): such a load reads past the non-coherent
+  //    caches, so it needs no invalidate. The acquire's L2 invalidate, once per workgroup, had
+  //    every workgroup of an XCD refetch the others' lines: 19.8 against 18.3 us per layer.
   if (PREF) {
     if (!SINGLE || n_rounds == 0 || wv < epi_waves) load_down(has_down, g, wv);
     if (n_rounds > 0 && wv < epi_waves) __builtin_amdgcn_s_waitcnt(AFFX_VMCNT(7));
@@ -687,7 +701,9 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
       }
       // every workgroup has read the epoch (each published epoch + 1): the next launch's epoch
       if (g == 0 && lane == 0) __hip_atomic_store(&A.sync[kEpochWord], ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      // (no acquire fence: the SwiGLU output is read with device-coherent loads, see the publish;
+      // the compiler may not move those loads above this point)
+      asm volatile("" ::: "memory");
     }
     if (!SINGLE && tid == 0 && NI > 0) {
       uint32_t* flag = A.sync + (kSyncHeader + g * kSyncFlagStride) / 4;
@@ -834,17 +850,25 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
     };
     uint32_t td0 = g;
     if constexpr (SINGLE) {
-      // Batch 1, the first output tile. The SwiGLU terms of all units (at most 12 units x 3
-      // terms x 1024 columns = 36 KiB, [slot][term][inter] as in memory) are copied into LDS over
-      // the codebook tables, which the barrier above frees (every wave's down fragments are
-      // decoded): one coalesced 16-byte load per thread and round instead of each wave's
-      // scattered 256-byte runs, after the release when every request is a miss. Each wave then
-      // reads its B operand from LDS (only the lanes of used columns) for its eight MFMAs.
-      {
+      // Batch 1, the first output tile, its eight down steps already decoded (ad). When every
+      // workgroup has one output tile (the grid covers the hidden rows: the device-filling case),
+      // the SwiGLU terms of all units (at most 12 units x 3 terms x 1024 columns = 36 KiB,
+      // [slot][term][inter] as in memory) are copied into LDS over the codebook tables, which
+      // the barrier above frees: one coalesced 16-byte device-coherent load per thread and round
+      // (see the publish) instead of each wave's scattered 256-byte runs; each wave then reads
+      // its B operand from LDS (only the lanes of used columns). A workgroup with further tiles
+      // keeps the tables for them and reads its first tile's operand from memory as they do
+      // (plain loads after the acquire fence).
+      const bool staged = A.n_wg >= dtiles;
+      static_assert(Lut<KC, ROT>::kDwords * 4 >= (int)(kPollUnitsMax * kTerms * kTileCols), "staging fits the tables");
+      if (staged) {
         const uint32_t n16 = ns * kTerms * A.inter / 16u;
         u32x4* dst = reinterpret_cast<u32x4*>(lut_s);
-        const u32x4* src = reinterpret_cast<const u32x4*>(A.aq);
-        for (uint32_t i = tid; i < n16; i += kFT) dst[i] = src[i];
+        const __amdgpu_buffer_rsrc_t ar = buffer_rsrc(A.aq, n16 * 16u);
+        for (uint32_t i = tid; i < n16; i += kFT)
+          dst[i] = __builtin_amdgcn_raw_buffer_load_b128(ar, 16u * i, 0, kDevCoherent);
+      } else {
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
       }
       __syncthreads();
       {
@@ -853,8 +877,9 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
           const uint32_t slot = wv / nsi, S2 = wv % nsi;
           const uint32_t mask = __builtin_amdgcn_readfirstlane(slot_mask[slot]);
           const bool used = c < 3u && (mask & 1u) != 0u;
-          const uint8_t* bl = reinterpret_cast<const uint8_t*>(lut_s) + (slot * kTerms + (used ? c : 0u)) * A.inter +
-                              S2 * kTileCols + kg * kSegCols;
+          const uint64_t boff = (uint64_t)(slot * kTerms + (used ? c : 0u)) * A.inter + S2 * kTileCols + kg * kSegCols;
+          const uint8_t* bl = reinterpret_cast<const uint8_t*>(lut_s) + boff;
+          const u32x4* bg = reinterpret_cast<const u32x4*>(A.aq + boff);
           uint2 rsv = rs_d;
           AFFX_PIN(rsv.x);
           AFFX_PIN(rsv.y);
@@ -862,7 +887,7 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
 #pragma unroll
           for (int m = 0; m < 8; ++m) {
             v8i b = v8i{0, 0, 0, 0, 0, 0, 0, 0};
-            if (used) b = b_step_lds(bl, m);
+            if (used) b = staged ? b_step_lds(bl, m) : b_step(bg, m);
             acc = mfma(ad[m], b, acc);
           }
           const float rs[4] = {__uint_as_float(rsv.x << 16), __uint_as_float(rsv.x & 0xFFFF0000u),
@@ -889,20 +914,9 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
           float* dst = A.y + (uint64_t)(g * 16 + et) * A.yds;
           *dst = A.accumulate ? *dst + sum : sum;
         }
+        __syncthreads();  // (this tile's partial sums read before the next tile rewrites them)
       }
       td0 += A.n_wg;
-      if (td0 < dtiles) {
-        // further output tiles (a grid smaller than the tile count): the codebook tables again
-        __syncthreads();
-        uint32_t cb2[3];
-#pragma unroll
-        for (int i = 0; i < 3; ++i) {
-          const uint32_t ce = tid + (uint32_t)i * kFT;
-          cb2[i] = A.codebook[ce < 2048u ? ce : 0u];
-        }
-        build_lut<KC, kFT, 3, ROT>(lut_s, cb2, tid);
-        __syncthreads();
-      }
     }
     for (uint32_t td = td0; td < dtiles; td += A.n_wg) down_tile(td, std::false_type{});
   }

@@ -228,20 +228,22 @@ int affx_expert_gemv(const affx_matrix* m, const void* codebook, const float* x,
 /* ---- decode: M <= 8 tokens, fused gate/up -> SwiGLU -> down -> weighted combine ------------- */
 
 /* Workspace bytes affx_expert_ffn_decode needs for m tokens with top-k routing. The workspace
- * must be zero-filled before its first use: its first 33,024 bytes hold the fused decode's
- * cross-workgroup state (a 256-byte header with the publish counter, then one 128-byte release
- * flag per waiting workgroup), which every launch leaves zero again (no memset per call, safe
- * under graph capture). Word 2 (bytes 8..11) becomes nonzero if a launch ever gave up waiting
- * for the other workgroups (its output is then invalid); it is sticky until the caller clears it
- * (and the workspace should then be zero-filled again). */
+ * must be zero-filled before its first use: its first 41,216 bytes hold the fused decode's
+ * cross-workgroup state: a 256-byte header (the publish counter of the M > 1 kernels, the error
+ * word, the batch-1 kernel's launch epoch), one 128-byte release flag per waiting workgroup, and
+ * eight copies of one publish-flag dword per workgroup for the batch-1 kernel. Counter and release
+ * flags are zero again after every launch; epoch and publish flags only advance. So no call needs
+ * a memset, and the calls are safe under graph capture. Word 2 (bytes 8..11) becomes nonzero if a
+ * launch ever gave up waiting for the other workgroups (its output is then invalid); it is sticky
+ * until affx_decode_status resets the sync run. */
 size_t affx_decode_workspace_size(uint32_t m_tokens, uint32_t top_k, uint32_t hidden,
                                   uint32_t inter);
 
 /* Status of a decode workspace: AFFX_OK, or AFFX_ERR_DEVICE when a launch of
  * affx_expert_ffn_decode on it gave up waiting for its workgroups (error word 2 nonzero; that
  * launch's output was invalid). Copies 4 bytes to the host and synchronises `stream`. reset = 1
- * also zeroes the workspace's sync run (counter, error bits, release flags), which a timed-out
- * launch can leave raised. The counterpart of the reference's periodic device-status read that
+ * also zeroes the workspace's sync run (counter, error bits, release and publish flags, epoch),
+ * which a timed-out launch can leave raised. The counterpart of the reference's periodic device-status read that
  * aborts the process on a bad dispatch (src/gpu/static_placement.hip:1939-1961); the engine hook
  * affx_expert_ffn_batch makes this check itself after every decode call. */
 int affx_decode_status(void* workspace, int reset, void* stream);
@@ -257,7 +259,8 @@ int affx_decode_status(void* workspace, int reset, void* stream);
  * expert_kernel_hip.h:273) and the narrow NT=1 arm of the W8A8 GEMM that the engine's decode uses
  * (expert_kernel.hip:3049-3058). One persistent launch (routing plan, activation split, gate/up +
  * SwiGLU, down + combine; between gate/up and down, an agent-scope publish counter whose last
- * adder raises one release flag per down-phase workgroup); it needs every
+ * adder raises one release flag per down-phase workgroup, or at batch 1 one publish flag per
+ * workgroup that the down-phase workgroups poll); it needs every
  * workgroup of its grid resident at once, so the grid is sized to the device, and it falls back to
  * the staged launches below when the device cannot hold it. No host synchronisation. */
 int affx_expert_ffn_decode(const affx_layer* layer, const float* x, uint64_t x_tok_stride,
