@@ -514,17 +514,20 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
       }
     }
     AFFX_TRACE(3);
-    // one pass: a wave that stores no SwiGLU output issues its down unit now (its gate/up data is
-    // in), so that it has arrived when the wave decodes it during the publish and wait
-    if constexpr (SINGLE && PREF) {
-      if (wv >= epi_waves) load_down(has_down, g, wv);
-    }
     if (item != ~0u && S == 0 && lane < 32) {
       // opaque at the use: no conversion is hoisted next to the load (its wait would then cover
       // every weight load issued before it)
       uint32_t rv = rs_gu;
       AFFX_PIN(rv);
       rs_l[q * 32 + lane] = __uint_as_float(rv << 16);
+    }
+    // one pass: a wave that stores no SwiGLU output issues its down unit now (its gate/up data is
+    // in), so that it has arrived when the wave decodes it during the publish and wait. After the
+    // row-scale write above: where a branch that issues loads joins, the compiler's wait for a
+    // value loaded before the branch covers every load in flight, so the write would wait for
+    // this unit (about 1 us).
+    if constexpr (SINGLE && PREF) {
+      if (wv >= epi_waves) load_down(has_down, g, wv);
     }
     // the next round's weights go out now (this round's are consumed), so their latency is
     // spent on this round's epilogue

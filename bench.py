@@ -64,8 +64,62 @@ def rel_l2(got, ref) -> float:
     return float(np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30))
 
 
-def time_graph(torch, fn, steps, warmup):
-    """Captures fn into a HIP graph and times `steps` replays with events on the current stream."""
+class ClockSampler:
+    """The GPU's shader clock while a timed region runs: a thread reads amdsmi's current gfx clock
+    (the mean over the XCDs) every few milliseconds between start() and stop(). Records why when
+    the reading is unavailable (no amdsmi, no permission); never raises."""
+
+    def __init__(self, period_s: float = 0.002):
+        self.period = period_s
+        self.err = None
+        self.handle = None
+        try:
+            import amdsmi
+            amdsmi.amdsmi_init()
+            self.smi = amdsmi
+            self.handle = amdsmi.amdsmi_get_processor_handles()[0]
+            self.read()
+        except Exception as e:  # noqa: BLE001 - recorded in the result instead
+            self.err = f"{type(e).__name__}: {e}"
+            self.handle = None
+
+    def read(self) -> float:
+        m = self.smi.amdsmi_get_gpu_metrics_info(self.handle)
+        per_xcd = [v for v in m.get("current_gfxclks", []) if isinstance(v, (int, float)) and v < 65535]
+        if per_xcd:
+            return float(sum(per_xcd)) / len(per_xcd)
+        return float(self.smi.amdsmi_get_clock_info(self.handle, self.smi.AmdSmiClkType.GFX)["clk"])
+
+    def start(self) -> None:
+        import threading
+        self.samples, self.stop_flag = [], False
+
+        def run():
+            while not self.stop_flag:
+                try:
+                    self.samples.append(self.read())
+                except Exception as e:  # noqa: BLE001
+                    self.err = f"{type(e).__name__}: {e}"
+                    return
+                time.sleep(self.period)
+        if self.handle is not None:
+            self.thread = threading.Thread(target=run, daemon=True)
+            self.thread.start()
+
+    def stop(self) -> dict:
+        if self.handle is None:
+            return {"mhz": None, "why": self.err}
+        self.stop_flag = True
+        self.thread.join()
+        v = self.samples
+        if not v:
+            return {"mhz": None, "why": self.err or "no sample inside the timed region"}
+        return {"mhz": round(sum(v) / len(v), 1), "min": min(v), "max": max(v), "samples": len(v)}
+
+
+def time_graph(torch, fn, steps, warmup, clock=None, clock_key=None, clocks=None):
+    """Captures fn into a HIP graph and times `steps` replays with events on the current stream
+    (with `clock`, the shader clock over the timed replays goes to clocks[clock_key])."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -80,11 +134,15 @@ def time_graph(torch, fn, steps, warmup):
         g.replay()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    if clock is not None:
+        clock.start()
     start.record()
     for _ in range(steps):
         g.replay()
     end.record()
     torch.cuda.synchronize()
+    if clock is not None:
+        clocks[clock_key] = clock.stop()
     return start.elapsed_time(end) / steps, g, out
 
 
@@ -114,6 +172,8 @@ def main() -> int:
     ax.init()
     torch.cuda.set_device(0)
     cb_packed = synthetic.c1_codebook()
+    clock = ClockSampler()
+    clocks: dict = {}
     L = args.layers
 
     if args.calibrate:
@@ -157,7 +217,8 @@ def main() -> int:
     decode_step(x1, routes1, ws1, y1, 1)
     torch.cuda.synchronize()
     eager1 = y1.clone()
-    ms1, g1, _ = time_graph(torch, lambda: decode_step(x1, routes1, ws1, y1, 1), args.steps, args.warmup)
+    ms1, g1, _ = time_graph(torch, lambda: decode_step(x1, routes1, ws1, y1, 1), args.steps, args.warmup,
+                            clock, "c5_decode", clocks)
     torch.cuda.synchronize()
     assert torch.equal(y1, eager1), "graph replay differs from the eager decode"
     bytes_tok = L * K * STRIDE
@@ -197,7 +258,8 @@ def main() -> int:
             f"{bytes_tok / (mss * 1e-3) / 1e9:.0f} GB/s")
 
     # ---- C3: M = 8 tokens ------------------------------------------------------------------------
-    ms8, _, _ = time_graph(torch, lambda: decode_step(x8, routes8, ws8, y8, 8), args.steps, args.warmup)
+    ms8, _, _ = time_graph(torch, lambda: decode_step(x8, routes8, ws8, y8, 8), args.steps, args.warmup,
+                           clock, "c3_decode", clocks)
     distinct = sum(int(torch.unique(r[0]).numel()) for r in routes8)
     gbs8 = distinct * STRIDE / (ms8 * 1e-3) / 1e9
     log(f"C3 decode (M=8): {ms8 * 1e3:.1f} us/step, {distinct / L:.1f} experts/layer -> {gbs8:.0f} GB/s")
@@ -234,6 +296,8 @@ def main() -> int:
                "us_per_layer": round(ms8 * 1e3 / L, 2), "hbm_fraction": round(gbs8 * 1e9 / HBM_PEAK, 4),
                "distinct_experts_per_layer": round(distinct / L, 2)},
         "decode_status": {"m1": st1, "m8": st8},
+        "clock": {"source": "amdsmi current_gfxclks (mean over the XCDs), sampled every 2 ms in the timed "
+                            "region; MHz", "regions": clocks},
     }
 
     # ---- C4 prefill ------------------------------------------------------------------------------
@@ -251,11 +315,13 @@ def main() -> int:
             ax.expert_ffn_grouped(pools[0], xb, sel_t, w_t, y=yp, workspace=gws)
         torch.cuda.synchronize()
         st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        clock.start()
         st.record()
         for _ in range(args.prefill_steps):
             ax.expert_ffn_grouped(pools[0], xb, sel_t, w_t, y=yp, workspace=gws)
         en.record()
         torch.cuda.synchronize()
+        clocks["c4_prefill"] = clock.stop()
         msp = st.elapsed_time(en) / args.prefill_steps
         flops = T * K * FLOP_PER_SLOT
         tf = flops / (msp * 1e-3) / 1e12
@@ -269,11 +335,13 @@ def main() -> int:
         y3 = torch.zeros_like(yp)
         ax.expert_ffn_grouped(pools[0], xh, sel_t, w_t, y=y3, x_lo=xl, workspace=gws)
         torch.cuda.synchronize()
+        clock.start()
         st.record()
         for _ in range(args.prefill_steps):
             ax.expert_ffn_grouped(pools[0], xh, sel_t, w_t, y=y3, x_lo=xl, workspace=gws)
         en.record()
         torch.cuda.synchronize()
+        clocks["c4_prefill_hi_lo"] = clock.stop()
         msp3 = st.elapsed_time(en) / args.prefill_steps
         tf3 = flops / (msp3 * 1e-3) / 1e12
         del xh, xl, y3
@@ -322,7 +390,7 @@ def main() -> int:
                       "shared_expert_decode")
             return ys
 
-        ms_sh, _, _ = time_graph(torch, shared_step, args.steps, args.warmup)
+        ms_sh, _, _ = time_graph(torch, shared_step, args.steps, args.warmup, clock, "shared_decode", clocks)
         gbs_sh = L * sh_bytes / (ms_sh * 1e-3) / 1e9
         T = 4096
         xs_b = ax.gen_normal(S_X, T * H, 1.0).view(T, H).to(torch.bfloat16)
