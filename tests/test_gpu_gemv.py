@@ -4,8 +4,8 @@ affx_expert_gemv_batch (expert_gemv_batch_hip's, 152-153), the calls aff-gpuchec
 per-matrix check and its GEMV bandwidth figure (tools/aff_gpucheck.cpp:278, 544-548). Each
 matrix is uploaded on its own as aff-gpucheck does (host permutation, separate buffers) and the
 result is compared with the oracle's expert_gemv_reference (y += w * W x, double accumulation)
-at the 1e-3 relative-L2 bar, at the benchmark shapes 2048 x 4096 (gate/up) and 4096 x 2048
-(down)."""
+at aff-gpucheck's own 1e-4 relative-L2 bar, at the benchmark shapes 2048 x 4096 (gate/up) and
+4096 x 2048 (down)."""
 import ctypes as C
 
 import numpy as np
@@ -16,7 +16,9 @@ from gpu_util import planes, random_expert_container, rel_l2
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
-TOL = 1e-3
+# aff-gpucheck fails a matrix whose GEMV differs from the CPU path by more than 1e-4 relative L2
+# (tools/aff_gpucheck.cpp:295): the GEMVs are held to that bar, not to the FFN's 1e-3
+TOL = 1e-4
 H, I = 4096, 2048
 
 
