@@ -60,8 +60,10 @@ struct DecodePlan {
   int32_t x_sigma[kMaxTok][kMaxSeg];  // exponent of each (token, super-segment) activation split
   uint32_t expert[kMaxSlots];
   uint32_t tok_mask[kMaxSlots];
-  float w[kMaxSlots][kMaxTok];
+  float w[kMaxSlots][kMaxTok];  // last: a plan of n slots ends at w[n] (the pointer-table form's scratch)
 };
+static_assert(offsetof(DecodePlan, w) + sizeof(float) * kMaxSlots * kMaxTok == sizeof(DecodePlan),
+              "the weight table ends the plan");
 
 // Phase markers of the persistent decode kernel: expand to nothing (a profiling build can define
 // them to record timestamps).

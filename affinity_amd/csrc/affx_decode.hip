@@ -38,6 +38,7 @@ struct DecodeArgs {
   const uint32_t* codebook;
   const DecodePlan* plan;
   const uint8_t* xq;    // [M][3][hidden]
+  const float* x;       // one token's activation (the pointer-table form: its gate/up makes the terms)
   uint8_t* aq;          // [slot][M][3][inter]
   const uint8_t* zeros; // 256 zero bytes: the B source of unused columns
   float limit;
@@ -145,13 +146,24 @@ __device__ __forceinline__ float combine_terms(float d) {
 // ------------------------------------------------------------------------------------------------
 // gate/up + SwiGLU
 // ------------------------------------------------------------------------------------------------
-template <int CG>
+// XL (the pointer-table form, one token): the activation terms are made by every workgroup in its
+// own LDS from x, with the prep kernel's split (the same bits), instead of read from the caller's
+// scratch, which then has to hold only the plan and the SwiGLU terms: the reference's 2 * n * inter
+// floats are enough for any n >= 1.
+template <int CG, bool XL = false>
 __global__ void __launch_bounds__(256) decode_gateup_kernel(DecodeArgs A) {
   const uint32_t slot = blockIdx.y;
   if (slot >= A.plan->n_slots) return;
   const uint32_t rt = blockIdx.x, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const uint32_t e = A.plan->expert[slot], mask = A.plan->tok_mask[slot], M = A.m_tokens;
   const uint32_t nst = A.hidden / kTileCols;
+  // (XL: the activation loads go out before the weights, so waiting for them waits for nothing
+  // else; an absent segment reloads segment 0, unused)
+  float xv[XL ? 4 : 1][4];
+  if constexpr (XL) {
+#pragma unroll
+    for (uint32_t q = 0; q < 4; ++q) segment_load(A.x, 0, 1, 0, q < nst ? q : 0u, xv[q]);
+  }
 
   __shared__ uint32_t tbl[4 * kLut];
   __shared__ float part[4][2][CG][16][16];
@@ -172,9 +184,18 @@ __global__ void __launch_bounds__(256) decode_gateup_kernel(DecodeArgs A) {
     load_unit(uu, plane_ptr(A, e, kUpCodes), plane_ptr(A, e, kUpFields), tile, lane);
   }
   build_table(tbl, A.codebook);
+  __shared__ __align__(16) uint8_t xl[XL ? kTerms * 4 * kTileCols : 16];
+  __shared__ float red[4];
+  if constexpr (XL) {
+#pragma unroll
+    for (uint32_t q = 0; q < 4; ++q) {
+      if (q < nst) segment_split(xv[q], 0, q, A.hidden, xl, red);
+      __syncthreads();  // (red is rewritten by the next segment)
+    }
+  }
   __syncthreads();
   if (S < nst) {
-    const BSrc<CG> b = b_source<CG>(A.xq, A.hidden, (uint64_t)S * kTileCols, lane, M, mask, A.zeros);
+    const BSrc<CG> b = b_source<CG>(XL ? xl : A.xq, A.hidden, (uint64_t)S * kTileCols, lane, M, mask, A.zeros);
     // software pipeline: the table reads and B loads of step m+1 are issued before step m is
     // finished and multiplied; the scheduling barrier keeps the compiler from hoisting all
     // eight steps (register blow-up)
@@ -553,8 +574,10 @@ int affx_expert_ffn(const affx_device_expert* experts, const float* weights, uin
       A.tbl[k][3 * i + 2] = (const uint8_t*)m[i]->rscales;
     }
   }
-  // scratch: the reference's contract is 2 * n * inter floats
-  const uint64_t plan = 0, zeros = a256(sizeof(DecodePlan)), xq = zeros + 256, aq = xq + a256(3ull * hidden);
+  // scratch: the reference's contract is 2 * n * inter floats. It holds the plan (only its first
+  // n slots' weights: the weight table is the plan's last member), the zero row and the SwiGLU
+  // terms; the activation terms are made in each gate/up workgroup's LDS.
+  const uint64_t plan = 0, zeros = a256(offsetof(DecodePlan, w) + sizeof(float) * kMaxTok * n), aq = zeros + 256;
   const uint64_t need = aq + 3ull * n * inter, have = 8ull * n * inter;
   if (need > have)
     return set_error(AFFX_DECLINED, "expert_ffn: needs %llu bytes of scratch, the 2 * n * inter floats hold %llu",
@@ -567,7 +590,8 @@ int affx_expert_ffn(const affx_device_expert* experts, const float* weights, uin
   A.m_tokens = 1;
   A.codebook = (const uint32_t*)codebook;
   A.plan = (const DecodePlan*)(ws + plan);
-  A.xq = ws + xq;
+  A.xq = nullptr;
+  A.x = x;
   A.aq = ws + aq;
   A.zeros = ws + zeros;
   A.limit = swiglu_limit;
@@ -579,10 +603,10 @@ int affx_expert_ffn(const affx_device_expert* experts, const float* weights, uin
   hipStream_t st = (hipStream_t)stream;
   hipLaunchKernelGGL(decode_prep_kernel, dim3(hidden / kTileCols + 1), dim3(256), 0, st, x, (uint64_t)hidden,
                      (uint64_t)1, 1u, (const uint32_t*)nullptr, weights, n, n, hidden, (DecodePlan*)(ws + plan),
-                     ws + xq, ws + zeros);
+                     (uint8_t*)nullptr, ws + zeros);
   int rc = check_launch("decode_prep_kernel");
   if (rc) return rc;
-  hipLaunchKernelGGL(decode_gateup_kernel<1>, dim3(inter / kTileRows, n), dim3(256), 0, st, A);
+  hipLaunchKernelGGL((decode_gateup_kernel<1, true>), dim3(inter / kTileRows, n), dim3(256), 0, st, A);
   if ((rc = check_launch("decode_gateup_kernel"))) return rc;
   const uint32_t units = n * (inter / kTileCols);
   if (units <= (uint32_t)kDownWaves)

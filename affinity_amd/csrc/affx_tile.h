@@ -171,38 +171,49 @@ __device__ __forceinline__ void split3(float v, uint32_t& b0, uint32_t& b1, uint
 // One (token t, 1024-column super-segment S) of the decode input x (f32, element (t, h) at
 // x[t * xts + h * xds]): its exponent sigma (returned: the segment's largest magnitude times
 // 2^sigma lies in [128, 256), below E4M3's 448 with one binade of headroom) and three E4M3 terms
-// of every element times 2^sigma, natural column order, term j at xq + (3 t + j) * hidden + h.
-// All 256 threads of the workgroup call it (red: 4 floats of LDS).
-__device__ __forceinline__ int segment_terms(const float* __restrict__ x, uint64_t xts, uint64_t xds, uint32_t t,
-                                             uint32_t S, uint32_t hidden, uint8_t* __restrict__ xq, float* red) {
+// of every element times 2^sigma, natural column order, term j at xq + (3 t + j) * hidden + h
+// (nothing written when xq is null). All 256 threads of the workgroup call it (red: 4 floats of
+// LDS). In two parts, so that a caller can issue the loads before others and split later.
+__device__ __forceinline__ void segment_load(const float* __restrict__ x, uint64_t xts, uint64_t xds, uint32_t t,
+                                             uint32_t S, float (&v)[4]) {
+  const uint32_t h0 = S * kTileCols + 4 * threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = x[t * xts + (h0 + i) * xds];
+}
+__device__ __forceinline__ int segment_split(const float (&v)[4], uint32_t t, uint32_t S, uint32_t hidden,
+                                             uint8_t* xq, float* red) {
   const uint32_t tid = threadIdx.x;
   const uint32_t h0 = S * kTileCols + 4 * tid;
-  float v[4];
   float amax = 0.f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    v[i] = x[t * xts + (h0 + i) * xds];
-    amax = fmaxf(amax, fabsf(v[i]));
-  }
+  for (int i = 0; i < 4; ++i) amax = fmaxf(amax, fabsf(v[i]));
   for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
   if ((tid & 63) == 0) red[tid >> 6] = amax;
   __syncthreads();
   amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const int sigma = amax > 0.f ? 7 - ilogbf(amax) : 0;
-  uint32_t q0 = 0, q1 = 0, q2 = 0;
+  if (xq) {
+    uint32_t q0 = 0, q1 = 0, q2 = 0;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    uint32_t b0, b1, b2;
-    split3(ldexpf(v[i], sigma), b0, b1, b2);
-    q0 |= b0 << (8 * i);
-    q1 |= b1 << (8 * i);
-    q2 |= b2 << (8 * i);
+    for (int i = 0; i < 4; ++i) {
+      uint32_t b0, b1, b2;
+      split3(ldexpf(v[i], sigma), b0, b1, b2);
+      q0 |= b0 << (8 * i);
+      q1 |= b1 << (8 * i);
+      q2 |= b2 << (8 * i);
+    }
+    uint32_t* dst = reinterpret_cast<uint32_t*>(xq + (uint64_t)t * kTerms * hidden + h0);
+    dst[0] = q0;
+    dst[hidden / 4] = q1;
+    dst[2 * (hidden / 4)] = q2;
   }
-  uint32_t* dst = reinterpret_cast<uint32_t*>(xq + (uint64_t)t * kTerms * hidden + h0);
-  dst[0] = q0;
-  dst[hidden / 4] = q1;
-  dst[2 * (hidden / 4)] = q2;
   return sigma;
+}
+__device__ __forceinline__ int segment_terms(const float* __restrict__ x, uint64_t xts, uint64_t xds, uint32_t t,
+                                             uint32_t S, uint32_t hidden, uint8_t* xq, float* red) {
+  float v[4];
+  segment_load(x, xts, xds, t, S, v);
+  return segment_split(v, t, S, hidden, xq, red);
 }
 
 // B operand of one unit: per lane, 256 consecutive activation bytes of one (token, term) column

@@ -299,10 +299,11 @@ int affx_decode_noalloc_status(int reset, void* stream);
  * aff-gpucheck makes (tools/aff_gpucheck.cpp:498, 585). weights: device f32[n_experts]; x: device
  * f32[hidden]; out: device f32[hidden], accumulated; codebook: device uint32[2048] (the packed
  * quads the reference passes through a float pointer). scratch: device, the reference's
- * 2 * n_experts * inter floats, no clearing needed. n_experts <= 16 (the reference's 32 matrices
- * per launch); shapes as the layer entries. Three stream-ordered launches (the staged decode:
- * routing plan and activation split, gate/up + SwiGLU, down + combine), no synchronisation.
- * AFFX_DECLINED when a shape or the scratch size is outside this. */
+ * 2 * n_experts * inter floats, no clearing needed (it holds the plan and the SwiGLU terms; each
+ * gate/up workgroup makes the activation terms in its own LDS), for any n_experts from 1 to 16
+ * (the reference's 32 matrices per launch); shapes as the layer entries. Three stream-ordered
+ * launches (the staged decode: routing plan, gate/up + SwiGLU, down + combine), no
+ * synchronisation. AFFX_DECLINED when a shape or the count is outside this. */
 int affx_expert_ffn(const affx_device_expert* experts, const float* weights, uint32_t n_experts,
                     const void* codebook, const float* x, float swiglu_limit, float* scratch,
                     float* out, void* stream);

@@ -80,6 +80,8 @@ CASES = {
     "timeout_m1": (("timeout", 1024, 1024, 6, 1, 1, 8), 6),
     "slots": (("slots", 1024, 1024, 4, 6, 2, 9), 4),
     "ffnptr": (("ffnptr", 1024, 1024, 3, 12), 4),
+    # one expert at hidden 4096, inter 1024: the smallest scratch the reference's contract gives
+    "ffnptr_n1": (("ffnptr", 4096, 1024, 1, 13), 4),
     "route": (("route", 21, 100, 6, 4), 4),
     # the single-matrix GEMV entries: 3 down matrices (1024 x 2048) in one batch, one alone
     "gemv": (("gemv", 1024, 2048, 3, 5), 4),
@@ -89,7 +91,7 @@ CASES = {
 }
 # longest first, so the three lanes finish together
 ORDER = ["decode_m8_wide", "decode_m6_dm16", "decode_m6_two_cg", "slots", "shared", "decode_m1_single", "grouped",
-         "decode_m1", "ffnptr", "quant", "timeout", "timeout_m1", "route", "gemv", "steps", "decode_allpad", "dequant"]
+         "decode_m1", "ffnptr", "ffnptr_n1", "quant", "timeout", "timeout_m1", "route", "gemv", "steps", "decode_allpad", "dequant"]
 
 
 @pytest.fixture(scope="module")
@@ -174,6 +176,11 @@ def test_grouped_slot_list_emulated(runs):
 def test_expert_ffn_pointer_table_emulated(runs):
     out = result(runs, "ffnptr")
     assert "identical to staged=1" in out, out
+
+
+def test_expert_ffn_pointer_table_one_expert_emulated(runs):
+    out = result(runs, "ffnptr_n1")
+    assert "ffnptr rc=0 identical to staged=1" in out, out
 
 
 def test_gemv_emulated(runs):

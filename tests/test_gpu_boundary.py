@@ -37,11 +37,13 @@ def _upload_matrix(lib, ex, lay, which, rows, cols, keep):
     return AffxMatrix(bufs[0].data_ptr(), bufs[1].data_ptr(), bufs[2].data_ptr(), rows, cols)
 
 
-@pytest.mark.parametrize("n", [6, 16])
-def test_expert_ffn_pointer_table(ax, orc, c1_codebook, n):
+# every n from one expert up (the reference's expert_ffn_hip takes any n >= 1 with its 2 * n *
+# inter floats of scratch), at the benchmark shape and at inter 1024 (the smallest scratch)
+@pytest.mark.parametrize("n,inter", [(1, 2048), (2, 2048), (5, 2048), (6, 2048), (16, 2048), (1, 1024), (3, 1024)])
+def test_expert_ffn_pointer_table(ax, orc, c1_codebook, n, inter):
     from affinity_amd._lib import AffxDeviceExpert, lib, last_error
-    hidden, inter = 4096, 2048
-    rng = np.random.default_rng(40 + n)
+    hidden = 4096
+    rng = np.random.default_rng(40 + n + inter)
     lay = ax.expert_layout(hidden, inter)
     ex = np.stack([random_expert_container(rng, hidden, inter, lay) for _ in range(n)])
     keep = []
@@ -76,23 +78,35 @@ def test_expert_ffn_pointer_table(ax, orc, c1_codebook, n):
     assert err <= TOL
 
 
-def test_expert_ffn_declines_small_scratch_and_bad_shapes(ax, c1_codebook):
-    """One expert needs more than the reference's 2 * inter floats of scratch here: declined, with
-    nothing launched; a matrix of the wrong shape is an argument error."""
+def test_expert_ffn_declines_and_refuses_before_launching(ax, c1_codebook):
+    """What the pointer-table form declines (more than 16 experts, hidden above 4096, no clamp
+    limit) or refuses (a matrix of the wrong shape) is decided on the host: nothing is launched
+    (the planes here are a small zero buffer that a launch would read past)."""
     from affinity_amd._lib import AffxDeviceExpert, AffxMatrix, lib, last_error
     hidden, inter = 4096, 2048
     buf = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
     p = buf.data_ptr()
-    des = (AffxDeviceExpert * 1)()
-    des[0].gate = AffxMatrix(p, p, p, inter, hidden)
-    des[0].up = AffxMatrix(p, p, p, inter, hidden)
-    des[0].down = AffxMatrix(p, p, p, hidden, inter)
-    rc = lib().affx_expert_ffn(des, p, 1, p, p, 10.0, p, p, None)
-    assert rc == 1 and "scratch" in last_error()
-    des[0].down = AffxMatrix(p, p, p, hidden, hidden)
-    des2 = (AffxDeviceExpert * 2)(des[0], des[0])
-    rc = lib().affx_expert_ffn(des2, p, 2, p, p, 10.0, p, p, None)
+    e = AffxDeviceExpert()
+    e.gate = AffxMatrix(p, p, p, inter, hidden)
+    e.up = AffxMatrix(p, p, p, inter, hidden)
+    e.down = AffxMatrix(p, p, p, hidden, inter)
+    des17 = (AffxDeviceExpert * 17)(*([e] * 17))
+    rc = lib().affx_expert_ffn(des17, p, 17, p, p, 10.0, p, p, None)
+    assert rc == 1 and "at most" in last_error()
+    wide = AffxDeviceExpert()
+    wide.gate = AffxMatrix(p, p, p, inter, 2 * hidden)
+    wide.up = AffxMatrix(p, p, p, inter, 2 * hidden)
+    wide.down = AffxMatrix(p, p, p, 2 * hidden, inter)
+    rc = lib().affx_expert_ffn((AffxDeviceExpert * 1)(wide), p, 1, p, p, 10.0, p, p, None)
+    assert rc == 1 and "hidden" in last_error()
+    rc = lib().affx_expert_ffn((AffxDeviceExpert * 1)(e), p, 1, p, p, 0.0, p, p, None)
+    assert rc == 1 and "limit" in last_error()
+    bad = AffxDeviceExpert()
+    bad.gate, bad.up = e.gate, e.up
+    bad.down = AffxMatrix(p, p, p, hidden, hidden)
+    rc = lib().affx_expert_ffn((AffxDeviceExpert * 2)(e, bad), p, 2, p, p, 10.0, p, p, None)
     assert rc == -1 and "expected" in last_error()
+    torch.cuda.synchronize()
 
 
 def _grouped_slots(ax, pool, xb, lists, T, K):
