@@ -395,14 +395,16 @@ int affx_expert_swiglu_quant(const uint16_t* g, const uint16_t* u, const float* 
  * expert_scatter_slots_hip with its arguments unchanged (src/gpu/expert_kernel_hip.h:249-251,
  * expert_kernel.hip:935-947, 2837-2843). block[h * nb_stride + t] += sum over i in
  * run[t] .. run[t+1]-1, in that order from zero, of y[h * total + ord[i]]; tokens whose run is
- * empty are not written. Deterministic (no atomics). dim <= 65535. */
+ * empty are not written. Every ord[i] < total (not checked, as in the reference). Deterministic (no
+ * atomics). dim <= 65535. */
 int affx_expert_scatter_slots(const uint16_t* y, float* block, const uint32_t* ord, const uint32_t* run,
                               uint32_t dim, uint32_t nb_tok, uint32_t nb_stride, uint32_t total,
                               void* stream);
 
 /* nt token columns of a dim-major [dim][nb] arena into a compact [dim][nt] tile:
- * dst[c * nt + t] = src[c * nb + tok[t]]. expert_gather_tokens_hip with its arguments unchanged
- * (src/gpu/expert_kernel_hip.h:255-256, expert_kernel.hip:828-835, 1673-1680). */
+ * dst[c * nt + t] = src[c * nb + tok[t]], every tok[t] < nb (not checked, as in the reference).
+ * expert_gather_tokens_hip with its arguments unchanged (src/gpu/expert_kernel_hip.h:255-256,
+ * expert_kernel.hip:828-835, 1673-1680). */
 int affx_expert_gather_tokens(const float* src, float* dst, const uint32_t* tok, uint32_t dim,
                               uint32_t nb, uint32_t nt, void* stream);
 
