@@ -120,6 +120,14 @@ int decode_check(const affx_layer* L, uint32_t M, uint32_t K, const void* ws, si
 // Set-up of the allocation-free decode's scratch array on device `dev` (current), from affx_init.
 int noalloc_init_device(int dev);
 
+// ---- plain bf16 GEMM (hipBLASLt; affx_blas.cpp) -------------------------------------------------
+// D[n][m] = sum_k A[m][k] B[n][k] (+ D[n][m] when beta_one), f32 accumulation and output: A [M][K]
+// and B [N][K] bf16 row-major with row strides lda, ldb (elements), D [N][M] f32 with row stride
+// ldd. AFFX_DECLINED, with nothing enqueued, when the library has no algorithm for the shape. The
+// first call for a shape asks the library's heuristic on the host (not under graph capture).
+int blas_gemm_bf16_nt(uint32_t M, uint32_t N, uint32_t K, const void* A, uint32_t lda, const void* B, uint32_t ldb,
+                      float* D, uint32_t ldd, int beta_one, hipStream_t stream);
+
 // ---- status ------------------------------------------------------------------------------------
 int set_error(int code, const char* fmt, ...);
 int check_hip(hipError_t e, const char* what);

@@ -26,6 +26,9 @@
 //   shexp_gemm<1>    (256 rows of hidden, token tile): down, y (+)= result
 // The hyper-connection post: DenseGpu::hc_post (src/gpu/dense_gpu.hip:2394-2465, kernels
 // 1674-1724) and batch_hc_post (4517-4534, kernels src/gpu/batch_kernels.hip:1977-2019).
+#include <cstdlib>
+#include <cstring>
+
 #include "affx_lut.h"
 
 namespace affx {
@@ -661,6 +664,77 @@ __global__ void __launch_bounds__(256) hc_add_batch_kernel(uint16_t* __restrict_
   if (zb) block[i] = 0.0f;
 }
 
+// ------------------------------------------------------------------------------------------------
+// batch, library-GEMM form
+// ------------------------------------------------------------------------------------------------
+// The weights widened to bf16 row-major, each value E4M3 x its tile's 2^(e - 127), exactly (an
+// E4M3 value has at most four significant bits, and the product is a bf16 normal for tile exponents
+// 10..254; below 10, scales under 2^-117 that no checkpoint holds, the product's low bits are cut;
+// the exponent byte 255 and the E4M3 NaN codes give NaN). One launch for the three matrices, which
+// have the same size; one thread per 16-byte piece of the tile layout (16 weights of one row): two
+// hardware conversions per four bytes, the tile scale, the f32 product's high half (exact) packed,
+// 32 bytes out, written `copies` times at column offsets 0 and copy_off of the output row.
+struct WidenArgs {
+  const uint8_t* w[3];
+  const uint8_t* s[3];
+  uint16_t* out[3];
+  uint32_t rows[3], cols[3], ldo[3], copies[3], copy_off[3];
+  uint32_t wg_per;  // workgroups per matrix
+};
+
+__global__ void __launch_bounds__(256) shexp_widen_kernel(WidenArgs W) {
+  typedef float v2f __attribute__((ext_vector_type(2)));
+  const uint32_t mi = blockIdx.x / W.wg_per;
+  const uint32_t rows = W.rows[mi], cols = W.cols[mi];
+  const uint64_t q = (uint64_t)(blockIdx.x - mi * W.wg_per) * 256u + threadIdx.x;
+  if (mi >= 3u || q >= (uint64_t)rows * cols / 16u) return;
+  const uint32_t steps = cols >> 7, chunk = (uint32_t)(q >> 7), lane = (uint32_t)q & 63u;
+  const uint32_t half = ((uint32_t)q >> 6) & 1u, rt = chunk / steps, m = chunk - rt * steps;
+  const uint32_t row = 16u * rt + (lane & 15u), col = 128u * m + 64u * half + 16u * (lane >> 4);
+  const u32x4 v = *reinterpret_cast<const u32x4*>(W.w[mi] + q * 16u);
+  const uint32_t e = W.s[mi][(uint64_t)(row >> 7) * steps + m];
+  const float sc = e == 255u ? __uint_as_float(0x7FC00000u) : e ? __uint_as_float(e << 23) : __uint_as_float(0x00400000u);
+  u32x4 o[2];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const v2f lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)v[d], false), hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)v[d], true);
+    o[d >> 1][(d & 1) * 2] = __builtin_amdgcn_perm(__float_as_uint(lo[1] * sc), __float_as_uint(lo[0] * sc), 0x07060302u);
+    o[d >> 1][(d & 1) * 2 + 1] = __builtin_amdgcn_perm(__float_as_uint(hi[1] * sc), __float_as_uint(hi[0] * sc), 0x07060302u);
+  }
+  uint16_t* p = W.out[mi] + (uint64_t)row * W.ldo[mi] + col;
+  for (uint32_t c = 0; c < W.copies[mi]; ++c, p += W.copy_off[mi]) {
+    reinterpret_cast<u32x4*>(p)[0] = o[0];
+    reinterpret_cast<u32x4*>(p)[1] = o[1];
+  }
+}
+
+// The SwiGLU between the two GEMMs: g [T][2 inter] f32 (gate columns, then up) -> a [T][2 inter]
+// bf16, the output's high bf16 at column j and the rounded remainder at column inter + j (their
+// sum carries 16 significant bits). Four columns a thread.
+__global__ void __launch_bounds__(256) shexp_swiglu_split_kernel(const float* __restrict__ g, uint16_t* __restrict__ a,
+                                                                 uint32_t inter, uint64_t quads, float limit) {
+  const uint64_t q = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+  if (q >= quads) return;
+  const uint32_t per_row = inter >> 2;
+  const uint64_t t = q / per_row;
+  const uint32_t j = (uint32_t)(q - t * per_row) * 4u;
+  const float* gr = g + t * 2u * inter;
+  const float4 gv = *reinterpret_cast<const float4*>(gr + j), uv = *reinterpret_cast<const float4*>(gr + inter + j);
+  const float r[4] = {swiglu_clamped(gv.x, uv.x, limit), swiglu_clamped(gv.y, uv.y, limit),
+                      swiglu_clamped(gv.z, uv.z, limit), swiglu_clamped(gv.w, uv.w, limit)};
+  uint32_t hi[2], lo[2];
+#pragma unroll
+  for (int i = 0; i < 4; i += 2) {
+    const uint32_t h0 = hc_bf16(r[i]), h1 = hc_bf16(r[i + 1]);
+    const uint32_t l0 = hc_bf16(r[i] - __uint_as_float(h0 << 16)), l1 = hc_bf16(r[i + 1] - __uint_as_float(h1 << 16));
+    hi[i >> 1] = h0 | (h1 << 16);
+    lo[i >> 1] = l0 | (l1 << 16);
+  }
+  uint16_t* ar = a + t * 2u * inter;
+  *reinterpret_cast<uint64_t*>(ar + j) = (uint64_t)hi[0] | ((uint64_t)hi[1] << 32);
+  *reinterpret_cast<uint64_t*>(ar + inter + j) = (uint64_t)lo[0] | ((uint64_t)lo[1] << 32);
+}
+
 }  // namespace affx
 
 using namespace affx;
@@ -689,6 +763,68 @@ SharedWs shared_batch_ws(uint32_t T, uint32_t hidden, uint32_t inter) {
   w.aq = w.xq + a256((uint64_t)T * kTerms * hidden);
   w.total = w.aq + a256((uint64_t)T * kTerms * inter);
   return w;
+}
+
+// batch, library-GEMM form: [w_gu bf16 2 inter x hidden][w_d2 bf16 hidden x 2 inter]
+// [g f32 T x 2 inter][a bf16 T x 2 inter]
+struct SharedBlasWs {
+  uint64_t w_gu, w_d2, g, a, total;
+};
+
+SharedBlasWs shared_blas_ws(uint32_t T, uint32_t hidden, uint32_t inter) {
+  SharedBlasWs w;
+  const uint64_t wb = 4ull * inter * hidden;
+  w.w_gu = 0;
+  w.w_d2 = a256(wb);
+  w.g = w.w_d2 + a256(wb);
+  w.a = w.g + a256(8ull * T * inter);
+  w.total = w.a + a256(4ull * T * inter);
+  return w;
+}
+
+// the batch's form: the library GEMMs unless AFFX_SHARED_BATCH=mfma asks for the fp8 MFMA kernels
+bool shared_batch_mfma_only() {
+  const char* v = getenv("AFFX_SHARED_BATCH");
+  return v && strcmp(v, "mfma") == 0;
+}
+
+// The library-GEMM form of the batch: widen the three weight matrices to bf16 (gate rows then up
+// rows in one [2 inter][hidden] matrix; down twice along K as [hidden][2 inter]); G = X W_gu^T
+// (+ X_lo W_gu^T); the SwiGLU as two bf16 terms; y (+)= A W_d2^T, both terms summed by the GEMM.
+// AFFX_DECLINED before y is touched when the library has no algorithm for a shape.
+int shared_batch_blas(const affx_shared_expert* S, const void* x, const void* x_lo, uint32_t n_tok, float* y,
+                      int accumulate, uint8_t* b, hipStream_t s) {
+  const uint32_t H = S->hidden, I = S->inter;
+  const SharedBlasWs lay = shared_blas_ws(n_tok, H, I);
+  uint16_t* w_gu = (uint16_t*)(b + lay.w_gu);
+  uint16_t* w_d2 = (uint16_t*)(b + lay.w_d2);
+  float* g = (float*)(b + lay.g);
+  uint16_t* a = (uint16_t*)(b + lay.a);
+  WidenArgs W;
+  const affx_dense_fp8* mats[3] = {&S->gate, &S->up, &S->down};
+  for (int i = 0; i < 3; ++i) {
+    W.w[i] = (const uint8_t*)mats[i]->data;
+    W.s[i] = mats[i]->scales;
+    W.rows[i] = i < 2 ? I : H;
+    W.cols[i] = i < 2 ? H : I;
+    W.ldo[i] = i < 2 ? H : 2u * I;
+    W.copies[i] = i < 2 ? 1u : 2u;
+    W.copy_off[i] = i < 2 ? 0u : I;
+  }
+  W.out[0] = w_gu;
+  W.out[1] = w_gu + (uint64_t)I * H;
+  W.out[2] = w_d2;
+  W.wg_per = (uint32_t)((uint64_t)I * H / 16u / 256u);  // I * H is a multiple of 2^20
+  hipLaunchKernelGGL(shexp_widen_kernel, dim3(3u * W.wg_per), dim3(256), 0, s, W);
+  int rc = check_launch("shexp_widen_kernel");
+  if (rc) return rc;
+  if ((rc = blas_gemm_bf16_nt(2u * I, n_tok, H, w_gu, H, x, H, g, 2u * I, 0, s))) return rc;
+  if (x_lo && (rc = blas_gemm_bf16_nt(2u * I, n_tok, H, w_gu, H, x_lo, H, g, 2u * I, 1, s))) return rc;
+  const uint64_t quads = (uint64_t)n_tok * I / 4u;
+  hipLaunchKernelGGL(shexp_swiglu_split_kernel, dim3((uint32_t)((quads + 255u) / 256u)), dim3(256), 0, s, g, a, I,
+                     quads, S->swiglu_limit);
+  if ((rc = check_launch("shexp_swiglu_split_kernel"))) return rc;
+  return blas_gemm_bf16_nt(H, n_tok, 2u * I, w_d2, 2u * I, a, 2u * I, y, H, accumulate ? 1 : 0, s);
 }
 
 int shared_check(const affx_shared_expert* S, const char* what, uint32_t max_hidden) {
@@ -761,7 +897,8 @@ size_t affx_shared_decode_workspace_size(uint32_t m_tokens, uint32_t hidden, uin
 }
 
 size_t affx_shared_batch_workspace_size(uint32_t n_tok, uint32_t hidden, uint32_t inter) {
-  return (size_t)shared_batch_ws(n_tok, hidden, inter).total;
+  const uint64_t own = shared_batch_ws(n_tok, hidden, inter).total, lib = shared_blas_ws(n_tok, hidden, inter).total;
+  return (size_t)(own > lib ? own : lib);
 }
 
 int affx_shared_expert_decode(const affx_shared_expert* S, const float* x, uint64_t x_ts, uint64_t x_ds,
@@ -819,13 +956,19 @@ int affx_shared_expert_batch(const affx_shared_expert* S, const void* x, const v
     return set_error(AFFX_ERR_ARG, "shared_expert_batch: x, x_lo and y must be 16-byte aligned");
   if (n_tok == 0) return AFFX_OK;
   const SharedWs lay = shared_batch_ws(n_tok, S->hidden, S->inter);
-  if (lay.total > (1ull << 32))
+  const uint64_t need = affx_shared_batch_workspace_size(n_tok, S->hidden, S->inter);
+  if (lay.total > (1ull << 32) || need > (1ull << 33))
     return set_error(AFFX_DECLINED, "shared_expert_batch: batch too large (split it)");
-  if (ws_bytes < lay.total)
+  if (ws_bytes < need)
     return set_error(AFFX_ERR_ARG, "shared_expert_batch: workspace %zu < %llu bytes", ws_bytes,
-                     (unsigned long long)lay.total);
+                     (unsigned long long)need);
   uint8_t* b = (uint8_t*)ws;
   hipStream_t s = (hipStream_t)stream;
+  if (!shared_batch_mfma_only()) {
+    rc = shared_batch_blas(S, x, x_lo, n_tok, y, accumulate, b, s);
+    if (rc != AFFX_DECLINED) return rc;
+  }
+  // the fp8 MFMA kernels (a shape the library declines, or asked for by name)
   const uint32_t tx = x_lo ? 3 : 2;
   const uint32_t zmax = S->hidden > S->inter ? S->hidden : S->inter;
   hipLaunchKernelGGL(shexp_prep_rows_kernel, dim3(n_tok), dim3(256), 0, s, (const uint16_t*)x, (const uint16_t*)x_lo,

@@ -465,6 +465,8 @@ typedef struct affx_shared_expert {
 int affx_dense_fp8_to_device_layout(const void* src, void* dst, uint64_t rows, uint64_t cols, void* stream);
 
 size_t affx_shared_decode_workspace_size(uint32_t m_tokens, uint32_t hidden, uint32_t inter);
+/* The batch's workspace: 8 * inter * hidden bytes of widened weights plus 12 * inter bytes a token
+ * (n_tok = 4096, hidden 4096, inter 2048: 160 MiB). */
 size_t affx_shared_batch_workspace_size(uint32_t n_tok, uint32_t hidden, uint32_t inter);
 
 /* The shared expert on m_tokens <= 8 tokens: y[t] (+)= W_d . swiglu(W_g x[t], W_u x[t]).
@@ -484,7 +486,14 @@ int affx_shared_expert_decode(const affx_shared_expert* shexp, const float* x, u
  * every token. Replaces BatchOps::shexp (src/engine/model.h:504-505; DenseGpu::batch_shexp,
  * src/gpu/dense_gpu.hip:4897-4950, which accumulates into the batch block). x (and x_lo, or NULL)
  * bf16 [n_tok][hidden] as in affx_expert_ffn_grouped (x_lo carries the low part of an f32
- * input); y f32 [n_tok][hidden]; all 16-byte aligned. Three launches, no synchronisation. */
+ * input); y f32 [n_tok][hidden]; all 16-byte aligned. accumulate = 0 stores without reading y.
+ * The weights are widened to bf16 in the workspace (exact) and the two GEMMs run in hipBLASLt with
+ * f32 accumulation, the SwiGLU output between them as two bf16 terms (about 16 significant
+ * bits); a shape the library has no algorithm for, or the environment variable
+ * AFFX_SHARED_BATCH=mfma, takes the library's own fp8 MFMA kernels instead (activations as E4M3
+ * terms, about 3e-4 relative L2 on random codes). Four launches (five with x_lo), no
+ * synchronisation; the first call for a token count asks hipBLASLt's heuristic on the host, so it
+ * must not be the one a graph capture records. */
 int affx_shared_expert_batch(const affx_shared_expert* shexp, const void* x, const void* x_lo, uint32_t n_tok,
                              float* y, int accumulate, void* workspace, size_t workspace_bytes, void* stream);
 

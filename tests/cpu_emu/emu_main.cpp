@@ -39,6 +39,29 @@ extern "C" {
 #include <random>
 #include <string>
 
+// The library GEMM of affx_blas.cpp (hipBLASLt on the device) as a plain loop with the same
+// contract: D[n][m] = sum_k A[m][k] B[n][k] (+ D[n][m]), bf16 operands, products summed in double.
+namespace affx {
+int blas_gemm_bf16_nt(uint32_t M, uint32_t N, uint32_t K, const void* A, uint32_t lda, const void* B, uint32_t ldb,
+                      float* D, uint32_t ldd, int beta_one, hipStream_t) {
+  const uint16_t* a = (const uint16_t*)A;
+  const uint16_t* b = (const uint16_t*)B;
+  auto wide = [](uint16_t v) {
+    const uint32_t u = (uint32_t)v << 16;
+    float r;
+    memcpy(&r, &u, 4);
+    return (double)r;
+  };
+  for (uint32_t n = 0; n < N; ++n)
+    for (uint32_t m = 0; m < M; ++m) {
+      double acc = beta_one ? (double)D[(size_t)n * ldd + m] : 0.0;
+      for (uint32_t k = 0; k < K; ++k) acc += wide(a[(size_t)m * lda + k]) * wide(b[(size_t)n * ldb + k]);
+      D[(size_t)n * ldd + m] = (float)acc;
+    }
+  return 0;
+}
+}  // namespace affx
+
 namespace {
 
 constexpr uint32_t kCbFloats = kVariants * kLut * 4;  // a codebook as floats [2][1024][4]
@@ -506,8 +529,14 @@ int run_shared(int argc, char** argv) {
     printf("shared decode M=%u%s: rc=%d rel_l2=%.3e\n", Md, dim_major ? " (dim-major)" : "", rc, e);
     ok = ok && rc == 0 && e <= 1e-3;
   }
-  // batch: T bf16 tokens, with and without a low part, stored (accumulate 0)
-  for (int lo = 0; lo < 2; ++lo) {
+  // batch: T bf16 tokens, with and without a low part, stored (accumulate 0); the library-GEMM
+  // form (bf16 weights, the SwiGLU output as two bf16 terms) and the fp8 MFMA form
+  for (int form = 0; form < 4; ++form) {
+    const int lo = form & 1, mfma = form >> 1;
+    if (mfma)
+      setenv("AFFX_SHARED_BATCH", "mfma", 1);
+    else
+      unsetenv("AFFX_SHARED_BATCH");
     std::vector<float> xf((size_t)T * H), xr((size_t)T * H);
     std::vector<uint16_t> xh((size_t)T * H), xl((size_t)T * H);
     for (size_t i = 0; i < xf.size(); ++i) {
@@ -530,9 +559,10 @@ int run_shared(int argc, char** argv) {
       orc_shared_expert(w[0].data(), sc[0].data(), w[1].data(), sc[1].data(), w[2].data(), sc[2].data(), H, I, 10.0f,
                         xr.data() + (size_t)t * H, yref.data() + (size_t)t * H);
     const double e = rel_l2(y, yref);
-    printf("shared batch T=%u lo=%d: rc=%d rel_l2=%.3e\n", T, lo, rc, e);
-    ok = ok && rc == 0 && e <= 1e-3;
+    printf("shared batch T=%u lo=%d %s: rc=%d rel_l2=%.3e\n", T, lo, mfma ? "mfma" : "lib", rc, e);
+    ok = ok && rc == 0 && e <= (mfma ? 1e-3 : 1e-5);
   }
+  unsetenv("AFFX_SHARED_BATCH");
   // hyper-connection post: single token (every n_hc), batch, and the no-control adds; bit for bit
   for (uint32_t nh : {1u, 2u, 4u, 8u}) {
     std::vector<float> hc((size_t)nh * H), blk(H), post(nh), comb(nh * nh), out((size_t)nh * H), ref((size_t)nh * H);
