@@ -156,6 +156,37 @@ def test_shared_batch_prefill_shape_sampled(ax, orc, shexp, form):
     assert err <= BATCH_TOL[form]
 
 
+def test_shared_batch_graph_replay(ax, shexp, form):
+    """The batch captured in a HIP graph (after an eager call of the same token count, which
+    resolves the library GEMM's plan outside the capture) and replayed three times on new inputs,
+    with eager work between the replays: every replay equals the eager call on the same inputs
+    bit for bit (the library GEMM records one kernel launch per GEMM and no memset)."""
+    S, _ = shexp
+    T = 300
+    g = torch.Generator(device="cuda").manual_seed(23)
+    xs = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+    ys = torch.zeros((T, H), device="cuda")
+    xs.copy_(torch.randn((T, H), generator=g, device="cuda").to(torch.bfloat16))
+    S.batch(xs, ys, accumulate=False)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        S.batch(xs, ys, accumulate=False)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        S.batch(xs, ys, accumulate=False)
+    for rep in range(3):
+        xn = torch.randn((T, H), generator=g, device="cuda").to(torch.bfloat16)
+        want = S.batch(xn, torch.zeros((T, H), device="cuda"), accumulate=False)
+        xs.copy_(xn)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(ys, want), f"replay {rep} differs from the eager call"
+
+
 def test_shared_declines(ax, shexp):
     from affinity_amd._lib import AffxDeclined, AffxError
     S, _ = shexp
