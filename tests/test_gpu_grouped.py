@@ -76,6 +76,49 @@ def test_grouped_random_planes(ax, orc, c1_codebook, layer, T, k, skew, lo):
     assert err <= TOL
 
 
+@pytest.mark.parametrize("case", ["single", "one_expert", "one_expert_lo", "every_expert", "all_padding"])
+def test_grouped_route_edges(ax, orc, c1_codebook, layer, case):
+    """Route shapes at the edges of the grouping: one token with one route; every token on one
+    expert (200 tokens: two full wide tiles and a narrow tail with bf16 input, three full tiles
+    and a tail with the hi/lo input's 60-token tiles); every token on every expert (k = n); every
+    route padding (the output, accumulated into, stays as it was, bit for bit)."""
+    ex, pool, hidden, inter = layer
+    n = ex.shape[0]
+    rng = np.random.default_rng({"single": 1, "one_expert": 2, "one_expert_lo": 3, "every_expert": 4,
+                                 "all_padding": 5}[case])
+    T, k = {"single": (1, 1), "one_expert": (200, 1), "one_expert_lo": (200, 1), "every_expert": (25, n),
+            "all_padding": (5, 2)}[case]
+    lo = case == "one_expert_lo"
+    xf = rng.standard_normal((T, hidden)).astype(np.float32)
+    hi = bf16_bits(xf)
+    xl = bf16_bits(xf - (hi.astype(np.uint32) << 16).view(np.float32))
+    x = (hi.astype(np.uint32) << 16).view(np.float32)
+    if lo:
+        x = x + (xl.astype(np.uint32) << 16).view(np.float32)
+    w = rng.uniform(0.05, 1.0, (T, k)).astype(np.float32)
+    if case == "every_expert":
+        sel = np.stack([rng.permutation(n) for _ in range(T)]).astype(np.uint32)
+    elif case == "all_padding":
+        sel = np.full((T, k), 999, np.uint32)
+    else:
+        sel = np.full((T, k), 3, np.uint32)
+    gx = torch.from_numpy(hi.view(np.int16)).cuda().view(torch.bfloat16)
+    gl = torch.from_numpy(xl.view(np.int16)).cuda().view(torch.bfloat16) if lo else None
+    y0 = (torch.from_numpy(rng.standard_normal((T, hidden)).astype(np.float32)).cuda() if case == "all_padding"
+          else torch.zeros((T, hidden), device="cuda"))
+    y = ax.expert_ffn_grouped(pool, gx, torch.from_numpy(sel.astype(np.int32)).cuda(), torch.from_numpy(w).cuda(),
+                              y=y0.clone(), accumulate=True, x_lo=gl)
+    torch.cuda.synchronize()
+    got = (y - y0).cpu().numpy()
+    if case == "all_padding":
+        assert torch.equal(y, y0)
+        return
+    ref = _oracle(orc, ex, orc.unpack_codebook(c1_codebook), x, sel, w, hidden, inter)
+    err = rel_l2(got, ref)
+    print(f"{case}: T={T} k={k} rel_l2={err:.3e}")
+    assert err <= TOL
+
+
 def test_grouped_is_deterministic(ax, layer):
     ex, pool, hidden, inter = layer
     rng = np.random.default_rng(3)
