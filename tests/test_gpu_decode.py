@@ -182,12 +182,15 @@ def random_layer(ax, c1_codebook):
     return ex, _pool_from_numpy(ax, ex, c1_codebook, hidden, inter), hidden, inter
 
 
-@pytest.mark.parametrize("M,k", [(1, 6), (3, 4), (5, 6), (6, 6), (8, 6), (2, 1)])
+@pytest.mark.parametrize("M,k", [(1, 6), (3, 4), (5, 6), (6, 6), (8, 6), (2, 1), (1, 12), (8, 12), (1, 16), (8, 16)])
 def test_decode_random_planes(ax, orc, c1_codebook, random_layer, M, k):
+    """Up to the plan's limits: top-k 16 (the reference's limit) and 8 x 16 = 128 routes; k = 16
+    exceeds the layer's 12 experts, so those routes repeat experts (each repeat counts again)."""
     ex, pool, hidden, inter = random_layer
     rng = np.random.default_rng(M * 10 + k)
     x = (rng.standard_normal((M, hidden)) * 0.5).astype(np.float32)
-    sel = np.stack([rng.choice(ex.shape[0], k, replace=False) for _ in range(M)]).astype(np.uint32)
+    n = ex.shape[0]
+    sel = np.stack([rng.choice(n, k, replace=k > n) for _ in range(M)]).astype(np.uint32)
     w = rng.uniform(0.05, 1.0, (M, k)).astype(np.float32)
     got = _run_decode(ax, pool, x, sel, w)
     ref = _oracle_ffn(orc, ex, orc.unpack_codebook(c1_codebook), x, sel, w, hidden, inter)
