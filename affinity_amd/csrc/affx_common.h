@@ -135,6 +135,20 @@ int check_launch(const char* what);
 
 // ---- device helpers ----------------------------------------------------------------------------
 
+// Lanes of this wave whose BITS-bit key equals this lane's, among `valid` ones (one ballot per key
+// bit: a fixed cost, whatever the number of distinct keys).
+template <int BITS>
+__device__ __forceinline__ uint64_t same_key_lanes(uint32_t k, bool valid) {
+  uint64_t m = __ballot(valid);
+#pragma unroll
+  for (int b = 0; b < BITS; ++b) {
+    const uint32_t bit = (k >> b) & 1u;
+    const uint64_t bal = __ballot(bit);
+    m &= bit ? bal : ~bal;
+  }
+  return m;
+}
+
 // Exact E4M3 (OCP fn) -> f32 for a non-NaN byte.
 __device__ __forceinline__ float e4m3_to_f32(uint32_t b) {
   const uint32_t e = (b >> 3) & 15u, m = b & 7u;

@@ -92,19 +92,6 @@ __device__ __forceinline__ uint32_t nearest_entry(const float4* cent, float4 x, 
   return best;
 }
 
-// Lanes of this wave whose 10-bit (BITS = 10) or 1-bit key equals this lane's, among `valid` ones.
-template <int BITS>
-__device__ __forceinline__ uint64_t same_key_lanes(uint32_t k, bool valid) {
-  uint64_t m = __ballot(valid);
-#pragma unroll
-  for (int b = 0; b < BITS; ++b) {
-    const uint32_t bit = (k >> b) & 1u;
-    const uint64_t bal = __ballot(bit);
-    m &= bit ? bal : ~bal;
-  }
-  return m;
-}
-
 __device__ __forceinline__ double wave_sum(double v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = v + __shfl_xor(v, o);

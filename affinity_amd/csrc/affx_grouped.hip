@@ -110,13 +110,12 @@ __device__ __forceinline__ void put_tiles(Tile* tiles, uint32_t e, uint32_t b0, 
 // start_in: a caller's slot list, expert e owning slots [start_in[e], start_in[e+1]) of n_slots_in
 // (each bound clamped to n_slots_in; a range that runs backwards is empty); null: count the routes.
 __global__ void __launch_bounds__(kPlanThreads) grouped_plan_kernel(
-    const uint32_t* __restrict__ sel, uint32_t n_pairs, uint32_t n_experts, uint32_t tt1,
+    uint32_t* __restrict__ hist, uint32_t n_chunks, uint32_t n_experts, uint32_t tt1,
     uint32_t tt2, uint32_t nar1, uint32_t nar2, uint32_t mid1, uint32_t mid2, uint32_t tx,
     const uint32_t* __restrict__ start_in,
     uint32_t n_slots_in, uint32_t max_tiles1, uint32_t max_tiles2, GroupedHdr* __restrict__ hdr,
     uint32_t* __restrict__ offsets, Tile* __restrict__ tiles1, Tile* __restrict__ tiles2) {
   static_assert(AFFX_MAX_EXPERTS <= kPlanThreads, "one thread per expert in the scan");
-  __shared__ uint32_t cnt[AFFX_MAX_EXPERTS];
   __shared__ uint32_t wsum[(1 + 2 * kNCls) * (kPlanThreads / 64)];
   const uint32_t tid = threadIdx.x;
   uint32_t c = 0, b0 = 0;
@@ -126,24 +125,9 @@ __global__ void __launch_bounds__(kPlanThreads) grouped_plan_kernel(
       c = b > a ? b - a : 0u;
       b0 = a;
     }
-  } else {
-    for (uint32_t e = tid; e < AFFX_MAX_EXPERTS; e += kPlanThreads) cnt[e] = 0;
-    __syncthreads();
-    // counts per expert: eight routes per thread in flight at a time
-    constexpr uint32_t kU = 8;
-    for (uint32_t i0 = 0; i0 < n_pairs; i0 += kU * kPlanThreads) {
-      uint32_t ev[kU];
-#pragma unroll
-      for (uint32_t u = 0; u < kU; ++u) {
-        const uint32_t i = i0 + u * kPlanThreads + tid;
-        ev[u] = i < n_pairs ? sel[i] : ~0u;
-      }
-#pragma unroll
-      for (uint32_t u = 0; u < kU; ++u)
-        if (ev[u] < n_experts) atomicAdd(&cnt[ev[u]], 1u);
-    }
-    __syncthreads();
-    c = tid < n_experts ? cnt[tid] : 0u;
+  } else if (tid < n_experts) {
+    // an expert's count: the sum of its chunk counts (grouped_hist_kernel), in chunk order
+    for (uint32_t b = 0; b < n_chunks; ++b) c += hist[(uint64_t)b * n_experts + tid];
   }
   // slot offsets and tile offsets: one exclusive scan (expert order) of the count and the tiles of
   // each width class of both GEMMs
@@ -162,6 +146,16 @@ __global__ void __launch_bounds__(kPlanThreads) grouped_plan_kernel(
   for (int k = 0; k < kNCls; ++k) { need1 += tot[1 + k]; need2 += tot[1 + kNCls + k]; }
   // a caller's overlapping ranges could ask for more tiles than the workspace holds: then no tile
   const bool fits = need1 <= max_tiles1 && need2 <= max_tiles2;
+  if (!start_in && tid < n_experts) {
+    // each chunk's first slot of this expert: its offset plus the counts of the chunks before
+    uint32_t at = v[0];
+    for (uint32_t b = 0; b < n_chunks; ++b) {
+      const uint64_t hi = (uint64_t)b * n_experts + tid;
+      const uint32_t cb = hist[hi];
+      hist[hi] = at;
+      at += cb;
+    }
+  }
   if (fits && tid < n_experts) {
     if (!start_in) offsets[tid] = v[0];
     uint32_t at1[kNCls], at2[kNCls], base1 = 0, base2 = 0;
@@ -188,70 +182,94 @@ __global__ void __launch_bounds__(kPlanThreads) grouped_plan_kernel(
   }
 }
 
-// The routes form's ord/run: token t owns entries t k .. t k + k - 1 of ord, in route order
-// (run[t] = t k); a route that names no expert of the layer keeps ~0u there (the consumers skip
-// slot numbers past the slot count), grouped_place writes the slot of every other.
-__global__ void __launch_bounds__(256) grouped_run_kernel(const uint32_t* __restrict__ sel, uint32_t n_tok,
-                                                          uint32_t top_k, uint32_t n_experts,
-                                                          uint32_t* __restrict__ run, uint32_t* __restrict__ ord) {
-  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
-  if (i < n_tok * top_k && !(sel[i] < n_experts)) ord[i] = ~0u;
-  if (i <= n_tok) run[i] = i * top_k;
+// The routes form's placement, in two passes over chunks of kPlaceChunk routes (four rounds of
+// 256): grouped_hist_kernel counts each expert's routes per chunk, grouped_plan_kernel turns the
+// counts into each chunk's first slot per expert, grouped_place_kernel gives every route its slot.
+// A route's slot is its expert's offset plus the number of that expert's routes before it, so
+// each expert's slots hold its routes in route order, whatever the grid.
+constexpr uint32_t kPlaceChunk = 1024;
+
+// Counts of chunk blockIdx.x into hist[chunk][expert]. Also the routes form's ord/run for the
+// indices it covers: token t owns entries t k .. t k + k - 1 of ord, in route order (run[t] = t k);
+// a route that names no expert of the layer keeps ~0u there (the consumers skip slot numbers past
+// the slot count), grouped_place_kernel writes the slot of every other.
+__global__ void __launch_bounds__(256) grouped_hist_kernel(const uint32_t* __restrict__ sel, uint32_t n_pairs,
+                                                           uint32_t n_tok, uint32_t top_k, uint32_t n_experts,
+                                                           uint32_t* __restrict__ hist, uint32_t* __restrict__ run,
+                                                           uint32_t* __restrict__ ord) {
+  __shared__ uint32_t cnt[AFFX_MAX_EXPERTS];
+  const uint32_t b = blockIdx.x, tid = threadIdx.x;
+  for (uint32_t e = tid; e < n_experts; e += 256) cnt[e] = 0u;
+  __syncthreads();
+  uint32_t ev[kPlaceChunk / 256];
+#pragma unroll
+  for (uint32_t r = 0; r < kPlaceChunk / 256; ++r) {
+    const uint32_t i = b * kPlaceChunk + r * 256u + tid;
+    ev[r] = i < n_pairs ? sel[i] : ~0u;
+  }
+#pragma unroll
+  for (uint32_t r = 0; r < kPlaceChunk / 256; ++r) {
+    const uint32_t i = b * kPlaceChunk + r * 256u + tid;
+    if (ev[r] < n_experts)
+      atomicAdd(&cnt[ev[r]], 1u);
+    else if (i < n_pairs)
+      ord[i] = ~0u;
+    if (i <= n_tok) run[i] = i * top_k;
+  }
+  __syncthreads();
+  for (uint32_t e = tid; e < n_experts; e += 256) hist[(uint64_t)b * n_experts + e] = cnt[e];
 }
 
-// One workgroup per expert: walks all pairs in order and gives this expert's pairs consecutive
-// slots (pair i's slot goes to ord[i]). Thread tid takes 8 consecutive pairs of each 2048-pair
-// block (so thread order is pair order), an exclusive scan of the match counts places them; the
-// next block's routes are loaded before this block is placed.
-__global__ void __launch_bounds__(256) grouped_place_kernel(
-    const uint32_t* __restrict__ sel, const float* __restrict__ w, uint32_t n_pairs, uint32_t top_k,
-    const uint32_t* __restrict__ offsets, uint32_t* __restrict__ slot_tok, float* __restrict__ slot_w,
-    uint32_t* __restrict__ ord) {
-  const uint32_t e = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  uint32_t base = offsets[e];
-  const uint32_t end = offsets[e + 1];
-  if (end == base) return;
-  __shared__ uint32_t wsum[2][4];
-  constexpr uint32_t kPer = 8, kBlock = 256 * kPer;
-  auto load = [&](uint32_t i0, uint32_t (&v)[kPer]) {
+// The slots of chunk blockIdx.x. first[chunk][expert] is the chunk's first slot of each expert
+// (grouped_plan_kernel). Routes i = chunk start + 256 r + 64 w + lane: within a wave, the lanes of
+// the same expert are ranked by one ballot per expert-id bit; the (round, wave) groups are ranked
+// by an exclusive scan of their per-expert counts in LDS.
+__global__ void __launch_bounds__(256) grouped_place_kernel(const uint32_t* __restrict__ sel,
+                                                            const float* __restrict__ w, uint32_t n_pairs,
+                                                            uint32_t top_k, uint32_t n_experts,
+                                                            const uint32_t* __restrict__ first,
+                                                            uint32_t* __restrict__ slot_tok,
+                                                            float* __restrict__ slot_w, uint32_t* __restrict__ ord) {
+  static_assert(AFFX_MAX_EXPERTS <= 512, "expert ids ranked by 9 ballots");
+  constexpr uint32_t NR = kPlaceChunk / 256, NG = NR * 4;  // rounds, (round, wave) groups
+  __shared__ uint32_t grp[NG][AFFX_MAX_EXPERTS];
+  const uint32_t b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  for (uint32_t q = tid; q < NG * AFFX_MAX_EXPERTS; q += 256) (&grp[0][0])[q] = 0u;
+  uint32_t ev[NR], rank[NR];
 #pragma unroll
-    for (uint32_t k = 0; k < kPer; ++k) {
-      const uint32_t i = i0 + tid * kPer + k;
-      v[k] = i < n_pairs ? sel[i] : ~0u;
+  for (uint32_t r = 0; r < NR; ++r) {
+    const uint32_t i = b * kPlaceChunk + r * 256u + tid;
+    ev[r] = i < n_pairs ? sel[i] : ~0u;
+  }
+  __syncthreads();
+  const uint64_t below = (1ull << lane) - 1ull;
+#pragma unroll
+  for (uint32_t r = 0; r < NR; ++r) {
+    const bool ok = ev[r] < n_experts;
+    const uint64_t m = same_key_lanes<9>(ok ? ev[r] : 0u, ok);
+    rank[r] = (uint32_t)__popcll(m & below);
+    if (ok && (uint32_t)__builtin_ctzll(m) == lane) grp[r * 4u + wv][ev[r]] = (uint32_t)__popcll(m);
+  }
+  __syncthreads();
+  for (uint32_t e = tid; e < n_experts; e += 256) {
+    uint32_t at = 0;
+#pragma unroll
+    for (uint32_t g = 0; g < NG; ++g) {
+      const uint32_t c = grp[g][e];
+      grp[g][e] = at;
+      at += c;
     }
-  };
-  uint32_t cur[kPer], nxt[kPer];
-  load(0, cur);
-  for (uint32_t i0 = 0, it = 0; i0 < n_pairs && base < end; i0 += kBlock, ++it) {
-    if (i0 + kBlock < n_pairs) load(i0 + kBlock, nxt);
-    uint32_t m = 0;
+  }
+  __syncthreads();
+  const uint32_t* fb = first + (uint64_t)b * n_experts;
 #pragma unroll
-    for (uint32_t k = 0; k < kPer; ++k) m |= (cur[k] == e ? 1u : 0u) << k;
-    const uint32_t cnt = __popc(m);
-    uint32_t inc = cnt;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint32_t n = __shfl_up(inc, o);
-      if (lane >= (uint32_t)o) inc += n;
-    }
-    uint32_t* ws = wsum[it & 1];  // alternating: a wave may run one block ahead of a slow one
-    if (lane == 63) ws[wv] = inc;
-    __syncthreads();
-    uint32_t pos = base + inc - cnt;
-    for (uint32_t q = 0; q < wv; ++q) pos += ws[q];
-    const uint32_t total = ws[0] + ws[1] + ws[2] + ws[3];
-#pragma unroll
-    for (uint32_t k = 0; k < kPer; ++k)
-      if ((m >> k) & 1u) {
-        const uint32_t i = i0 + tid * kPer + k;
-        slot_tok[pos] = i / top_k;
-        slot_w[pos] = w[i];
-        ord[i] = pos;
-        ++pos;
-      }
-    base += total;
-#pragma unroll
-    for (uint32_t k = 0; k < kPer; ++k) cur[k] = nxt[k];
+  for (uint32_t r = 0; r < NR; ++r) {
+    if (!(ev[r] < n_experts)) continue;
+    const uint32_t i = b * kPlaceChunk + r * 256u + tid;
+    const uint32_t pos = fb[ev[r]] + grp[r * 4u + wv][ev[r]] + rank[r];
+    slot_tok[pos] = i / top_k;
+    slot_w[pos] = w[i];
+    ord[i] = pos;
   }
 }
 
@@ -986,12 +1004,18 @@ namespace {
 
 
 struct GroupedWs {
-  uint64_t hdr, offsets, run, slot_tok, slot_w, ord, tiles1, tiles2, sigma, zeros, xq, aq, z, total;
+  uint64_t hdr, offsets, run, slot_tok, slot_w, ord, hist, tiles1, tiles2, sigma, zeros, xq, aq, z, total;
   uint32_t max_tiles1, max_tiles2;
 };
 
 // tokens per workgroup tile: kGCT column tiles of 16 / terms tokens each
 uint32_t tile_tokens(uint32_t terms) { return kGCT * (16 / terms); }
+
+// chunks of the routes form's placement: they cover the routes and the run entries 0 .. T
+uint64_t place_chunks(uint32_t T, uint64_t P) {
+  const uint64_t n = P > T ? P : (uint64_t)T + 1;
+  return (n + kPlaceChunk - 1) / kPlaceChunk;
+}
 
 // T tokens, room for P slots (the routes form: T * top_k)
 GroupedWs grouped_ws(uint32_t T, uint64_t P, uint32_t E, uint32_t hidden, uint32_t inter, uint32_t tx) {
@@ -1006,6 +1030,7 @@ GroupedWs grouped_ws(uint32_t T, uint64_t P, uint32_t E, uint32_t hidden, uint32
   w.slot_tok = o; o += a256(4 * P);
   w.slot_w = o; o += a256(4 * P);
   w.ord = o; o += a256(4 * P);
+  w.hist = o; o += a256(4ull * place_chunks(T, P) * E);
   w.tiles1 = o; o += a256(sizeof(Tile) * w.max_tiles1);
   w.tiles2 = o; o += a256(sizeof(Tile) * w.max_tiles2);
   w.sigma = o; o += a256(4 * P);  // per slot
@@ -1077,19 +1102,22 @@ int grouped_body(const affx_layer* L, const void* x, const void* x_lo, uint32_t 
   // column tiles
   const uint32_t nar1 = kGNarrow * (16 / tx), nar2 = kGNarrow * (16 / 3);
   const uint32_t mid1 = kGMid * (16 / tx), mid2 = kGMid * (16 / 3);
-  hipLaunchKernelGGL(grouped_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, sel, Pp, L->n_experts, tt1, tt2, nar1,
+  const uint32_t nch = sel ? (uint32_t)place_chunks(T, Pp) : 0u;
+  if (sel) {
+    hipLaunchKernelGGL(grouped_hist_kernel, dim3(nch), dim3(256), 0, s, sel, Pp, T, K, L->n_experts,
+                       (uint32_t*)(b + lay.hist), (uint32_t*)(b + lay.run), (uint32_t*)(b + lay.ord));
+    if (int rc0 = check_launch("grouped_hist_kernel")) return rc0;
+  }
+  hipLaunchKernelGGL(grouped_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, (uint32_t*)(b + lay.hist), nch,
+                     L->n_experts, tt1, tt2, nar1,
                      nar2, mid1, mid2, tx, sel ? nullptr : start, sel ? 0u : n_slots, lay.max_tiles1, lay.max_tiles2,
                      (GroupedHdr*)(b + lay.hdr), (uint32_t*)(b + lay.offsets), (Tile*)(b + lay.tiles1),
                      (Tile*)(b + lay.tiles2));
   int rc = check_launch("grouped_plan_kernel");
   if (rc) return rc;
   if (sel) {
-    const uint32_t nr = Pp > T ? Pp : T + 1;
-    hipLaunchKernelGGL(grouped_run_kernel, dim3((nr + 255) / 256), dim3(256), 0, s, sel, T, K, L->n_experts,
-                       (uint32_t*)(b + lay.run), (uint32_t*)(b + lay.ord));
-    if ((rc = check_launch("grouped_run_kernel"))) return rc;
-    hipLaunchKernelGGL(grouped_place_kernel, dim3(L->n_experts), dim3(256), 0, s, sel, w, Pp, K,
-                       (const uint32_t*)(b + lay.offsets), (uint32_t*)(b + lay.slot_tok), (float*)(b + lay.slot_w),
+    hipLaunchKernelGGL(grouped_place_kernel, dim3(nch), dim3(256), 0, s, sel, w, Pp, K, L->n_experts,
+                       (const uint32_t*)(b + lay.hist), (uint32_t*)(b + lay.slot_tok), (float*)(b + lay.slot_w),
                        (uint32_t*)(b + lay.ord));
     if ((rc = check_launch("grouped_place_kernel"))) return rc;
   }
