@@ -952,8 +952,9 @@ int affx_shared_expert_batch(const affx_shared_expert* S, const void* x, const v
   int rc = shared_check(S, "shared_expert_batch", 8192);
   if (rc) return rc;
   if (!x || !y || !ws) return set_error(AFFX_ERR_ARG, "shared_expert_batch: null pointer");
-  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(x_lo) | reinterpret_cast<uintptr_t>(y)) & 15u)
-    return set_error(AFFX_ERR_ARG, "shared_expert_batch: x, x_lo and y must be 16-byte aligned");
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(x_lo) | reinterpret_cast<uintptr_t>(y) |
+       reinterpret_cast<uintptr_t>(ws)) & 15u)
+    return set_error(AFFX_ERR_ARG, "shared_expert_batch: x, x_lo, y and the workspace must be 16-byte aligned");
   if (n_tok == 0) return AFFX_OK;
   const SharedWs lay = shared_batch_ws(n_tok, S->hidden, S->inter);
   const uint64_t need = affx_shared_batch_workspace_size(n_tok, S->hidden, S->inter);

@@ -486,7 +486,8 @@ int affx_shared_expert_decode(const affx_shared_expert* shexp, const float* x, u
  * every token. Replaces BatchOps::shexp (src/engine/model.h:504-505; DenseGpu::batch_shexp,
  * src/gpu/dense_gpu.hip:4897-4950, which accumulates into the batch block). x (and x_lo, or NULL)
  * bf16 [n_tok][hidden] as in affx_expert_ffn_grouped (x_lo carries the low part of an f32
- * input); y f32 [n_tok][hidden]; all 16-byte aligned. accumulate = 0 stores without reading y.
+ * input); y f32 [n_tok][hidden]; these and the workspace 16-byte aligned. accumulate = 0 stores
+ * without reading y.
  * The weights are widened to bf16 in the workspace (exact) and the two GEMMs run in hipBLASLt with
  * f32 accumulation, the SwiGLU output between them as two bf16 terms (about 16 significant
  * bits); a shape the library has no algorithm for, or the environment variable

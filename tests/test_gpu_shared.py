@@ -210,6 +210,14 @@ def test_shared_declines(ax, shexp):
     with pytest.raises(AffxError):                   # workspace too small
         check(lib().affx_shared_expert_decode(ctypes.byref(S.abi), x.data_ptr(), H, 1, 1, y.data_ptr(), H, 1, 0,
                                               ws.data_ptr(), 16, 0), "decode")
+    # the batch: a workspace off 16-byte alignment, and one too small, are refused before any launch
+    xb = torch.zeros((4, H), dtype=torch.bfloat16, device="cuda")
+    yb = torch.zeros((4, H), device="cuda")
+    wsb = torch.empty(lib().affx_shared_batch_workspace_size(4, H, I) + 256, dtype=torch.uint8, device="cuda")
+    for ptr, n in ((wsb.data_ptr() + 8, wsb.numel() - 8), (wsb.data_ptr(), 1024)):
+        with pytest.raises(AffxError):
+            check(lib().affx_shared_expert_batch(ctypes.byref(S.abi), xb.data_ptr(), 0, 4, yb.data_ptr(), 0, ptr, n,
+                                                 0), "batch")
 
 
 @pytest.mark.parametrize("n_hc", [1, 2, 4, 8])
