@@ -24,6 +24,12 @@ class AffxMatrix(C.Structure):
     _fields_ = [("codes", _vp), ("fields", _vp), ("rscales", _vp), ("rows", _u32), ("cols", _u32)]
 
 
+class AffxExpertTile(C.Structure):
+    """affx_expert_tile: one expert matrix's share of a W8A8 GEMM launch (ExpertTile's fields)."""
+    _fields_ = [("codes", _vp), ("fields", _vp), ("rscales", _vp), ("tok", _vp), ("y", _vp), ("nt", _u32),
+                ("ld", _u32)]
+
+
 class AffxDeviceExpert(C.Structure):
     _fields_ = [("gate", AffxMatrix), ("up", AffxMatrix), ("down", AffxMatrix)]
 
@@ -99,6 +105,7 @@ _SIGS = {
     "affx_expert_swiglu_quant": ([_vp, _vp, _vp, _vp, _vp, _u32, _u32, C.c_float, _vp], C.c_int),
     "affx_expert_scatter_slots": ([_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp], C.c_int),
     "affx_expert_gather_tokens": ([_vp, _vp, _vp, _u32, _u32, _u32, _vp], C.c_int),
+    "affx_expert_gemm_w8a8": ([_vp, _u32, _u32, _vp, _vp, _vp, _u32, _u32, C.c_float, C.c_int, _vp], C.c_int),
     "affx_route_topk": ([_vp, _u64, _u64, _vp, _u32, _u32, _u32, C.c_int, C.c_int, C.c_float, _vp, _vp, _vp],
                         C.c_int),
     "affx_dense_fp8_to_device_layout": ([_vp, _vp, _u64, _u64, _vp], C.c_int),

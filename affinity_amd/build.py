@@ -12,7 +12,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libaffx.so")
 SOURCES = ["affx_layout.hip", "affx_decode.hip", "affx_fused.hip", "affx_quant.hip", "affx_grouped.hip", "affx_api.hip",
-           "affx_noalloc.hip", "affx_route.hip", "affx_shared.hip", "affx_fit.hip", "affx_gemv.hip", "affx_steps.hip",
+           "affx_noalloc.hip", "affx_route.hip", "affx_shared.hip", "affx_fit.hip", "affx_gemv.hip", "affx_steps.hip", "affx_w8a8.hip",
            "affx_container.cpp", "affx_blas.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 

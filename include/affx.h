@@ -408,6 +408,37 @@ int affx_expert_scatter_slots(const uint16_t* y, float* block, const uint32_t* o
 int affx_expert_gather_tokens(const float* src, float* dst, const uint32_t* tok, uint32_t dim,
                               uint32_t nb, uint32_t nt, void* stream);
 
+/* One expert matrix's share of a W8A8 GEMM launch. Mirrors ExpertTile (src/gpu/expert_kernel_hip.h:
+ * 200-215) field for field: codes/fields/rscales are one matrix's planes in device layout (as in
+ * affx_matrix), tok = nt token ids into the activation's rows (NULL: 0 .. nt-1), y = the output
+ * [rows][ld] (ld = 0: a compact [rows][nt] block), f32 or bf16 by the launch's y_bf16. */
+typedef struct affx_expert_tile {
+  const void* codes;
+  const void* fields;
+  const void* rscales;
+  const uint32_t* tok;
+  void* y;
+  uint32_t nt;
+  uint32_t ld;
+} affx_expert_tile;
+
+/* The single-matrix W8A8 GEMM between the steps above: expert_gemm_wmma_hip with its arguments
+ * (src/gpu/expert_kernel_hip.h:217-228; kernel expert_kernel.hip:364-825, host 3018-3062). tiles:
+ * a DEVICE array of n_tiles descriptors (nt = 0 is a pad and writes nothing), every nt <= max_nt <=
+ * 64. x8: E4M3 activations token-major [tokens][cols]; xs: f32 [tokens][cols / 128], one scale per
+ * (token, 128-column block); codebook: the packed uint32[2048] (the reference passes the same bytes
+ * as `const float* cb`). For each tile, row r < rows and column j < nt, t = tok ? tok[j] : j:
+ *   out = sum over blocks kb in order of fmaf(raw_kb, xs[t][kb], out), raw_kb = sum over the
+ *         block's 128 columns of W8[r][k] * x8[t][k] (W8: the weight's E4M3 value without the row
+ *         scale: codebook entry, block exponent add, sign, rotation);
+ *   y[r * (ld ? ld : nt) + j] = out * (bf16 rscales[r] * wscale), stored f32, or bf16 rounded to
+ *         nearest even when y_bf16.
+ * rows % 16 == 0, cols % 1024 == 0 (AFFX_DECLINED otherwise, as for max_nt > 64); x8 and xs
+ * 16-byte aligned. Stream-ordered, no synchronisation. */
+int affx_expert_gemm_w8a8(const affx_expert_tile* tiles, uint32_t n_tiles, uint32_t max_nt, const void* x8,
+                          const float* xs, const uint32_t* codebook, uint32_t rows, uint32_t cols, float wscale,
+                          int y_bf16, void* stream);
+
 /* ---- routing on the device ------------------------------------------------------------------ */
 
 #define AFFX_ROUTE_ENGINE 0  /* the engine router: sqrtsoftplus scores, bias for selection only */

@@ -101,6 +101,8 @@ class Oracle:
         L.orc_swiglu_quant.argtypes = [_u16p, _u16p, _f32p, _u8p, _f32p, C.c_uint32, C.c_uint32, C.c_float]
         L.orc_scatter_slots.argtypes = [_u16p, _f32p, _u32p, _u32p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32]
         L.orc_gather_tokens.argtypes = [_f32p, _f32p, _u32p, C.c_uint32, C.c_uint32, C.c_uint32]
+        L.orc_expert_gemm_w8a8.argtypes = [_u8p, _u8p, _u16p, _u32p, C.c_uint32, C.c_uint32, _u8p, _f32p, _f32p,
+                                           C.c_uint64, C.c_uint64, C.c_float, C.c_int, C.c_void_p]
 
     # -- threads ---------------------------------------------------------------------------
     def set_threads(self, n: int) -> None:
@@ -145,6 +147,25 @@ class Oracle:
         self.lib.orc_gather_tokens(_p(np.ascontiguousarray(src, np.float32), _f32p), _p(dst, _f32p),
                                    _p(np.ascontiguousarray(tok, np.uint32), _u32p), dim, nb, nt)
         return dst
+
+    def expert_gemm_w8a8(self, codes: np.ndarray, fields: np.ndarray, rscales: np.ndarray, tok, nt: int,
+                         x8: np.ndarray, xs: np.ndarray, cb: np.ndarray, rows: int, cols: int, wscale: float,
+                         y_bf16: bool = False, ld: int = 0, y: np.ndarray | None = None) -> np.ndarray:
+        """One tile of the W8A8 GEMM: planes in container layout (one matrix), tok uint32 [nt] or
+        None, x8 uint8 [tokens][cols], xs f32 [tokens][cols/128] -> y [rows][ld or nt] (f32, or
+        uint16 bf16 bits); an existing y keeps its other columns."""
+        yld = ld if ld else nt
+        if y is None:
+            y = np.zeros((rows, yld), np.uint16 if y_bf16 else np.float32)
+        tp = None if tok is None else _p(np.ascontiguousarray(tok, np.uint32), _u32p)
+        self.lib.orc_expert_gemm_w8a8(_p(np.ascontiguousarray(codes, np.uint8), _u8p),
+                                      _p(np.ascontiguousarray(fields, np.uint8), _u8p),
+                                      _p(np.ascontiguousarray(rscales).view(np.uint16), _u16p), tp, nt, ld,
+                                      _p(np.ascontiguousarray(x8, np.uint8), _u8p),
+                                      _p(np.ascontiguousarray(xs, np.float32), _f32p),
+                                      _p(np.ascontiguousarray(cb, np.float32), _f32p), rows, cols, float(wscale),
+                                      int(bool(y_bf16)), y.ctypes.data)
+        return y
 
     def e4m3_nearest(self, f: float) -> int:
         return int(self.lib.orc_e4m3_nearest(f))

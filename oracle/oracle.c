@@ -827,3 +827,54 @@ void orc_gather_tokens(const float* src, float* dst, const uint32_t* tok, uint32
   for (uint32_t c = 0; c < dim; ++c)
     for (uint32_t t = 0; t < nt; ++t) dst[(size_t)c * nt + t] = src[(size_t)c * nb + tok[t]];
 }
+
+/* The reference's single-matrix W8A8 GEMM for one tile (expert_gemm_wmma_kernel,
+ * src/gpu/expert_kernel.hip:364-825): for row r and column j < nt, t = tok ? tok[j] : j,
+ *   out = fold over the 128-column blocks kb in order of fmaf(raw_kb, xs[t][kb], out), raw_kb =
+ *         the block's sum of W8[r][k] * x8[t][k] (the products are exact in f32; summed here in
+ *         double and rounded once), W8 = the weight's value without its row scale, i.e.
+ *         dequantize_matrix (blockquant.cpp:793-833) with rscale 1: 2^s * (+-1) * e[(p + rh) % 4];
+ *   y[r * yld + j] = out * (bf16 rscales[r] * wscale) (expert_kernel.hip:808-837), f32 or, with
+ *         y_bf16, bf16 by round to nearest even. yld = ld ? ld : nt. Planes in the container's
+ *         row-major bit streams; cb the unpacked f32 codebook [2][1024][4]. */
+void orc_expert_gemm_w8a8(const uint8_t* codes, const uint8_t* fields, const uint16_t* rscales, const uint32_t* tok,
+                          uint32_t nt, uint32_t ld, const uint8_t* x8, const float* xs, const float* cb,
+                          uint64_t rows, uint64_t cols, float wscale, int y_bf16, void* y) {
+  const uint64_t nblk = cols / ORC_BLOCK, codes_row = cols / 4, nkb = cols / 128;
+  const uint32_t yld = ld ? ld : nt;
+  float x8f[256];
+  for (int i = 0; i < 256; ++i) x8f[i] = orc_e4m3_to_float((uint8_t)i);
+#pragma omp parallel for num_threads(NT) schedule(static)
+  for (uint64_t r = 0; r < rows; ++r) {
+    float* w8 = (float*)malloc(cols * sizeof(float));
+    for (uint64_t b = 0; b < nblk; ++b) {
+      const uint32_t f = orc_unpack_bits(fields, r * nblk + b, 6);
+      const uint32_t s = f & 7u, g = (f >> 3) & 3u;
+      const uint32_t v = (f >> 5) < 1u ? (f >> 5) : 1u;
+      const float bs = (float)(1u << s) * ((g & 1u) ? -1.0f : 1.0f);
+      const uint32_t rh = (g & 2u) ? 2u : 0u;
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t c = orc_unpack_bits(codes, r * codes_row + b * 4 + i, 10);
+        const float* e = cb + ((size_t)v * ORC_LUT + c) * 4;
+        for (uint32_t p = 0; p < 4; ++p) w8[b * ORC_BLOCK + i * 4 + p] = bs * e[(p + rh) % 4];
+      }
+    }
+    const float rs = orc_bf16_to_f32(rscales[r]) * wscale;
+    for (uint32_t j = 0; j < nt; ++j) {
+      const uint32_t t = tok ? tok[j] : j;
+      const uint8_t* xr = x8 + (size_t)t * cols;
+      float out = 0.0f;
+      for (uint64_t kb = 0; kb < nkb; ++kb) {
+        double acc = 0.0;
+        for (uint64_t k = kb * 128; k < kb * 128 + 128; ++k) acc += (double)w8[k] * (double)x8f[xr[k]];
+        out = fmaf((float)acc, xs[(size_t)t * nkb + kb], out);
+      }
+      const float val = out * rs;
+      if (y_bf16)
+        ((uint16_t*)y)[r * yld + j] = orc_f32_to_bf16(val);
+      else
+        ((float*)y)[r * yld + j] = val;
+    }
+    free(w8);
+  }
+}

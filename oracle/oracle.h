@@ -102,6 +102,9 @@ void orc_swiglu_quant(const uint16_t* g, const uint16_t* u, const float* w, uint
 void orc_scatter_slots(const uint16_t* y, float* block, const uint32_t* ord, const uint32_t* run, uint32_t dim,
                        uint32_t nb_tok, uint32_t nb_stride, uint32_t total);
 void orc_gather_tokens(const float* src, float* dst, const uint32_t* tok, uint32_t dim, uint32_t nb, uint32_t nt);
+void orc_expert_gemm_w8a8(const uint8_t* codes, const uint8_t* fields, const uint16_t* rscales, const uint32_t* tok,
+                          uint32_t nt, uint32_t ld, const uint8_t* x8, const float* xs, const float* cb,
+                          uint64_t rows, uint64_t cols, float wscale, int y_bf16, void* y);
 
 #ifdef __cplusplus
 }

@@ -17,6 +17,8 @@
 //   emu_main fit     rows cols budget iters seed [seq]    -> sample collection, the codebook fit
 //                    (with `seq` every k-means++ draw by the sequential sums), projection, packing
 //                    and unpacking, each bit for bit vs the oracle
+//   emu_main w8a8    hidden inter seed                    -> the single-matrix W8A8 GEMM (three
+//                    tiles, f32 and bf16 outputs, a strided arena) vs the oracle
 //   emu_main timeout hidden inter n_experts M K seed      -> a decode whose waiters give up (spin
 //                    limit 0 from the host) fails the engine hook and affx_decode_status; after
 //                    the reset, the next calls are correct
@@ -384,6 +386,71 @@ int run_gemv(int argc, char** argv) {
   const double e = rel_l2(y, yref), e1 = rel_l2(y1, y1ref);
   printf("gemv rc=%d batch rel_l2=%.3e single rel_l2=%.3e %s\n", rc, e, e1, rc ? affx_last_error() : "");
   return rc == 0 && e <= 1e-3 && e1 <= 1e-3 ? 0 : 1;
+}
+
+// The single-matrix W8A8 GEMM against the oracle: one launch of three tiles (each a different
+// expert's down matrix: 64 tokens by identity into a compact block, 13 listed tokens into a strided
+// arena, a pad), then a bf16 launch of 5 tokens; the other columns of the strided arena untouched.
+int run_w8a8(int argc, char** argv) {
+  const uint32_t hidden = atoi(argv[2]), inter = atoi(argv[3]);
+  std::mt19937_64 rng(atoi(argv[4]));
+  Layer L(hidden, inter, 3, rng);
+  const uint32_t rows = hidden, cols = inter, nkb = cols / 128, ntok = 80;
+  std::vector<uint8_t> x8((size_t)ntok * cols);
+  for (auto& b : x8) {
+    b = (uint8_t)(rng() & 0xFF);
+    if ((b & 0x7F) == 0x7F) b ^= 1;
+  }
+  std::uniform_real_distribution<float> ud(0.01f, 2.0f);
+  std::vector<float> xs((size_t)ntok * nkb);
+  for (auto& v : xs) v = ud(rng);
+  std::vector<uint32_t> tok1(13);
+  for (auto& t : tok1) t = (uint32_t)(rng() % ntok);
+  const uint32_t ld1 = 20;
+  std::vector<float> y0((size_t)rows * 64, -1.f), y1((size_t)rows * ld1, 5.f), r0(y0.size()), r1(y1);
+  std::vector<uint16_t> yb((size_t)rows * 5), rb(yb.size());
+  auto tile = [&](uint32_t e, const uint32_t* tok, void* y, uint32_t nt, uint32_t ld) {
+    const uint8_t* d = L.dev.data() + (uint64_t)e * L.stride;
+    return affx_expert_tile{d + L.off[6], d + L.off[7], d + L.off[8], tok, y, nt, ld};
+  };
+  auto oracle = [&](uint32_t e, const uint32_t* tok, void* y, uint32_t nt, uint32_t ld, int bf) {
+    const uint8_t* c = L.cont.data() + (uint64_t)e * L.stride;
+    orc_expert_gemm_w8a8(c + L.off[6], c + L.off[7], (const uint16_t*)(c + L.off[8]), tok, nt, ld, x8.data(),
+                         xs.data(), L.cbf.data(), rows, cols, 0.5f, bf, y);
+  };
+  affx_expert_tile t3[3] = {tile(0, nullptr, y0.data(), 64, 0), tile(1, tok1.data(), y1.data(), 13, ld1),
+                            tile(2, nullptr, nullptr, 0, 0)};
+  int rc = affx_expert_gemm_w8a8(t3, 3, 64, x8.data(), xs.data(), L.cb.data(), rows, cols, 0.5f, 0, nullptr);
+  affx_expert_tile tb = tile(2, tok1.data() + 3, yb.data(), 5, 0);
+  if (rc == 0) rc = affx_expert_gemm_w8a8(&tb, 1, 5, x8.data(), xs.data(), L.cb.data(), rows, cols, 0.5f, 1, nullptr);
+  oracle(0, nullptr, r0.data(), 64, 0, 0);
+  oracle(1, tok1.data(), r1.data(), 13, ld1, 0);
+  oracle(2, tok1.data() + 3, rb.data(), 5, 0, 1);
+  // the worst error over each output's scale (its largest magnitude), and the relative L2
+  bool ok = rc == 0;
+  double num = 0.0, den = 0.0, emax = 0.0, rmax = 0.0;
+  for (size_t i = 0; i < y0.size(); ++i) {
+    num += (y0[i] - r0[i]) * (double)(y0[i] - r0[i]);
+    den += (double)r0[i] * r0[i];
+    emax = std::max(emax, (double)std::fabs(y0[i] - r0[i]));
+    rmax = std::max(rmax, (double)std::fabs(r0[i]));
+  }
+  for (size_t i = 0; i < y1.size(); ++i) {
+    if (i % ld1 >= 13) {
+      ok = ok && y1[i] == 5.f;
+      continue;
+    }
+    num += (y1[i] - r1[i]) * (double)(y1[i] - r1[i]);
+    den += (double)r1[i] * r1[i];
+    emax = std::max(emax, (double)std::fabs(y1[i] - r1[i]));
+    rmax = std::max(rmax, (double)std::fabs(r1[i]));
+  }
+  const double worst = emax / rmax, l2 = std::sqrt(num / den);
+  int bf_off = 0;
+  for (size_t i = 0; i < yb.size(); ++i) bf_off = std::max(bf_off, std::abs((int)(int16_t)yb[i] - (int)(int16_t)rb[i]));
+  printf("w8a8 rc=%d rel_l2=%.3e worst/max=%.3e bf16_ulps=%d others_kept=%d %s\n", rc, l2, worst, bf_off, (int)ok,
+         rc ? affx_last_error() : "");
+  return ok && l2 <= 1e-5 && worst <= 1e-5 && bf_off <= 1 ? 0 : 1;
 }
 
 // The separable batch-pipeline steps against the oracle: gather and scatter bit for bit, the
@@ -846,6 +913,7 @@ int main(int argc, char** argv) {
   if (cmd == "fit" && argc >= 7) return run_fit(argc, argv);
   if (cmd == "gemv" && argc >= 6) return run_gemv(argc, argv);
   if (cmd == "steps" && argc >= 5) return run_steps(argc, argv);
+  if (cmd == "w8a8" && argc >= 5) return run_w8a8(argc, argv);
   fprintf(stderr, "usage: see header\n");
   return 2;
 }

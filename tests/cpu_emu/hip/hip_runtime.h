@@ -148,6 +148,7 @@ inline T emu_exchange(T v, uint32_t src) {
   T r; memcpy(&r, &got, sizeof(T)); return r;
 }
 template <typename T> inline T __shfl_xor(T v, int o, int width = 64) { return emu_exchange(v, emu_lane() ^ o); }
+template <typename T> inline T __shfl(T v, int src, int width = 64) { return emu_exchange(v, (uint32_t)src & 63u); }
 template <typename T> inline T __builtin_amdgcn_readlane(T v, uint32_t l) { return emu_exchange(v, l); }
 inline int __builtin_amdgcn_ds_bpermute(int addr, int v) { return emu_exchange(v, ((uint32_t)addr >> 2) & 63); }
 template <typename T> inline T __shfl_down(T v, int d, int width = 64) {
@@ -158,12 +159,14 @@ template <typename T> inline T __shfl_up(T v, int d, int width = 64) {
   uint32_t l = emu_lane(); uint32_t src = (l % width) >= (uint32_t)d ? l - d : l;
   return emu_exchange(v, src);
 }
-// DPP row shifts (dpp_ctrl 0x101-0x10F row_shl, 0x111-0x11F row_shr; rows of 16 lanes)
+// DPP row shifts (dpp_ctrl 0x101-0x10F row_shl, 0x111-0x11F row_shr; rows of 16 lanes) and quad
+// permutes (0x00-0xFF: lane 4q + i reads lane 4q + ((ctrl >> 2i) & 3))
 inline int __builtin_amdgcn_update_dpp(int old, int src, int ctrl, int, int, bool bound_ctrl) {
   const uint32_t l = emu_lane(), rl = l & 15;
   int from = -1;
   if (ctrl >= 0x101 && ctrl <= 0x10F && rl + (ctrl - 0x100) < 16) from = (int)l + (ctrl - 0x100);
   if (ctrl >= 0x111 && ctrl <= 0x11F && (int)rl - (ctrl - 0x110) >= 0) from = (int)l - (ctrl - 0x110);
+  if (ctrl >= 0 && ctrl <= 0xFF) from = (int)((l & ~3u) | ((uint32_t)(ctrl >> (2 * (l & 3))) & 3u));  // quad_perm
   const int v = emu_exchange(src, from < 0 ? l : (uint32_t)from);
   return from < 0 ? (bound_ctrl ? 0 : old) : v;
 }

@@ -17,7 +17,7 @@ CLANGXX = "/opt/rocm/llvm/bin/clang++"
 # the library sources the emulator links, each its own translation unit as in the device build
 SOURCES = ["affx_layout.hip", "affx_decode.hip", "affx_fused.hip", "affx_quant.hip", "affx_grouped.hip",
            "affx_api.hip", "affx_noalloc.hip", "affx_route.hip", "affx_shared.hip", "affx_fit.hip", "affx_gemv.hip",
-           "affx_steps.hip"]
+           "affx_steps.hip", "affx_w8a8.hip"]
 
 
 @pytest.fixture(scope="module")
@@ -87,11 +87,14 @@ CASES = {
     "gemv": (("gemv", 1024, 2048, 3, 5), 4),
     # gather / scatter / SwiGLU requantise against the oracle (bounds checked)
     "steps": (("steps", 256, 40, 3), 4),
+    # the single-matrix W8A8 GEMM: three tiles of down matrices (f32, strided arena, pad), one bf16
+    "w8a8": (("w8a8", 1024, 1024, 7), 4),
     "shared": (("shared", 1024, 1024, 6, 40, 5), 4),
 }
 # longest first, so the three lanes finish together
 ORDER = ["decode_m8_wide", "decode_m6_dm16", "decode_m6_two_cg", "slots", "shared", "decode_m1_single", "grouped",
-         "decode_m1", "ffnptr", "ffnptr_n1", "quant", "timeout", "timeout_m1", "route", "gemv", "steps", "decode_allpad", "dequant"]
+         "decode_m1", "ffnptr", "ffnptr_n1", "quant", "timeout", "timeout_m1", "route", "gemv", "w8a8", "steps", "decode_allpad",
+         "dequant"]
 
 
 @pytest.fixture(scope="module")
@@ -186,6 +189,13 @@ def test_expert_ffn_pointer_table_one_expert_emulated(runs):
 def test_gemv_emulated(runs):
     out = result(runs, "gemv")
     assert "gemv rc=0" in out, out
+
+
+def test_w8a8_gemm_emulated(runs):
+    """affx_expert_gemm_w8a8 within 1e-5 of the oracle (f32 outputs) and 1 bf16 ulp (bf16 output),
+    the strided arena's other columns untouched."""
+    out = result(runs, "w8a8")
+    assert "w8a8 rc=0" in out and "others_kept=1" in out, out
 
 
 def test_separable_steps_emulated(runs):

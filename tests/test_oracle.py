@@ -619,3 +619,46 @@ def test_scatter_slots_and_gather_tokens_oracle_brute_force(orc):
     src = rng.normal(0, 1, (dim, nb_stride)).astype(np.float32)
     tok = rng.integers(0, nb_stride, 11).astype(np.uint32)
     np.testing.assert_array_equal(orc.gather_tokens(src, tok), src[:, tok])
+
+
+def test_expert_gemm_w8a8_oracle_pinned(orc, c1_codebook):
+    """orc_expert_gemm_w8a8 against numpy built on the closed-form dequant above (row scale 1
+    gives each weight's E4M3 value): each 128-column block's sum in float64, the fold over blocks
+    as an f32 fma in block order (a product of two f32 is exact in float64), the row scale times
+    wscale last. Token ids with a repeat, a strided output (the other columns untouched) and the
+    bf16 output (round to nearest even of the f32 result). The per-block activation scales differ
+    by block, so a block mix-up or a fold out of order fails."""
+    rng = np.random.default_rng(21)
+    rows, cols, ntok = 32, 1024, 10
+    nkb = cols // 128
+    cb = orc.unpack_codebook(c1_codebook)
+    codes = rng.integers(0, 256, rows * cols * 10 // 32, dtype=np.uint8)
+    fields = rng.integers(0, 256, rows * cols * 6 // 128, dtype=np.uint8)
+    rs = (rng.uniform(4e-4, 2e-3, rows).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    w8 = _numpy_dequant(codes, fields, np.full(rows, 0x3F80, np.uint16), rows, cols, cb).astype(np.float64)
+    x8 = rng.integers(0, 256, (ntok, cols), dtype=np.uint8)
+    x8[(x8 & 0x7F) == 0x7F] ^= 1                       # no NaN codes
+    e4 = np.array([orc.e4m3_to_float(b) for b in range(256)], np.float64)
+    xs = rng.uniform(0.01, 2.0, (ntok, nkb)).astype(np.float32)
+    tok = np.array([3, 0, 9, 4, 4, 7, 1], np.uint32)
+    nt, wscale = len(tok), 0.75
+    rsw = (rs.astype(np.uint32) << 16).view(np.float32) * np.float32(wscale)
+    want = np.zeros((rows, nt), np.float32)
+    for j, t in enumerate(tok):
+        raw = (w8.reshape(rows, nkb, 128) * e4[x8[t]].reshape(1, nkb, 128)).sum(axis=2).astype(np.float32)
+        out = np.zeros(rows, np.float32)
+        for kb in range(nkb):
+            out = (raw[:, kb].astype(np.float64) * np.float64(xs[t, kb]) + out.astype(np.float64)).astype(np.float32)
+        want[:, j] = out * rsw
+    got = orc.expert_gemm_w8a8(codes, fields, rs, tok, nt, x8, xs, cb, rows, cols, wscale)
+    np.testing.assert_allclose(got, want, rtol=1e-6, atol=0)
+    # strided into an existing output: columns past nt keep their values
+    y = np.full((rows, 9), 7.0, np.float32)
+    got9 = orc.expert_gemm_w8a8(codes, fields, rs, tok, nt, x8, xs, cb, rows, cols, wscale, ld=9, y=y)
+    np.testing.assert_array_equal(got9[:, :nt].view(np.uint32), got.view(np.uint32))
+    assert (got9[:, nt:] == 7.0).all()
+    # bf16: the f32 result rounded to nearest even; identity token ids
+    gb = orc.expert_gemm_w8a8(codes, fields, rs, None, 5, x8, xs, cb, rows, cols, wscale, y_bf16=True)
+    gf = orc.expert_gemm_w8a8(codes, fields, rs, None, 5, x8, xs, cb, rows, cols, wscale)
+    u = gf.view(np.uint32).astype(np.uint64)
+    np.testing.assert_array_equal(gb, ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16))
