@@ -133,6 +133,7 @@ __global__ void __launch_bounds__(kW8T) w8a8_gemm_kernel(W8a8Args A) {
           pin_step(u, m);
           lut_lookup_step<kW8KC, true>(u, lut, nullptr, copy4, m, raw, bv);
           a[m] = lut_finish(raw, bv);
+          asm volatile("" ::: "memory");  // one step's table reads in flight at a time (registers)
         }
       }
       __builtin_amdgcn_s_waitcnt(AFFX_VMCNT(0));
@@ -172,6 +173,13 @@ __global__ void __launch_bounds__(kW8T) w8a8_gemm_kernel(W8a8Args A) {
           o = __builtin_fmaf(quad_lane<3>(acc1[v]), sb[7], o);
           out[q][v] = o;
         }
+        // one quad at a time: the next quad's B reads are not hoisted over this one's MFMAs (a
+        // compiler memory barrier; the registers of every quad's operands at once would cut the
+        // waves a SIMD holds to one)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) AFFX_PIN(out[q][v]);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
   }
