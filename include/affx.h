@@ -506,8 +506,8 @@ size_t affx_shared_batch_workspace_size(uint32_t n_tok, uint32_t hidden, uint32_
  * the device block the routed experts wrote), 0 stores. x and y as in affx_expert_ffn_decode
  * (element (t, h) at x[t * x_tok_stride + h * x_dim_stride]). The host composition it matches is
  * src/engine/model.cpp:1214-1222. Accumulating after the routed experts on the same stream gives
- * the host's order: block = routed sum, then block += shared. Three launches, no
- * synchronisation. */
+ * the host's order: block = routed sum, then block += shared. Two launches (gate/up + SwiGLU,
+ * down), no synchronisation. */
 int affx_shared_expert_decode(const affx_shared_expert* shexp, const float* x, uint64_t x_tok_stride,
                               uint64_t x_dim_stride, uint32_t m_tokens, float* y, uint64_t y_tok_stride,
                               uint64_t y_dim_stride, int accumulate, void* workspace, size_t workspace_bytes,
