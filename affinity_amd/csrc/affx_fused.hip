@@ -130,6 +130,19 @@ __device__ __forceinline__ void load_pair(Unit& g, Unit& u, const uint8_t* gc, c
   }
 }
 
+// Compacted columns (one 16-column group serving up to eight tokens): in pass p over a slot's
+// weights, column c < 15 holds term c % 3 of the slot's (5p + c/3)-th token in ascending order
+// (mask: the slot's tokens). Returns whether the column is used; t is then its token.
+__device__ __forceinline__ bool cmp_column(uint32_t mask, uint32_t p, uint32_t c, uint32_t& t) {
+  const uint32_t j = 5u * p + c / 3u;
+  uint32_t tt = 0;
+#pragma unroll
+  for (int b = 0; b < AFFX_MAX_DECODE_TOKENS; ++b)
+    if (((mask >> b) & 1u) && (uint32_t)__builtin_popcount(mask & ((1u << b) - 1u)) == j) tt = (uint32_t)b;
+  t = tt;
+  return c < 15u && j < (uint32_t)__builtin_popcount(mask);
+}
+
 // value of the three E4M3 term columns c, c+1, c+2 (valid in lanes whose column is a multiple of 3)
 __device__ __forceinline__ float fused_terms(float d) {
   const float d1 = row_shl<1>(d), d2 = row_shl<2>(d);  // (DPP row shifts)
@@ -151,7 +164,10 @@ __device__ __forceinline__ float wave_max(float v) {
 
 // ------------------------------------------------------------------------------------------------
 // The kernel. CG: 16-column groups of the MFMA B operand (5 tokens each). KC: codebook copies.
-// MAXM: largest M this instantiation serves (sizes the per-thread activation registers).
+// MAXM: largest M this instantiation serves (sizes the per-thread activation registers). One
+// column group with MAXM > 5 compacts the columns: each slot's tokens fill the group pass by pass
+// (cmp_column), so a slot serving five tokens or fewer (almost all of them in a decode batch)
+// costs one MFMA per weight fragment instead of one per five tokens of the batch.
 // The down weights of the first unit are prefetched before the wait when CG = 1. SINGLE: at most
 // one gate/up item and one down unit (per output tile) per wave, which keeps those two phases
 // loop-free (batch 1). ROT: the codebook copies include the rotated tables (one VALU op less
@@ -162,6 +178,9 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   AFFX_DYN_LDS(lds);
   // the first down unit is loaded while gate/up runs (one column group leaves the registers)
   constexpr bool PREF = CG == 1;
+  // compacted columns: a slot with more than five tokens takes a second pass over its weights
+  // (decoded again from the registers that hold them)
+  constexpr bool CMP = CG == 1 && MAXM > 5;
   // the down phase loads its whole B operand at once (one column group fits the registers)
   constexpr bool BPRE = CG == 1;
   const uint32_t tid = threadIdx.x, lane = tid & 63, g = blockIdx.x;
@@ -459,57 +478,96 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   for (uint32_t rho = 0; rho < n_rounds; ++rho) {
     const uint32_t item = gu_item(rho);
     v4f acc[2][CG];
+    // this lane's token in each column group, and whether the lane writes that token's partial
+    // sums (lanes of the first term column of a token)
+    uint32_t tk[CG];
+    bool tw[CG];
+#pragma unroll
+    for (int cg = 0; cg < CG; ++cg) {
+      tk[cg] = 0u;
+      tw[cg] = false;
+    }
+    // partial sums of this wave's segment, term-combined, at the segment's exponent:
+    // part[wave][mat][row][token]. Accumulator lane l, element v = D[4(l/16)+v][l%16].
+    auto write_part = [&]() {
+#pragma unroll
+      for (int mm = 0; mm < 2; ++mm)
+#pragma unroll
+        for (int cg = 0; cg < CG; ++cg)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const float val = fused_terms(acc[mm][cg][v]);
+            if (tw[cg]) part[((wv * 2 + mm) * 16 + 4 * kg + v) * M + tk[cg]] = ldexpf(val, -sigma_l[tk[cg] * 4 + S]);
+          }
+    };
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
       for (int cg = 0; cg < CG; ++cg) acc[mm][cg] = v4f{0.f, 0.f, 0.f, 0.f};
-    uint32_t mask = 0;
     if (item != ~0u) {
       const uint32_t slot = item / rt_per;
-      mask = __builtin_amdgcn_readfirstlane(slot_mask[slot]);
+      const uint32_t mask = __builtin_amdgcn_readfirstlane(slot_mask[slot]);
+      const uint32_t npass = CMP ? ((uint32_t)__builtin_popcount(mask) + 4u) / 5u : 1u;
+      for (uint32_t p = 0; p < npass; ++p) {
+        if (CMP && p > 0) {
+          // (a slot with more than five tokens) the first pass's tokens are done
+          write_part();
 #pragma unroll
-      for (int cg = 0; cg < CG; ++cg) {
-        const uint32_t t = cg * 5 + c / 3, tau = c % 3;
-        const bool valid = c < 15 && t < M && ((mask >> t) & 1u);
-        bsrc[cg] = valid ? xq + (t * 3 + tau) * kXqRow + (S * 4 + kg) * kXqChunk : zero_l;
-      }
-      uint32_t rg[8], ru[8];
-      uint32_t bg[2], bu[2];
-      pin_step(ug, 0);
-      pin_step(uu, 0);
-      lut_lookup_step<KC, ROT>(ug, lut, btbl, copy4, 0, rg, bg);
-      lut_lookup_step<KC, ROT>(uu, lut, btbl, copy4, 0, ru, bu);
-      v8i bc[CG];
-#pragma unroll
-      for (int cg = 0; cg < CG; ++cg) bc[cg] = b_step_lds(bsrc[cg], 0);
-#pragma unroll
-      for (int m = 0; m < 8; ++m) {
-        uint32_t ng[8], nu[8];
-        uint32_t nbg[2], nbu[2];
-        v8i bn[CG];
-        if (m < 7) {
-#pragma unroll
-          for (int cg = 0; cg < CG; ++cg) { AFFX_PIN(acc[0][cg]); AFFX_PIN(acc[1][cg]); }
-          pin_step(ug, m + 1);
-          pin_step(uu, m + 1);
-          lut_lookup_step<KC, ROT>(ug, lut, btbl, copy4, m + 1, ng, nbg);
-          lut_lookup_step<KC, ROT>(uu, lut, btbl, copy4, m + 1, nu, nbu);
-#pragma unroll
-          for (int cg = 0; cg < CG; ++cg) bn[cg] = b_step_lds(bsrc[cg], m + 1);
+          for (int mm = 0; mm < 2; ++mm) acc[mm][0] = v4f{0.f, 0.f, 0.f, 0.f};
         }
-        const v8i ag = lut_finish(rg, bg), au = lut_finish(ru, bu);
 #pragma unroll
         for (int cg = 0; cg < CG; ++cg) {
-          acc[0][cg] = mfma(ag, bc[cg], acc[0][cg]);
-          acc[1][cg] = mfma(au, bc[cg], acc[1][cg]);
+          uint32_t t;
+          bool valid;
+          if constexpr (CMP) {
+            valid = cmp_column(mask, p, c, t);
+          } else {
+            t = cg * 5 + c / 3;
+            valid = c < 15 && t < M && ((mask >> t) & 1u);
+          }
+          const uint32_t tau = c % 3;
+          bsrc[cg] = valid ? xq + (t * 3 + tau) * kXqRow + (S * 4 + kg) * kXqChunk : zero_l;
+          tk[cg] = t;
+          tw[cg] = tau == 0 && (CMP ? valid : (c < 15 && t < M));
         }
-        __builtin_amdgcn_sched_barrier(0);
-        if (m < 7) {
+        uint32_t rg[8], ru[8];
+        uint32_t bg[2], bu[2];
+        pin_step(ug, 0);
+        pin_step(uu, 0);
+        lut_lookup_step<KC, ROT>(ug, lut, btbl, copy4, 0, rg, bg);
+        lut_lookup_step<KC, ROT>(uu, lut, btbl, copy4, 0, ru, bu);
+        v8i bc[CG];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) { rg[i] = ng[i]; ru[i] = nu[i]; }
-          bg[0] = nbg[0]; bg[1] = nbg[1]; bu[0] = nbu[0]; bu[1] = nbu[1];
+        for (int cg = 0; cg < CG; ++cg) bc[cg] = b_step_lds(bsrc[cg], 0);
 #pragma unroll
-          for (int cg = 0; cg < CG; ++cg) bc[cg] = bn[cg];
+        for (int m = 0; m < 8; ++m) {
+          uint32_t ng[8], nu[8];
+          uint32_t nbg[2], nbu[2];
+          v8i bn[CG];
+          if (m < 7) {
+#pragma unroll
+            for (int cg = 0; cg < CG; ++cg) { AFFX_PIN(acc[0][cg]); AFFX_PIN(acc[1][cg]); }
+            pin_step(ug, m + 1);
+            pin_step(uu, m + 1);
+            lut_lookup_step<KC, ROT>(ug, lut, btbl, copy4, m + 1, ng, nbg);
+            lut_lookup_step<KC, ROT>(uu, lut, btbl, copy4, m + 1, nu, nbu);
+#pragma unroll
+            for (int cg = 0; cg < CG; ++cg) bn[cg] = b_step_lds(bsrc[cg], m + 1);
+          }
+          const v8i ag = lut_finish(rg, bg), au = lut_finish(ru, bu);
+#pragma unroll
+          for (int cg = 0; cg < CG; ++cg) {
+            acc[0][cg] = mfma(ag, bc[cg], acc[0][cg]);
+            acc[1][cg] = mfma(au, bc[cg], acc[1][cg]);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+          if (m < 7) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) { rg[i] = ng[i]; ru[i] = nu[i]; }
+            bg[0] = nbg[0]; bg[1] = nbg[1]; bu[0] = nbu[0]; bu[1] = nbu[1];
+#pragma unroll
+            for (int cg = 0; cg < CG; ++cg) bc[cg] = bn[cg];
+          }
         }
       }
     }
@@ -534,19 +592,7 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
     if constexpr (!SINGLE) {
       if (rho + 1 < n_rounds) load_gu(gu_item(rho + 1));
     }
-    // partial sums of this wave's segment, term-combined, at the segment's exponent:
-    // part[wave][mat][row][token]. Accumulator lane l, element v = D[4(l/16)+v][l%16].
-#pragma unroll
-    for (int mm = 0; mm < 2; ++mm)
-#pragma unroll
-      for (int cg = 0; cg < CG; ++cg)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const float val = fused_terms(acc[mm][cg][v]);
-          const uint32_t t = cg * 5 + c / 3;
-          if (item != ~0u && c < 15 && c % 3 == 0 && t < M)
-            part[((wv * 2 + mm) * 16 + 4 * kg + v) * M + t] = ldexpf(val, -sigma_l[t * 4 + S]);
-        }
+    write_part();  // (the last pass's tokens)
     __syncthreads();
     AFFX_TRACE(11);
 
@@ -730,114 +776,135 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
     // instantiation, so that those fragments are not live across the loop over further tiles)
     auto down_tile = [&](uint32_t td, auto prec) {
       constexpr bool PRE = decltype(prec)::value;
+      // per (row, token) sums of this wave's units: in registers by column (the column's token is
+      // fixed), or, with compacted columns (the token of a column changes from unit to unit),
+      // added in place in this wave's rows of part[wave][row][token], in the same unit order
       float yacc[CG][4];
 #pragma unroll
       for (int cg = 0; cg < CG; ++cg)
 #pragma unroll
         for (int v = 0; v < 4; ++v) yacc[cg][v] = 0.f;
+      if constexpr (CMP) {
+        for (uint32_t i = lane; i < 16u * M; i += 64u) part[wv * 16u * M + i] = 0.f;
+      }
 #pragma unroll 1
       for (uint32_t u = wv; u < (SINGLE ? (wv < NU ? wv + 1 : 0u) : NU); u += kFW) {
         if (!(PRE || (PREF && td == g && u == wv))) load_down(true, td, u);  // else loaded before the wait
         const uint32_t slot = u / nsi, S2 = u % nsi;
-        const uint32_t e = __builtin_amdgcn_readfirstlane(slot_expert[slot]);
         const uint32_t mask = __builtin_amdgcn_readfirstlane(slot_mask[slot]);
-        const uint8_t* ex = A.base + (uint64_t)e * A.stride;
-        const BSrc<CG> b = b_source<CG>(A.aq + (uint64_t)slot * M * kTerms * A.inter, A.inter,
-                                        (uint64_t)S2 * kTileCols, lane, M, mask, A.zeros);
         uint2 rsv = rs_d;
         AFFX_PIN(rsv.x);  // opaque at the use (see the gate/up row scales)
         AFFX_PIN(rsv.y);
-        __builtin_amdgcn_sched_barrier(0);
-        v4f acc[CG];
-#pragma unroll
-        for (int cg = 0; cg < CG; ++cg) acc[cg] = v4f{0.f, 0.f, 0.f, 0.f};
-        // B: one column group (64 registers) is loaded whole up front, so the eight steps wait
-        // for one round trip; two column groups are loaded one step ahead
-        v8i bpre[BPRE ? 8 : 1];
-        v8i bc[CG];
-        if constexpr (BPRE) {
-          // only the lanes of used columns load (exec-masked); the others hold zeros, with no
-          // address-unit time spent on a zero run
-#pragma unroll
-          for (int m = 0; m < 8; ++m) bpre[m] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
-          if (b.used) {
-#pragma unroll
-            for (int m = 0; m < 8; ++m) bpre[m] = b_step(b.p[0], m);
+        const uint32_t npass = CMP ? ((uint32_t)__builtin_popcount(mask) + 4u) / 5u : 1u;
+        for (uint32_t p = 0; p < npass; ++p) {
+          BSrc<CG> b;
+          uint32_t tcol = 0;  // (compacted columns) this lane's token
+          if constexpr (CMP) {
+            b.used = cmp_column(mask, p, c, tcol);
+            b.p[0] = b.used ? reinterpret_cast<const u32x4*>(A.aq + ((uint64_t)(slot * M + tcol) * kTerms + c % 3) * A.inter +
+                                                             (uint64_t)S2 * kTileCols + kg * kSegCols)
+                            : reinterpret_cast<const u32x4*>(A.zeros);
+          } else {
+            b = b_source<CG>(A.aq + (uint64_t)slot * M * kTerms * A.inter, A.inter, (uint64_t)S2 * kTileCols, lane, M,
+                             mask, A.zeros);
           }
           __builtin_amdgcn_sched_barrier(0);
-        } else {
+          v4f acc[CG];
 #pragma unroll
-          for (int cg = 0; cg < CG; ++cg) bc[cg] = b_step(b.p[cg], 0);
-        }
-        // steps [m0, 8) decode their A fragments here (PRE: the first kPreSteps are in ad)
-        constexpr int m0 = PRE ? kPreSteps : 0;
-        if constexpr (PRE) {
+          for (int cg = 0; cg < CG; ++cg) acc[cg] = v4f{0.f, 0.f, 0.f, 0.f};
+          // B: one column group (64 registers) is loaded whole up front, so the eight steps wait
+          // for one round trip; two column groups are loaded one step ahead
+          v8i bpre[BPRE ? 8 : 1];
+          v8i bc[CG];
+          if constexpr (BPRE) {
+            // only the lanes of used columns load (exec-masked); the others hold zeros, with no
+            // address-unit time spent on a zero run
 #pragma unroll
-          for (int m = 0; m < m0; ++m) acc[0] = mfma(ad[SINGLE ? m : 0], bpre[BPRE ? m : 0], acc[0]);
-        }
-        {
-          uint32_t raw[8];
-          uint32_t bv[2];
-          pin_step(ud, m0);
-          lut_lookup_step<KC, ROT>(ud, lut, btbl, copy4, m0, raw, bv);
+            for (int m = 0; m < 8; ++m) bpre[m] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+            if (b.used) {
 #pragma unroll
-          for (int m = m0; m < 8; ++m) {
-            uint32_t nraw[8];
-            uint32_t nbv[2];
-            v8i bn[CG];
-            if (m < 7) {
-              // the previous step's MFMA stays ahead of these reads (else the compiler sinks every
-              // MFMA below all eight steps' table reads and holds them all in registers)
-#pragma unroll
-              for (int cg = 0; cg < CG; ++cg) AFFX_PIN(acc[cg]);
-              pin_step(ud, m + 1);
-              lut_lookup_step<KC, ROT>(ud, lut, btbl, copy4, m + 1, nraw, nbv);
-              if constexpr (!BPRE) {
-#pragma unroll
-                for (int cg = 0; cg < CG; ++cg) bn[cg] = b_step(b.p[cg], m + 1);
-              }
-            }
-            const v8i a = lut_finish(raw, bv);
-            if constexpr (BPRE) {
-              acc[0] = mfma(a, bpre[m], acc[0]);
-            } else {
-#pragma unroll
-              for (int cg = 0; cg < CG; ++cg) acc[cg] = mfma(a, bc[cg], acc[cg]);
+              for (int m = 0; m < 8; ++m) bpre[m] = b_step(b.p[0], m);
             }
             __builtin_amdgcn_sched_barrier(0);
-            if (m < 7) {
+          } else {
 #pragma unroll
-              for (int i = 0; i < 8; ++i) raw[i] = nraw[i];
-              bv[0] = nbv[0]; bv[1] = nbv[1];
-              if constexpr (!BPRE) {
+            for (int cg = 0; cg < CG; ++cg) bc[cg] = b_step(b.p[cg], 0);
+          }
+          // steps [m0, 8) decode their A fragments here (PRE: the first kPreSteps are in ad)
+          constexpr int m0 = PRE ? kPreSteps : 0;
+          if constexpr (PRE) {
 #pragma unroll
-                for (int cg = 0; cg < CG; ++cg) bc[cg] = bn[cg];
+            for (int m = 0; m < m0; ++m) acc[0] = mfma(ad[SINGLE ? m : 0], bpre[BPRE ? m : 0], acc[0]);
+          }
+          {
+            uint32_t raw[8];
+            uint32_t bv[2];
+            pin_step(ud, m0);
+            lut_lookup_step<KC, ROT>(ud, lut, btbl, copy4, m0, raw, bv);
+#pragma unroll
+            for (int m = m0; m < 8; ++m) {
+              uint32_t nraw[8];
+              uint32_t nbv[2];
+              v8i bn[CG];
+              if (m < 7) {
+                // the previous step's MFMA stays ahead of these reads (else the compiler sinks every
+                // MFMA below all eight steps' table reads and holds them all in registers)
+#pragma unroll
+                for (int cg = 0; cg < CG; ++cg) AFFX_PIN(acc[cg]);
+                pin_step(ud, m + 1);
+                lut_lookup_step<KC, ROT>(ud, lut, btbl, copy4, m + 1, nraw, nbv);
+                if constexpr (!BPRE) {
+#pragma unroll
+                  for (int cg = 0; cg < CG; ++cg) bn[cg] = b_step(b.p[cg], m + 1);
+                }
+              }
+              const v8i a = lut_finish(raw, bv);
+              if constexpr (BPRE) {
+                acc[0] = mfma(a, bpre[m], acc[0]);
+              } else {
+#pragma unroll
+                for (int cg = 0; cg < CG; ++cg) acc[cg] = mfma(a, bc[cg], acc[cg]);
+              }
+              __builtin_amdgcn_sched_barrier(0);
+              if (m < 7) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) raw[i] = nraw[i];
+                bv[0] = nbv[0]; bv[1] = nbv[1];
+                if constexpr (!BPRE) {
+#pragma unroll
+                  for (int cg = 0; cg < CG; ++cg) bc[cg] = bn[cg];
+                }
               }
             }
           }
-        }
-        const float rs[4] = {__uint_as_float(rsv.x << 16), __uint_as_float(rsv.x & 0xFFFF0000u),
-                             __uint_as_float(rsv.y << 16), __uint_as_float(rsv.y & 0xFFFF0000u)};
+          const float rs[4] = {__uint_as_float(rsv.x << 16), __uint_as_float(rsv.x & 0xFFFF0000u),
+                               __uint_as_float(rsv.y << 16), __uint_as_float(rsv.y & 0xFFFF0000u)};
 #pragma unroll
-        for (int cg = 0; cg < CG; ++cg) {
-          const uint32_t t = cg * 5 + c / 3;
-          const bool mine = c < 15 && (c % 3) == 0 && t < M && ((mask >> t) & 1u);
-          const float wt = mine ? ldexpf(slot_w[slot * M + t], -A.sigma_a) : 0.f;
+          for (int cg = 0; cg < CG; ++cg) {
+            const uint32_t t = CMP ? tcol : cg * 5 + c / 3;
+            const bool mine = CMP ? b.used && (c % 3) == 0 : c < 15 && (c % 3) == 0 && t < M && ((mask >> t) & 1u);
+            const float wt = mine ? ldexpf(slot_w[slot * M + t], -A.sigma_a) : 0.f;
 #pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const float val = fused_terms(acc[cg][v]);
-            if (mine) yacc[cg][v] += val * rs[v] * wt;
+            for (int v = 0; v < 4; ++v) {
+              const float val = fused_terms(acc[cg][v]);
+              if (mine) {
+                if constexpr (CMP) part[(wv * 16 + 4 * rg4 + v) * M + t] += val * rs[v] * wt;
+                else yacc[cg][v] += val * rs[v] * wt;
+              }
+            }
           }
         }
       }
       AFFX_TRACE(6);
       // per-wave partials [wave][row][token], summed over the waves in order
+      if constexpr (!CMP) {
 #pragma unroll
-      for (int cg = 0; cg < CG; ++cg) {
-        const uint32_t t = cg * 5 + c / 3;
-        if (c < 15 && c % 3 == 0 && t < M)
+        for (int cg = 0; cg < CG; ++cg) {
+          const uint32_t t = cg * 5 + c / 3;
+          if (c < 15 && c % 3 == 0 && t < M)
 #pragma unroll
-          for (int v = 0; v < 4; ++v) part[(wv * 16 + 4 * rg4 + v) * M + t] = yacc[cg][v];
+            for (int v = 0; v < 4; ++v) part[(wv * 16 + 4 * rg4 + v) * M + t] = yacc[cg][v];
+        }
       }
       __syncthreads();
       uint32_t et = tid;
@@ -964,7 +1031,7 @@ std::mutex g_fused_mu;
 FusedVariant g_fused[kMaxDev][4][3];
 
 // variants (all with the rotated tables): 0 M = 1 in one pass (8 codebook copies), 1 M = 1 in
-// rounds, 2 M <= 5 (4 copies), 3 M <= 8 (2 copies, 2 column groups). The larger M, the more LDS
+// rounds, 2 M <= 5 (4 copies), 3 M <= 8 (2 copies, compacted columns). The larger M, the more LDS
 // the activation terms take; the copies fill what is left.
 int fused_variant(uint32_t M, bool single) { return M == 1 ? (single ? 0 : 1) : M <= 5 ? 2 : 3; }
 
@@ -997,8 +1064,8 @@ int fused_prepare(int dev, int v, int xf, FusedVariant* out) {
          fused_entry<1, 8, 1, false, kXDimMajor>()},
         {fused_entry<1, 4, 5, false, kXStrided>(), fused_entry<1, 4, 5, false, kXTokenMajor>(),
          fused_entry<1, 4, 5, false, kXDimMajor>()},
-        {fused_entry<2, 2, 8, false, kXStrided>(), fused_entry<2, 2, 8, false, kXTokenMajor>(),
-         fused_entry<2, 2, 8, false, kXDimMajor>()}};
+        {fused_entry<1, 2, 8, false, kXStrided>(), fused_entry<1, 2, 8, false, kXTokenMajor>(),
+         fused_entry<1, 2, 8, false, kXDimMajor>()}};
     if (!table[v][xf].fn) return set_error(AFFX_ERR_ARG, "ffn_decode: no fused kernel for variant %d form %d", v, xf);
     f = table[v][xf];
     const uint32_t lds = fused_lds(f.maxm).total;  // dynamic part (the codebook copies are static)

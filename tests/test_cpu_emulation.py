@@ -70,9 +70,12 @@ CASES = {
     "decode_m1": (("decode", 1024, 1024, 7, 1, 6, 1), 4),   # 4 workgroups: gate/up in rounds
     "decode_allpad": (("decode", 1024, 1024, 5, 2, 3, 4, "allpad"), 3),
     "decode_m1_single": (("decode", 1024, 1024, 5, 1, 1, 9), 6),
-    "decode_m6_two_cg": (("decode", 2048, 1024, 5, 6, 2, 2), 4),
+    "decode_m6": (("decode", 2048, 1024, 5, 6, 2, 2), 4),
     "decode_m6_dm16": (("decode", 2048, 1024, 5, 6, 2, 2, "dm16"), 4),
     "decode_m8_wide": (("decode", 1024, 1024, 7, 8, 3, 6), 3),
+    # three experts, every token routed to all three (token 0's last route padding): every slot
+    # serves seven or eight tokens, so each one takes two passes of the compacted column group
+    "decode_m8_full": (("decode", 1024, 1024, 3, 8, 3, 7), 3),
     "quant": (("quant", 4, 256, 3), 4),
     "grouped": (("grouped", 1024, 1024, 5, 12, 3, 4, 1), 4),
     "timeout": (("timeout", 1024, 1024, 6, 2, 3, 8), 4),
@@ -92,7 +95,7 @@ CASES = {
     "shared": (("shared", 1024, 1024, 6, 40, 5), 4),
 }
 # longest first, so the three lanes finish together
-ORDER = ["decode_m8_wide", "decode_m6_dm16", "decode_m6_two_cg", "slots", "shared", "decode_m1_single", "grouped",
+ORDER = ["decode_m8_wide", "decode_m8_full", "decode_m6_dm16", "decode_m6", "slots", "shared", "decode_m1_single", "grouped",
          "decode_m1", "ffnptr", "ffnptr_n1", "quant", "timeout", "timeout_m1", "route", "gemv", "w8a8", "steps", "decode_allpad",
          "dequant"]
 
@@ -131,8 +134,10 @@ def test_decode_emulated_m1_single_pass(runs):
     assert "identical to staged=1" in result(runs, "decode_m1_single")
 
 
-def test_decode_emulated_m6_two_column_groups(runs):
-    assert "identical to staged=1" in result(runs, "decode_m6_two_cg")
+def test_decode_emulated_m6_compacted_columns(runs):
+    # six tokens: each slot's tokens fill the one column group of the fused kernel in order (the
+    # staged launches keep two fixed groups of five tokens)
+    assert "identical to staged=1" in result(runs, "decode_m6")
 
 
 def test_decode_emulated_m6_dim_major_arena(runs):
@@ -145,6 +150,12 @@ def test_decode_emulated_m8_wide_epilogue(runs):
     # 12 gate/up groups x 16 rows x 8 tokens: the epilogue takes two passes of the workgroup
     # (hidden 1024: one column segment, so 12 wave groups; inter 1024 keeps the emulation short)
     assert "identical to staged=1" in result(runs, "decode_m8_wide")
+
+
+def test_decode_emulated_m8_two_passes(runs):
+    # every slot serves more than five tokens: a second pass over the same weight registers, and
+    # the down phase's per-token sums across both passes
+    assert "identical to staged=1" in result(runs, "decode_m8_full")
 
 
 def test_quantizer_emulated(runs):

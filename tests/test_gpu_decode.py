@@ -257,16 +257,18 @@ def _random_device_pool(ax, c1_codebook, n, hidden, inter, seed):
     return pool
 
 
-@pytest.mark.parametrize("M,k", [(1, 6), (2, 6), (5, 6), (8, 6)])
-def test_fused_decode_identical_to_staged_full_layer(ax, orc, c1_codebook, M, k):
+@pytest.mark.parametrize("M,k,pick", [(1, 6, 256), (2, 6, 256), (5, 6, 256), (8, 6, 256), (8, 6, 8)])
+def test_fused_decode_identical_to_staged_full_layer(ax, orc, c1_codebook, M, k, pick):
     """The benchmark layer shape (256 experts, hidden 4096, inter 2048): the one-launch decode
     equals the three staged launches bit for bit (same MFMA operands, same summation order),
-    leaves its counters zero, and matches the oracle on every token."""
+    leaves its counters zero, and matches the oracle on every token. pick = 8: every route names
+    one of 8 experts, so most slots serve six or more tokens and take the fused kernel's second
+    pass over their weights."""
     hidden, inter, n = 4096, 2048, 256
     pool = _random_device_pool(ax, c1_codebook, n, hidden, inter, seed=17 + M)
-    rng = np.random.default_rng(100 + M)
+    rng = np.random.default_rng(100 + M + pick)
     x = torch.from_numpy((rng.standard_normal((M, hidden)) * 0.7).astype(np.float32)).cuda()
-    sel_np = np.stack([rng.choice(n, k, replace=False) for _ in range(M)]).astype(np.int32)
+    sel_np = np.stack([rng.choice(pick, k, replace=False) for _ in range(M)]).astype(np.int32)
     sel = torch.from_numpy(sel_np).cuda()
     w = torch.from_numpy(rng.uniform(0.05, 1.0, (M, k)).astype(np.float32)).cuda()
     ws = ax.DecodeWorkspace(M, k, hidden, inter)
