@@ -88,8 +88,8 @@ __host__ __device__ inline FusedLds fused_lds(uint32_t M) {
   L.part = L.zero + 256u;
   const uint32_t part_bytes = (uint32_t)kFW * 2u * 16u * M * 4u;  // gate/up [wave][mat][row][tok]
   L.plan = L.part + part_bytes;
-  // slot_expert[128] slot_mask[128] rs[12][32] sigma[32] slot_w[128][M]
-  L.count = L.plan + (2u * kPlanRoutes + kFW * 32u + 32u) * 4u + kPlanRoutes * M * 4u;
+  // slot_expert[128] slot_mask[128] rs[12][32] sigma[32] slot_w[128][M] slot_tok[128]
+  L.count = L.plan + (3u * kPlanRoutes + kFW * 32u + 32u) * 4u + kPlanRoutes * M * 4u;
   L.total = L.count + 16u;
   return L;
 }
@@ -131,16 +131,25 @@ __device__ __forceinline__ void load_pair(Unit& g, Unit& u, const uint8_t* gc, c
 }
 
 // Compacted columns (one 16-column group serving up to eight tokens): in pass p over a slot's
-// weights, column c < 15 holds term c % 3 of the slot's (5p + c/3)-th token in ascending order
-// (mask: the slot's tokens). Returns whether the column is used; t is then its token.
-__device__ __forceinline__ bool cmp_column(uint32_t mask, uint32_t p, uint32_t c, uint32_t& t) {
+// weights, column c < 15 holds term c % 3 of the slot's (5p + c/3)-th token in ascending order.
+// tl: the slot's tokens in that order, four bits each; nt: their count. Returns whether the
+// column is used; t is then its token.
+__device__ __forceinline__ bool cmp_column(uint32_t tl, uint32_t nt, uint32_t p, uint32_t c, uint32_t& t) {
   const uint32_t j = 5u * p + c / 3u;
-  uint32_t tt = 0;
+  t = (tl >> ((4u * j) & 31u)) & 15u;
+  return c < 15u && j < nt;
+}
+
+// Packed ascending token list of a token mask (at most eight tokens: four bits each).
+__device__ __forceinline__ uint32_t token_list(uint32_t mask) {
+  uint32_t tl = 0, k = 0;
 #pragma unroll
   for (int b = 0; b < AFFX_MAX_DECODE_TOKENS; ++b)
-    if (((mask >> b) & 1u) && (uint32_t)__builtin_popcount(mask & ((1u << b) - 1u)) == j) tt = (uint32_t)b;
-  t = tt;
-  return c < 15u && j < (uint32_t)__builtin_popcount(mask);
+    if ((mask >> b) & 1u) {
+      tl |= (uint32_t)b << (4u * k);
+      ++k;
+    }
+  return tl;
 }
 
 // value of the three E4M3 term columns c, c+1, c+2 (valid in lanes whose column is a multiple of 3)
@@ -201,6 +210,8 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   float* rs_l = reinterpret_cast<float*>(slot_mask + kPlanRoutes);  // [group][gate 16 | up 16]
   int32_t* sigma_l = reinterpret_cast<int32_t*>(rs_l + kFW * 32);
   float* slot_w = reinterpret_cast<float*>(sigma_l + 32);
+  // (compacted columns) each slot's tokens in ascending order, four bits each
+  uint32_t* slot_tok = reinterpret_cast<uint32_t*>(slot_w + kPlanRoutes * M);
 
   AFFX_TRACE_INIT;
   AFFX_TRACE(0);
@@ -392,6 +403,11 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
         atomicOr(&slot_mask[sl], 1u << lane);
       }
     }
+    if constexpr (CMP) {
+      // (the masks are complete: one wave's LDS operations take effect in order)
+      __builtin_amdgcn_wave_barrier();
+      for (uint32_t i = lane; i < ns; i += 64u) slot_tok[i] = token_list(slot_mask[i]);
+    }
   }
   AFFX_TRACE(9);
 
@@ -507,7 +523,9 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
     if (item != ~0u) {
       const uint32_t slot = item / rt_per;
       const uint32_t mask = __builtin_amdgcn_readfirstlane(slot_mask[slot]);
-      const uint32_t npass = CMP ? ((uint32_t)__builtin_popcount(mask) + 4u) / 5u : 1u;
+      const uint32_t nt = (uint32_t)__builtin_popcount(mask);
+      const uint32_t tl = CMP ? __builtin_amdgcn_readfirstlane(slot_tok[slot]) : 0u;
+      const uint32_t npass = CMP ? (nt + 4u) / 5u : 1u;
       for (uint32_t p = 0; p < npass; ++p) {
         if (CMP && p > 0) {
           // (a slot with more than five tokens) the first pass's tokens are done
@@ -520,7 +538,7 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
           uint32_t t;
           bool valid;
           if constexpr (CMP) {
-            valid = cmp_column(mask, p, c, t);
+            valid = cmp_column(tl, nt, p, c, t);
           } else {
             t = cg * 5 + c / 3;
             valid = c < 15 && t < M && ((mask >> t) & 1u);
@@ -795,12 +813,14 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
         uint2 rsv = rs_d;
         AFFX_PIN(rsv.x);  // opaque at the use (see the gate/up row scales)
         AFFX_PIN(rsv.y);
-        const uint32_t npass = CMP ? ((uint32_t)__builtin_popcount(mask) + 4u) / 5u : 1u;
+        const uint32_t nt = (uint32_t)__builtin_popcount(mask);
+        const uint32_t tl = CMP ? __builtin_amdgcn_readfirstlane(slot_tok[slot]) : 0u;
+        const uint32_t npass = CMP ? (nt + 4u) / 5u : 1u;
         for (uint32_t p = 0; p < npass; ++p) {
           BSrc<CG> b;
           uint32_t tcol = 0;  // (compacted columns) this lane's token
           if constexpr (CMP) {
-            b.used = cmp_column(mask, p, c, tcol);
+            b.used = cmp_column(tl, nt, p, c, tcol);
             b.p[0] = b.used ? reinterpret_cast<const u32x4*>(A.aq + ((uint64_t)(slot * M + tcol) * kTerms + c % 3) * A.inter +
                                                              (uint64_t)S2 * kTileCols + kg * kSegCols)
                             : reinterpret_cast<const u32x4*>(A.zeros);
