@@ -351,15 +351,29 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   };
   // unconditional loads (an absent item or unit reads expert 0's first tile, never used): the
   // wait-count tracking then sees straight-line code and waits for exactly what each step needs
+  // rounds kernels: the next round's gate/up pair is requested step by step during this round's
+  // MFMA steps, each part into the registers the steps before it left dead (a ring), so the
+  // requests reach the vector memory address unit spread over the round instead of as one burst
+  // after it (which the unit took about 2 us per round to accept, with every wave stalled on it
+  // and the decode idle); the row scales then come first, so that the wait for them at the start
+  // of a round covers no weights
+  constexpr bool RING = !SINGLE;
   auto load_gu = [&](uint32_t item) {
     const bool ok = item != ~0u;
     const uint32_t slot = ok ? item / rt_per : 0u, rt = ok ? item % rt_per : 0u;
     const uint32_t e = ok ? slot_expert_of(slot) : 0u;
     const uint8_t* ex = A.base + (uint64_t)e * A.stride;
     const uint64_t tile = ok ? (uint64_t)rt * nst + S : 0u;
+    auto row_scale = [&]() {
+      return reinterpret_cast<const uint16_t*>(ex + A.off[lane < 16 ? kGateRs : kUpRs])[rt * 16 + (lane & 15)];
+    };
+    if constexpr (RING) {
+      rs_gu = row_scale();
+      __builtin_amdgcn_sched_barrier(0);
+    }
     load_pair(ug, uu, ex + A.off[kGateCodes], ex + A.off[kGateFields], ex + A.off[kUpCodes],
               ex + A.off[kUpFields], tile, lane);
-    rs_gu = reinterpret_cast<const uint16_t*>(ex + A.off[lane < 16 ? kGateRs : kUpRs])[rt * 16 + (lane & 15)];
+    if constexpr (!RING) rs_gu = row_scale();
     __builtin_amdgcn_sched_barrier(0);
   };
   auto load_down = [&](bool ok, uint32_t td, uint32_t u) {
@@ -520,19 +534,69 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
     for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
       for (int cg = 0; cg < CG; ++cg) acc[mm][cg] = v4f{0.f, 0.f, 0.f, 0.f};
+    if (RING && item != ~0u && S == 0 && lane < 32) {
+      // (the previous round's epilogue read rs_l before the round's closing barrier; the wait
+      // covers the row scales alone: they were requested first)
+      uint32_t rv = rs_gu;
+      AFFX_PIN(rv);
+      rs_l[q * 32 + lane] = __uint_as_float(rv << 16);
+    }
     if (item != ~0u) {
       const uint32_t slot = item / rt_per;
       const uint32_t mask = __builtin_amdgcn_readfirstlane(slot_mask[slot]);
       const uint32_t nt = (uint32_t)__builtin_popcount(mask);
       const uint32_t tl = CMP ? __builtin_amdgcn_readfirstlane(slot_tok[slot]) : 0u;
       const uint32_t npass = CMP ? (nt + 4u) / 5u : 1u;
-      for (uint32_t p = 0; p < npass; ++p) {
-        if (CMP && p > 0) {
-          // (a slot with more than five tokens) the first pass's tokens are done
-          write_part();
+      // the ring's part after step m of the last pass (unconditional: an absent next item reads
+      // expert 0's first tile, never used, and straight-line loads keep the compiler's wait counts
+      // exact). Step m + 1's table reads, issued before it, were the last reads of the registers
+      // each part overwrites: chunk 0 after step 1's, field dword 0 after step 2's, chunk 1 after
+      // step 3's, chunk 2 after step 4's, field dword 1 after step 5's, chunk 3 after step 6's,
+      // chunk 4 and field dword 2 after step 7's.
+      const uint32_t nit = RING ? gu_item(rho + 1) : ~0u;
+      const bool nok = nit != ~0u;
+      const uint32_t nrt = nok ? nit % rt_per : 0u;
+      const uint8_t* nex = A.base + (uint64_t)(nok ? slot_expert_of(nit / rt_per) : 0u) * A.stride;
+      const uint64_t ntile = nok ? (uint64_t)nrt * nst + S : 0u;
+      const uint8_t* ngc = nex + A.off[kGateCodes] + ntile * kTileCodeBytes + lane * 16;
+      const uint8_t* nuc = nex + A.off[kUpCodes] + ntile * kTileCodeBytes + lane * 16;
+      const uint32_t* ngf = reinterpret_cast<const uint32_t*>(nex + A.off[kGateFields] + ntile * kTileFieldBytes + lane * 12);
+      const uint32_t* nuf = reinterpret_cast<const uint32_t*>(nex + A.off[kUpFields] + ntile * kTileFieldBytes + lane * 12);
+      auto ring = [&](int m) {
+        auto chunk = [&](int j) {
+          const u32x4 x0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ngc + j * 1024));
+          const u32x4 x1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(nuc + j * 1024));
 #pragma unroll
-          for (int mm = 0; mm < 2; ++mm) acc[mm][0] = v4f{0.f, 0.f, 0.f, 0.f};
+          for (int i = 0; i < 4; ++i) {
+            ug.c[4 * j + i] = x0[i];
+            uu.c[4 * j + i] = x1[i];
+          }
+        };
+        auto field = [&](int i) {
+          ug.f[i] = __builtin_nontemporal_load(ngf + i);
+          uu.f[i] = __builtin_nontemporal_load(nuf + i);
+        };
+        if (m == 0) {
+          rs_gu = reinterpret_cast<const uint16_t*>(nex + A.off[lane < 16 ? kGateRs : kUpRs])[nrt * 16 + (lane & 15)];
+          chunk(0);
+        } else if (m == 1) {
+          field(0);
+        } else if (m == 2) {
+          chunk(1);
+        } else if (m == 3) {
+          chunk(2);
+        } else if (m == 4) {
+          field(1);
+        } else if (m == 5) {
+          chunk(3);
+        } else if (m == 6) {
+          chunk(4);
+          field(2);
         }
+      };
+      // one pass over the weight registers per group of five of the slot's tokens; the ring runs in
+      // the last pass only (an earlier pass must leave the registers as they are)
+      auto gu_pass = [&](uint32_t p, auto ringc) {
 #pragma unroll
         for (int cg = 0; cg < CG; ++cg) {
           uint32_t t;
@@ -579,6 +643,10 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
             acc[1][cg] = mfma(au, bc[cg], acc[1][cg]);
           }
           __builtin_amdgcn_sched_barrier(0);
+          if constexpr (decltype(ringc)::value) {
+            ring(m);
+            __builtin_amdgcn_sched_barrier(0);
+          }
           if (m < 7) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) { rg[i] = ng[i]; ru[i] = nu[i]; }
@@ -587,10 +655,19 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
             for (int cg = 0; cg < CG; ++cg) bc[cg] = bn[cg];
           }
         }
+      };
+      if constexpr (CMP) {
+        if (npass > 1) {
+          gu_pass(0u, std::false_type{});
+          write_part();  // (a slot with more than five tokens) the first pass's tokens are done
+#pragma unroll
+          for (int mm = 0; mm < 2; ++mm) acc[mm][0] = v4f{0.f, 0.f, 0.f, 0.f};
+        }
       }
+      gu_pass(npass - 1u, std::integral_constant<bool, RING>{});
     }
     AFFX_TRACE(3);
-    if (item != ~0u && S == 0 && lane < 32) {
+    if (!RING && item != ~0u && S == 0 && lane < 32) {
       // opaque at the use: no conversion is hoisted next to the load (its wait would then cover
       // every weight load issued before it)
       uint32_t rv = rs_gu;
@@ -604,11 +681,6 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
     // this unit (about 1 us).
     if constexpr (SINGLE && PREF) {
       if (wv >= epi_waves) load_down(has_down, g, wv);
-    }
-    // the next round's weights go out now (this round's are consumed), so their latency is
-    // spent on this round's epilogue
-    if constexpr (!SINGLE) {
-      if (rho + 1 < n_rounds) load_gu(gu_item(rho + 1));
     }
     write_part();  // (the last pass's tokens)
     __syncthreads();
