@@ -305,12 +305,21 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
     const uint32_t v = e[h] | (r < R ? 0u : ~0u);
     e[h] = v < A.n_experts ? v : ~0u;
   }
+  // Rounds kernels: only the plan wave (wave 0) finds every slot. The others stop once they know
+  // the slot of their round-0 item, issue its loads, and take the rest from the plan in LDS after
+  // the set-up barrier: with some 44 distinct experts at M = 8, every wave's full pass (one ballot
+  // round per slot, the three waves of a SIMD sharing its issue) took about 4 us of the set-up.
+  const uint32_t rt_per = A.inter / kTileRows;          // gate/up row tiles per expert
+  const uint32_t groups = kFW / nst;                    // items in flight per workgroup
+  const uint32_t q = wv / nst, S = wv % nst;            // this wave: group, column segment
+  const uint32_t item0 = g + A.n_wg * q;                // this wave's round-0 item (if there is one)
+  const uint32_t stop_at = (SINGLE || wv == 0) ? ~0u : item0 / rt_per + 1u;
   uint32_t se[2] = {~0u, ~0u};
   uint32_t rslot[2] = {~0u, ~0u};  // slot of route lane + 64 h
   uint32_t ns = 0;
   {
     uint64_t pend0 = __ballot(e[0] != ~0u), pend1 = __ballot(e[1] != ~0u);
-    while (pend0 | pend1) {
+    while ((pend0 | pend1) && (SINGLE || ns < stop_at)) {
       const uint32_t ex = pend0 ? __builtin_amdgcn_readlane(e[0], (uint32_t)__builtin_ctzll(pend0))
                                 : __builtin_amdgcn_readlane(e[1], (uint32_t)__builtin_ctzll(pend1));
       pend0 &= ~__ballot(e[0] == ex);
@@ -325,19 +334,24 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
     }
   }
   AFFX_TRACE(12);
-  // expert of slot s (s wave-uniform)
+  // expert of slot s (s wave-uniform): from the registers, or (rounds kernels, once the set-up
+  // barrier has passed) from the plan in LDS
+  bool plan_in_lds = false;
   auto slot_expert_of = [&](uint32_t s) -> uint32_t {
+    if (!SINGLE && plan_in_lds) return __builtin_amdgcn_readfirstlane(slot_expert[s]);
     return s < 64u ? __builtin_amdgcn_readlane(se[0], s) : __builtin_amdgcn_readlane(se[1], s - 64u);
   };
-
-  const uint32_t rt_per = A.inter / kTileRows;          // gate/up row tiles per expert
-  const uint32_t NI = ns * rt_per;                      // gate/up items of the layer
-  const uint32_t groups = kFW / nst;                    // items in flight per workgroup
-  const uint32_t q = wv / nst, S = wv % nst;            // this wave: group, column segment
-  const uint32_t my_items = g < NI ? (NI - g + A.n_wg - 1) / A.n_wg : 0;
-  const uint32_t rounds = (my_items + groups - 1) / groups;
+  // the counts that follow from the number of slots (rounds kernels: set again after the set-up
+  // barrier, when every wave knows it)
+  uint32_t NI, my_items, rounds, NU;
+  auto set_counts = [&]() {
+    NI = ns * rt_per;                                   // gate/up items of the layer
+    my_items = g < NI ? (NI - g + A.n_wg - 1) / A.n_wg : 0;
+    rounds = (my_items + groups - 1) / groups;
+    NU = ns * nsi;                                      // down units per output tile
+  };
+  set_counts();
   const uint32_t dtiles = A.hidden / kTileRows;
-  const uint32_t NU = ns * nsi;                         // down units per output tile
   const uint32_t copy4 = ((lane >> 1) & (KC - 1)) * 4u;
 
   // ---- 2. loads: gate/up pair of round 0 (+ its row scales), and the first down unit (+ row
@@ -385,11 +399,11 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
     rs_d = *reinterpret_cast<const uint2*>(ex + A.off[kDownRs] + (uint64_t)(tdd * 16 + 4 * (lane >> 4)) * 2);
     __builtin_amdgcn_sched_barrier(0);
   };
-  const bool has_down = g < dtiles && wv < NU;
+  bool has_down = g < dtiles && wv < NU;
   // the waves that write the SwiGLU output drain their memory counter before the release
   const uint32_t epi_waves = (groups * 16 * M + 63) / 64;
   // (batch 1 issues them after its share of the LDS set-up, step 3)
-  if constexpr (!SINGLE) load_gu(rounds > 0 ? gu_item(0) : ~0u);
+  if constexpr (!SINGLE) load_gu(q < groups && item0 / rt_per < ns ? item0 : ~0u);
   AFFX_TRACE(13);
   AFFX_TRACE(2);
 
@@ -399,6 +413,7 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   // Batch 1: the last wave writes it (the first waves split the activation; with both on wave 0
   // that wave's share of the set-up was the last to finish); larger batches: wave 0.
   if (wv == (SINGLE ? (uint32_t)kFW - 1u : 0u)) {
+    if (lane == 0) parts_in[1] = ns;  // (rounds kernels: the slot count for the other waves)
     if (lane < ns) slot_expert[lane] = se[0];
     if (lane + 64u < ns) slot_expert[lane + 64u] = se[1];
     for (uint32_t i = lane; i < ns * M; i += 64u) slot_w[i] = 0.f;
@@ -496,6 +511,10 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
   } else {
     __syncthreads();  // plan, activation terms and codebook copies visible
+    ns = __builtin_amdgcn_readfirstlane(parts_in[1]);
+    set_counts();
+    has_down = g < dtiles && wv < NU;
+    plan_in_lds = true;
   }
   AFFX_TRACE(1);
 
