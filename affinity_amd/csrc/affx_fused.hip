@@ -221,6 +221,8 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   if constexpr (SINGLE) {
     if (tid == 0) *parts_in = 0u;
     __syncthreads();
+  } else {
+    if (tid == 0) parts_in[2] = 0u;  // epilogue waves done (the set-up barrier publishes the zero)
   }
   // ---- 1. the small loads first (routes, then codebook and activation: loads complete in issue
   // order, so waiting for them never waits for the weight stream issued after them); every wave
@@ -553,13 +555,22 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
     for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
       for (int cg = 0; cg < CG; ++cg) acc[mm][cg] = v4f{0.f, 0.f, 0.f, 0.f};
-    if (RING && item != ~0u && S == 0 && lane < 32) {
-      // (the previous round's epilogue read rs_l before the round's closing barrier; the wait
-      // covers the row scales alone: they were requested first)
-      uint32_t rv = rs_gu;
-      AFFX_PIN(rv);
-      rs_l[q * 32 + lane] = __uint_as_float(rv << 16);
-    }
+    // (rounds kernels) this round's row scales: the ring requests the next round's into rs_gu
+    // during the steps; they were requested first, so this copy waits for them alone
+    const uint32_t rs_cur = rs_gu;
+    // Rounds kernels: the previous round's epilogue reads the partial sums and row scales in LDS
+    // that this round rewrites. Instead of a workgroup barrier after that epilogue (every wave
+    // idle for it), each wave counts itself in when its share of it is done, and a wave waits for
+    // all of them only where it first writes those arrays: almost always long done by then.
+    auto wait_epilogue = [&]() {
+      if (!SINGLE && rho > 0) {
+        if (lane == 0)
+          while (__hip_atomic_load(parts_in + 2, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < (uint32_t)kFW * rho)
+            __builtin_amdgcn_s_sleep(1);
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      }
+    };
     if (item != ~0u) {
       const uint32_t slot = item / rt_per;
       const uint32_t mask = __builtin_amdgcn_readfirstlane(slot_mask[slot]);
@@ -678,6 +689,7 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
       if constexpr (CMP) {
         if (npass > 1) {
           gu_pass(0u, std::false_type{});
+          wait_epilogue();
           write_part();  // (a slot with more than five tokens) the first pass's tokens are done
 #pragma unroll
           for (int mm = 0; mm < 2; ++mm) acc[mm][0] = v4f{0.f, 0.f, 0.f, 0.f};
@@ -701,6 +713,8 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
     if constexpr (SINGLE && PREF) {
       if (wv >= epi_waves) load_down(has_down, g, wv);
     }
+    wait_epilogue();
+    if (RING && item != ~0u && S == 0 && lane < 32) rs_l[q * 32 + lane] = __uint_as_float(rs_cur << 16);
     write_part();  // (the last pass's tokens)
     __syncthreads();
     AFFX_TRACE(11);
@@ -749,7 +763,10 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
       for (uint32_t et = et0; et < groups * 16 * M; et += kFT) epilogue(et);
     }
     if constexpr (!SINGLE) {
-      if (rho + 1 < n_rounds) __syncthreads();  // this round's partial sums read before they are rewritten
+      // this wave's reads of the round's partial sums and row scales are done (release: ordered
+      // before the next round's writes of the other waves, which acquire the count)
+      __builtin_amdgcn_wave_barrier();
+      if (lane == 0) __hip_atomic_fetch_add(parts_in + 2, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
   }
 
