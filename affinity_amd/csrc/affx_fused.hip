@@ -580,9 +580,9 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
       // the ring's part after step m of the last pass (unconditional: an absent next item reads
       // expert 0's first tile, never used, and straight-line loads keep the compiler's wait counts
       // exact). Step m + 1's table reads, issued before it, were the last reads of the registers
-      // each part overwrites: chunk 0 after step 1's, field dword 0 after step 2's, chunk 1 after
-      // step 3's, chunk 2 after step 4's, field dword 1 after step 5's, chunk 3 after step 6's,
-      // chunk 4 and field dword 2 after step 7's.
+      // each part overwrites: chunk 0 after step 1's, chunk 1 after step 3's, chunk 2 after step
+      // 4's, chunk 3 after step 6's, chunk 4 and the three field dwords (the last read by step 7's)
+      // after step 7's.
       const uint32_t nit = RING ? gu_item(rho + 1) : ~0u;
       const bool nok = nit != ~0u;
       const uint32_t nrt = nok ? nit % rt_per : 0u;
@@ -602,26 +602,27 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
             uu.c[4 * j + i] = x1[i];
           }
         };
-        auto field = [&](int i) {
-          ug.f[i] = __builtin_nontemporal_load(ngf + i);
-          uu.f[i] = __builtin_nontemporal_load(nuf + i);
+        auto fields = [&]() {  // (one 12-byte load each: fewer requests for the address unit)
+          const u32x3a gv = __builtin_nontemporal_load(reinterpret_cast<const u32x3a*>(ngf));
+          const u32x3a uv = __builtin_nontemporal_load(reinterpret_cast<const u32x3a*>(nuf));
+#pragma unroll
+          for (int i = 0; i < 3; ++i) {
+            ug.f[i] = gv[i];
+            uu.f[i] = uv[i];
+          }
         };
         if (m == 0) {
           rs_gu = reinterpret_cast<const uint16_t*>(nex + A.off[lane < 16 ? kGateRs : kUpRs])[nrt * 16 + (lane & 15)];
           chunk(0);
-        } else if (m == 1) {
-          field(0);
         } else if (m == 2) {
           chunk(1);
         } else if (m == 3) {
           chunk(2);
-        } else if (m == 4) {
-          field(1);
         } else if (m == 5) {
           chunk(3);
         } else if (m == 6) {
           chunk(4);
-          field(2);
+          fields();
         }
       };
       // one pass over the weight registers per group of five of the slot's tokens; the ring runs in

@@ -9,6 +9,8 @@ namespace affx {
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+// a unit's 12-byte field run (4-byte aligned): one global_load_dwordx3
+typedef uint32_t u32x3a __attribute__((ext_vector_type(3), aligned(4)));
 
 // ------------------------------------------------------------------------------------------------
 // shared pieces of the GEMV and GEMM kernels
