@@ -90,6 +90,8 @@ __host__ __device__ inline FusedLds fused_lds(uint32_t M) {
   L.plan = L.part + part_bytes;
   // slot_expert[128] slot_mask[128] rs[12][32] sigma[32] slot_w[128][M] slot_tok[128]
   L.count = L.plan + (3u * kPlanRoutes + kFW * 32u + 32u) * 4u + kPlanRoutes * M * 4u;
+  // four words: [0] waves counted in after the set-up (batch 1), [1] the slot count (rounds
+  // kernels, from the plan wave), [2] waves done with the current round's epilogue (rounds kernels)
   L.total = L.count + 16u;
   return L;
 }
@@ -309,8 +311,8 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   }
   // Rounds kernels: only the plan wave (wave 0) finds every slot. The others stop once they know
   // the slot of their round-0 item, issue its loads, and take the rest from the plan in LDS after
-  // the set-up barrier: with some 44 distinct experts at M = 8, every wave's full pass (one ballot
-  // round per slot, the three waves of a SIMD sharing its issue) took about 4 us of the set-up.
+  // the set-up barrier (with some 44 distinct experts at M = 8, every wave otherwise ran 44 ballot
+  // rounds before it requested its weights, the three waves of a SIMD sharing its issue).
   const uint32_t rt_per = A.inter / kTileRows;          // gate/up row tiles per expert
   const uint32_t groups = kFW / nst;                    // items in flight per workgroup
   const uint32_t q = wv / nst, S = wv % nst;            // this wave: group, column segment
@@ -555,8 +557,9 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
     for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
       for (int cg = 0; cg < CG; ++cg) acc[mm][cg] = v4f{0.f, 0.f, 0.f, 0.f};
-    // (rounds kernels) this round's row scales: the ring requests the next round's into rs_gu
-    // during the steps; they were requested first, so this copy waits for them alone
+    // (rounds kernels) this round's row scales, kept apart: the ring requests the next round's into
+    // rs_gu during the steps (row scales are requested first, so the wait for them at their use
+    // covers no weights)
     const uint32_t rs_cur = rs_gu;
     // Rounds kernels: the previous round's epilogue reads the partial sums and row scales in LDS
     // that this round rewrites. Instead of a workgroup barrier after that epilogue (every wave
