@@ -257,13 +257,15 @@ def _random_device_pool(ax, c1_codebook, n, hidden, inter, seed):
     return pool
 
 
-@pytest.mark.parametrize("M,k,pick", [(1, 6, 256), (2, 6, 256), (5, 6, 256), (8, 6, 256), (8, 6, 8)])
+@pytest.mark.parametrize("M,k,pick", [(1, 6, 256), (2, 6, 256), (5, 6, 256), (8, 6, 256), (8, 6, 8), (1, 16, 256),
+                                      (4, 16, 256)])
 def test_fused_decode_identical_to_staged_full_layer(ax, orc, c1_codebook, M, k, pick):
     """The benchmark layer shape (256 experts, hidden 4096, inter 2048): the one-launch decode
     equals the three staged launches bit for bit (same MFMA operands, same summation order),
     leaves its counters zero, and matches the oracle on every token. pick = 8: every route names
     one of 8 experts, so most slots serve six or more tokens and take the fused kernel's second
-    pass over their weights."""
+    pass over their weights. Top-16 routes give more gate/up items than one pass of the grid holds,
+    so batch 1 runs the rounds kernel too."""
     hidden, inter, n = 4096, 2048, 256
     pool = _random_device_pool(ax, c1_codebook, n, hidden, inter, seed=17 + M)
     rng = np.random.default_rng(100 + M + pick)
