@@ -174,12 +174,12 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// The kernel. CG: 16-column groups of the MFMA B operand (5 tokens each). KC: codebook copies.
-// MAXM: largest M this instantiation serves (sizes the per-thread activation registers). One
-// column group with MAXM > 5 compacts the columns: each slot's tokens fill the group pass by pass
+// The kernel. CG: 16-column groups of the MFMA B operand (five tokens each; one). KC: codebook
+// copies. MAXM: largest M this instantiation serves (sizes the per-thread activation registers).
+// With MAXM > 5 the columns are compacted: each slot's tokens fill the group pass by pass
 // (cmp_column), so a slot serving five tokens or fewer (almost all of them in a decode batch)
-// costs one MFMA per weight fragment instead of one per five tokens of the batch.
-// The down weights of the first unit are prefetched before the wait when CG = 1. SINGLE: at most
+// costs one MFMA per weight fragment. The down weights of each wave's first unit are requested
+// before the wait for the SwiGLU output. SINGLE: at most
 // one gate/up item and one down unit (per output tile) per wave, which keeps those two phases
 // loop-free (batch 1). ROT: the codebook copies include the rotated tables (one VALU op less
 // per code, twice the LDS). XF: how x is read (an XForm; the host picks it from the strides).
@@ -187,13 +187,15 @@ __device__ __forceinline__ float wave_max(float v) {
 template <int CG, int KC, int MAXM, bool SINGLE, bool ROT, int XF>
 __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   AFFX_DYN_LDS(lds);
+  // One column group: M <= 5 in fixed columns, M > 5 in compacted ones (two fixed groups of five
+  // tokens, the earlier form for M > 5, cost a second MFMA per weight fragment and did not leave
+  // the registers for the whole down B operand).
+  static_assert(CG == 1, "the fused decode holds one column group");
   // the first down unit is loaded while gate/up runs (one column group leaves the registers)
-  constexpr bool PREF = CG == 1;
+  constexpr bool PREF = true;
   // compacted columns: a slot with more than five tokens takes a second pass over its weights
   // (decoded again from the registers that hold them)
-  constexpr bool CMP = CG == 1 && MAXM > 5;
-  // the down phase loads its whole B operand at once (one column group fits the registers)
-  constexpr bool BPRE = CG == 1;
+  constexpr bool CMP = MAXM > 5;
   const uint32_t tid = threadIdx.x, lane = tid & 63, g = blockIdx.x;
   const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar registers
   const uint32_t M = A.M, K = A.K, R = M * K;
@@ -803,12 +805,8 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   //    poll, the workgroup barrier for the other waves): such a load reads past the non-coherent
   //    caches, so it needs no invalidate. The acquire's L2 invalidate, once per workgroup, had
   //    every workgroup of an XCD refetch the others' lines: 19.8 against 18.3 us per layer.
-  if (PREF) {
-    if (!SINGLE || n_rounds == 0 || wv < epi_waves) load_down(has_down, g, wv);
-    if (n_rounds > 0 && wv < epi_waves) __builtin_amdgcn_s_waitcnt(AFFX_VMCNT(7));
-  } else {
-    if (n_rounds > 0 && wv < epi_waves) __builtin_amdgcn_s_waitcnt(0);
-  }
+  if (!SINGLE || n_rounds == 0 || wv < epi_waves) load_down(has_down, g, wv);
+  if (n_rounds > 0 && wv < epi_waves) __builtin_amdgcn_s_waitcnt(AFFX_VMCNT(7));
   AFFX_TRACE(10);
   __syncthreads();
   // Batch 1 (one pass): no counter. Every workgroup, items or not, publishes epoch + 1 in its own
@@ -843,7 +841,7 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   // before the publish) do not depend on the activations, so all eight steps are decoded now,
   // while the layer publishes and this workgroup waits; after the release only the staging of
   // the activations and eight MFMAs remain for it
-  static_assert(!SINGLE || (CG == 1 && BPRE), "the one-pass down phase holds one column group");
+
   constexpr int kPreSteps = 8;
   v8i ad[SINGLE ? kPreSteps : 1];
   if constexpr (SINGLE) {
@@ -944,29 +942,22 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
           v4f acc[CG];
 #pragma unroll
           for (int cg = 0; cg < CG; ++cg) acc[cg] = v4f{0.f, 0.f, 0.f, 0.f};
-          // B: one column group (64 registers) is loaded whole up front, so the eight steps wait
-          // for one round trip; two column groups are loaded one step ahead
-          v8i bpre[BPRE ? 8 : 1];
-          v8i bc[CG];
-          if constexpr (BPRE) {
-            // only the lanes of used columns load (exec-masked); the others hold zeros, with no
-            // address-unit time spent on a zero run
+          // B: the column group (64 registers) is loaded whole up front, so the eight steps wait
+          // for one round trip; only the lanes of used columns load (exec-masked), the others hold
+          // zeros, with no address-unit time spent on a zero run
+          v8i bpre[8];
 #pragma unroll
-            for (int m = 0; m < 8; ++m) bpre[m] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
-            if (b.used) {
+          for (int m = 0; m < 8; ++m) bpre[m] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+          if (b.used) {
 #pragma unroll
-              for (int m = 0; m < 8; ++m) bpre[m] = b_step(b.p[0], m);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-          } else {
-#pragma unroll
-            for (int cg = 0; cg < CG; ++cg) bc[cg] = b_step(b.p[cg], 0);
+            for (int m = 0; m < 8; ++m) bpre[m] = b_step(b.p[0], m);
           }
+          __builtin_amdgcn_sched_barrier(0);
           // steps [m0, 8) decode their A fragments here (PRE: the first kPreSteps are in ad)
           constexpr int m0 = PRE ? kPreSteps : 0;
           if constexpr (PRE) {
 #pragma unroll
-            for (int m = 0; m < m0; ++m) acc[0] = mfma(ad[SINGLE ? m : 0], bpre[BPRE ? m : 0], acc[0]);
+            for (int m = 0; m < m0; ++m) acc[0] = mfma(ad[SINGLE ? m : 0], bpre[m], acc[0]);
           }
           {
             uint32_t raw[8];
@@ -977,7 +968,6 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
             for (int m = m0; m < 8; ++m) {
               uint32_t nraw[8];
               uint32_t nbv[2];
-              v8i bn[CG];
               if (m < 7) {
                 // the previous step's MFMA stays ahead of these reads (else the compiler sinks every
                 // MFMA below all eight steps' table reads and holds them all in registers)
@@ -985,27 +975,13 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
                 for (int cg = 0; cg < CG; ++cg) AFFX_PIN(acc[cg]);
                 pin_step(ud, m + 1);
                 lut_lookup_step<KC, ROT>(ud, lut, btbl, copy4, m + 1, nraw, nbv);
-                if constexpr (!BPRE) {
-#pragma unroll
-                  for (int cg = 0; cg < CG; ++cg) bn[cg] = b_step(b.p[cg], m + 1);
-                }
               }
-              const v8i a = lut_finish(raw, bv);
-              if constexpr (BPRE) {
-                acc[0] = mfma(a, bpre[m], acc[0]);
-              } else {
-#pragma unroll
-                for (int cg = 0; cg < CG; ++cg) acc[cg] = mfma(a, bc[cg], acc[cg]);
-              }
+              acc[0] = mfma(lut_finish(raw, bv), bpre[m], acc[0]);
               __builtin_amdgcn_sched_barrier(0);
               if (m < 7) {
 #pragma unroll
                 for (int i = 0; i < 8; ++i) raw[i] = nraw[i];
                 bv[0] = nbv[0]; bv[1] = nbv[1];
-                if constexpr (!BPRE) {
-#pragma unroll
-                  for (int cg = 0; cg < CG; ++cg) bc[cg] = bn[cg];
-                }
               }
             }
           }
