@@ -323,7 +323,41 @@ __global__ void __launch_bounds__(kFT) decode_fused_kernel(FusedArgs A) {
   uint32_t se[2] = {~0u, ~0u};
   uint32_t rslot[2] = {~0u, ~0u};  // slot of route lane + 64 h
   uint32_t ns = 0;
-  {
+  if (!SINGLE && MAXM > 1 && wv == 0 && M >= 2u) {
+    // The plan wave of the rounds kernels finds every slot at once (the ballot loop below takes one
+    // round per slot: some 4 us at M = 8, on the path to the set-up barrier). The LDS of the
+    // partial sums, unused until the rounds (1536 M bytes: room for 384 M experts), holds per
+    // expert its lowest route, then its slot. A route is its expert's first occurrence where it is
+    // that lowest route; its slot is its rank among the first occurrences.
+    uint32_t* fr = reinterpret_cast<uint32_t*>(lds + L.part);
+    for (uint32_t i = lane; i < A.n_experts; i += 64u) fr[i] = ~0u;
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      if (e[h] != ~0u) atomicMin(&fr[e[h]], lane + 64u * h);
+    __builtin_amdgcn_wave_barrier();
+    bool lead[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) lead[h] = e[h] != ~0u && fr[e[h]] == lane + 64u * h;
+    const uint64_t b0 = __ballot(lead[0]), b1 = __ballot(lead[1]);
+    const uint32_t n0 = (uint32_t)__builtin_popcountll(b0);
+    const uint32_t rank[2] = {
+        __builtin_amdgcn_mbcnt_hi((uint32_t)(b0 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b0, 0u)),
+        __builtin_amdgcn_mbcnt_hi((uint32_t)(b1 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b1, n0))};
+    ns = n0 + (uint32_t)__builtin_popcountll(b1);
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      if (lead[h]) {
+        fr[e[h]] = rank[h];
+        slot_expert[rank[h]] = e[h];
+      }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int h = 0; h < 2; ++h) rslot[h] = e[h] != ~0u ? fr[e[h]] : ~0u;
+    se[0] = lane < ns ? slot_expert[lane] : ~0u;
+    se[1] = lane + 64u < ns ? slot_expert[lane + 64u] : ~0u;
+  } else {
     uint64_t pend0 = __ballot(e[0] != ~0u), pend1 = __ballot(e[1] != ~0u);
     while ((pend0 | pend1) && (SINGLE || ns < stop_at)) {
       const uint32_t ex = pend0 ? __builtin_amdgcn_readlane(e[0], (uint32_t)__builtin_ctzll(pend0))
