@@ -100,6 +100,7 @@ inline uint32_t __builtin_amdgcn_perm(uint32_t s0, uint32_t s1, uint32_t sel) {
 #define __builtin_amdgcn_sched_barrier(x) ((void)0)
 #define __builtin_amdgcn_sched_group_barrier(m, n, id) ((void)0)
 #define __builtin_amdgcn_s_sleep(x) std::this_thread::yield()
+#define __builtin_amdgcn_s_setprio(x) ((void)0)
 #define __builtin_amdgcn_s_waitcnt(x) std::atomic_thread_fence(std::memory_order_seq_cst)
 // __hip_atomic_* are clang builtins on the host too; their scope constants are clang's
 #ifndef __HIP_MEMORY_SCOPE_AGENT
